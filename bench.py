@@ -1,0 +1,316 @@
+#!/usr/bin/env python3
+"""Throughput of wgblas's hot path on one MI355X, against its roofline.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
+
+Headline ("step"): BASELINE config 3 — sgemm fp32 column-major
+m = n = k = 8192 in all four (transA, transB) combinations, alpha = 1.5,
+beta = 0.5; one step = the four GEMMs. `value` = 4 * 2mnk / step time.
+Inputs: A, B, C drawn consecutively from one mulberry32(2) stream,
+uniform[-1, 1) (wgblas's randomFloat32Array), generated and resident in HBM
+before timing. Timing: HIP events recorded on the library's stream around
+the K timed steps.
+
+Also reported under "components", each timed the same way: sgemm 512^3
+(config 1), the ragged sgemm 8191 x 8193 x 4097 with ld = 1 (mod 64)
+(config 3), dgemm 4096^3 N/T alpha = beta = 1 (config 4), ssyrk lower
+n = 8192, k = 4096, 10 chained resident calls (config 5), and sdot / sasum /
+snrm2 / isamax at n = 2^28 plus the incx = 3, n = 2^26 variants (config 2).
+
+`roofline` is for the headline kernel: algorithmic flops per launch (2mnk)
+over the mean launch duration measured with events around each launch,
+against the fp32 dense MFMA peak (157.3 TFLOP/s). `cpu_baseline` times the
+oracle's restatement of the reference's per-element fp32 order on the host
+(one thread) over a bounded sample of the same workload.
+"""
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_FP32 = 157.3e12
+PEAK_FP64 = 78.6e12
+PEAK_HBM = 8.0e12
+METRIC = "sgemm/dgemm TFLOP/s + sdot/snrm2 GB/s on 1 MI355X, % of roofline"
+
+
+class HipEvents:
+    """hipEvent pairs on a given stream (libamdhip64 through ctypes)."""
+
+    def __init__(self, stream):
+        self.hip = C.CDLL("libamdhip64.so")
+        self.stream = C.c_void_p(stream)
+        self.a, self.b = C.c_void_p(), C.c_void_p()
+        assert self.hip.hipEventCreate(C.byref(self.a)) == 0
+        assert self.hip.hipEventCreate(C.byref(self.b)) == 0
+
+    def start(self):
+        assert self.hip.hipEventRecord(self.a, self.stream) == 0
+
+    def stop_ms(self):
+        assert self.hip.hipEventRecord(self.b, self.stream) == 0
+        assert self.hip.hipEventSynchronize(self.b) == 0
+        ms = C.c_float()
+        assert self.hip.hipEventElapsedTime(C.byref(ms), self.a, self.b) == 0
+        return ms.value
+
+
+def timed(ctx, ev, fn, steps, warmup):
+    """Runs fn() warmup + steps times; returns ms per step from events
+    recorded on the library's stream around the timed steps."""
+    for _ in range(warmup):
+        fn()
+    ctx.synchronize()
+    ev.start()
+    for _ in range(steps):
+        fn()
+    total = ev.stop_ms()
+    return total / steps
+
+
+def per_launch_ms(ctx, fn, reps):
+    """Mean duration of one library call measured by the library's events
+    (wgb_set_timing), i.e. around that call's kernels only."""
+    ctx.set_timing(True)
+    acc = 0.0
+    for _ in range(reps):
+        fn()
+        acc += ctx.last_time_ms()
+    ctx.set_timing(False)
+    return acc / reps
+
+
+def rf(bound, achieved, peak, unit, traffic=None):
+    return {"bound": bound, "achieved": achieved, "peak": peak, "unit": unit,
+            "frac": achieved / peak, "traffic": traffic}
+
+
+def load_traffic(name):
+    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE +
+    WRITE_SIZE, scaled by a copy-kernel calibration), recorded as
+    `name = bytes` lines in profiles/traffic.txt; None when not measured."""
+    path = os.path.join(ROOT, "profiles", "traffic.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if "=" in line and not line.lstrip().startswith("#"):
+            k, v = line.split("=", 1)
+            if k.strip() == name:
+                try:
+                    return float(v.split()[0])
+                except ValueError:
+                    return None
+    return None
+
+
+def bench_gemm_headline(ctx, ev, steps, warmup):
+    from wgblas_amd import NO_TRANS, TRANS
+
+    n = 8192
+    buf = ctx.empty(3 * n * n, np.float32)
+    ctx.fill_uniform(buf, -1.0, 1.0, 2)
+    A, B, Cm = buf.offset(0), buf.offset(n * n), buf.offset(2 * n * n)
+    combos = [(NO_TRANS, NO_TRANS), (NO_TRANS, TRANS), (TRANS, NO_TRANS), (TRANS, TRANS)]
+
+    def step():
+        for ta, tb in combos:
+            ctx.sgemm(ta, tb, n, n, n, 1.5, A, n, B, n, 0.5, Cm, n)
+
+    ms = timed(ctx, ev, step, steps, warmup)
+    launch_ms = {}
+    for ta, tb in combos:
+        launch_ms["NT"[ta] + "NT"[tb]] = per_launch_ms(
+            ctx, lambda: ctx.sgemm(ta, tb, n, n, n, 1.5, A, n, B, n, 0.5, Cm, n), max(3, steps))
+    buf.free()
+    flops = 2.0 * n * n * n
+    mean_launch = sum(launch_ms.values()) / len(launch_ms)
+    return ms, flops, launch_ms, mean_launch
+
+
+def bench_components(ctx, ev, quick):
+    from wgblas_amd import LOWER, NO_TRANS, TRANS
+
+    comps = {}
+    reps = 3 if quick else 10
+
+    # config 1: sgemm 512^3 NN, alpha 1, beta 0
+    n = 512
+    buf = ctx.empty(3 * n * n, np.float32)
+    ctx.fill_uniform(buf, -1.0, 1.0, 0)
+    A, B, Cm = buf.offset(0), buf.offset(n * n), buf.offset(2 * n * n)
+    f = lambda: ctx.sgemm(NO_TRANS, NO_TRANS, n, n, n, 1.0, A, n, B, n, 0.0, Cm, n)
+    ms = per_launch_ms(ctx, f, 20)
+    comps["sgemm_512"] = {"ms": ms, "tflops": 2 * n ** 3 / ms / 1e9,
+                          "frac_fp32_peak": 2 * n ** 3 / ms / 1e-3 / PEAK_FP32}
+    buf.free()
+
+    # config 3 ragged: 8191 x 8193 x 4097, ld = 1 (mod 64)
+    m, n, k = 8191, 8193, 4097
+    ld = lambda r: ((r + 63) // 64) * 64 + 1
+    lda, ldb, ldc = ld(m), ld(k), ld(m)
+    sa, sb, sc = lda * k, ldb * n, ldc * n
+    buf = ctx.empty(sa + sb + sc, np.float32)
+    ctx.fill_uniform(buf, -1.0, 1.0, 2)
+    A, B, Cm = buf.offset(0), buf.offset(sa), buf.offset(sa + sb)
+    f = lambda: ctx.sgemm(NO_TRANS, NO_TRANS, m, n, k, 1.5, A, lda, B, ldb, 0.5, Cm, ldc)
+    f()
+    ms = per_launch_ms(ctx, f, reps)
+    fl = 2.0 * m * n * k
+    comps["sgemm_ragged_8191x8193x4097"] = {"ms": ms, "tflops": fl / ms / 1e9,
+                                           "frac_fp32_peak": fl / ms / 1e-3 / PEAK_FP32,
+                                           "ld": [lda, ldb, ldc]}
+    buf.free()
+
+    # config 4: dgemm 4096^3, A N, B T, alpha = beta = 1, seed 3
+    n = 4096
+    buf = ctx.empty(3 * n * n, np.float64)
+    ctx.fill_uniform(buf, -1.0, 1.0, 3)
+    A, B, Cm = buf.offset(0), buf.offset(n * n), buf.offset(2 * n * n)
+    f = lambda: ctx.dgemm(NO_TRANS, TRANS, n, n, n, 1.0, A, n, B, n, 1.0, Cm, n)
+    f()
+    ms = per_launch_ms(ctx, f, reps)
+    fl = 2.0 * n ** 3
+    comps["dgemm_4096"] = {"ms": ms, "tflops": fl / ms / 1e9, "frac_fp64_peak": fl / ms / 1e-3 / PEAK_FP64,
+                           "traffic_bytes": load_traffic("dgemm_4096")}
+    buf.free()
+
+    # config 5: ssyrk lower, n = 8192, k = 4096, alpha 1, beta 0.25, 10 chained
+    n, k = 8192, 4096
+    dA = ctx.empty(n * k, np.float32)
+    ctx.fill_normal(dA, 4)
+    dC = ctx.empty(n * n, np.float32)
+    ctx.fill_uniform(dC, -1.0, 1.0, 5)
+    f = lambda: ctx.ssyrk(LOWER, NO_TRANS, n, k, 1.0, dA, n, 0.25, dC, n)
+    f()
+    ctx.synchronize()
+    ev.start()
+    for _ in range(10):
+        f()
+    ms = ev.stop_ms() / 10
+    fl = float(n) * (n + 1) * k
+    comps["ssyrk_8192x4096_x10"] = {"ms_per_call": ms, "tflops": fl / ms / 1e9,
+                                    "frac_fp32_peak": fl / ms / 1e-3 / PEAK_FP32}
+    dA.free()
+    dC.free()
+
+    # config 2: reductions at n = 2^28 (normal seed 1 / 2, planted duplicate max)
+    n = 1 << 28
+    dx, dy = ctx.empty(n, np.float32), ctx.empty(n, np.float32)
+    ctx.fill_normal(dx, 1)
+    ctx.fill_normal(dy, 2)
+    M = np.array([1e3, -1e3], np.float32)
+    ctx.h2d(dx.offset(n // 3), M[:1])
+    ctx.h2d(dx.offset(2 * n // 3), M[1:])
+    out = ctx.empty(4, np.float32)
+    iout = ctx.empty(1, np.int64)
+    lreps = 20 if quick else 100
+    red = {
+        "sdot": (lambda inc, nn: ctx.sdot_dev(nn, dx, inc, dy, inc, out), 8),
+        "sasum": (lambda inc, nn: ctx.sasum_dev(nn, dx, inc, out), 4),
+        "snrm2": (lambda inc, nn: ctx.snrm2_dev(nn, dx, inc, out), 4),
+        "isamax": (lambda inc, nn: ctx.isamax_dev(nn, dx, inc, iout), 4),
+    }
+    for name, (fn, bpe) in red.items():
+        fn(1, n)
+        ms = per_launch_ms(ctx, lambda: fn(1, n), lreps)
+        gbs = bpe * n / ms / 1e6
+        comps[f"{name}_2^28"] = {"ms": ms, "GB/s": gbs, "frac_hbm_peak": gbs * 1e9 / PEAK_HBM,
+                                 "traffic_bytes": load_traffic(f"{name}_2^28")}
+        ns = 1 << 26
+        ms = per_launch_ms(ctx, lambda: fn(3, ns), lreps)
+        useful = bpe * ns / ms / 1e6
+        comps[f"{name}_2^26_incx3"] = {"ms": ms, "GB/s_useful": useful,
+                                       "GB/s_span": 3 * useful,
+                                       "frac_hbm_peak_span": 3 * useful * 1e9 / PEAK_HBM}
+    dx.free()
+    dy.free()
+    return comps
+
+
+def cpu_baseline(budget_s=12.0):
+    """The oracle's fp32 restatement of the reference's per-element order
+    (oracle/oracle.c orc_sgemm_wgsl), one host thread, on a bounded sample of
+    the headline workload: the first columns of C for the (T, N) combination
+    of the 8192^3 problem, until `budget_s` seconds of CPU work."""
+    from oracle import orc
+
+    n = 8192
+    A = orc.random_f32(n * n, -1.0, 1.0, 2)
+    B = orc.random_f32(n * n, -1.0, 1.0, 3)
+    cols, flops, t_total = 0, 0.0, 0.0
+    chunk = 8
+    while t_total < budget_s and cols < n:
+        Cc = np.zeros(n * chunk, np.float32)
+        Bc = B[cols * n:(cols + chunk) * n]
+        t0 = time.perf_counter()
+        orc.sgemm_wgsl(0, 1, 0, n, chunk, n, 1.5, A, n, Bc, n, 0.5, Cc, n)
+        t_total += time.perf_counter() - t0
+        cols += chunk
+        flops += 2.0 * n * chunk * n
+    return {"value": flops / t_total / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
+            "sample": f"oracle orc_sgemm_wgsl (reference per-element fp32 order), transA=T transB=N, "
+                      f"m=k=8192, first {cols} columns of C ({flops:.3g} flop in {t_total:.1f} s)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--quick", action="store_true", help="fewer repetitions for the components")
+    ap.add_argument("--no-components", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
+              "the multi-GPU sharding is a design note, not a measured path.", file=sys.stderr)
+        return 2
+    rank = int(os.environ.get("RANK", "0"))
+
+    from wgblas_amd import Context
+
+    ctx = Context(0)
+    ev = HipEvents(ctx.stream)
+    name, arch = ctx.name()
+    ms, flops, launch_ms, mean_launch = bench_gemm_headline(ctx, ev, args.steps, args.warmup)
+    value = 4 * flops / (ms * 1e-3) / 1e12
+    achieved = flops / (mean_launch * 1e-3) / 1e12
+    comps = {} if args.no_components else bench_components(ctx, ev, args.quick)
+    ctx.close()
+    line = {
+        "metric": METRIC,
+        "value": value,
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (mulberry32 seeded uniform[-1,1), resident in HBM)",
+        "config": {"workload": "sgemm fp32 column-major m=n=k=8192, transA/transB in {N,T}^2 "
+                               "(4 GEMMs per step), alpha=1.5, beta=0.5, seed 2",
+                   "m": 8192, "n": 8192, "k": 8192, "device": name, "arch": arch},
+        "roofline": rf("mfma", achieved, PEAK_FP32 / 1e12, "TFLOP/s",
+                       load_traffic("sgemm_8192")),
+        "sgemm_launch_ms": launch_ms,
+        "components": comps,
+    }
+    if rank == 0 and not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline()
+    if rank == 0:
+        print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,196 @@
+/*
+ * wgblas_hip.h — C ABI of libwgblas_hip, the MI355X (gfx950) implementation
+ * of wgblas's data-parallel hot path: the GEMM family (sgemm, sgemmtr, ssyrk,
+ * dgemm) and the level-1 reductions (sdot, sasum, snrm2, isamax).
+ *
+ * Every entry point takes plain pointers and sizes. Matrices are
+ * COLUMN-MAJOR (element (i, j) of an ld-strided matrix sits at p[i + j*ld]);
+ * the JavaScript shim maps wgblas's row-major/column-major `layout` argument
+ * onto this frame. All device pointers must come from wgb_malloc (or any
+ * hipMalloc allocation on the context's device). Calls on one context are
+ * ordered on that context's single HIP stream.
+ *
+ * Each routine here replaces the WGSL dispatch path of the reference routine
+ * cited beside it (paths relative to the wgblas repository root). The
+ * reference does its argument checks in JavaScript; this library repeats the
+ * checks that protect memory (sizes, leading dimensions, null pointers) and
+ * reports them as WGB_ERR_INVALID_VALUE with a message from wgb_last_error().
+ *
+ * Return value of every function: WGB_OK (0) or a negative wgb_status.
+ */
+#ifndef WGBLAS_HIP_H
+#define WGBLAS_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum wgb_status {
+  WGB_OK = 0,
+  WGB_ERR_INVALID_VALUE = -1, /* bad argument (see wgb_last_error) */
+  WGB_ERR_HIP = -2,           /* a HIP runtime call failed */
+  WGB_ERR_ALLOC = -3,         /* device allocation failed */
+  WGB_ERR_NO_DEVICE = -4,     /* no HIP device with that index */
+  WGB_ERR_NOT_INITIALIZED = -5
+} wgb_status;
+
+/* trans arguments: wgblas's 'no-transpose' / 'transpose' strings. */
+enum { WGB_NO_TRANS = 0, WGB_TRANS = 1 };
+/* uplo arguments: wgblas's 'lower' / 'upper' strings (column-major frame). */
+enum { WGB_LOWER = 1, WGB_UPPER = 2 };
+
+typedef struct wgb_ctx wgb_ctx;
+
+/* ---- device / context ---------------------------------------------------- */
+
+/* Opens HIP device `device` and creates the context's stream.
+ * Replaces init() (src/init.mjs:31-108): returns a device handle in place of
+ * a GPUDevice. */
+int wgb_init(int device, wgb_ctx **out);
+
+/* Waits for the context's work, frees its scratch and stream.
+ * Replaces cleanup(device) (src/init.mjs:110-131). */
+int wgb_destroy(wgb_ctx *ctx);
+
+/* Writes the device's marketing name and gfx architecture name.
+ * Replaces gpuName() (src/init.mjs:133-143). */
+int wgb_device_name(wgb_ctx *ctx, char *name, size_t name_len, char *arch,
+                    size_t arch_len);
+
+/* Number of visible HIP devices (0 when none). */
+int wgb_device_count(int *count);
+
+/* Turns per-call GPU timing on or off. When on, every routine records HIP
+ * events around its kernels and wgb_last_time_ms() returns the span.
+ * Replaces init({benchmark:true}) + timestamp queries
+ * (src/util/benchmark.mjs:14-103, the routines' `gpuTimeMs`). */
+int wgb_set_timing(wgb_ctx *ctx, int enabled);
+int wgb_last_time_ms(wgb_ctx *ctx, float *ms);
+
+/* Blocks until all work on the context's stream is done. */
+int wgb_synchronize(wgb_ctx *ctx);
+
+/* The context's HIP stream (a hipStream_t), for callers that order their own
+ * work with the library's. */
+void *wgb_stream(wgb_ctx *ctx);
+
+/* Message for the last failure on the calling thread ("" if none). */
+const char *wgb_last_error(void);
+const char *wgb_status_string(int status);
+
+/* ---- device memory (GpuVector / GpuMatrix residency) ----------------------- */
+
+/* Device allocation of `bytes` (256-byte aligned). Replaces the GPUBuffer
+ * that GpuVector.from / GpuMatrix.from create through uploadBuffer
+ * (src/classes/GpuVector.mjs:41-74, src/classes/GpuMatrix.mjs:149-246,
+ * src/util/buffer.mjs:58-77). */
+int wgb_malloc(wgb_ctx *ctx, size_t bytes, void **dptr);
+/* Replaces GpuVector/GpuMatrix.destroy() (GpuVector.mjs:102, GpuMatrix.mjs:310). */
+int wgb_free(wgb_ctx *ctx, void *dptr);
+/* Host -> device copy, ordered on the context's stream and complete on return.
+ * Replaces queue.writeBuffer (src/util/buffer.mjs:73-74). */
+int wgb_memcpy_h2d(wgb_ctx *ctx, void *dst, const void *src, size_t bytes);
+/* Device -> host copy, complete on return. Replaces stageReadback +
+ * extractResult (src/util/buffer.mjs:160-185, src/util/result.mjs:18-30). */
+int wgb_memcpy_d2h(wgb_ctx *ctx, void *dst, const void *src, size_t bytes);
+/* Device -> device copy on the context's stream (asynchronous). */
+int wgb_memcpy_d2d(wgb_ctx *ctx, void *dst, const void *src, size_t bytes);
+
+/* ---- seeded synthetic inputs --------------------------------------------- */
+
+/* Fills d_out[0..n) with wgblas's randomFloat32Array(n, low, high, seed)
+ * sequence, bit for bit (mulberry32, src/random/random.mjs:4-19), generated
+ * on the device. */
+int wgb_fill_uniform_f32(wgb_ctx *ctx, float *d_out, int64_t n, double low,
+                         double high, uint32_t seed);
+/* randomFloat64Array(n, low, high, seed) (src/random/random.mjs:21-26). */
+int wgb_fill_uniform_f64(wgb_ctx *ctx, double *d_out, int64_t n, double low,
+                         double high, uint32_t seed);
+/* normal(0,1) samples, defined by this library (the reference has none):
+ * Box-Muller over the same mulberry32(seed) stream. Pair p uses draws
+ * u1 = next() (the 2p-th) and u2 = next() (the (2p+1)-th), r = sqrt(-2 ln(1-u1)),
+ * t = 2 pi u2; element 2p = r cos t, element 2p+1 = r sin t, in float64,
+ * rounded to float32. */
+int wgb_fill_normal_f32(wgb_ctx *ctx, float *d_out, int64_t n, uint32_t seed);
+
+/* ---- level 3 ------------------------------------------------------------- */
+
+/* C <- alpha*op(A)*op(B) + beta*C, C m-by-n, op(A) m-by-k, op(B) k-by-n.
+ * beta == 0 never reads C; alpha == 0 or k == 0 reads neither A nor B
+ * (C <- beta*C). m == 0 or n == 0 is a no-op.
+ * Replaces sgemm (src/sgemm/sgemm.mjs:25-269, kernels
+ * src/shaders/sgemm_large.wgsl, sgemm_small.wgsl). */
+int wgb_sgemm(wgb_ctx *ctx, int transA, int transB, int64_t m, int64_t n,
+              int64_t k, float alpha, const float *A, int64_t lda,
+              const float *B, int64_t ldb, float beta, float *C, int64_t ldc);
+
+/* Same as wgb_sgemm on the uplo triangle of the m-by-n C only
+ * (WGB_LOWER: i >= j, WGB_UPPER: i <= j); the other triangle is never read
+ * nor written. Replaces sgemmtr (src/sgemmtr/sgemmtr.mjs:25-278). */
+int wgb_sgemmtr(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m,
+                int64_t n, int64_t k, float alpha, const float *A, int64_t lda,
+                const float *B, int64_t ldb, float beta, float *C,
+                int64_t ldc);
+
+/* C <- alpha*op(A)*op(A)^T + beta*C on the uplo triangle of the n-by-n C;
+ * op(A) is n-by-k (trans == WGB_NO_TRANS) or A^T for a k-by-n A.
+ * Replaces ssyrk (src/ssyrk/ssyrk.mjs:28-244), without its A->B copy. */
+int wgb_ssyrk(wgb_ctx *ctx, int uplo, int trans, int64_t n, int64_t k,
+              float alpha, const float *A, int64_t lda, float beta, float *C,
+              int64_t ldc);
+
+/* Native-FP64 dgemm with wgblas's dgemm contract, including the quick return
+ * (alpha == 0 or k == 0) and beta == 1 -> C untouched.
+ * Replaces dgemm (src/dgemm/dgemm.mjs:23-318, kernel
+ * src/shaders/dgemm_small.wgsl and the double-double library
+ * src/shaders/f64/). */
+int wgb_dgemm(wgb_ctx *ctx, int transA, int transB, int64_t m, int64_t n,
+              int64_t k, double alpha, const double *A, int64_t lda,
+              const double *B, int64_t ldb, double beta, double *C,
+              int64_t ldc);
+
+/* ---- level 1 reductions --------------------------------------------------- */
+/* n <= 0 returns 0 (index -1) without touching the device. incx, incy must be
+ * positive. The host-result forms block until the value is on the host; the
+ * `_dev` forms write the result to device memory and return without
+ * synchronising. Both run a fixed two-pass reduction whose summation order
+ * depends only on n, so results are reproducible run to run. */
+
+/* sum x[i*incx]*y[i*incy] in float32. Replaces sdot (src/sdot/sdot.mjs:18-117,
+ * src/shaders/sdot.wgsl, src/shaders/reduction/sum.wgsl). */
+int wgb_sdot(wgb_ctx *ctx, int64_t n, const float *x, int64_t incx,
+             const float *y, int64_t incy, float *result);
+int wgb_sdot_dev(wgb_ctx *ctx, int64_t n, const float *x, int64_t incx,
+                 const float *y, int64_t incy, float *d_result);
+
+/* sum |x[i*incx]|. Replaces sasum (src/sasum/sasum.mjs, src/shaders/sasum.wgsl). */
+int wgb_sasum(wgb_ctx *ctx, int64_t n, const float *x, int64_t incx,
+              float *result);
+int wgb_sasum_dev(wgb_ctx *ctx, int64_t n, const float *x, int64_t incx,
+                  float *d_result);
+
+/* Overflow-safe Euclidean norm: Blue's three accumulators with wgblas's
+ * thresholds and LAPACK 3.10 combine. Replaces snrm2 (src/snrm2/snrm2.mjs,
+ * src/shaders/snrm2.wgsl, src/shaders/reduction/scaledSum.wgsl). */
+int wgb_snrm2(wgb_ctx *ctx, int64_t n, const float *x, int64_t incx,
+              float *result);
+int wgb_snrm2_dev(wgb_ctx *ctx, int64_t n, const float *x, int64_t incx,
+                  float *d_result);
+
+/* 0-based logical index of the first max |x[i*incx]|; NaN never wins, an
+ * all-NaN vector gives 0, n <= 0 gives -1. Replaces isamax
+ * (src/isamax/isamax.mjs, src/shaders/isamax.wgsl,
+ * src/shaders/reduction/argmax.wgsl). */
+int wgb_isamax(wgb_ctx *ctx, int64_t n, const float *x, int64_t incx,
+               int64_t *result);
+int wgb_isamax_dev(wgb_ctx *ctx, int64_t n, const float *x, int64_t incx,
+                   int64_t *d_result);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* WGBLAS_HIP_H */

@@ -1,0 +1,436 @@
+/*
+ * oracle.c — CPU restatement of wgblas's hot path, used ONLY as the checker
+ * in tests, in __graft_entry__.smoke() and in bench.py's cpu_baseline leg.
+ * Nothing in the product (wgblas_amd/) links, loads or calls this file.
+ *
+ * Two kinds of functions live here:
+ *
+ *  1. "wgsl" restatements: the reference's own arithmetic order, in IEEE
+ *     float32, so they reproduce what wgblas's WGSL kernels compute (up to a
+ *     shader compiler's choice to fuse a multiply-add):
+ *       orc_random_f32/f64  src/random/random.mjs:4-26 (mulberry32)
+ *       orc_sdot_wgsl       src/shaders/sdot.wgsl:19-53 + reduction/sum.wgsl:12-26,
+ *                           dispatch src/sdot/sdot.mjs:89-92 (2*WGS workgroups of WGS=64)
+ *       orc_sasum_wgsl      src/shaders/sasum.wgsl:17-51 + reduction/sum.wgsl
+ *       orc_snrm2_wgsl      src/shaders/snrm2.wgsl:33-95 + reduction/scaledSum.wgsl:32-101
+ *       orc_isamax_wgsl     src/shaders/isamax.wgsl:19-82 + reduction/argmax.wgsl:96-125
+ *       orc_sgemm_wgsl      src/shaders/sgemm_large.wgsl:112-308 per-element order
+ *                           (sequential k, then alpha*acc, then + beta*C, masks)
+ *
+ *  2. extended-precision references that the error bounds are measured
+ *     against: orc_gemm_ld (long double accumulation, any uplo/trans, with the
+ *     reference's alpha/beta rules of sgemm_large.wgsl:299-304 and
+ *     dgemm.mjs:177-179), orc_dot_ld, orc_sum_abs_ld, orc_nrm2_ld,
+ *     orc_isamax_brute (first index of max |x|, NaN skipped).
+ *
+ * The normal(0,1) sampler (orc_random_normal_f32) restates the sampler this
+ * build defines (include/wgblas_hip.h, wgb_fill_normal_f32); the reference
+ * has none.
+ *
+ * Matrices are column-major with a leading dimension, as in the C ABI.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+
+#define WGS 64
+#define NWG (2 * WGS)
+
+/* ---- mulberry32 (src/random/random.mjs:4-12) ---------------------------- */
+
+static uint32_t mulberry_next(uint32_t *state) {
+  uint32_t a = *state + 0x6d2b79f5u;
+  *state = a;
+  uint32_t t = (a ^ (a >> 15)) * (1u | a);
+  t = (t + (t ^ (t >> 7)) * (61u | t)) ^ t;
+  return t ^ (t >> 14);
+}
+
+/* randomFloat32Array(n, low, high, seed): low + next()*(high-low) in double,
+ * stored to float32 (src/random/random.mjs:14-19). */
+void orc_random_f32(int64_t n, double low, double high, uint32_t seed, float *out) {
+  uint32_t s = seed;
+  volatile double range = high - low;
+  for (int64_t i = 0; i < n; ++i) {
+    volatile double u = (double)mulberry_next(&s) / 4294967296.0;
+    volatile double prod = u * range;
+    out[i] = (float)(low + prod);
+  }
+}
+
+void orc_random_f64(int64_t n, double low, double high, uint32_t seed, double *out) {
+  uint32_t s = seed;
+  volatile double range = high - low;
+  for (int64_t i = 0; i < n; ++i) {
+    volatile double u = (double)mulberry_next(&s) / 4294967296.0;
+    volatile double prod = u * range;
+    out[i] = low + prod;
+  }
+}
+
+/* The build's normal(0,1) sampler: Box-Muller over the mulberry32 stream,
+ * pair p from draws 2p and 2p+1, r = sqrt(-2 ln(1-u1)), t = 2 pi u2. */
+void orc_random_normal_f32(int64_t n, uint32_t seed, float *out) {
+  uint32_t s = seed;
+  const double two_pi = 6.283185307179586476925286766559;
+  for (int64_t i = 0; i < n; i += 2) {
+    double u1 = (double)mulberry_next(&s) / 4294967296.0;
+    double u2 = (double)mulberry_next(&s) / 4294967296.0;
+    double r = sqrt(-2.0 * log(1.0 - u1));
+    double t = two_pi * u2;
+    out[i] = (float)(r * cos(t));
+    if (i + 1 < n) out[i + 1] = (float)(r * sin(t));
+  }
+}
+
+/* ---- level-1 reductions in the reference's order -------------------------- */
+
+/* LDS tree over WGS values: for s = 32..1, tile[l] += tile[l+s]. */
+static float tree_sum(float *t, int len) {
+  for (int s = len / 2; s > 0; s >>= 1)
+    for (int l = 0; l < s; ++l) t[l] = t[l] + t[l + s];
+  return t[0];
+}
+
+/* reduction/sum.wgsl:12-26: tile[i] = p[i] + p[i+WGS], then the tree. */
+static float sum_pass2(const float *partials) {
+  float tile[WGS];
+  for (int i = 0; i < WGS; ++i) tile[i] = partials[i] + partials[i + WGS];
+  return tree_sum(tile, WGS);
+}
+
+float orc_sdot_wgsl(int64_t n, const float *x, int64_t incx, const float *y, int64_t incy) {
+  if (n <= 0) return 0.0f; /* src/sdot/sdot.mjs:40 */
+  float partials[NWG];
+  float tile[WGS];
+  const int64_t stride = (int64_t)NWG * WGS;
+  const int64_t n4_floor = (n / (4 * stride)) * (4 * stride);
+  for (int w = 0; w < NWG; ++w) {
+    for (int l = 0; l < WGS; ++l) {
+      int64_t gid = (int64_t)w * WGS + l;
+      float a0 = 0, a1 = 0, a2 = 0, a3 = 0;
+      for (int64_t id = gid; id < n4_floor; id += 4 * stride) {
+        a0 += x[id * incx] * y[id * incy];
+        a1 += x[(id + stride) * incx] * y[(id + stride) * incy];
+        a2 += x[(id + 2 * stride) * incx] * y[(id + 2 * stride) * incy];
+        a3 += x[(id + 3 * stride) * incx] * y[(id + 3 * stride) * incy];
+      }
+      for (int64_t id = n4_floor + gid; id < n; id += stride) a0 += x[id * incx] * y[id * incy];
+      tile[l] = a0 + a1 + a2 + a3;
+    }
+    partials[w] = tree_sum(tile, WGS);
+  }
+  return sum_pass2(partials);
+}
+
+float orc_sasum_wgsl(int64_t n, const float *x, int64_t incx) {
+  if (n <= 0) return 0.0f; /* src/sasum/sasum.mjs:28 */
+  float partials[NWG];
+  float tile[WGS];
+  const int64_t stride = (int64_t)NWG * WGS;
+  const int64_t n4_floor = (n / (4 * stride)) * (4 * stride);
+  for (int w = 0; w < NWG; ++w) {
+    for (int l = 0; l < WGS; ++l) {
+      int64_t gid = (int64_t)w * WGS + l;
+      float a0 = 0, a1 = 0, a2 = 0, a3 = 0;
+      for (int64_t id = gid; id < n4_floor; id += 4 * stride) {
+        a0 += fabsf(x[id * incx]);
+        a1 += fabsf(x[(id + stride) * incx]);
+        a2 += fabsf(x[(id + 2 * stride) * incx]);
+        a3 += fabsf(x[(id + 3 * stride) * incx]);
+      }
+      for (int64_t id = n4_floor + gid; id < n; id += stride) a0 += fabsf(x[id * incx]);
+      tile[l] = a0 + a1 + a2 + a3;
+    }
+    partials[w] = tree_sum(tile, WGS);
+  }
+  return sum_pass2(partials);
+}
+
+/* snrm2.wgsl:33-36 */
+#define TSML 0x1p-63f
+#define TBIG 0x1p50f
+#define SSML 0x1p75f
+#define SBIG 0x1p-76f
+
+typedef struct {
+  float big, med, sml;
+} nrm3;
+
+/* snrm2.wgsl:40-51 accum(): NaN fails both tests and lands in medium. */
+static nrm3 nrm_accum(nrm3 s, float xi) {
+  float ax = fabsf(xi);
+  int big = ax > TBIG;
+  int sml = ax < TSML;
+  float yb = ax * SBIG;
+  float ys = ax * SSML;
+  nrm3 r;
+  r.big = s.big + (big ? yb * yb : 0.0f);
+  r.med = s.med + ((big || sml) ? 0.0f : ax * ax);
+  r.sml = s.sml + (sml ? ys * ys : 0.0f);
+  return r;
+}
+
+static nrm3 nrm_add(nrm3 a, nrm3 b) {
+  nrm3 r = {a.big + b.big, a.med + b.med, a.sml + b.sml};
+  return r;
+}
+
+/* scaledSum.wgsl:117-136 */
+static int is_nan_bits(float v) {
+  uint32_t b;
+  memcpy(&b, &v, 4);
+  return (b & 0x7fffffffu) > 0x7f800000u;
+}
+
+static float ldexp_bits(float v, int e) {
+  uint32_t bits;
+  memcpy(&bits, &v, 4);
+  uint32_t sign = bits & 0x80000000u;
+  int ev = (int)((bits >> 23) & 0xffu);
+  if (ev == 255) return v;
+  int en = ev + e;
+  uint32_t out;
+  if (ev == 0 || en <= 0) out = sign;
+  else if (en >= 255) out = sign | 0x7f800000u;
+  else out = (bits & 0x807fffffu) | ((uint32_t)en << 23);
+  float r;
+  memcpy(&r, &out, 4);
+  return r;
+}
+
+/* scaledSum.wgsl:159-196: the LAPACK 3.10 combine. */
+float orc_nrm_combine(float abig, float amed, float asml) {
+  if (is_nan_bits(amed)) return amed;
+  int med_live = amed > 0.0f;
+  float scl = 1.0f;
+  float sumsq = amed;
+  if (abig > 0.0f) {
+    if (med_live) abig = abig + ldexp_bits(amed, -152);
+    scl = 1.0f / SBIG;
+    sumsq = abig;
+  } else if (asml > 0.0f) {
+    if (med_live) {
+      amed = sqrtf(amed);
+      asml = sqrtf(asml) / SSML;
+      float ymax = asml > amed ? asml : amed;
+      float ymin = asml < amed ? asml : amed;
+      float q = ymin / ymax;
+      sumsq = ymax * ymax * (1.0f + q * q);
+    } else {
+      scl = 1.0f / SSML;
+      sumsq = asml;
+    }
+  }
+  return scl * sqrtf(sumsq);
+}
+
+float orc_snrm2_wgsl(int64_t n, const float *x, int64_t incx) {
+  if (n <= 0) return 0.0f; /* src/snrm2/snrm2.mjs:28 */
+  nrm3 partials[NWG];
+  nrm3 tile[WGS];
+  const int64_t stride = (int64_t)NWG * WGS;
+  const int64_t n4_floor = (n / (4 * stride)) * (4 * stride);
+  const nrm3 zero = {0, 0, 0};
+  for (int w = 0; w < NWG; ++w) {
+    for (int l = 0; l < WGS; ++l) {
+      int64_t gid = (int64_t)w * WGS + l;
+      nrm3 a0 = zero, a1 = zero, a2 = zero, a3 = zero;
+      for (int64_t id = gid; id < n4_floor; id += 4 * stride) {
+        a0 = nrm_accum(a0, x[id * incx]);
+        a1 = nrm_accum(a1, x[(id + stride) * incx]);
+        a2 = nrm_accum(a2, x[(id + 2 * stride) * incx]);
+        a3 = nrm_accum(a3, x[(id + 3 * stride) * incx]);
+      }
+      for (int64_t id = n4_floor + gid; id < n; id += stride) a0 = nrm_accum(a0, x[id * incx]);
+      tile[l] = nrm_add(nrm_add(a0, a1), nrm_add(a2, a3)); /* snrm2.wgsl:80 */
+    }
+    for (int s = WGS / 2; s > 0; s >>= 1)
+      for (int l = 0; l < s; ++l) tile[l] = nrm_add(tile[l], tile[l + s]);
+    partials[w] = tile[0];
+  }
+  for (int i = 0; i < WGS; ++i) tile[i] = nrm_add(partials[i], partials[i + WGS]);
+  for (int s = WGS / 2; s > 0; s >>= 1)
+    for (int l = 0; l < s; ++l) tile[l] = nrm_add(tile[l], tile[l + s]);
+  return orc_nrm_combine(tile[0].big, tile[0].med, tile[0].sml);
+}
+
+/* isamax.wgsl:51-58 / argmax.wgsl: b wins when larger, or equal and lower index. */
+static int amax_better(float bv, uint32_t bi, float av, uint32_t ai) {
+  return bv > av || (bv == av && bi < ai);
+}
+
+int64_t orc_isamax_wgsl(int64_t n, const float *x, int64_t incx) {
+  if (n <= 0) return -1; /* src/isamax/isamax.mjs:30 */
+  float pv[NWG];
+  uint32_t pi[NWG];
+  float tv[WGS];
+  uint32_t ti[WGS];
+  const int64_t stride = (int64_t)NWG * WGS;
+  const int64_t n4_floor = (n / (4 * stride)) * (4 * stride);
+  for (int w = 0; w < NWG; ++w) {
+    for (int l = 0; l < WGS; ++l) {
+      int64_t gid = (int64_t)w * WGS + l;
+      float bv[4] = {-1.0f, -1.0f, -1.0f, -1.0f};
+      uint32_t bi[4] = {0, 0, 0, 0};
+      for (int64_t id = gid; id < n4_floor; id += 4 * stride)
+        for (int u = 0; u < 4; ++u) {
+          float v = fabsf(x[(id + u * stride) * incx]);
+          if (v > bv[u]) {
+            bv[u] = v;
+            bi[u] = (uint32_t)(id + u * stride);
+          }
+        }
+      for (int64_t id = n4_floor + gid; id < n; id += stride) {
+        float v = fabsf(x[id * incx]);
+        if (v > bv[0]) {
+          bv[0] = v;
+          bi[0] = (uint32_t)id;
+        }
+      }
+      for (int u = 1; u < 4; ++u)
+        if (amax_better(bv[u], bi[u], bv[0], bi[0])) {
+          bv[0] = bv[u];
+          bi[0] = bi[u];
+        }
+      tv[l] = bv[0];
+      ti[l] = bi[0];
+    }
+    for (int s = WGS / 2; s > 0; s >>= 1)
+      for (int l = 0; l < s; ++l)
+        if (amax_better(tv[l + s], ti[l + s], tv[l], ti[l])) {
+          tv[l] = tv[l + s];
+          ti[l] = ti[l + s];
+        }
+    pv[w] = tv[0];
+    pi[w] = ti[0];
+  }
+  for (int i = 0; i < WGS; ++i) {
+    if (amax_better(pv[i + WGS], pi[i + WGS], pv[i], pi[i])) {
+      tv[i] = pv[i + WGS];
+      ti[i] = pi[i + WGS];
+    } else {
+      tv[i] = pv[i];
+      ti[i] = pi[i];
+    }
+  }
+  for (int s = WGS / 2; s > 0; s >>= 1)
+    for (int l = 0; l < s; ++l)
+      if (amax_better(tv[l + s], ti[l + s], tv[l], ti[l])) {
+        tv[l] = tv[l + s];
+        ti[l] = ti[l + s];
+      }
+  return (int64_t)ti[0];
+}
+
+/* ---- extended-precision references for the bounds ------------------------ */
+
+double orc_dot_ld(int64_t n, const float *x, int64_t incx, const float *y, int64_t incy,
+                  double *sum_abs) {
+  long double s = 0, a = 0;
+  for (int64_t i = 0; i < n; ++i) {
+    long double p = (long double)x[i * incx] * (long double)y[i * incy];
+    s += p;
+    a += fabsl(p);
+  }
+  if (sum_abs) *sum_abs = (double)a;
+  return (double)s;
+}
+
+double orc_sum_abs_ld(int64_t n, const float *x, int64_t incx) {
+  long double a = 0;
+  for (int64_t i = 0; i < n; ++i) a += fabsl((long double)x[i * incx]);
+  return (double)a;
+}
+
+double orc_nrm2_ld(int64_t n, const float *x, int64_t incx) {
+  long double s = 0;
+  for (int64_t i = 0; i < n; ++i) {
+    long double v = (long double)x[i * incx];
+    s += v * v;
+  }
+  return (double)sqrtl(s);
+}
+
+/* First index of max |x|, NaN never selected, all-NaN -> 0, n <= 0 -> -1
+ * (src/isamax/isamax.d.mts; tests/isamax/src/test.isamax.js:97-139). */
+int64_t orc_isamax_brute(int64_t n, const float *x, int64_t incx) {
+  if (n <= 0) return -1;
+  int64_t best = 0;
+  float bv = -1.0f;
+  for (int64_t i = 0; i < n; ++i) {
+    float v = fabsf(x[i * incx]);
+    if (v > bv) {
+      bv = v;
+      best = i;
+    }
+  }
+  return best;
+}
+
+/* op(M)[r][c] of a column-major matrix with leading dimension ld. */
+static inline double op_elem(const double *M, int64_t ld, int trans, int64_t r, int64_t c) {
+  return trans ? M[c + r * ld] : M[r + c * ld];
+}
+
+/* out (m x n, leading dimension ldo, column-major) <- alpha*op(A)op(B) + beta*C
+ * in long double, on the uplo part (0 full, 1 lower i>=j, 2 upper i<=j);
+ * elements outside it are copied from C. absdot (may be NULL) receives
+ * sum_p |op(A)[i,p]*op(B)[p,j]|. alpha == 0 or k == 0 never reads A or B,
+ * beta == 0 never reads C (src/shaders/sgemm_large.wgsl:299-304). */
+void orc_gemm_ld(int uplo, int transA, int transB, int64_t m, int64_t n, int64_t k, double alpha,
+                 const double *A, int64_t lda, const double *B, int64_t ldb, double beta,
+                 const double *C, int64_t ldc, double *out, int64_t ldo, double *absdot) {
+  for (int64_t j = 0; j < n; ++j) {
+    for (int64_t i = 0; i < m; ++i) {
+      int in_tri = uplo == 0 || (uplo == 1 && i >= j) || (uplo == 2 && i <= j);
+      if (!in_tri) {
+        out[i + j * ldo] = C[i + j * ldc];
+        if (absdot) absdot[i + j * ldo] = 0.0;
+        continue;
+      }
+      long double s = 0, a = 0;
+      if (alpha != 0.0)
+        for (int64_t p = 0; p < k; ++p) {
+          long double prod =
+              (long double)op_elem(A, lda, transA, i, p) * (long double)op_elem(B, ldb, transB, p, j);
+          s += prod;
+          a += fabsl(prod);
+        }
+      long double v = (alpha == 0.0) ? 0.0L : (long double)alpha * s;
+      if (beta != 0.0) v += (long double)beta * (long double)C[i + j * ldc];
+      out[i + j * ldo] = (double)v;
+      if (absdot) absdot[i + j * ldo] = (double)a;
+    }
+  }
+}
+
+/* The reference's per-element fp32 order (sgemm_large.wgsl:221-233, 288-308):
+ * acc += a*b sequentially over k (product rounded, then the sum), then
+ * alpha*acc, then acc + beta*C; alpha == 0 gives a 0 product term and
+ * beta == 0 leaves C unread. Used as the timed CPU baseline. C is updated in
+ * place on the uplo part. */
+void orc_sgemm_wgsl(int uplo, int transA, int transB, int64_t m, int64_t n, int64_t k,
+                    float alpha, const float *A, int64_t lda, const float *B, int64_t ldb,
+                    float beta, float *Cm, int64_t ldc) {
+  for (int64_t j = 0; j < n; ++j) {
+    for (int64_t i = 0; i < m; ++i) {
+      int in_tri = uplo == 0 || (uplo == 1 && i >= j) || (uplo == 2 && i <= j);
+      if (!in_tri) continue;
+      float acc = 0.0f;
+      for (int64_t p = 0; p < k; ++p) {
+        float a = transA ? A[p + i * lda] : A[i + p * lda];
+        float b = transB ? B[j + p * ldb] : B[p + j * ldb];
+        volatile float prod = a * b;
+        acc = acc + prod;
+      }
+      float r = alpha == 0.0f ? 0.0f : alpha * acc;
+      float *cp = &Cm[i + j * ldc];
+      if (beta != 0.0f) {
+        volatile float bc = beta * *cp;
+        r = r + bc;
+      }
+      *cp = r;
+    }
+  }
+}

@@ -1,0 +1,159 @@
+"""ctypes wrapper of the CPU oracle (oracle/oracle.c) — TEST INFRASTRUCTURE.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import
+this module, and only as the checker (or the timed CPU baseline). The product
+(wgblas_amd/) never loads it.
+
+Function provenance (reference file:line each one restates) is in oracle.c.
+"""
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB = os.path.join(HERE, "lib", "liborc.so")
+
+_i64, _f32p, _f64p = C.c_int64, C.POINTER(C.c_float), C.POINTER(C.c_double)
+_SIG = {
+    "orc_random_f32": (None, [_i64, C.c_double, C.c_double, C.c_uint32, _f32p]),
+    "orc_random_f64": (None, [_i64, C.c_double, C.c_double, C.c_uint32, _f64p]),
+    "orc_random_normal_f32": (None, [_i64, C.c_uint32, _f32p]),
+    "orc_sdot_wgsl": (C.c_float, [_i64, _f32p, _i64, _f32p, _i64]),
+    "orc_sasum_wgsl": (C.c_float, [_i64, _f32p, _i64]),
+    "orc_snrm2_wgsl": (C.c_float, [_i64, _f32p, _i64]),
+    "orc_isamax_wgsl": (_i64, [_i64, _f32p, _i64]),
+    "orc_nrm_combine": (C.c_float, [C.c_float, C.c_float, C.c_float]),
+    "orc_dot_ld": (C.c_double, [_i64, _f32p, _i64, _f32p, _i64, _f64p]),
+    "orc_sum_abs_ld": (C.c_double, [_i64, _f32p, _i64]),
+    "orc_nrm2_ld": (C.c_double, [_i64, _f32p, _i64]),
+    "orc_isamax_brute": (_i64, [_i64, _f32p, _i64]),
+    "orc_gemm_ld": (None, [C.c_int, C.c_int, C.c_int, _i64, _i64, _i64, C.c_double, _f64p, _i64,
+                           _f64p, _i64, C.c_double, _f64p, _i64, _f64p, _i64, _f64p]),
+    "orc_sgemm_wgsl": (None, [C.c_int, C.c_int, C.c_int, _i64, _i64, _i64, C.c_float, _f32p, _i64,
+                              _f32p, _i64, C.c_float, _f32p, _i64]),
+}
+
+_lib = None
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB):
+            build()
+        l = C.CDLL(LIB)
+        for name, (res, args) in _SIG.items():
+            fn = getattr(l, name)
+            fn.restype, fn.argtypes = res, args
+        _lib = l
+    return _lib
+
+
+def _f32(a):
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    return a, a.ctypes.data_as(_f32p)
+
+
+def _f64(a):
+    a = np.ascontiguousarray(a, dtype=np.float64)
+    return a, a.ctypes.data_as(_f64p)
+
+
+# ---- seeded inputs ----
+def random_f32(n, low=-1.0, high=1.0, seed=0):
+    out = np.empty(n, np.float32)
+    lib().orc_random_f32(n, low, high, seed & 0xffffffff, out.ctypes.data_as(_f32p))
+    return out
+
+
+def random_f64(n, low=-1.0, high=1.0, seed=0):
+    out = np.empty(n, np.float64)
+    lib().orc_random_f64(n, low, high, seed & 0xffffffff, out.ctypes.data_as(_f64p))
+    return out
+
+
+def random_normal_f32(n, seed=0):
+    out = np.empty(n, np.float32)
+    lib().orc_random_normal_f32(n, seed & 0xffffffff, out.ctypes.data_as(_f32p))
+    return out
+
+
+# ---- level 1 ----
+def sdot_wgsl(n, x, incx, y, incy):
+    x, xp = _f32(x)
+    y, yp = _f32(y)
+    return np.float32(lib().orc_sdot_wgsl(n, xp, incx, yp, incy))
+
+
+def sasum_wgsl(n, x, incx):
+    x, xp = _f32(x)
+    return np.float32(lib().orc_sasum_wgsl(n, xp, incx))
+
+
+def snrm2_wgsl(n, x, incx):
+    x, xp = _f32(x)
+    return np.float32(lib().orc_snrm2_wgsl(n, xp, incx))
+
+
+def isamax_wgsl(n, x, incx):
+    x, xp = _f32(x)
+    return int(lib().orc_isamax_wgsl(n, xp, incx))
+
+
+def nrm_combine(abig, amed, asml):
+    return np.float32(lib().orc_nrm_combine(abig, amed, asml))
+
+
+def dot_ld(n, x, incx, y, incy):
+    """(sum x*y, sum |x*y|) in long double."""
+    x, xp = _f32(x)
+    y, yp = _f32(y)
+    a = C.c_double(0)
+    s = lib().orc_dot_ld(n, xp, incx, yp, incy, C.byref(a))
+    return s, a.value
+
+
+def sum_abs_ld(n, x, incx):
+    x, xp = _f32(x)
+    return lib().orc_sum_abs_ld(n, xp, incx)
+
+
+def nrm2_ld(n, x, incx):
+    x, xp = _f32(x)
+    return lib().orc_nrm2_ld(n, xp, incx)
+
+
+def isamax_brute(n, x, incx):
+    x, xp = _f32(x)
+    return int(lib().orc_isamax_brute(n, xp, incx))
+
+
+# ---- level 3 (column-major flat arrays) ----
+def gemm_ld(uplo, transA, transB, m, n, k, alpha, A, lda, B, ldb, beta, Cin, ldc):
+    """Returns (out, absdot) as (ldc*n)-long column-major float64 arrays:
+    out holds alpha*op(A)op(B)+beta*C on the uplo part (long double), C
+    elsewhere (including the ld padding); absdot = sum_p |a*b|."""
+    A, Ap = _f64(A if A is not None and len(A) else np.zeros(1))
+    B, Bp = _f64(B if B is not None and len(B) else np.zeros(1))
+    Cin, Cp = _f64(Cin)
+    out = Cin.copy()
+    absdot = np.zeros_like(Cin)
+    lib().orc_gemm_ld(uplo, transA, transB, m, n, k, alpha, Ap, lda, Bp, ldb, beta, Cp, ldc,
+                      out.ctypes.data_as(_f64p), ldc, absdot.ctypes.data_as(_f64p))
+    return out, absdot
+
+
+def sgemm_wgsl(uplo, transA, transB, m, n, k, alpha, A, lda, B, ldb, beta, Cin, ldc):
+    """The reference's fp32 per-element order; returns the updated C."""
+    A, Ap = _f32(A if A is not None and len(A) else np.zeros(1))
+    B, Bp = _f32(B if B is not None and len(B) else np.zeros(1))
+    out = np.array(Cin, dtype=np.float32, copy=True)
+    lib().orc_sgemm_wgsl(uplo, transA, transB, m, n, k, alpha, Ap, lda, Bp, ldb, beta,
+                         out.ctypes.data_as(_f32p), ldc)
+    return out

@@ -1,0 +1,61 @@
+// Internal declarations shared by the libwgblas_hip translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "../../include/wgblas_hip.h"
+
+struct wgb_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  hipEvent_t ev_start = nullptr;
+  hipEvent_t ev_stop = nullptr;
+  bool timing = false;
+  bool timed_once = false;
+  float last_ms = 0.0f;
+  int num_cus = 0;
+  // Device scratch for the two-pass reductions: per-block partials followed
+  // by a result slot. Stream order makes reuse across calls safe.
+  void *scratch = nullptr;
+  size_t scratch_bytes = 0;
+  // Pinned host slot the host-result reductions copy their scalar into.
+  void *host_result = nullptr;
+  char name[256] = {0};
+  char arch[64] = {0};
+};
+
+namespace wgb {
+
+// Records `msg` as the calling thread's last error and returns `status`.
+int fail(int status, const std::string &msg);
+int fail_hip(hipError_t err, const char *what);
+
+// Makes ctx's device current; every entry point calls it first.
+int enter(wgb_ctx *ctx);
+
+// Brackets a routine's kernels with the context's timing events.
+void timing_begin(wgb_ctx *ctx);
+void timing_end(wgb_ctx *ctx);
+
+// Largest number of first-pass blocks a reduction may use; the scratch
+// buffer is sized for this many 16-byte partials plus the result slot.
+constexpr int kMaxReduceBlocks = 2048;
+constexpr size_t kScratchBytes = (size_t)kMaxReduceBlocks * 16 + 256;
+
+}  // namespace wgb
+
+#define WGB_CHECK_HIP(expr)                               \
+  do {                                                    \
+    hipError_t _e = (expr);                               \
+    if (_e != hipSuccess) return wgb::fail_hip(_e, #expr); \
+  } while (0)
+
+#define WGB_CHECK_LAUNCH(what)                                  \
+  do {                                                          \
+    hipError_t _e = hipGetLastError();                          \
+    if (_e != hipSuccess) return wgb::fail_hip(_e, what);       \
+  } while (0)

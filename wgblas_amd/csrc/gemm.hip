@@ -1,0 +1,571 @@
+// GEMM family on CDNA4 matrix cores: sgemm, sgemmtr, ssyrk (fp32) and dgemm
+// (native fp64).
+//
+// wgblas computes these with LDS-tiled, register-blocked WGSL kernels in a
+// row-major frame (src/shaders/sgemm_large.wgsl, sgemm_small.wgsl) and
+// emulates f64 with double-double pairs (src/shaders/dgemm_small.wgsl,
+// src/shaders/f64/). Here the frame is column-major (BLAS's own) and the
+// contraction runs on MFMA: v_mfma_f32_16x16x4f32 for fp32 and
+// v_mfma_f64_16x16x4f64 for fp64, one template for both.
+//
+// Block: 256 threads = 4 waves in a 2x2 grid, block tile BT x BT of C
+// (BT = 128 large tier, 64 small tier), k-tile BK = 128 bytes of k
+// (32 floats / 16 doubles). Each operand tile is staged in LDS, double
+// buffered, in the orientation it has in memory so the global->LDS path is
+// plain 16-byte copies:
+//   * k-contiguous operands (op(A) with A transposed, op(B) with B not
+//     transposed) are stored [row][k] with a 16-byte row pad;
+//   * mn-contiguous operands (A not transposed, B transposed) are stored
+//     [k][row].
+// MFMA operand fetch from either layout is one 16-byte (or 8-byte) LDS read
+// per lane:
+//   * from [row][k], a lane reads 4 consecutive k and feeds them to 4
+//     successive MFMAs: in MFMA step s lane-group g = lane/16 supplies
+//     k = 4g + s (the k order inside a 16-k chunk is permuted the same way
+//     for both operands, so the sum is unchanged);
+//   * from [k][row], a lane reads RW consecutive rows and feeds each to a
+//     different 16-row MFMA block ("virtual blocks"), which permutes rows
+//     inside the wave tile; the epilogue undoes it.
+// Each lane therefore holds runs of consecutive C rows, which the epilogue
+// writes as 16-byte vectors when alignment allows.
+//
+// Tiles are scheduled XCD-aware: the hardware deals workgroups round-robin
+// over MI355X's 8 XCDs, so workgroup w is remapped to logical tile
+// (w % 8) * (tiles / 8) + w / 8, giving each XCD (and its L2) a contiguous
+// run of tiles; inside that run tiles are grouped 8 tile-rows at a time so
+// concurrent tiles share A and B panels. sgemmtr/ssyrk launch only the
+// tiles that meet the requested triangle (wgblas launches all of them and
+// returns early, src/shaders/sgemm_large.wgsl:78-83) and mask stores inside
+// the diagonal tiles.
+//
+// Result rules kept from wgblas (src/shaders/sgemm_large.wgsl:288-308,
+// src/shaders/dgemm_small.wgsl:230-273): beta == 0 never reads C;
+// alpha == 0 (and k == 0) gives beta*C without reading A or B; rows and
+// columns outside m x n, and the other triangle for sgemmtr/ssyrk, are
+// never written.
+#include "common.h"
+
+#include <cmath>
+
+namespace {
+
+template <typename T>
+struct Ty;
+
+template <>
+struct Ty<float> {
+  typedef float v16 __attribute__((ext_vector_type(4)));
+  typedef float v4 __attribute__((ext_vector_type(4)));
+  typedef float v2 __attribute__((ext_vector_type(2)));
+  typedef float acc __attribute__((ext_vector_type(4)));
+  static constexpr int VW = 4;
+  __device__ static acc mfma(float a, float b, acc c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+  }
+};
+
+template <>
+struct Ty<double> {
+  typedef double v16 __attribute__((ext_vector_type(2)));
+  typedef double v4 __attribute__((ext_vector_type(4)));
+  typedef double v2 __attribute__((ext_vector_type(2)));
+  typedef double acc __attribute__((ext_vector_type(4)));
+  static constexpr int VW = 2;
+  __device__ static acc mfma(double a, double b, acc c) {
+    return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
+  }
+};
+
+template <typename T>
+struct GemmArgs {
+  int64_t m, n, k;
+  T alpha, beta;
+  const T *A;
+  int64_t lda;
+  const T *B;
+  int64_t ldb;
+  T *C;
+  int64_t ldc;
+  int tiles_m, tiles_n, ntiles;
+  int uplo;  // 0 = full C, WGB_LOWER, WGB_UPPER
+};
+
+constexpr int kThreads = 256;
+constexpr int kGroupM = 8;
+constexpr int kXcds = 8;
+
+// Number of tiles of a tiles_m x tiles_n grid (square tiles) that meet the
+// lower (tile row >= tile col) triangle; upper swaps the roles.
+int64_t triangle_tiles(int64_t rows, int64_t cols) {
+  int64_t t = 0;
+  int64_t full = rows < cols ? rows : cols;
+  t = full * (full + 1) / 2;  // rows 0..full-1 hold tm+1 tiles each
+  if (rows > cols) t += (rows - cols) * cols;
+  return t;
+}
+
+// Decodes the L-th tile (row-major over the triangle) of a grid whose row r
+// holds min(r+1, cols) tiles.
+__device__ inline void triangle_decode(int L, int cols, int &r, int &c) {
+  int64_t t0 = (int64_t)cols * (cols + 1) / 2;
+  if ((int64_t)L < t0) {
+    int rr = (int)((sqrt(8.0 * (double)L + 1.0) - 1.0) * 0.5);
+    while ((int64_t)(rr + 1) * (rr + 2) / 2 <= L) ++rr;
+    while ((int64_t)rr * (rr + 1) / 2 > L) --rr;
+    r = rr;
+    c = L - (int)((int64_t)rr * (rr + 1) / 2);
+  } else {
+    int64_t rem = (int64_t)L - t0;
+    r = cols + (int)(rem / cols);
+    c = (int)(rem % cols);
+  }
+}
+
+__device__ inline void tile_of(int w, int ntiles, int tiles_m, int tiles_n, int uplo, int &tm,
+                               int &tn) {
+  // XCD-aware remap: workgroup w runs on XCD w % 8; give each XCD a
+  // contiguous run of logical tiles.
+  int x = w % kXcds, j = w / kXcds;
+  int q = ntiles / kXcds, r = ntiles % kXcds;
+  int L = x * q + (x < r ? x : r) + j;
+  if (uplo == WGB_LOWER) {
+    triangle_decode(L, tiles_n, tm, tn);
+  } else if (uplo == WGB_UPPER) {
+    triangle_decode(L, tiles_m, tn, tm);
+  } else {
+    int group_size = kGroupM * tiles_n;
+    int gid = L / group_size;
+    int first_m = gid * kGroupM;
+    int gm = tiles_m - first_m < kGroupM ? tiles_m - first_m : kGroupM;
+    int in_group = L % group_size;
+    tm = first_m + in_group % gm;
+    tn = in_group / gm;
+  }
+}
+
+// Global -> register -> LDS staging of one operand's BT x BK tile.
+// KC: k-contiguous in memory, staged [row][k] (row stride BK + VW).
+// !KC: row-contiguous in memory, staged [k][row] (row stride BT).
+template <typename T, int BT, bool KC, bool VEC>
+struct Stager {
+  typedef typename Ty<T>::v16 V;
+  static constexpr int VW = Ty<T>::VW;
+  static constexpr int BK = 128 / (int)sizeof(T);
+  static constexpr int LOADS = BT / 32;      // 16-byte vectors per thread
+  static constexpr int VPK = BT / VW;        // vectors per k-row (!KC)
+  static constexpr int KROWS = kThreads / VPK;  // k-rows per load step (!KC)
+  static constexpr int LDK = BK + VW;
+  static constexpr int LDM = BT;
+  static constexpr int ELEMS = KC ? BT * LDK : BK * LDM;
+
+  const T *base;      // this thread's element for k-tile 0, r = 0
+  int64_t r_step;     // element distance between load steps r
+  int64_t k_step;     // element advance per k-tile
+  int lds_off;        // LDS element offset for r = 0
+  int lds_r_step;
+  int64_t row_first;  // KC: global row of r = 0;   !KC: first global row of the vector
+  int k_first;        // KC: k offset of the vector; !KC: k-row of r = 0
+  int64_t rows_total, K;
+
+  __device__ void init(const T *P, int64_t ld, int64_t row0, int t, int64_t rows_total_,
+                       int64_t K_) {
+    rows_total = rows_total_;
+    K = K_;
+    if (KC) {
+      int row = t / 8, kv = t % 8;
+      row_first = row0 + row;
+      k_first = kv * VW;
+      base = P + (row0 + row) * ld + kv * VW;
+      r_step = 32 * ld;
+      k_step = BK;
+      lds_off = row * LDK + kv * VW;
+      lds_r_step = 32 * LDK;
+    } else {
+      int mv = t % VPK, kk = t / VPK;
+      row_first = row0 + mv * VW;
+      k_first = kk;
+      base = P + row0 + mv * VW + (int64_t)kk * ld;
+      r_step = KROWS * ld;
+      k_step = (int64_t)BK * ld;
+      lds_off = kk * LDM + mv * VW;
+      lds_r_step = KROWS * LDM;
+    }
+  }
+
+  __device__ static V load_n(const T *p, int64_t nvalid) {
+    V v;
+#pragma unroll
+    for (int c = 0; c < VW; ++c) v[c] = (c < nvalid) ? p[c] : (T)0;
+    return v;
+  }
+
+  __device__ static V load_full(const T *p) {
+    if (VEC) return *reinterpret_cast<const V *>(p);
+    V v;
+#pragma unroll
+    for (int c = 0; c < VW; ++c) v[c] = p[c];
+    return v;
+  }
+
+  template <bool GUARD>
+  __device__ void load(V (&regs)[LOADS], int kt) const {
+    const T *p = base + (int64_t)kt * k_step;
+#pragma unroll
+    for (int r = 0; r < LOADS; ++r) {
+      const T *q = p + r * r_step;
+      if (!GUARD) {
+        regs[r] = load_full(q);
+      } else if (KC) {
+        int64_t row = row_first + 32 * r;
+        int64_t nv = K - ((int64_t)kt * BK + k_first);
+        regs[r] = (row < rows_total && nv > 0) ? (nv >= VW ? load_full(q) : load_n(q, nv)) : V(0);
+      } else {
+        int64_t kk = (int64_t)kt * BK + k_first + KROWS * r;
+        int64_t nv = rows_total - row_first;
+        regs[r] = (kk < K && nv > 0) ? (nv >= VW ? load_full(q) : load_n(q, nv)) : V(0);
+      }
+    }
+  }
+
+  __device__ void store(T *stage, const V (&regs)[LOADS]) const {
+#pragma unroll
+    for (int r = 0; r < LOADS; ++r)
+      *reinterpret_cast<V *>(stage + lds_off + r * lds_r_step) = regs[r];
+  }
+};
+
+// Fetches the MFMA operands of one 16-k chunk for MB 16-row blocks.
+// out[s][b] = operand of MFMA step s (s = 0..3) for block b.
+template <typename T, int BT, bool KC, int MB>
+__device__ __forceinline__ void fetch_operands(const T *stage, int wrow, int kc, int lane,
+                                               T (&out)[4][MB]) {
+  typedef typename Ty<T>::v4 V4;
+  constexpr int VW = Ty<T>::VW;
+  constexpr int BK = 128 / (int)sizeof(T);
+  constexpr int LDK = BK + VW;
+  constexpr int LDM = BT;
+  constexpr int RW = MB < VW ? MB : VW;
+  const int g = lane >> 4, i16 = lane & 15;
+  if (KC) {
+#pragma unroll
+    for (int b = 0; b < MB; ++b) {
+      V4 v = *reinterpret_cast<const V4 *>(stage + (wrow + 16 * b + i16) * LDK + kc + 4 * g);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) out[s][b] = v[s];
+    }
+  } else {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+#pragma unroll
+      for (int h = 0; h < MB / RW; ++h) {
+        const T *p = stage + (kc + 4 * g + s) * LDM + wrow + 16 * RW * h + RW * i16;
+        if (RW == 4) {
+          V4 v = *reinterpret_cast<const V4 *>(p);
+#pragma unroll
+          for (int c = 0; c < RW; ++c) out[s][h * RW + c] = v[c];
+        } else {
+          typedef typename Ty<T>::v2 V2;
+          V2 v = *reinterpret_cast<const V2 *>(p);
+#pragma unroll
+          for (int c = 0; c < RW; ++c) out[s][h * RW + c] = v[c];
+        }
+      }
+    }
+  }
+}
+
+// Row (or column) inside the wave tile held by lane `lane` for MFMA block b
+// and accumulator register q (for columns pass q = 0 and use the i16 form).
+template <bool KC, int MB, int VW>
+__device__ __forceinline__ int out_row(int b, int q, int lane) {
+  constexpr int RW = MB < VW ? MB : VW;
+  const int g = lane >> 4;
+  if (KC) return 16 * b + 4 * g + q;
+  return 16 * RW * (b / RW) + RW * (4 * g + q) + (b % RW);
+}
+
+template <bool KC, int MB, int VW>
+__device__ __forceinline__ int out_col(int b, int lane) {
+  constexpr int RW = MB < VW ? MB : VW;
+  const int i16 = lane & 15;
+  if (KC) return 16 * b + i16;
+  return 16 * RW * (b / RW) + RW * i16 + (b % RW);
+}
+
+template <typename T, int BT, bool AKC, bool BKC, bool VEC>
+__global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs<T> p) {
+  typedef typename Ty<T>::acc Acc;
+  typedef typename Ty<T>::v16 V;
+  constexpr int VW = Ty<T>::VW;
+  constexpr int BK = 128 / (int)sizeof(T);
+  constexpr int WT = BT / 2;
+  constexpr int MB = WT / 16;
+  typedef Stager<T, BT, AKC, VEC> SA;
+  typedef Stager<T, BT, BKC, VEC> SB;
+  constexpr int STAGE = SA::ELEMS + SB::ELEMS;
+  __shared__ __attribute__((aligned(16))) T smem[2 * STAGE];
+
+  int tm, tn;
+  tile_of(blockIdx.x, p.ntiles, p.tiles_m, p.tiles_n, p.uplo, tm, tn);
+  if (tm < 0 || tn < 0 || tm >= p.tiles_m || tn >= p.tiles_n) return;  // block-uniform
+  const int64_t m0 = (int64_t)tm * BT, n0 = (int64_t)tn * BT;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int wm = (wave & 1) * WT, wn = (wave >> 1) * WT;
+
+  SA sa;
+  SB sb;
+  sa.init(p.A, p.lda, m0, t, p.m, p.k);
+  sb.init(p.B, p.ldb, n0, t, p.n, p.k);
+  const bool interior = (m0 + BT <= p.m) && (n0 + BT <= p.n);
+  const int nkt = (int)((p.k + BK - 1) / BK);
+  const int nkt_full = interior ? (int)(p.k / BK) : 0;
+
+  Acc acc[MB][MB];
+#pragma unroll
+  for (int i = 0; i < MB; ++i)
+#pragma unroll
+    for (int j = 0; j < MB; ++j) acc[i][j] = Acc(0);
+
+  V ra[SA::LOADS], rb[SB::LOADS];
+  if (0 < nkt_full) {
+    sa.template load<false>(ra, 0);
+    sb.template load<false>(rb, 0);
+  } else {
+    sa.template load<true>(ra, 0);
+    sb.template load<true>(rb, 0);
+  }
+  sa.store(smem, ra);
+  sb.store(smem + SA::ELEMS, rb);
+  __syncthreads();
+
+  for (int kt = 0; kt < nkt; ++kt) {
+    const bool more = kt + 1 < nkt;
+    if (more) {
+      if (kt + 1 < nkt_full) {
+        sa.template load<false>(ra, kt + 1);
+        sb.template load<false>(rb, kt + 1);
+      } else {
+        sa.template load<true>(ra, kt + 1);
+        sb.template load<true>(rb, kt + 1);
+      }
+    }
+    const T *As = smem + (kt & 1) * STAGE;
+    const T *Bs = As + SA::ELEMS;
+#pragma unroll
+    for (int kc = 0; kc < BK; kc += 16) {
+      T a[4][MB], b[4][MB];
+      fetch_operands<T, BT, AKC, MB>(As, wm, kc, lane, a);
+      fetch_operands<T, BT, BKC, MB>(Bs, wn, kc, lane, b);
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+#pragma unroll
+          for (int j = 0; j < MB; ++j) acc[i][j] = Ty<T>::mfma(a[s][i], b[s][j], acc[i][j]);
+    }
+    if (more) {
+      T *next = smem + ((kt + 1) & 1) * STAGE;
+      sa.store(next, ra);
+      sb.store(next + SA::ELEMS, rb);
+    }
+    __syncthreads();
+  }
+
+  // Epilogue: C = alpha*acc + beta*C on the tile's in-range (and, for
+  // sgemmtr/ssyrk, in-triangle) elements.
+  const T alpha = p.alpha, beta = p.beta;
+  const bool tri_diag = p.uplo != 0 && tm == tn;
+#pragma unroll
+  for (int i = 0; i < MB; ++i) {
+#pragma unroll
+    for (int j = 0; j < MB; ++j) {
+      const int64_t col = n0 + wn + out_col<BKC, MB, VW>(j, lane);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int64_t row = m0 + wm + out_row<AKC, MB, VW>(i, q, lane);
+        bool ok = row < p.m && col < p.n;
+        if (tri_diag) ok = ok && (p.uplo == WGB_LOWER ? row >= col : row <= col);
+        if (ok) {
+          T *cp = p.C + row + col * p.ldc;
+          T v = alpha * acc[i][j][q];
+          if (beta != (T)0) v = fma(beta, *cp, v);
+          *cp = v;
+        }
+      }
+    }
+  }
+}
+
+// C <- beta*C (or 0 when beta == 0) on the uplo part of the m x n C: the
+// alpha == 0 / k == 0 path, which reads neither A nor B.
+template <typename T>
+__global__ void scale_kernel(int64_t m, int64_t n, T beta, T *C, int64_t ldc, int uplo) {
+  for (int64_t col = blockIdx.y; col < n; col += gridDim.y) {
+    for (int64_t row = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; row < m;
+         row += (int64_t)gridDim.x * blockDim.x) {
+      if (uplo == WGB_LOWER && row < col) continue;
+      if (uplo == WGB_UPPER && row > col) continue;
+      T *cp = C + row + col * ldc;
+      *cp = beta == (T)0 ? (T)0 : beta * *cp;
+    }
+  }
+}
+
+template <typename T, int BT, bool AKC, bool BKC, bool VEC>
+void launch_one(const GemmArgs<T> &a, hipStream_t s) {
+  gemm_kernel<T, BT, AKC, BKC, VEC><<<a.ntiles, kThreads, 0, s>>>(a);
+}
+
+template <typename T, int BT>
+void launch_tier(const GemmArgs<T> &a, bool akc, bool bkc, bool vec, hipStream_t s) {
+  if (vec) {
+    if (akc) {
+      if (bkc) launch_one<T, BT, true, true, true>(a, s);
+      else launch_one<T, BT, true, false, true>(a, s);
+    } else {
+      if (bkc) launch_one<T, BT, false, true, true>(a, s);
+      else launch_one<T, BT, false, false, true>(a, s);
+    }
+  } else {
+    if (akc) {
+      if (bkc) launch_one<T, BT, true, true, false>(a, s);
+      else launch_one<T, BT, true, false, false>(a, s);
+    } else {
+      if (bkc) launch_one<T, BT, false, true, false>(a, s);
+      else launch_one<T, BT, false, false, false>(a, s);
+    }
+  }
+}
+
+bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+int64_t imax(int64_t a, int64_t b) { return a > b ? a : b; }
+
+int check_gemm_args(int uplo, bool want_uplo, int transA, int transB, int64_t m, int64_t n,
+                    int64_t k, const void *A, int64_t lda, const void *B, int64_t ldb,
+                    const void *C, int64_t ldc) {
+  using wgb::fail;
+  if (want_uplo && uplo != WGB_LOWER && uplo != WGB_UPPER)
+    return fail(WGB_ERR_INVALID_VALUE, "uplo must be WGB_LOWER or WGB_UPPER");
+  if (transA != WGB_NO_TRANS && transA != WGB_TRANS)
+    return fail(WGB_ERR_INVALID_VALUE, "transA must be WGB_NO_TRANS or WGB_TRANS");
+  if (transB != WGB_NO_TRANS && transB != WGB_TRANS)
+    return fail(WGB_ERR_INVALID_VALUE, "transB must be WGB_NO_TRANS or WGB_TRANS");
+  if (m < 0 || n < 0 || k < 0) return fail(WGB_ERR_INVALID_VALUE, "m, n, and k must be non-negative");
+  if (m > INT32_MAX || n > INT32_MAX || k > INT32_MAX)
+    return fail(WGB_ERR_INVALID_VALUE, "m, n, and k must be below 2^31");
+  // Column-major: A is m x k (no-transpose) or k x m (transpose).
+  int64_t a_rows = transA == WGB_NO_TRANS ? m : k;
+  int64_t b_rows = transB == WGB_NO_TRANS ? k : n;
+  if (lda < imax(1, a_rows)) return fail(WGB_ERR_INVALID_VALUE, "lda must be >= max(1, rows of A)");
+  if (ldb < imax(1, b_rows)) return fail(WGB_ERR_INVALID_VALUE, "ldb must be >= max(1, rows of B)");
+  if (ldc < imax(1, m)) return fail(WGB_ERR_INVALID_VALUE, "ldc must be >= max(1, m)");
+  if (m > 0 && n > 0) {
+    if (!C) return fail(WGB_ERR_INVALID_VALUE, "C is null");
+    if (k > 0 && (!A || !B)) return fail(WGB_ERR_INVALID_VALUE, "A or B is null");
+  }
+  return WGB_OK;
+}
+
+template <typename T>
+int gemm_run(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64_t n, int64_t k,
+             T alpha, const T *A, int64_t lda, const T *B, int64_t ldb, T beta, T *C,
+             int64_t ldc) {
+  if (m == 0 || n == 0) return WGB_OK;
+  wgb::timing_begin(ctx);
+  if (alpha == (T)0 || k == 0) {
+    dim3 block(256);
+    int64_t gx = (m + 255) / 256;
+    dim3 grid((unsigned)(gx > 1024 ? 1024 : gx), (unsigned)(n > 65535 ? 65535 : n));
+    scale_kernel<T><<<grid, block, 0, ctx->stream>>>(m, n, beta, C, ldc, uplo);
+    WGB_CHECK_LAUNCH("scale_kernel");
+    wgb::timing_end(ctx);
+    return WGB_OK;
+  }
+  GemmArgs<T> a;
+  a.m = m;
+  a.n = n;
+  a.k = k;
+  a.alpha = alpha;
+  a.beta = beta;
+  a.A = A;
+  a.lda = lda;
+  a.B = B;
+  a.ldb = ldb;
+  a.C = C;
+  a.ldc = ldc;
+  a.uplo = uplo;
+  const int VW = Ty<T>::VW;
+  const bool akc = transA == WGB_TRANS;
+  const bool bkc = transB == WGB_NO_TRANS;
+  const bool vec = (lda % VW == 0) && (ldb % VW == 0) && aligned16(A) && aligned16(B);
+  // Large tier once the 128-tiles alone fill the chip; small tier otherwise.
+  auto count = [&](int64_t bt, int64_t &tmn, int64_t &tnn) {
+    tmn = (m + bt - 1) / bt;
+    tnn = (n + bt - 1) / bt;
+    if (uplo == WGB_LOWER) return triangle_tiles(tmn, tnn);
+    if (uplo == WGB_UPPER) return triangle_tiles(tnn, tmn);
+    return tmn * tnn;
+  };
+  int64_t tm128, tn128;
+  int64_t tiles128 = count(128, tm128, tn128);
+  const int64_t fill = ctx->num_cus > 0 ? ctx->num_cus : 256;
+  const int bt = tiles128 >= fill ? 128 : 64;
+  int64_t tmn, tnn;
+  int64_t ntiles = count(bt, tmn, tnn);
+  if (ntiles > INT32_MAX) return wgb::fail(WGB_ERR_INVALID_VALUE, "problem too large for one launch");
+  a.tiles_m = (int)tmn;
+  a.tiles_n = (int)tnn;
+  a.ntiles = (int)ntiles;
+  if (bt == 128)
+    launch_tier<T, 128>(a, akc, bkc, vec, ctx->stream);
+  else
+    launch_tier<T, 64>(a, akc, bkc, vec, ctx->stream);
+  WGB_CHECK_LAUNCH("gemm_kernel");
+  wgb::timing_end(ctx);
+  return WGB_OK;
+}
+
+}  // namespace
+
+extern "C" int wgb_sgemm(wgb_ctx *ctx, int transA, int transB, int64_t m, int64_t n, int64_t k,
+                         float alpha, const float *A, int64_t lda, const float *B, int64_t ldb,
+                         float beta, float *C, int64_t ldc) {
+  int st = wgb::enter(ctx);
+  if (st) return st;
+  if ((st = check_gemm_args(0, false, transA, transB, m, n, k, A, lda, B, ldb, C, ldc))) return st;
+  return gemm_run<float>(ctx, 0, transA, transB, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc);
+}
+
+extern "C" int wgb_sgemmtr(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64_t n,
+                           int64_t k, float alpha, const float *A, int64_t lda, const float *B,
+                           int64_t ldb, float beta, float *C, int64_t ldc) {
+  int st = wgb::enter(ctx);
+  if (st) return st;
+  if ((st = check_gemm_args(uplo, true, transA, transB, m, n, k, A, lda, B, ldb, C, ldc))) return st;
+  return gemm_run<float>(ctx, uplo, transA, transB, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc);
+}
+
+extern "C" int wgb_ssyrk(wgb_ctx *ctx, int uplo, int trans, int64_t n, int64_t k, float alpha,
+                         const float *A, int64_t lda, float beta, float *C, int64_t ldc) {
+  int st = wgb::enter(ctx);
+  if (st) return st;
+  if (trans != WGB_NO_TRANS && trans != WGB_TRANS)
+    return wgb::fail(WGB_ERR_INVALID_VALUE, "trans must be WGB_NO_TRANS or WGB_TRANS");
+  // C = alpha*op(A)*op(A)^T + beta*C is sgemmtr with B = A and the opposite
+  // trans flag: no copy of A is made.
+  const int transB = trans == WGB_NO_TRANS ? WGB_TRANS : WGB_NO_TRANS;
+  if ((st = check_gemm_args(uplo, true, trans, transB, n, n, k, A, lda, A, lda, C, ldc))) return st;
+  return gemm_run<float>(ctx, uplo, trans, transB, n, n, k, alpha, A, lda, A, lda, beta, C, ldc);
+}
+
+extern "C" int wgb_dgemm(wgb_ctx *ctx, int transA, int transB, int64_t m, int64_t n, int64_t k,
+                         double alpha, const double *A, int64_t lda, const double *B, int64_t ldb,
+                         double beta, double *C, int64_t ldc) {
+  int st = wgb::enter(ctx);
+  if (st) return st;
+  if ((st = check_gemm_args(0, false, transA, transB, m, n, k, A, lda, B, ldb, C, ldc))) return st;
+  // Reference BLAS quick return kept by wgblas (src/dgemm/dgemm.mjs:177-179).
+  if ((alpha == 0.0 || k == 0) && beta == 1.0) return WGB_OK;
+  return gemm_run<double>(ctx, 0, transA, transB, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc);
+}

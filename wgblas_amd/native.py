@@ -1,0 +1,282 @@
+"""ctypes binding of libwgblas_hip's C ABI (include/wgblas_hip.h).
+
+This is the Python view of the same boundary the Node-API addon binds: plain
+pointers and sizes, column-major matrices, status codes turned into
+WgblasError. It loads the in-tree library built by `python -m wgblas_amd.build`
+and raises if it is missing: there is no CPU fallback.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "lib", "libwgblas_hip.so")
+
+NO_TRANS, TRANS = 0, 1
+LOWER, UPPER = 1, 2
+
+_i64 = C.c_int64
+_ptr = C.c_void_p
+
+# name -> argtypes (every entry point returns int status unless listed in _RESTYPES)
+_SIGNATURES = {
+    "wgb_init": [C.c_int, C.POINTER(_ptr)],
+    "wgb_destroy": [_ptr],
+    "wgb_device_name": [_ptr, C.c_char_p, C.c_size_t, C.c_char_p, C.c_size_t],
+    "wgb_device_count": [C.POINTER(C.c_int)],
+    "wgb_set_timing": [_ptr, C.c_int],
+    "wgb_last_time_ms": [_ptr, C.POINTER(C.c_float)],
+    "wgb_synchronize": [_ptr],
+    "wgb_stream": [_ptr],
+    "wgb_last_error": [],
+    "wgb_status_string": [C.c_int],
+    "wgb_malloc": [_ptr, C.c_size_t, C.POINTER(_ptr)],
+    "wgb_free": [_ptr, _ptr],
+    "wgb_memcpy_h2d": [_ptr, _ptr, _ptr, C.c_size_t],
+    "wgb_memcpy_d2h": [_ptr, _ptr, _ptr, C.c_size_t],
+    "wgb_memcpy_d2d": [_ptr, _ptr, _ptr, C.c_size_t],
+    "wgb_fill_uniform_f32": [_ptr, _ptr, _i64, C.c_double, C.c_double, C.c_uint32],
+    "wgb_fill_uniform_f64": [_ptr, _ptr, _i64, C.c_double, C.c_double, C.c_uint32],
+    "wgb_fill_normal_f32": [_ptr, _ptr, _i64, C.c_uint32],
+    "wgb_sgemm": [_ptr, C.c_int, C.c_int, _i64, _i64, _i64, C.c_float, _ptr, _i64, _ptr, _i64,
+                  C.c_float, _ptr, _i64],
+    "wgb_sgemmtr": [_ptr, C.c_int, C.c_int, C.c_int, _i64, _i64, _i64, C.c_float, _ptr, _i64,
+                    _ptr, _i64, C.c_float, _ptr, _i64],
+    "wgb_ssyrk": [_ptr, C.c_int, C.c_int, _i64, _i64, C.c_float, _ptr, _i64, C.c_float, _ptr,
+                  _i64],
+    "wgb_dgemm": [_ptr, C.c_int, C.c_int, _i64, _i64, _i64, C.c_double, _ptr, _i64, _ptr, _i64,
+                  C.c_double, _ptr, _i64],
+    "wgb_sdot": [_ptr, _i64, _ptr, _i64, _ptr, _i64, C.POINTER(C.c_float)],
+    "wgb_sdot_dev": [_ptr, _i64, _ptr, _i64, _ptr, _i64, _ptr],
+    "wgb_sasum": [_ptr, _i64, _ptr, _i64, C.POINTER(C.c_float)],
+    "wgb_sasum_dev": [_ptr, _i64, _ptr, _i64, _ptr],
+    "wgb_snrm2": [_ptr, _i64, _ptr, _i64, C.POINTER(C.c_float)],
+    "wgb_snrm2_dev": [_ptr, _i64, _ptr, _i64, _ptr],
+    "wgb_isamax": [_ptr, _i64, _ptr, _i64, C.POINTER(_i64)],
+    "wgb_isamax_dev": [_ptr, _i64, _ptr, _i64, _ptr],
+}
+_RESTYPES = {
+    "wgb_stream": _ptr,
+    "wgb_last_error": C.c_char_p,
+    "wgb_status_string": C.c_char_p,
+}
+
+_lib = None
+
+
+class WgblasError(RuntimeError):
+    def __init__(self, status, where, message):
+        super().__init__(f"{where} failed with status {status}: {message}")
+        self.status = status
+
+
+def library():
+    """Loads libwgblas_hip.so once; raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `python -m wgblas_amd.build` "
+                "(the HIP library is required; there is no CPU fallback)")
+        lib = C.CDLL(LIB_PATH)
+        for name, argtypes in _SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.argtypes = argtypes
+            fn.restype = _RESTYPES.get(name, C.c_int)
+        _lib = lib
+    return _lib
+
+
+def exported_symbols():
+    return sorted(_SIGNATURES)
+
+
+def _check(status, where):
+    if status != 0:
+        msg = library().wgb_last_error().decode(errors="replace")
+        raise WgblasError(status, where, msg)
+
+
+def device_count():
+    c = C.c_int(0)
+    _check(library().wgb_device_count(C.byref(c)), "wgb_device_count")
+    return c.value
+
+
+class DeviceArray:
+    """A device allocation with a numpy dtype and shape (no layout implied)."""
+
+    def __init__(self, ctx, ptr, nbytes, dtype, shape):
+        self.ctx, self.ptr, self.nbytes = ctx, ptr, nbytes
+        self.dtype, self.shape = np.dtype(dtype), tuple(shape)
+
+    @property
+    def size(self):
+        return int(np.prod(self.shape, dtype=np.int64))
+
+    def offset(self, elems):
+        """Raw pointer `elems` elements into the allocation (no bounds kept)."""
+        return self.ptr + int(elems) * self.dtype.itemsize
+
+    def to_host(self):
+        out = np.empty(self.shape, dtype=self.dtype)
+        if out.nbytes:
+            self.ctx.d2h(out, self.ptr)
+        return out
+
+    def free(self):
+        if self.ptr:
+            self.ctx.free(self.ptr)
+            self.ptr = 0
+
+
+class Context:
+    """One HIP device and stream (wgb_ctx)."""
+
+    def __init__(self, device=0):
+        self.lib = library()
+        h = _ptr()
+        _check(self.lib.wgb_init(device, C.byref(h)), "wgb_init")
+        self.handle = h.value
+        self.device = device
+
+    def close(self):
+        if self.handle:
+            self.lib.wgb_destroy(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    # ---- device info / timing ----
+    def name(self):
+        name = C.create_string_buffer(256)
+        arch = C.create_string_buffer(64)
+        _check(self.lib.wgb_device_name(self.handle, name, 256, arch, 64), "wgb_device_name")
+        return name.value.decode(), arch.value.decode()
+
+    @property
+    def stream(self):
+        return self.lib.wgb_stream(self.handle)
+
+    def set_timing(self, on):
+        _check(self.lib.wgb_set_timing(self.handle, 1 if on else 0), "wgb_set_timing")
+
+    def last_time_ms(self):
+        ms = C.c_float(0)
+        _check(self.lib.wgb_last_time_ms(self.handle, C.byref(ms)), "wgb_last_time_ms")
+        return ms.value
+
+    def synchronize(self):
+        _check(self.lib.wgb_synchronize(self.handle), "wgb_synchronize")
+
+    # ---- memory ----
+    def malloc(self, nbytes):
+        p = _ptr()
+        _check(self.lib.wgb_malloc(self.handle, int(nbytes), C.byref(p)), "wgb_malloc")
+        return p.value
+
+    def free(self, ptr):
+        _check(self.lib.wgb_free(self.handle, ptr), "wgb_free")
+
+    def h2d(self, dst_ptr, host):
+        host = np.ascontiguousarray(host)
+        _check(self.lib.wgb_memcpy_h2d(self.handle, dst_ptr, host.ctypes.data, host.nbytes),
+               "wgb_memcpy_h2d")
+
+    def d2h(self, host, src_ptr):
+        assert host.flags.c_contiguous
+        _check(self.lib.wgb_memcpy_d2h(self.handle, host.ctypes.data, src_ptr, host.nbytes),
+               "wgb_memcpy_d2h")
+
+    def empty(self, shape, dtype):
+        shape = (shape,) if np.isscalar(shape) else tuple(shape)
+        dt = np.dtype(dtype)
+        nbytes = int(np.prod(shape, dtype=np.int64)) * dt.itemsize
+        return DeviceArray(self, self.malloc(nbytes), nbytes, dt, shape)
+
+    def upload(self, host):
+        host = np.ascontiguousarray(host)
+        arr = self.empty(host.shape, host.dtype)
+        if host.nbytes:
+            self.h2d(arr.ptr, host)
+        return arr
+
+    # ---- seeded inputs ----
+    def fill_uniform(self, arr, low, high, seed, n=None):
+        n = arr.size if n is None else n
+        fn = {np.float32: self.lib.wgb_fill_uniform_f32,
+              np.float64: self.lib.wgb_fill_uniform_f64}[arr.dtype.type]
+        _check(fn(self.handle, arr.ptr, n, float(low), float(high), seed & 0xffffffff),
+               "wgb_fill_uniform")
+
+    def fill_normal(self, arr, seed, n=None):
+        assert arr.dtype == np.float32
+        n = arr.size if n is None else n
+        _check(self.lib.wgb_fill_normal_f32(self.handle, arr.ptr, n, seed & 0xffffffff),
+               "wgb_fill_normal_f32")
+
+    # ---- level 3 (column-major, device pointers) ----
+    def sgemm(self, transA, transB, m, n, k, alpha, A, lda, B, ldb, beta, C_, ldc):
+        _check(self.lib.wgb_sgemm(self.handle, transA, transB, m, n, k, alpha, _p(A), lda,
+                                  _p(B), ldb, beta, _p(C_), ldc), "wgb_sgemm")
+
+    def sgemmtr(self, uplo, transA, transB, m, n, k, alpha, A, lda, B, ldb, beta, C_, ldc):
+        _check(self.lib.wgb_sgemmtr(self.handle, uplo, transA, transB, m, n, k, alpha, _p(A),
+                                    lda, _p(B), ldb, beta, _p(C_), ldc), "wgb_sgemmtr")
+
+    def ssyrk(self, uplo, trans, n, k, alpha, A, lda, beta, C_, ldc):
+        _check(self.lib.wgb_ssyrk(self.handle, uplo, trans, n, k, alpha, _p(A), lda, beta,
+                                  _p(C_), ldc), "wgb_ssyrk")
+
+    def dgemm(self, transA, transB, m, n, k, alpha, A, lda, B, ldb, beta, C_, ldc):
+        _check(self.lib.wgb_dgemm(self.handle, transA, transB, m, n, k, alpha, _p(A), lda,
+                                  _p(B), ldb, beta, _p(C_), ldc), "wgb_dgemm")
+
+    # ---- level 1 ----
+    def sdot(self, n, x, incx, y, incy):
+        r = C.c_float(0)
+        _check(self.lib.wgb_sdot(self.handle, n, _p(x), incx, _p(y), incy, C.byref(r)),
+               "wgb_sdot")
+        return np.float32(r.value)
+
+    def sdot_dev(self, n, x, incx, y, incy, out):
+        _check(self.lib.wgb_sdot_dev(self.handle, n, _p(x), incx, _p(y), incy, _p(out)),
+               "wgb_sdot_dev")
+
+    def sasum(self, n, x, incx):
+        r = C.c_float(0)
+        _check(self.lib.wgb_sasum(self.handle, n, _p(x), incx, C.byref(r)), "wgb_sasum")
+        return np.float32(r.value)
+
+    def sasum_dev(self, n, x, incx, out):
+        _check(self.lib.wgb_sasum_dev(self.handle, n, _p(x), incx, _p(out)), "wgb_sasum_dev")
+
+    def snrm2(self, n, x, incx):
+        r = C.c_float(0)
+        _check(self.lib.wgb_snrm2(self.handle, n, _p(x), incx, C.byref(r)), "wgb_snrm2")
+        return np.float32(r.value)
+
+    def snrm2_dev(self, n, x, incx, out):
+        _check(self.lib.wgb_snrm2_dev(self.handle, n, _p(x), incx, _p(out)), "wgb_snrm2_dev")
+
+    def isamax(self, n, x, incx):
+        r = _i64(0)
+        _check(self.lib.wgb_isamax(self.handle, n, _p(x), incx, C.byref(r)), "wgb_isamax")
+        return int(r.value)
+
+    def isamax_dev(self, n, x, incx, out):
+        _check(self.lib.wgb_isamax_dev(self.handle, n, _p(x), incx, _p(out)), "wgb_isamax_dev")
+
+
+def _p(x):
+    """Device pointer of a DeviceArray, or a raw integer pointer / None."""
+    if x is None:
+        return None
+    if isinstance(x, DeviceArray):
+        return x.ptr
+    return int(x)

@@ -59,6 +59,9 @@ struct Ty<float> {
   typedef float v2 __attribute__((ext_vector_type(2)));
   typedef float acc __attribute__((ext_vector_type(4)));
   static constexpr int VW = 4;
+  // Row of the 16x16 result held by accumulator register q of lane-group g
+  // (lane / 16): rows 4g .. 4g+3 (checked on gfx950 with one-hot operands).
+  __device__ static int drow(int g, int q) { return 4 * g + q; }
   __device__ static acc mfma(float a, float b, acc c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
   }
@@ -71,6 +74,9 @@ struct Ty<double> {
   typedef double v2 __attribute__((ext_vector_type(2)));
   typedef double acc __attribute__((ext_vector_type(4)));
   static constexpr int VW = 2;
+  // The fp64 16x16x4 MFMA interleaves instead: register q of lane-group g
+  // holds row g + 4q.
+  __device__ static int drow(int g, int q) { return g + 4 * q; }
   __device__ static acc mfma(double a, double b, acc c) {
     return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
   }
@@ -274,16 +280,18 @@ __device__ __forceinline__ void fetch_operands(const T *stage, int wrow, int kc,
   }
 }
 
-// Row (or column) inside the wave tile held by lane `lane` for MFMA block b
-// and accumulator register q (for columns pass q = 0 and use the i16 form).
-template <bool KC, int MB, int VW>
+// Row inside the wave tile held by lane `lane` for MFMA block b and
+// accumulator register q.
+template <typename T, bool KC, int MB>
 __device__ __forceinline__ int out_row(int b, int q, int lane) {
+  constexpr int VW = Ty<T>::VW;
   constexpr int RW = MB < VW ? MB : VW;
-  const int g = lane >> 4;
-  if (KC) return 16 * b + 4 * g + q;
-  return 16 * RW * (b / RW) + RW * (4 * g + q) + (b % RW);
+  const int r = Ty<T>::drow(lane >> 4, q);
+  if (KC) return 16 * b + r;
+  return 16 * RW * (b / RW) + RW * r + (b % RW);
 }
 
+// Column inside the wave tile held by lane `lane` for MFMA block b.
 template <bool KC, int MB, int VW>
 __device__ __forceinline__ int out_col(int b, int lane) {
   constexpr int RW = MB < VW ? MB : VW;
@@ -382,7 +390,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs<T> p) {
       const int64_t col = n0 + wn + out_col<BKC, MB, VW>(j, lane);
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int64_t row = m0 + wm + out_row<AKC, MB, VW>(i, q, lane);
+        const int64_t row = m0 + wm + out_row<T, AKC, MB>(i, q, lane);
         bool ok = row < p.m && col < p.n;
         if (tri_diag) ok = ok && (p.uplo == WGB_LOWER ? row >= col : row <= col);
         if (ok) {

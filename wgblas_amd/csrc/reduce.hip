@@ -6,11 +6,13 @@
 // src/shaders/sdot.wgsl, src/shaders/reduction/sum.wgsl). This file keeps the
 // two-pass structure and its determinism, but sizes pass 1 for MI355X's HBM:
 //
-//  * pass 1 uses G = min(2048, ceil(n / 4096)) blocks of 256 threads; G
-//    depends only on n, so the summation order (and the result) is the same
-//    on every run and every device;
-//  * unit-stride, 16-byte-aligned operands are read as 16-byte vectors, eight loads in
-//    flight per lane per iteration; other strides read one element per lane;
+//  * pass 1 uses G = min(2048, ceil(n / 4096)) blocks of 256 threads, each
+//    reading one contiguous range of x (and y); G and the ranges depend only
+//    on n, so the summation order (and the result) is the same on every run
+//    and every device;
+//  * unit-stride, 16-byte-aligned operands are read with 16-byte
+//    non-temporal loads, eight in flight per lane per input; other strides
+//    read one element per lane;
 //  * a block folds its lanes with 64-lane shuffles, then its four waves in
 //    LDS, in a fixed order, and writes one partial;
 //  * pass 2 (one block) folds the G partials in a fixed order and, for snrm2
@@ -48,192 +50,58 @@ int reduce_blocks(int64_t n) {
 
 bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
-// ---- wave / block folds (fixed order) ------------------------------------
+// ---- the four reductions as accumulate / merge policies -------------------
+//
+// State: what one lane accumulates. Partial: what a block (and pass 2)
+// merges. add4 takes four consecutive elements starting at element index
+// `i`; add1 takes one element, `c` (0..3) naming an accumulation chain the
+// policy may use for ILP.
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
-}
+__device__ __forceinline__ v4f nt_load(const v4f *p) { return __builtin_nontemporal_load(p); }
 
-// Folds one float per thread into thread 0's return value.
-__device__ __forceinline__ float block_sum(float v, float *lds) {
-  v = wave_sum(v);
-  int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  if (lane == 0) lds[wave] = v;
-  __syncthreads();
-  float r = 0.0f;
-  if (threadIdx.x == 0) r = (lds[0] + lds[1]) + (lds[2] + lds[3]);
-  return r;
-}
-
-// isamax's pair order: b replaces a when larger, or equal with a lower index.
-__device__ __forceinline__ void amax_merge(float &av, int64_t &ai, float bv, int64_t bi) {
-  if (bv > av || (bv == av && bi < ai)) {
-    av = bv;
-    ai = bi;
+struct SdotOp {
+  static constexpr int NIN = 2;
+  typedef v4f State;
+  typedef float Partial;
+  __device__ static State init() { return v4f{0.f, 0.f, 0.f, 0.f}; }
+  __device__ static void add4(State &s, v4f a, v4f b, int64_t) {
+    s.x = fmaf(a.x, b.x, s.x);
+    s.y = fmaf(a.y, b.y, s.y);
+    s.z = fmaf(a.z, b.z, s.z);
+    s.w = fmaf(a.w, b.w, s.w);
   }
-}
+  __device__ static void add1(State &s, float a, float b, int64_t, int c) { s[c] = fmaf(a, b, s[c]); }
+  __device__ static Partial finish(State s) { return (s.x + s.y) + (s.z + s.w); }
+  __device__ static Partial identity() { return 0.0f; }
+  __device__ static Partial merge(Partial a, Partial b) { return a + b; }
+  __device__ static Partial shfl(Partial a, int off) { return __shfl_xor(a, off, 64); }
+};
 
-__device__ __forceinline__ void wave_amax(float &v, int64_t &i) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    float ov = __shfl_xor(v, off, 64);
-    int64_t oi = __shfl_xor(i, off, 64);
-    amax_merge(v, i, ov, oi);
+struct SasumOp {
+  static constexpr int NIN = 1;
+  typedef v4f State;
+  typedef float Partial;
+  __device__ static State init() { return v4f{0.f, 0.f, 0.f, 0.f}; }
+  __device__ static void add4(State &s, v4f a, v4f, int64_t) {
+    s.x += fabsf(a.x);
+    s.y += fabsf(a.y);
+    s.z += fabsf(a.z);
+    s.w += fabsf(a.w);
   }
-}
+  __device__ static void add1(State &s, float a, float, int64_t, int c) { s[c] += fabsf(a); }
+  __device__ static Partial finish(State s) { return (s.x + s.y) + (s.z + s.w); }
+  __device__ static Partial identity() { return 0.0f; }
+  __device__ static Partial merge(Partial a, Partial b) { return a + b; }
+  __device__ static Partial shfl(Partial a, int off) { return __shfl_xor(a, off, 64); }
+};
 
-__device__ __forceinline__ void block_amax(float &v, int64_t &i, float *lds_v, int64_t *lds_i) {
-  wave_amax(v, i);
-  int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  if (lane == 0) {
-    lds_v[wave] = v;
-    lds_i[wave] = i;
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    v = lds_v[0];
-    i = lds_i[0];
-    for (int w = 1; w < kThreads / 64; ++w) amax_merge(v, i, lds_v[w], lds_i[w]);
-  }
-}
-
-// ---- sdot / sasum ---------------------------------------------------------
-
-__global__ __launch_bounds__(kThreads) void sdot_pass1_vec(const float *__restrict__ x,
-                                                           const float *__restrict__ y, int64_t n,
-                                                           float *__restrict__ partials) {
-  __shared__ float lds[kThreads / 64];
-  const v4f *x4 = reinterpret_cast<const v4f *>(x);
-  const v4f *y4 = reinterpret_cast<const v4f *>(y);
-  const int64_t n4 = n >> 2;
-  const int64_t S = (int64_t)gridDim.x * kThreads;
-  int64_t q = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
-  for (; q + (kUnroll - 1) * S < n4; q += kUnroll * S) {
-    v4f a[kUnroll], b[kUnroll];
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      a[u] = __builtin_nontemporal_load(&x4[q + u * S]);
-      b[u] = __builtin_nontemporal_load(&y4[q + u * S]);
-    }
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      acc.x = fmaf(a[u].x, b[u].x, acc.x);
-      acc.y = fmaf(a[u].y, b[u].y, acc.y);
-      acc.z = fmaf(a[u].z, b[u].z, acc.z);
-      acc.w = fmaf(a[u].w, b[u].w, acc.w);
-    }
-  }
-  for (; q < n4; q += S) {
-    v4f a = x4[q], b = y4[q];
-    acc.x = fmaf(a.x, b.x, acc.x);
-    acc.y = fmaf(a.y, b.y, acc.y);
-    acc.z = fmaf(a.z, b.z, acc.z);
-    acc.w = fmaf(a.w, b.w, acc.w);
-  }
-  if (blockIdx.x == 0 && threadIdx.x == 0)
-    for (int64_t i = n4 * 4; i < n; ++i) acc.x = fmaf(x[i], y[i], acc.x);
-  float r = block_sum((acc.x + acc.y) + (acc.z + acc.w), lds);
-  if (threadIdx.x == 0) partials[blockIdx.x] = r;
-}
-
-__global__ __launch_bounds__(kThreads) void sdot_pass1_strided(const float *__restrict__ x,
-                                                               int64_t incx,
-                                                               const float *__restrict__ y,
-                                                               int64_t incy, int64_t n,
-                                                               float *__restrict__ partials) {
-  __shared__ float lds[kThreads / 64];
-  const int64_t S = (int64_t)gridDim.x * kThreads;
-  int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};
-  for (; i + (kUnroll - 1) * S < n; i += kUnroll * S) {
-    float a[kUnroll], b[kUnroll];
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      a[u] = x[(i + u * S) * incx];
-      b[u] = y[(i + u * S) * incy];
-    }
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) acc[u & 3] = fmaf(a[u], b[u], acc[u & 3]);
-  }
-  for (; i < n; i += S) acc[0] = fmaf(x[i * incx], y[i * incy], acc[0]);
-  float r = block_sum((acc[0] + acc[1]) + (acc[2] + acc[3]), lds);
-  if (threadIdx.x == 0) partials[blockIdx.x] = r;
-}
-
-__global__ __launch_bounds__(kThreads) void sasum_pass1_vec(const float *__restrict__ x, int64_t n,
-                                                            float *__restrict__ partials) {
-  __shared__ float lds[kThreads / 64];
-  const v4f *x4 = reinterpret_cast<const v4f *>(x);
-  const int64_t n4 = n >> 2;
-  const int64_t S = (int64_t)gridDim.x * kThreads;
-  int64_t q = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
-  for (; q + (kUnroll - 1) * S < n4; q += kUnroll * S) {
-    v4f a[kUnroll];
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) a[u] = __builtin_nontemporal_load(&x4[q + u * S]);
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      acc.x += fabsf(a[u].x);
-      acc.y += fabsf(a[u].y);
-      acc.z += fabsf(a[u].z);
-      acc.w += fabsf(a[u].w);
-    }
-  }
-  for (; q < n4; q += S) {
-    v4f a = x4[q];
-    acc.x += fabsf(a.x);
-    acc.y += fabsf(a.y);
-    acc.z += fabsf(a.z);
-    acc.w += fabsf(a.w);
-  }
-  if (blockIdx.x == 0 && threadIdx.x == 0)
-    for (int64_t i = n4 * 4; i < n; ++i) acc.x += fabsf(x[i]);
-  float r = block_sum((acc.x + acc.y) + (acc.z + acc.w), lds);
-  if (threadIdx.x == 0) partials[blockIdx.x] = r;
-}
-
-__global__ __launch_bounds__(kThreads) void sasum_pass1_strided(const float *__restrict__ x,
-                                                                int64_t incx, int64_t n,
-                                                                float *__restrict__ partials) {
-  __shared__ float lds[kThreads / 64];
-  const int64_t S = (int64_t)gridDim.x * kThreads;
-  int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};
-  for (; i + (kUnroll - 1) * S < n; i += kUnroll * S) {
-    float a[kUnroll];
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) a[u] = x[(i + u * S) * incx];
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) acc[u & 3] += fabsf(a[u]);
-  }
-  for (; i < n; i += S) acc[0] += fabsf(x[i * incx]);
-  float r = block_sum((acc[0] + acc[1]) + (acc[2] + acc[3]), lds);
-  if (threadIdx.x == 0) partials[blockIdx.x] = r;
-}
-
-// Pass 2 for sdot/sasum: one block folds G partials in a fixed order.
-__global__ __launch_bounds__(kThreads) void sum_pass2(const float *__restrict__ partials, int G,
-                                                      float *__restrict__ out) {
-  __shared__ float lds[kThreads / 64];
-  float acc = 0.0f;
-  for (int i = threadIdx.x; i < G; i += kThreads) acc += partials[i];
-  float r = block_sum(acc, lds);
-  if (threadIdx.x == 0) *out = r;
-}
-
-// ---- snrm2 ----------------------------------------------------------------
-
+// snrm2: (big, medium, small) sums of scaled squares.
 struct Nrm {
   float big, med, sml;
 };
 
-// Adds |v|'s contribution to (big, medium, small) as snrm2.wgsl's accum()
-// does: NaN fails both tests and lands in medium, which the combine turns
-// into a NaN result.
+// Adds |v|'s contribution as snrm2.wgsl's accum() does: NaN fails both
+// tests and lands in medium, which the combine turns into a NaN result.
 __device__ __forceinline__ void nrm_accum(Nrm &s, float v) {
   float ax = fabsf(v);
   bool big = ax > kTbig;
@@ -252,73 +120,178 @@ __device__ __forceinline__ bool nrm_odd(float v) {
   return !(ax <= kTbig) || (ax < kTsml && ax != 0.0f);
 }
 
-__device__ __forceinline__ void nrm_accum4(Nrm &s, v4f a) {
-  bool odd = nrm_odd(a.x) || nrm_odd(a.y) || nrm_odd(a.z) || nrm_odd(a.w);
-  if (__any(odd)) {
-    nrm_accum(s, a.x);
-    nrm_accum(s, a.y);
-    nrm_accum(s, a.z);
-    nrm_accum(s, a.w);
-  } else {
-    s.med = fmaf(a.x, a.x, s.med);
-    s.med = fmaf(a.y, a.y, s.med);
-    s.med = fmaf(a.z, a.z, s.med);
-    s.med = fmaf(a.w, a.w, s.med);
+struct Snrm2Op {
+  static constexpr int NIN = 1;
+  typedef Nrm State;
+  typedef v4f Partial;  // (big, medium, small, 0)
+  __device__ static State init() { return Nrm{0.f, 0.f, 0.f}; }
+  __device__ static void add4(State &s, v4f a, v4f, int64_t) {
+    // Whole-wave fast path: when no lane holds an element outside the
+    // medium band, the four squares go straight into the medium sum.
+    bool odd = nrm_odd(a.x) || nrm_odd(a.y) || nrm_odd(a.z) || nrm_odd(a.w);
+    if (__any(odd)) {
+      nrm_accum(s, a.x);
+      nrm_accum(s, a.y);
+      nrm_accum(s, a.z);
+      nrm_accum(s, a.w);
+    } else {
+      s.med = fmaf(a.x, a.x, s.med);
+      s.med = fmaf(a.y, a.y, s.med);
+      s.med = fmaf(a.z, a.z, s.med);
+      s.med = fmaf(a.w, a.w, s.med);
+    }
+  }
+  __device__ static void add1(State &s, float a, float, int64_t, int) { nrm_accum(s, a); }
+  __device__ static Partial finish(State s) { return v4f{s.big, s.med, s.sml, 0.f}; }
+  __device__ static Partial identity() { return v4f{0.f, 0.f, 0.f, 0.f}; }
+  __device__ static Partial merge(Partial a, Partial b) { return a + b; }
+  __device__ static Partial shfl(Partial a, int off) {
+    return v4f{__shfl_xor(a.x, off, 64), __shfl_xor(a.y, off, 64), __shfl_xor(a.z, off, 64), 0.f};
+  }
+};
+
+// isamax: (max |x|, its first index). A lane visits its elements in
+// increasing index order, so the strict '>' keeps the first occurrence;
+// merges prefer the larger value, then the lower index. The -1 sentinel
+// loses to every |x| >= 0, and NaN never compares greater, so it is skipped.
+struct AmaxPartial {
+  float val;
+  float pad;
+  int64_t idx;
+};
+
+__device__ __forceinline__ void amax_step(AmaxPartial &s, float v, int64_t i) {
+  float ax = fabsf(v);
+  if (ax > s.val) {
+    s.val = ax;
+    s.idx = i;
   }
 }
 
-__device__ __forceinline__ void block_nrm(Nrm &s, v4f *lds) {
-  s.big = wave_sum(s.big);
-  s.med = wave_sum(s.med);
-  s.sml = wave_sum(s.sml);
-  int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  if (lane == 0) lds[wave] = v4f{s.big, s.med, s.sml, 0.f};
+struct IsamaxOp {
+  static constexpr int NIN = 1;
+  typedef AmaxPartial State;
+  typedef AmaxPartial Partial;
+  __device__ static State init() { return AmaxPartial{-1.0f, 0.f, 0}; }
+  __device__ static void add4(State &s, v4f a, v4f, int64_t i) {
+    amax_step(s, a.x, i);
+    amax_step(s, a.y, i + 1);
+    amax_step(s, a.z, i + 2);
+    amax_step(s, a.w, i + 3);
+  }
+  __device__ static void add1(State &s, float a, float, int64_t i, int) { amax_step(s, a, i); }
+  __device__ static Partial finish(State s) { return s; }
+  __device__ static Partial identity() { return AmaxPartial{-1.0f, 0.f, 0}; }
+  __device__ static Partial merge(Partial a, Partial b) {
+    return (b.val > a.val || (b.val == a.val && b.idx < a.idx)) ? b : a;
+  }
+  __device__ static Partial shfl(Partial a, int off) {
+    return AmaxPartial{__shfl_xor(a.val, off, 64), 0.f, __shfl_xor(a.idx, off, 64)};
+  }
+};
+
+// ---- block merge (fixed order) --------------------------------------------
+
+template <class Op>
+__device__ __forceinline__ typename Op::Partial block_merge(typename Op::Partial p) {
+  __shared__ typename Op::Partial lds[kThreads / 64];
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) p = Op::merge(p, Op::shfl(p, off));
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) lds[wave] = p;
   __syncthreads();
   if (threadIdx.x == 0) {
-    v4f a = lds[0], b = lds[1], c = lds[2], d = lds[3];
-    s.big = (a.x + b.x) + (c.x + d.x);
-    s.med = (a.y + b.y) + (c.y + d.y);
-    s.sml = (a.z + b.z) + (c.z + d.z);
+    p = Op::merge(Op::merge(lds[0], lds[1]), Op::merge(lds[2], lds[3]));
   }
+  return p;
 }
 
-__global__ __launch_bounds__(kThreads) void snrm2_pass1_vec(const float *__restrict__ x, int64_t n,
-                                                            v4f *__restrict__ partials) {
-  __shared__ v4f lds[kThreads / 64];
+// Block b's share of [0, total) units: one contiguous range, its start a
+// multiple of 8 units, depending only on total and the grid size. Reading
+// whole contiguous ranges per block streams HBM better than a grid-stride
+// walk (measured on MI355X: ~7.0 vs ~5.5 TB/s for a read-only pass).
+__device__ __forceinline__ void chunk_of(int64_t total, int64_t &beg, int64_t &end) {
+  int64_t per = (total + gridDim.x - 1) / gridDim.x;
+  per = (per + 7) & ~(int64_t)7;
+  beg = per * blockIdx.x;
+  end = beg + per < total ? beg + per : total;
+  if (beg > end) beg = end;
+}
+
+// Pass 1 over unit-stride, 16-byte-aligned operands: 16-byte non-temporal
+// loads, kUnroll of them in flight per lane per input.
+template <class Op>
+__global__ __launch_bounds__(kThreads) void pass1_vec(const float *__restrict__ x,
+                                                      const float *__restrict__ y, int64_t n,
+                                                      typename Op::Partial *__restrict__ partials) {
   const v4f *x4 = reinterpret_cast<const v4f *>(x);
+  const v4f *y4 = reinterpret_cast<const v4f *>(y);
   const int64_t n4 = n >> 2;
-  const int64_t S = (int64_t)gridDim.x * kThreads;
-  int64_t q = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  Nrm s{0.f, 0.f, 0.f};
-  for (; q + (kUnroll - 1) * S < n4; q += kUnroll * S) {
-    v4f a[kUnroll];
+  int64_t beg, end;
+  chunk_of(n4, beg, end);
+  typename Op::State s = Op::init();
+  int64_t q = beg + threadIdx.x;
+  for (; q + (kUnroll - 1) * kThreads < end; q += kUnroll * kThreads) {
+    v4f a[kUnroll], b[kUnroll];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) a[u] = __builtin_nontemporal_load(&x4[q + u * S]);
+    for (int u = 0; u < kUnroll; ++u) {
+      a[u] = nt_load(x4 + q + u * kThreads);
+      b[u] = Op::NIN == 2 ? nt_load(y4 + q + u * kThreads) : a[u];
+    }
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) nrm_accum4(s, a[u]);
+    for (int u = 0; u < kUnroll; ++u) Op::add4(s, a[u], b[u], 4 * (q + u * kThreads));
   }
-  for (; q < n4; q += S) nrm_accum4(s, x4[q]);
-  if (blockIdx.x == 0 && threadIdx.x == 0)
-    for (int64_t i = n4 * 4; i < n; ++i) nrm_accum(s, x[i]);
-  block_nrm(s, lds);
-  if (threadIdx.x == 0) partials[blockIdx.x] = v4f{s.big, s.med, s.sml, 0.f};
+  for (; q < end; q += kThreads) {
+    v4f a = x4[q];
+    Op::add4(s, a, Op::NIN == 2 ? y4[q] : a, 4 * q);
+  }
+  // The n % 4 trailing elements follow the last block's range.
+  if (blockIdx.x == gridDim.x - 1 && threadIdx.x == 0)
+    for (int64_t i = n4 * 4; i < n; ++i) Op::add1(s, x[i], Op::NIN == 2 ? y[i] : 0.f, i, 0);
+  typename Op::Partial p = block_merge<Op>(Op::finish(s));
+  if (threadIdx.x == 0) partials[blockIdx.x] = p;
 }
 
-__global__ __launch_bounds__(kThreads) void snrm2_pass1_strided(const float *__restrict__ x,
-                                                                int64_t incx, int64_t n,
-                                                                v4f *__restrict__ partials) {
-  __shared__ v4f lds[kThreads / 64];
-  const int64_t S = (int64_t)gridDim.x * kThreads;
-  int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  Nrm s{0.f, 0.f, 0.f};
-  for (; i + 3 * S < n; i += 4 * S) {
-    v4f a = v4f{x[i * incx], x[(i + S) * incx], x[(i + 2 * S) * incx],
-                           x[(i + 3 * S) * incx]};
-    nrm_accum4(s, a);
+// Pass 1 for any positive stride (and misaligned unit stride): one element
+// per lane per step, kUnroll steps in flight.
+template <class Op>
+__global__ __launch_bounds__(kThreads) void pass1_strided(const float *__restrict__ x, int64_t incx,
+                                                          const float *__restrict__ y, int64_t incy,
+                                                          int64_t n,
+                                                          typename Op::Partial *__restrict__ partials) {
+  int64_t beg, end;
+  chunk_of(n, beg, end);
+  typename Op::State s = Op::init();
+  int64_t i = beg + threadIdx.x;
+  for (; i + (kUnroll - 1) * kThreads < end; i += kUnroll * kThreads) {
+    float a[kUnroll], b[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      a[u] = x[(i + u * kThreads) * incx];
+      b[u] = Op::NIN == 2 ? y[(i + u * kThreads) * incy] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) Op::add1(s, a[u], b[u], i + u * kThreads, u & 3);
   }
-  for (; i < n; i += S) nrm_accum(s, x[i * incx]);
-  block_nrm(s, lds);
-  if (threadIdx.x == 0) partials[blockIdx.x] = v4f{s.big, s.med, s.sml, 0.f};
+  for (; i < end; i += kThreads) Op::add1(s, x[i * incx], Op::NIN == 2 ? y[i * incy] : 0.f, i, 0);
+  typename Op::Partial p = block_merge<Op>(Op::finish(s));
+  if (threadIdx.x == 0) partials[blockIdx.x] = p;
+}
+
+// Pass 2: one block folds the G partials in a fixed order.
+template <class Op>
+__device__ __forceinline__ typename Op::Partial fold_partials(const typename Op::Partial *partials,
+                                                              int G) {
+  typename Op::Partial p = Op::identity();
+  for (int i = threadIdx.x; i < G; i += kThreads) p = Op::merge(p, partials[i]);
+  return block_merge<Op>(p);
+}
+
+template <class Op>
+__global__ __launch_bounds__(kThreads) void sum_pass2(const float *__restrict__ partials, int G,
+                                                      float *__restrict__ out) {
+  float p = fold_partials<Op>(partials, G);
+  if (threadIdx.x == 0) *out = p;
 }
 
 // v * 2^e by editing the exponent field, as scaledSum.wgsl's ldexpBits does:
@@ -367,104 +340,14 @@ __device__ float nrm_combine(float abig, float amed, float asml) {
 
 __global__ __launch_bounds__(kThreads) void snrm2_pass2(const v4f *__restrict__ partials, int G,
                                                         float *__restrict__ out) {
-  __shared__ v4f lds[kThreads / 64];
-  Nrm s{0.f, 0.f, 0.f};
-  for (int i = threadIdx.x; i < G; i += kThreads) {
-    v4f p = partials[i];
-    s.big += p.x;
-    s.med += p.y;
-    s.sml += p.z;
-  }
-  block_nrm(s, lds);
-  if (threadIdx.x == 0) *out = nrm_combine(s.big, s.med, s.sml);
-}
-
-// ---- isamax ---------------------------------------------------------------
-
-struct AmaxPartial {
-  float val;
-  float pad;
-  int64_t idx;
-};
-
-__device__ __forceinline__ void amax_step(float &best, int64_t &bi, float v, int64_t i) {
-  float ax = fabsf(v);
-  if (ax > best) {
-    best = ax;
-    bi = i;
-  }
-}
-
-__global__ __launch_bounds__(kThreads) void isamax_pass1_vec(const float *__restrict__ x, int64_t n,
-                                                             AmaxPartial *__restrict__ partials) {
-  __shared__ float lds_v[kThreads / 64];
-  __shared__ int64_t lds_i[kThreads / 64];
-  const v4f *x4 = reinterpret_cast<const v4f *>(x);
-  const int64_t n4 = n >> 2;
-  const int64_t S = (int64_t)gridDim.x * kThreads;
-  int64_t q = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  float best = -1.0f;
-  int64_t bi = 0;
-  for (; q + (kUnroll - 1) * S < n4; q += kUnroll * S) {
-    v4f a[kUnroll];
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) a[u] = __builtin_nontemporal_load(&x4[q + u * S]);
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      int64_t base = (q + u * S) * 4;
-      amax_step(best, bi, a[u].x, base);
-      amax_step(best, bi, a[u].y, base + 1);
-      amax_step(best, bi, a[u].z, base + 2);
-      amax_step(best, bi, a[u].w, base + 3);
-    }
-  }
-  for (; q < n4; q += S) {
-    v4f a = x4[q];
-    int64_t base = q * 4;
-    amax_step(best, bi, a.x, base);
-    amax_step(best, bi, a.y, base + 1);
-    amax_step(best, bi, a.z, base + 2);
-    amax_step(best, bi, a.w, base + 3);
-  }
-  if (blockIdx.x == 0 && threadIdx.x == 0)
-    for (int64_t i = n4 * 4; i < n; ++i) amax_step(best, bi, x[i], i);
-  block_amax(best, bi, lds_v, lds_i);
-  if (threadIdx.x == 0) partials[blockIdx.x] = AmaxPartial{best, 0.f, bi};
-}
-
-__global__ __launch_bounds__(kThreads) void isamax_pass1_strided(const float *__restrict__ x,
-                                                                 int64_t incx, int64_t n,
-                                                                 AmaxPartial *__restrict__ partials) {
-  __shared__ float lds_v[kThreads / 64];
-  __shared__ int64_t lds_i[kThreads / 64];
-  const int64_t S = (int64_t)gridDim.x * kThreads;
-  int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  float best = -1.0f;
-  int64_t bi = 0;
-  for (; i + (kUnroll - 1) * S < n; i += kUnroll * S) {
-    float a[kUnroll];
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) a[u] = x[(i + u * S) * incx];
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) amax_step(best, bi, a[u], i + u * S);
-  }
-  for (; i < n; i += S) amax_step(best, bi, x[i * incx], i);
-  block_amax(best, bi, lds_v, lds_i);
-  if (threadIdx.x == 0) partials[blockIdx.x] = AmaxPartial{best, 0.f, bi};
+  v4f p = fold_partials<Snrm2Op>(partials, G);
+  if (threadIdx.x == 0) *out = nrm_combine(p.x, p.y, p.z);
 }
 
 __global__ __launch_bounds__(kThreads) void isamax_pass2(const AmaxPartial *__restrict__ partials,
                                                          int G, int64_t *__restrict__ out) {
-  __shared__ float lds_v[kThreads / 64];
-  __shared__ int64_t lds_i[kThreads / 64];
-  float best = -1.0f;
-  int64_t bi = 0;
-  for (int i = threadIdx.x; i < G; i += kThreads) {
-    AmaxPartial p = partials[i];
-    amax_merge(best, bi, p.val, p.idx);
-  }
-  block_amax(best, bi, lds_v, lds_i);
-  if (threadIdx.x == 0) *out = bi;
+  AmaxPartial p = fold_partials<IsamaxOp>(partials, G);
+  if (threadIdx.x == 0) *out = p.idx;
 }
 
 // Writes the n <= 0 answer of a `_dev` call with a kernel rather than a
@@ -486,16 +369,23 @@ int check_vec(int64_t n, const float *x, int64_t incx, const char *xname, const 
 void *partials_of(wgb_ctx *ctx) { return ctx->scratch; }
 void *result_slot(wgb_ctx *ctx) { return (char *)ctx->scratch + (size_t)wgb::kMaxReduceBlocks * 16; }
 
+template <class Op>
+void launch_pass1(wgb_ctx *ctx, int G, int64_t n, const float *x, int64_t incx, const float *y,
+                  int64_t incy, typename Op::Partial *part) {
+  bool vec = incx == 1 && aligned16(x) && (Op::NIN == 1 || (incy == 1 && aligned16(y)));
+  if (vec)
+    pass1_vec<Op><<<G, kThreads, 0, ctx->stream>>>(x, y, n, part);
+  else
+    pass1_strided<Op><<<G, kThreads, 0, ctx->stream>>>(x, incx, y, incy, n, part);
+}
+
 int launch_sdot(wgb_ctx *ctx, int64_t n, const float *x, int64_t incx, const float *y,
                 int64_t incy, float *d_out) {
   int G = reduce_blocks(n);
   float *part = (float *)partials_of(ctx);
-  if (incx == 1 && incy == 1 && aligned16(x) && aligned16(y))
-    sdot_pass1_vec<<<G, kThreads, 0, ctx->stream>>>(x, y, n, part);
-  else
-    sdot_pass1_strided<<<G, kThreads, 0, ctx->stream>>>(x, incx, y, incy, n, part);
+  launch_pass1<SdotOp>(ctx, G, n, x, incx, y, incy, part);
   WGB_CHECK_LAUNCH("sdot pass 1");
-  sum_pass2<<<1, kThreads, 0, ctx->stream>>>(part, G, d_out);
+  sum_pass2<SdotOp><<<1, kThreads, 0, ctx->stream>>>(part, G, d_out);
   WGB_CHECK_LAUNCH("sdot pass 2");
   return WGB_OK;
 }
@@ -503,12 +393,9 @@ int launch_sdot(wgb_ctx *ctx, int64_t n, const float *x, int64_t incx, const flo
 int launch_sasum(wgb_ctx *ctx, int64_t n, const float *x, int64_t incx, float *d_out) {
   int G = reduce_blocks(n);
   float *part = (float *)partials_of(ctx);
-  if (incx == 1 && aligned16(x))
-    sasum_pass1_vec<<<G, kThreads, 0, ctx->stream>>>(x, n, part);
-  else
-    sasum_pass1_strided<<<G, kThreads, 0, ctx->stream>>>(x, incx, n, part);
+  launch_pass1<SasumOp>(ctx, G, n, x, incx, x, incx, part);
   WGB_CHECK_LAUNCH("sasum pass 1");
-  sum_pass2<<<1, kThreads, 0, ctx->stream>>>(part, G, d_out);
+  sum_pass2<SasumOp><<<1, kThreads, 0, ctx->stream>>>(part, G, d_out);
   WGB_CHECK_LAUNCH("sasum pass 2");
   return WGB_OK;
 }
@@ -516,10 +403,7 @@ int launch_sasum(wgb_ctx *ctx, int64_t n, const float *x, int64_t incx, float *d
 int launch_snrm2(wgb_ctx *ctx, int64_t n, const float *x, int64_t incx, float *d_out) {
   int G = reduce_blocks(n);
   v4f *part = (v4f *)partials_of(ctx);
-  if (incx == 1 && aligned16(x))
-    snrm2_pass1_vec<<<G, kThreads, 0, ctx->stream>>>(x, n, part);
-  else
-    snrm2_pass1_strided<<<G, kThreads, 0, ctx->stream>>>(x, incx, n, part);
+  launch_pass1<Snrm2Op>(ctx, G, n, x, incx, x, incx, part);
   WGB_CHECK_LAUNCH("snrm2 pass 1");
   snrm2_pass2<<<1, kThreads, 0, ctx->stream>>>(part, G, d_out);
   WGB_CHECK_LAUNCH("snrm2 pass 2");
@@ -529,10 +413,7 @@ int launch_snrm2(wgb_ctx *ctx, int64_t n, const float *x, int64_t incx, float *d
 int launch_isamax(wgb_ctx *ctx, int64_t n, const float *x, int64_t incx, int64_t *d_out) {
   int G = reduce_blocks(n);
   AmaxPartial *part = (AmaxPartial *)partials_of(ctx);
-  if (incx == 1 && aligned16(x))
-    isamax_pass1_vec<<<G, kThreads, 0, ctx->stream>>>(x, n, part);
-  else
-    isamax_pass1_strided<<<G, kThreads, 0, ctx->stream>>>(x, incx, n, part);
+  launch_pass1<IsamaxOp>(ctx, G, n, x, incx, x, incx, part);
   WGB_CHECK_LAUNCH("isamax pass 1");
   isamax_pass2<<<1, kThreads, 0, ctx->stream>>>(part, G, d_out);
   WGB_CHECK_LAUNCH("isamax pass 2");

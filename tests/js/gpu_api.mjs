@@ -1,0 +1,353 @@
+// End-to-end checks of the JavaScript API on the GPU (through the Node-API
+// addon and libwgblas_hip): the reference's edge-case fixtures (exact), its
+// regression scenarios (forward-error bound of tests/sgemm/helpers.js, bit
+// checks of untouched triangles / padding / k = 0), the GpuMatrix /
+// GpuVector residency forms, layouts, benchmark timing and device handling.
+// The expected values come from a plain double-precision triple loop here
+// (exact on the integer-valued fixtures); the kernels themselves are held to
+// the CPU oracle by the Python suites.
+import { readFileSync } from "fs";
+import { fileURLToPath } from "url";
+import { dirname, join } from "path";
+import { test, run, assert, assertEqual } from "./harness.mjs";
+import * as wg from "../../wgblas_amd/js/index.mjs";
+
+const here = dirname(fileURLToPath(import.meta.url));
+const fixture = (name) => JSON.parse(readFileSync(join(here, "..", "golden", "edge_cases", `${name}.json`), "utf8"));
+
+let device;
+
+// ---------------------------------------------------------------- reference
+const opElem = (M, ld, layout, trans, r, c) => {
+  const [sr, sc] = trans === "transpose" ? [c, r] : [r, c];
+  return layout === "column-major" ? M[sc * ld + sr] : M[sr * ld + sc];
+};
+const cIndex = (ldc, layout, r, c) => (layout === "column-major" ? c * ldc + r : r * ldc + c);
+const inTri = (uplo, r, c) => !uplo || (uplo === "lower" ? c <= r : c >= r);
+
+function refGemm(a) {
+  const layout = a.layout || "row-major";
+  const out = Float64Array.from(a.C);
+  const absdot = new Float64Array(a.C.length);
+  for (let i = 0; i < a.m; i++)
+    for (let j = 0; j < a.n; j++) {
+      if (!inTri(a.uplo, i, j)) continue;
+      let s = 0;
+      let ab = 0;
+      if (a.alpha !== 0)
+        for (let p = 0; p < a.k; p++) {
+          const prod = opElem(a.A, a.lda, layout, a.transA, i, p) * opElem(a.B, a.ldb, layout, a.transB, p, j);
+          s += prod;
+          ab += Math.abs(prod);
+        }
+      const idx = cIndex(a.ldc, layout, i, j);
+      out[idx] = (a.alpha === 0 ? 0 : a.alpha * s) + (a.beta === 0 ? 0 : a.beta * a.C[idx]);
+      absdot[idx] = ab;
+    }
+  return { out, absdot };
+}
+
+// Forward factor of tests/sgemm/helpers.js (eps 2^-23, (k+1)) or
+// tests/dgemm/helpers.js (eps 2^-48, (k+2), 3|beta||C|), plus a bit check of
+// everything outside the m x n part / triangle.
+function checkGemm(got, a, dd) {
+  const layout = a.layout || "row-major";
+  const { out, absdot } = refGemm(a);
+  const eps = dd ? 2 ** -48 : 2 ** -23;
+  let worst = 0;
+  const touched = new Uint8Array(a.C.length);
+  for (let i = 0; i < a.m; i++)
+    for (let j = 0; j < a.n; j++) {
+      if (!inTri(a.uplo, i, j)) continue;
+      const idx = cIndex(a.ldc, layout, i, j);
+      touched[idx] = 1;
+      const bound = eps * ((a.k + (dd ? 2 : 1)) * Math.abs(a.alpha) * absdot[idx] + (dd ? 3 : 1) * Math.abs(a.beta) * Math.abs(a.C[idx]));
+      const err = Math.abs(got[idx] - out[idx]);
+      const f = bound === 0 ? (err === 0 ? 0 : Infinity) : err / bound;
+      if (!(f <= worst)) worst = f;
+    }
+  assert(worst <= 1, `forward factor ${worst}`);
+  for (let i = 0; i < a.C.length; i++)
+    if (!touched[i]) assert(Object.is(got[i], a.C[i]), `C[${i}] outside the computed part changed`);
+}
+
+const gemmArgs = (c, Arr) => ({
+  uplo: c.uplo, transA: c.transA, transB: c.transB, m: c.m, n: c.n, k: c.k, alpha: c.alpha,
+  A: new Arr(c.A), lda: c.lda, B: new Arr(c.B), ldb: c.ldb, beta: c.beta, C: new Arr(c.C), ldc: c.ldc,
+  layout: c.layout || "row-major",
+});
+
+const call = {
+  sgemm: (a) => wg.sgemm(device, a.transA, a.transB, a.m, a.n, a.k, a.alpha, a.A, a.lda, a.B, a.ldb, a.beta, a.C, a.ldc, a.layout),
+  sgemmtr: (a) => wg.sgemmtr(device, a.uplo, a.transA, a.transB, a.m, a.n, a.k, a.alpha, a.A, a.lda, a.B, a.ldb, a.beta, a.C, a.ldc, a.layout),
+  dgemm: (a) => wg.dgemm(device, a.transA, a.transB, a.m, a.n, a.k, a.alpha, a.A, a.lda, a.B, a.ldb, a.beta, a.C, a.ldc, a.layout),
+};
+
+const exactEqual = (got, want, label) => {
+  assertEqual(got.length, want.length, `${label}: length`);
+  for (let i = 0; i < want.length; i++) assert(got[i] === want[i], `${label}: C[${i}] = ${got[i]}, want ${want[i]}`);
+};
+
+// GpuMatrix residency: the operand as wgblas's gpustorage tests build it
+// (padded to outer*ld, logical shape from trans and layout).
+function toGpuMatrix(X, opRows, opCols, trans, ld, layout, Arr) {
+  const [rows, cols] = trans === "transpose" ? [opCols, opRows] : [opRows, opCols];
+  const outer = layout === "column-major" ? cols : rows;
+  const padded = new Arr(Math.max(outer * ld, X.length));
+  padded.set(X);
+  return wg.GpuMatrix.from(device, padded, rows, cols, ld, layout);
+}
+
+async function residentGemm(routine, a, Arr) {
+  const layout = a.layout;
+  const A = toGpuMatrix(a.A, a.m, a.k, a.transA, a.lda, layout, Arr);
+  const B = toGpuMatrix(a.B, a.k, a.n, a.transB, a.ldb, layout, Arr);
+  const C = toGpuMatrix(a.C, a.m, a.n, "no-transpose", a.ldc, layout, Arr);
+  try {
+    const r = await call[routine](Object.assign({}, a, { A, B, C }));
+    assertEqual(Object.keys(r).length, 0, "resident call returns {}");
+    const raw = new Arr(Math.max((layout === "column-major" ? a.n : a.m) * a.ldc, a.C.length));
+    const dense = await C.read();
+    const inner = layout === "column-major" ? a.m : a.n;
+    const outer = layout === "column-major" ? a.n : a.m;
+    raw.set(a.C);
+    for (let o = 0; o < outer; o++) raw.set(dense.subarray(o * inner, o * inner + inner), o * a.ldc);
+    return raw.subarray(0, a.C.length);
+  } finally {
+    A.destroy();
+    B.destroy();
+    C.destroy();
+  }
+}
+
+// ------------------------------------------------------------------ device
+test("init / gpuName / cleanup", async () => {
+  device = await wg.init();
+  assert(device instanceof wg.HipDevice);
+  assert((await wg.init()) === device, "same options -> same device");
+  const name = wg.gpuName(device);
+  assert(/gfx950/.test(name.device), `arch ${name.device}`);
+  const bench = await wg.init({ benchmark: true });
+  assert(bench !== device);
+  const x = wg.GpuVector.from(bench, new Float32Array([3, 4]));
+  const r = await wg.snrm2(bench, 2, x, 1);
+  assertEqual(r.nrm2, 5);
+  assert(typeof r.gpuTimeMs === "number" && r.gpuTimeMs > 0, "gpuTimeMs in benchmark mode");
+  let threw = false;
+  try {
+    await wg.snrm2(device, 2, x, 1);
+  } catch (e) {
+    threw = /different GPUDevice/.test(e.message);
+  }
+  assert(threw, "foreign-device operand rejected");
+  x.destroy();
+  wg.cleanup(bench);
+  assert((await wg.init()) === device, "cleanup(one) keeps the others");
+});
+
+// ------------------------------------------------------------- fixtures
+for (const routine of ["sgemm", "sgemmtr", "dgemm"]) {
+  const Arr = routine === "dgemm" ? Float64Array : Float32Array;
+  for (const file of [`${routine}.edge-cases`, `${routine}.edge-cases-column-major`]) {
+    for (const c of fixture(file)) {
+      test(`${routine} ${file.includes("column") ? "cm" : "rm"}: ${c.label}`, async () => {
+        const a = gemmArgs(c, Arr);
+        const want = refGemm(a).out;
+        const got = await call[routine](a);
+        if (routine === "dgemm" && (a.alpha === 0 || a.k === 0) && a.beta === 1) {
+          assert(got.C === a.C, "quick return hands back the same C");
+          return;
+        }
+        exactEqual(got.C, want, c.label);
+        exactEqual(await residentGemm(routine, a, Arr), want, `${c.label} (GpuMatrix)`);
+      });
+    }
+  }
+}
+
+for (const file of ["ssyrk.edge-cases", "ssyrk.edge-cases-column-major"]) {
+  for (const c of fixture(file)) {
+    test(`ssyrk ${file.includes("column") ? "cm" : "rm"}: ${c.label}`, async () => {
+      const layout = c.layout || "row-major";
+      const A = new Float32Array(c.A);
+      const C = new Float32Array(c.C);
+      const transB = c.trans === "no-transpose" ? "transpose" : "no-transpose";
+      const want = refGemm({ uplo: c.uplo, transA: c.trans, transB, m: c.n, n: c.n, k: c.k, alpha: c.alpha, A, lda: c.lda, B: A, ldb: c.lda, beta: c.beta, C, ldc: c.ldc, layout }).out;
+      const got = await wg.ssyrk(device, c.uplo, c.trans, c.n, c.k, c.alpha, A, c.lda, c.beta, C, c.ldc, layout);
+      exactEqual(got.C, want, c.label);
+    });
+  }
+}
+
+const L1_EXPECT = {
+  sdot: [0, 25, 0, 0, 11, 12],
+  sasum: [9, 205, 0, 7, 6],
+  snrm2: [5, 5, 1, 0, 5, 5, Math.fround(3e19), Math.fround(3e19)],
+  isamax: [0, 0, 1, 1, 0, 3, 0, 1, 0, 1, 1],
+};
+const L1_KEY = { sdot: "dot", sasum: "asum", snrm2: "nrm2", isamax: "index" };
+for (const routine of Object.keys(L1_EXPECT)) {
+  fixture(`${routine}.edge-cases`).forEach((c, i) => {
+    if (i >= L1_EXPECT[routine].length) return;
+    test(`${routine}: ${c.label}`, async () => {
+      const x = new Float32Array(c.x);
+      const want = L1_EXPECT[routine][i];
+      const host = routine === "sdot" ? await wg.sdot(device, c.n, x, c.incx, new Float32Array(c.y), c.incy)
+        : await wg[routine](device, c.n, x, c.incx);
+      assertEqual(host[L1_KEY[routine]], want, "host arrays");
+      const gx = wg.GpuVector.from(device, x);
+      const gy = routine === "sdot" ? wg.GpuVector.from(device, new Float32Array(c.y)) : null;
+      try {
+        const res = routine === "sdot" ? await wg.sdot(device, c.n, gx, c.incx, gy, c.incy)
+          : await wg[routine](device, c.n, gx, c.incx);
+        assertEqual(res[L1_KEY[routine]], want, "GpuVector");
+      } finally {
+        gx.destroy();
+        if (gy) gy.destroy();
+      }
+    });
+  });
+}
+
+test("level 1: n <= 0 and NaN rules", async () => {
+  const x = wg.randomFloat32Array(8, -1, 1, 300);
+  assertEqual((await wg.sdot(device, 0, x, 1, x, 1)).dot, 0);
+  assertEqual((await wg.sasum(device, 0, x, 1)).asum, 0);
+  assertEqual((await wg.snrm2(device, 0, x, 1)).nrm2, 0);
+  assertEqual((await wg.isamax(device, 0, x, 1)).index, -1);
+  assertEqual((await wg.isamax(device, -3, x, 1)).index, -1);
+  const N = NaN;
+  const I = Infinity;
+  for (const [arr, want] of [[[1, N, 7, 3], 2], [[1, 2, 3, N], 2], [[N, N, N, N], 0], [[N, 5, 2, 3], 1],
+    [[N, I, 2, 3], 1], [[1, I, 2, 3], 1], [[1, -I, 2, 3], 1]])
+    assertEqual((await wg.isamax(device, 4, new Float32Array(arr), 1)).index, want, JSON.stringify(arr));
+  const big = new Float32Array(1 << 16).fill(0.5);
+  big[100] = Infinity;
+  assertEqual((await wg.snrm2(device, big.length, big, 1)).nrm2, Infinity);
+  big[200] = NaN;
+  assert(Number.isNaN((await wg.snrm2(device, big.length, big, 1)).nrm2));
+});
+
+// ------------------------------------------------------------ regressions
+for (const layout of ["row-major", "column-major"])
+  for (const transA of ["no-transpose", "transpose"])
+    for (const transB of ["no-transpose", "transpose"]) {
+      test(`sgemm ${layout} ${transA}/${transB}: 398x390x13 ld rounded to 4 (host and GpuMatrix)`, async () => {
+        const M = 398;
+        const N = 390;
+        const K = 13;
+        const cm = layout === "column-major";
+        const up4 = (v) => Math.ceil(v / 4) * 4;
+        const [aR, aC] = transA === "no-transpose" ? [M, K] : [K, M];
+        const [bR, bC] = transB === "no-transpose" ? [K, N] : [N, K];
+        const lda = up4(cm ? aR : aC);
+        const ldb = up4(cm ? bR : bC);
+        const a = { transA, transB, m: M, n: N, k: K, alpha: 1.5, beta: 0.5, lda, ldb, ldc: cm ? M : N, layout,
+          A: wg.randomFloat32Array((cm ? aC : aR) * lda, -1, 1, 111), B: wg.randomFloat32Array((cm ? bC : bR) * ldb, -1, 1, 112),
+          C: wg.randomFloat32Array(M * N, -1, 1, 113) };
+        checkGemm((await call.sgemm(a)).C, a, false);
+        checkGemm(await residentGemm("sgemm", a, Float32Array), a, false);
+      });
+    }
+
+for (const layout of ["row-major", "column-major"])
+  for (const [M, N] of [[150, 70], [70, 150]])
+    for (const uplo of ["lower", "upper"]) {
+      test(`sgemmtr ${layout} ${M}x${N} ${uplo}: other triangle untouched`, async () => {
+        const cm = layout === "column-major";
+        const K = 9;
+        const a = { uplo, transA: "transpose", transB: "no-transpose", m: M, n: N, k: K, alpha: 1.5, beta: 0.5,
+          A: wg.randomFloat32Array(K * M, -1, 1, 51), lda: cm ? K : M, B: wg.randomFloat32Array(K * N, -1, 1, 52),
+          ldb: cm ? K : N, C: wg.randomFloat32Array(M * N, -1, 1, 53), ldc: cm ? M : N, layout };
+        checkGemm((await call.sgemmtr(a)).C, a, false);
+      });
+    }
+
+for (const layout of ["row-major", "column-major"])
+  for (const uplo of ["lower", "upper"])
+    for (const trans of ["no-transpose", "transpose"]) {
+      test(`ssyrk ${layout} ${uplo} ${trans}: 301x64, GpuMatrix chained x3`, async () => {
+        const n = 301;
+        const k = 64;
+        const cm = layout === "column-major";
+        const [aR, aC] = trans === "no-transpose" ? [n, k] : [k, n];
+        const lda = cm ? aR : aC;
+        const A = wg.randomFloat32Array(aR * aC, -1, 1, 61);
+        let C = wg.randomFloat32Array(n * n, -1, 1, 62);
+        const gA = wg.GpuMatrix.from(device, A, aR, aC, lda, layout);
+        const gC = wg.GpuMatrix.from(device, C, n, n, n, layout);
+        const transB = trans === "no-transpose" ? "transpose" : "no-transpose";
+        try {
+          for (let it = 0; it < 3; it++) {
+            const a = { uplo, transA: trans, transB, m: n, n, k, alpha: 1, beta: 0.25, A, lda, B: A, ldb: lda, C, ldc: n, layout };
+            const r = await wg.ssyrk(device, uplo, trans, n, k, 1, gA, lda, 0.25, gC, n);
+            assertEqual(Object.keys(r).length, 0, "resident call returns {}");
+            const got = await gC.read();
+            checkGemm(got, a, false);
+            C = got;
+          }
+        } finally {
+          gA.destroy();
+          gC.destroy();
+        }
+      });
+    }
+
+test("sgemm k = 0 is beta*C bit-exact; alpha = 0 reads neither A nor B", async () => {
+  const C = wg.randomFloat32Array(16, -5, 5, 300);
+  const r = await wg.sgemm(device, "no-transpose", "transpose", 4, 4, 0, 1.5, new Float32Array(3), 1, new Float32Array(3), 1, 0.5, C, 4);
+  for (let i = 0; i < 16; i++) assert(Object.is(r.C[i], Math.fround(0.5 * C[i])), `element ${i}`);
+  for (const beta of [0, 0.5]) {
+    const n = 400;
+    const A = wg.randomFloat32Array(n * n, -1, 1, 1);
+    const B = wg.randomFloat32Array(n * n, -1, 1, 2);
+    const C2 = wg.randomFloat32Array(n * n, -1, 1, 3);
+    A[n + 2] = NaN;
+    B[2 * n + 3] = Infinity;
+    if (beta === 0) C2[4 * n + 4] = NaN;
+    const g = await wg.sgemm(device, "no-transpose", "no-transpose", n, n, n, 0, A, n, B, n, beta, C2, n);
+    for (let i = 0; i < n * n; i++) assert(Object.is(g.C[i], beta === 0 ? 0 : Math.fround(beta * C2[i])), `alpha=0 C[${i}]`);
+  }
+});
+
+test("dgemm: random 150x133x77 within the double-double bound, all layouts/trans", async () => {
+  for (const layout of ["row-major", "column-major"])
+    for (const transA of ["no-transpose", "transpose"])
+      for (const transB of ["no-transpose", "transpose"]) {
+        const M = 150;
+        const N = 133;
+        const K = 77;
+        const cm = layout === "column-major";
+        const [aR, aC] = transA === "no-transpose" ? [M, K] : [K, M];
+        const [bR, bC] = transB === "no-transpose" ? [K, N] : [N, K];
+        const a = { transA, transB, m: M, n: N, k: K, alpha: 1.25, beta: -0.5, layout,
+          A: wg.randomFloat64Array(aR * aC, -1, 1, 3), lda: cm ? aR : aC,
+          B: wg.randomFloat64Array(bR * bC, -1, 1, 4), ldb: cm ? bR : bC,
+          C: wg.randomFloat64Array(M * N, -1, 1, 5), ldc: cm ? M : N };
+        checkGemm((await call.dgemm(a)).C, a, true);
+      }
+});
+
+test("GpuMatrix.read strips lda padding; GpuVector round trip", async () => {
+  const data = new Float32Array([1, 2, 99, 3, 4, 99]);
+  const g = wg.GpuMatrix.from(device, data, 2, 2, 3);
+  exactEqual(await g.read(), new Float32Array([1, 2, 3, 4]), "row-major read");
+  g.destroy();
+  const v = wg.GpuVector.from(device, new Float64Array([Math.PI, -0, 1e300]));
+  const back = await v.read();
+  assert(back instanceof Float64Array && back[0] === Math.PI && Object.is(back[1], -0) && back[2] === 1e300);
+  v.destroy();
+});
+
+test("cleanup() releases everything", async () => {
+  wg.cleanup();
+  let threw = false;
+  try {
+    wg.gpuName();
+  } catch (e) {
+    threw = /init\(\)/.test(e.message);
+  }
+  assert(threw);
+});
+
+run();

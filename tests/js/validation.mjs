@@ -1,0 +1,215 @@
+// Argument-validation contract of the JavaScript API, driven by the
+// reference's own parameter specs (tests/golden/validation_params/*.json,
+// copied data of wgblas's tests/validation/params). For every routine on the
+// path, each spec's `invalid` entries are substituted one at a time into a
+// valid baseline call and must throw an Error whose message contains the
+// spec's `error` text; with --gpu, each `edge` entry must run without
+// throwing. The baseline assembly follows the behaviour of wgblas's
+// tests/helpers/validation.js (loadParam, runValidation, minimal/tooShort
+// array sizing); the spec composition per routine follows wgblas's
+// tests/<routine>/src/test.<routine>.js.
+//
+//   node tests/js/validation.mjs          # invalid cases, no GPU needed
+//   node tests/js/validation.mjs --gpu    # invalid + edge cases on the GPU
+import { readFileSync } from "fs";
+import { fileURLToPath } from "url";
+import { dirname, join } from "path";
+import { test, run, assertRejects } from "./harness.mjs";
+import * as wg from "../../wgblas_amd/js/index.mjs";
+
+const here = dirname(fileURLToPath(import.meta.url));
+const PARAMS = join(here, "..", "golden", "validation_params");
+const GPU = process.argv.includes("--gpu");
+
+function loadParam(name) {
+  if (name.endsWith("64")) return derive64(loadParam(name.slice(0, -2)));
+  return JSON.parse(readFileSync(join(PARAMS, `${name}.json`), "utf8"));
+}
+
+// The Float64Array variant of a float32 spec: same cases, f64 wording, and a
+// GpuMatrix-of-the-wrong-dtype case for matrix specs.
+function derive64(base) {
+  const isArray = base.type !== "float";
+  const isMatrix = (base.dependsOn || []).some((d) => d.startsWith("ld"));
+  const invalid = (base.invalid || []).map((e) =>
+    Object.assign({}, e, { error: typeof e.error === "string" ? e.error.replace("Float32Array", "Float64Array") : e.error }));
+  if (base.type === "float32array" && isMatrix)
+    invalid.push({ scenario: "wrongDtypeGpuMatrix", error: "must be a Float64Array-backed GpuMatrix", label: "GpuMatrix of Float32Array" });
+  return Object.assign({}, base, { type: isArray ? "float64array" : "float64", invalid });
+}
+
+const SPECIALS = { NaN: NaN, Infinity: Infinity, "-Infinity": -Infinity, null: null, undefined: undefined,
+  string: "100", array: [], object: {}, number: 42 };
+
+const ctorOf = (type) => (type === "float64array" ? Float64Array : Float32Array);
+
+// Logical {outer, inner} of a matrix param from its dependsOn (the cases the
+// path needs: a level-3 operand with its own trans flag, or a plain m x n /
+// n x n matrix).
+function matrixShape(dependsOn, dims) {
+  const deps = new Set(dependsOn || []);
+  const transKey = (dependsOn || []).find((d) => d.startsWith("trans"));
+  const cm = dims.layout === "column-major";
+  if (transKey && deps.has("k")) {
+    const [d1, d2] = dependsOn.filter((d) => d === "m" || d === "n" || d === "k");
+    const rows = cm ? dims[d2] : dims[d1];
+    const cols = cm ? dims[d1] : dims[d2];
+    const noTrans = (dims[transKey] || "no-transpose") === "no-transpose";
+    return noTrans ? { outer: rows, inner: cols } : { outer: cols, inner: rows };
+  }
+  if (deps.has("m") && deps.has("n")) return cm ? { outer: dims.n, inner: dims.m } : { outer: dims.m, inner: dims.n };
+  if (deps.has("n")) return { outer: dims.n, inner: dims.n };
+  return null;
+}
+
+function minLength(dependsOn, dims) {
+  const ldKey = (dependsOn || []).find((d) => d.startsWith("ld"));
+  if (ldKey) {
+    const s = matrixShape(dependsOn, dims);
+    if (s) return Math.max(0, (s.outer - 1) * dims[ldKey] + s.inner);
+  }
+  const inc = (dependsOn || []).includes("incx") ? (dims.incx || 1) : (dims.incy || 1);
+  return ((dims.n === undefined ? 4 : dims.n) - 1) * inc + 1;
+}
+
+function resolve(entry, name, spec, baselines, device) {
+  if ("scenario" in entry) {
+    if (entry.scenario === "wrongDtypeGpuMatrix") {
+      const data = new Float32Array(16).fill(1);
+      return wg.GpuMatrix.from(device, data, 2, 2, 2, baselines.layout || "row-major");
+    }
+    const len = minLength(spec.dependsOn, baselines);
+    const Ctor = ctorOf(spec.type);
+    if (entry.scenario === "minimal") return new Ctor(len).fill(1);
+    if (entry.scenario === "tooShort") return new Ctor(Math.max(0, len - 1)).fill(1);
+    throw new Error(`unknown scenario ${entry.scenario}`);
+  }
+  if ("value" in entry) {
+    if (Array.isArray(entry.value) && /array$/.test(spec.type || "")) return new (ctorOf(spec.type))(entry.value);
+    return entry.value;
+  }
+  return SPECIALS[entry.special];
+}
+
+function baselinesOf(specs, device) {
+  const b = { device };
+  for (const [name, spec] of Object.entries(specs)) {
+    if (!("baseline" in spec)) continue;
+    b[name] = Array.isArray(spec.baseline) ? new (ctorOf(spec.type))(spec.baseline) : spec.baseline;
+  }
+  for (const [name, spec] of Object.entries(specs)) {
+    if (b[name] !== undefined || !/array$/.test(spec.type || "")) continue;
+    const deps = new Set(spec.dependsOn || []);
+    const dims = Object.assign({}, b);
+    // sized so the baseline survives every leading-dimension / stride edge case
+    if (deps.has("lda") && specs.lda && specs.lda.range) dims.lda = specs.lda.range.max;
+    if (deps.has("incx") && specs.incx && specs.incx.range) dims.incx = specs.incx.range.max;
+    if (deps.has("incy") && specs.incy && specs.incy.range) dims.incy = specs.incy.range.max;
+    b[name] = new (ctorOf(spec.type))(minLength(spec.dependsOn, dims)).fill(1);
+  }
+  return b;
+}
+
+function register(routine, specs, call, device) {
+  const baselines = baselinesOf(specs, device);
+  for (const [name, spec] of Object.entries(specs)) {
+    for (const entry of spec.invalid || []) {
+      if (!GPU && entry.scenario === "wrongDtypeGpuMatrix") continue;
+      test(`${routine} ${name} invalid: ${entry.label || JSON.stringify(entry)}`, async () => {
+        const args = Object.assign({}, baselines);
+        args[name] = resolve(entry, name, spec, baselines, device);
+        try {
+          await assertRejects(() => call(args), entry.error);
+        } finally {
+          if (args[name] instanceof wg.GpuMatrix) args[name].destroy();
+        }
+      });
+    }
+    if (!GPU) continue;
+    for (const entry of spec.edge || []) {
+      test(`${routine} ${name} edge: ${entry.label || JSON.stringify(entry)}`, async () => {
+        const args = Object.assign({}, baselines);
+        args[name] = resolve(entry, name, spec, baselines, device);
+        await call(args);
+      });
+    }
+  }
+}
+
+function nWithNegative(error) {
+  const n = loadParam("n");
+  return Object.assign({}, n, {
+    baseline: 2,
+    edge: n.edge.filter((e) => e.value !== -1),
+    invalid: n.invalid.concat([{ value: -1, error, label: "negative" }]),
+  });
+}
+
+function gemmSpecs(f64) {
+  const ld = loadParam("ld");
+  const A = f64 ? loadParam("A64") : loadParam("A");
+  const lvl3 = loadParam("A")["level-3"];
+  const aSpec = Object.assign({}, A, {
+    dependsOn: lvl3.dependsOn,
+    edge: lvl3.edge,
+    invalid: lvl3.invalid
+      .map((e) => Object.assign({}, e, { error: f64 ? e.error.replace("Float32Array", "Float64Array") : e.error }))
+      .concat(f64 ? A.invalid.filter((e) => e.scenario === "wrongDtypeGpuMatrix") : []),
+  });
+  return {
+    device: loadParam("device"),
+    transA: loadParam("trans"),
+    transB: loadParam("trans"),
+    layout: loadParam("layout"),
+    m: Object.assign({}, loadParam("m"), { baseline: 2 }),
+    n: nWithNegative("m, n, and k must be non-negative"),
+    k: loadParam("k"),
+    alpha: loadParam("alpha"),
+    beta: loadParam("beta"),
+    A: aSpec,
+    lda: ld,
+    B: f64 ? loadParam("B64") : loadParam("B"),
+    ldb: ld,
+    C: f64 ? loadParam("C64") : loadParam("C"),
+    ldc: ld,
+  };
+}
+
+async function main() {
+  const device = GPU ? await wg.init() : Object.create(wg.HipDevice.prototype);
+  const g = gemmSpecs(false);
+  register("sgemm", g, (a) => wg.sgemm(a.device, a.transA, a.transB, a.m, a.n, a.k, a.alpha, a.A, a.lda, a.B, a.ldb, a.beta, a.C, a.ldc, a.layout), device);
+  register("sgemmtr", Object.assign({ uplo: loadParam("uplo") }, g),
+    (a) => wg.sgemmtr(a.device, a.uplo, a.transA, a.transB, a.m, a.n, a.k, a.alpha, a.A, a.lda, a.B, a.ldb, a.beta, a.C, a.ldc, a.layout), device);
+  register("dgemm", gemmSpecs(true),
+    (a) => wg.dgemm(a.device, a.transA, a.transB, a.m, a.n, a.k, a.alpha, a.A, a.lda, a.B, a.ldb, a.beta, a.C, a.ldc, a.layout), device);
+  const A = loadParam("A");
+  register("ssyrk", {
+    device: loadParam("device"),
+    uplo: loadParam("uplo"),
+    trans: loadParam("trans"),
+    layout: loadParam("layout"),
+    n: nWithNegative("must be non-negative"),
+    k: loadParam("k"),
+    alpha: loadParam("alpha"),
+    beta: loadParam("beta"),
+    A: Object.assign({}, A, A["level-3"], { dependsOn: ["n", "k", "lda", "trans"] }),
+    lda: loadParam("ld"),
+    C: Object.assign({}, loadParam("C"), { dependsOn: ["n", "ldc"] }),
+    ldc: loadParam("ld"),
+  }, (a) => wg.ssyrk(a.device, a.uplo, a.trans, a.n, a.k, a.alpha, a.A, a.lda, a.beta, a.C, a.ldc, a.layout), device);
+  register("sdot", {
+    device: loadParam("device"), n: loadParam("n"), incx: loadParam("incx"), incy: loadParam("incy"),
+    x: loadParam("x"), y: loadParam("y"),
+  }, (a) => wg.sdot(a.device, a.n, a.x, a.incx, a.y, a.incy), device);
+  for (const r of ["sasum", "snrm2", "isamax"])
+    register(r, { device: loadParam("device"), n: loadParam("n"), incx: loadParam("incx"), x: loadParam("x") },
+      (a) => wg[r](a.device, a.n, a.x, a.incx), device);
+  await run();
+  if (GPU) wg.cleanup();
+}
+
+main().catch((e) => {
+  console.error(e);
+  process.exitCode = 1;
+});

@@ -1,0 +1,45 @@
+"""Runs the JavaScript-layer suites (tests/js/*.mjs) with node.
+
+CPU: the reference's validation specs (invalid cases) against the JS API and
+the seeded generators against the reference's golden vectors.
+GPU: the validation edge cases (valid calls must run) and the end-to-end
+API suite through the Node-API addon and libwgblas_hip.
+"""
+import os
+import shutil
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+NODE = shutil.which("node")
+
+pytestmark = pytest.mark.skipif(NODE is None, reason="node is not installed")
+
+
+def run_node(script, *args, timeout=600):
+    res = subprocess.run([NODE, os.path.join(ROOT, "tests", "js", script), *args], cwd=ROOT,
+                         capture_output=True, text=True, timeout=timeout)
+    tail = "\n".join((res.stdout + res.stderr).splitlines()[-40:])
+    assert res.returncode == 0, f"{script} {' '.join(args)} failed:\n{tail}"
+    assert " 0 failed" in res.stdout, tail
+    return res.stdout
+
+
+def test_js_validation_specs():
+    out = run_node("validation.mjs")
+    assert int(out.strip().splitlines()[-1].split()[0]) > 300
+
+
+def test_js_random_matches_reference_golden():
+    run_node("random.mjs")
+
+
+@pytest.mark.gpu
+def test_js_validation_edge_cases_on_gpu():
+    run_node("validation.mjs", "--gpu")
+
+
+@pytest.mark.gpu
+def test_js_api_end_to_end_on_gpu():
+    run_node("gpu_api.mjs")

@@ -1,0 +1,375 @@
+// Node-API addon: the JavaScript side of wgblas binds the C ABI of
+// libwgblas_hip (include/wgblas_hip.h) through these functions. Each one
+// converts its arguments, calls one wgb_* entry point and turns a failing
+// status into a thrown Error carrying wgb_last_error(). Device pointers
+// travel to JavaScript as napi_external values; the JavaScript classes
+// (GpuVector, GpuMatrix, the device handle) own them and free them.
+#include <node_api.h>
+
+#include <cstdint>
+#include <cstring>
+#include <string>
+
+#include "wgblas_hip.h"
+
+namespace {
+
+#define NAPI_OK(call)                                          \
+  do {                                                         \
+    if ((call) != napi_ok) {                                   \
+      napi_throw_error(env, nullptr, "wgblas_hip addon: " #call); \
+      return nullptr;                                          \
+    }                                                          \
+  } while (0)
+
+napi_value throw_status(napi_env env, int status, const char *what) {
+  std::string msg = std::string(what) + " failed (" + wgb_status_string(status) + "): " + wgb_last_error();
+  napi_throw_error(env, nullptr, msg.c_str());
+  return nullptr;
+}
+
+#define WGB_OK_OR_THROW(call, what)               \
+  do {                                            \
+    int _st = (call);                             \
+    if (_st != WGB_OK) return throw_status(env, _st, what); \
+  } while (0)
+
+struct Args {
+  napi_value v[16];
+  size_t n = 16;
+};
+
+bool get_args(napi_env env, napi_callback_info info, Args &a, size_t want) {
+  a.n = 16;
+  if (napi_get_cb_info(env, info, &a.n, a.v, nullptr, nullptr) != napi_ok) return false;
+  if (a.n < want) {
+    napi_throw_type_error(env, nullptr, "wgblas_hip addon: too few arguments");
+    return false;
+  }
+  return true;
+}
+
+bool get_ptr(napi_env env, napi_value v, void **out) {
+  napi_valuetype t;
+  if (napi_typeof(env, v, &t) != napi_ok) return false;
+  if (t == napi_null || t == napi_undefined) {
+    *out = nullptr;
+    return true;
+  }
+  if (t != napi_external) {
+    napi_throw_type_error(env, nullptr, "wgblas_hip addon: expected a device handle");
+    return false;
+  }
+  return napi_get_value_external(env, v, out) == napi_ok;
+}
+
+bool get_i64(napi_env env, napi_value v, int64_t *out) {
+  if (napi_get_value_int64(env, v, out) != napi_ok) {
+    napi_throw_type_error(env, nullptr, "wgblas_hip addon: expected an integer");
+    return false;
+  }
+  return true;
+}
+
+bool get_f64(napi_env env, napi_value v, double *out) {
+  if (napi_get_value_double(env, v, out) != napi_ok) {
+    napi_throw_type_error(env, nullptr, "wgblas_hip addon: expected a number");
+    return false;
+  }
+  return true;
+}
+
+bool get_i32(napi_env env, napi_value v, int *out) {
+  int32_t x;
+  if (napi_get_value_int32(env, v, &x) != napi_ok) {
+    napi_throw_type_error(env, nullptr, "wgblas_hip addon: expected an int32");
+    return false;
+  }
+  *out = x;
+  return true;
+}
+
+// (data pointer, byte length) of a TypedArray.
+bool get_typed(napi_env env, napi_value v, void **data, size_t *bytes) {
+  bool is_ta = false;
+  if (napi_is_typedarray(env, v, &is_ta) != napi_ok || !is_ta) {
+    napi_throw_type_error(env, nullptr, "wgblas_hip addon: expected a TypedArray");
+    return false;
+  }
+  napi_typedarray_type type;
+  size_t length, offset;
+  napi_value ab;
+  void *base;
+  if (napi_get_typedarray_info(env, v, &type, &length, &base, &ab, &offset) != napi_ok) return false;
+  size_t elem = 1;
+  switch (type) {
+    case napi_float32_array: case napi_int32_array: case napi_uint32_array: elem = 4; break;
+    case napi_float64_array: case napi_bigint64_array: case napi_biguint64_array: elem = 8; break;
+    case napi_int16_array: case napi_uint16_array: elem = 2; break;
+    default: elem = 1; break;
+  }
+  *data = base;  // already points at the view's first element
+  *bytes = length * elem;
+  return true;
+}
+
+napi_value make_external(napi_env env, void *p) {
+  napi_value out;
+  if (napi_create_external(env, p, nullptr, nullptr, &out) != napi_ok) return nullptr;
+  return out;
+}
+
+napi_value num(napi_env env, double d) {
+  napi_value out;
+  napi_create_double(env, d, &out);
+  return out;
+}
+
+wgb_ctx *ctx_of(napi_env env, napi_value v) {
+  void *p = nullptr;
+  if (!get_ptr(env, v, &p)) return nullptr;
+  if (!p) napi_throw_error(env, nullptr, "wgblas_hip addon: device handle was released (cleanup() called?)");
+  return (wgb_ctx *)p;
+}
+
+// ---- device ----------------------------------------------------------------
+
+napi_value DeviceCount(napi_env env, napi_callback_info) {
+  int c = 0;
+  WGB_OK_OR_THROW(wgb_device_count(&c), "wgb_device_count");
+  return num(env, c);
+}
+
+napi_value Init(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 1)) return nullptr;
+  int dev;
+  if (!get_i32(env, a.v[0], &dev)) return nullptr;
+  wgb_ctx *ctx = nullptr;
+  WGB_OK_OR_THROW(wgb_init(dev, &ctx), "wgb_init");
+  return make_external(env, ctx);
+}
+
+napi_value Destroy(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 1)) return nullptr;
+  void *p;
+  if (!get_ptr(env, a.v[0], &p)) return nullptr;
+  WGB_OK_OR_THROW(wgb_destroy((wgb_ctx *)p), "wgb_destroy");
+  return nullptr;
+}
+
+napi_value DeviceName(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 1)) return nullptr;
+  wgb_ctx *ctx = ctx_of(env, a.v[0]);
+  if (!ctx) return nullptr;
+  char name[256], arch[64];
+  WGB_OK_OR_THROW(wgb_device_name(ctx, name, sizeof name, arch, sizeof arch), "wgb_device_name");
+  napi_value obj, s1, s2;
+  NAPI_OK(napi_create_object(env, &obj));
+  NAPI_OK(napi_create_string_utf8(env, name, NAPI_AUTO_LENGTH, &s1));
+  NAPI_OK(napi_create_string_utf8(env, arch, NAPI_AUTO_LENGTH, &s2));
+  NAPI_OK(napi_set_named_property(env, obj, "name", s1));
+  NAPI_OK(napi_set_named_property(env, obj, "arch", s2));
+  return obj;
+}
+
+napi_value SetTiming(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 2)) return nullptr;
+  wgb_ctx *ctx = ctx_of(env, a.v[0]);
+  if (!ctx) return nullptr;
+  bool on = false;
+  NAPI_OK(napi_get_value_bool(env, a.v[1], &on));
+  WGB_OK_OR_THROW(wgb_set_timing(ctx, on ? 1 : 0), "wgb_set_timing");
+  return nullptr;
+}
+
+napi_value LastTimeMs(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 1)) return nullptr;
+  wgb_ctx *ctx = ctx_of(env, a.v[0]);
+  if (!ctx) return nullptr;
+  float ms = 0;
+  WGB_OK_OR_THROW(wgb_last_time_ms(ctx, &ms), "wgb_last_time_ms");
+  return num(env, ms);
+}
+
+napi_value Synchronize(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 1)) return nullptr;
+  wgb_ctx *ctx = ctx_of(env, a.v[0]);
+  if (!ctx) return nullptr;
+  WGB_OK_OR_THROW(wgb_synchronize(ctx), "wgb_synchronize");
+  return nullptr;
+}
+
+// ---- memory ------------------------------------------------------------------
+
+napi_value Malloc(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 2)) return nullptr;
+  wgb_ctx *ctx = ctx_of(env, a.v[0]);
+  if (!ctx) return nullptr;
+  int64_t bytes;
+  if (!get_i64(env, a.v[1], &bytes)) return nullptr;
+  if (bytes < 0) {
+    napi_throw_range_error(env, nullptr, "wgblas_hip addon: negative allocation size");
+    return nullptr;
+  }
+  void *p = nullptr;
+  WGB_OK_OR_THROW(wgb_malloc(ctx, (size_t)bytes, &p), "wgb_malloc");
+  return make_external(env, p);
+}
+
+napi_value Free(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 2)) return nullptr;
+  wgb_ctx *ctx = ctx_of(env, a.v[0]);
+  if (!ctx) return nullptr;
+  void *p;
+  if (!get_ptr(env, a.v[1], &p)) return nullptr;
+  WGB_OK_OR_THROW(wgb_free(ctx, p), "wgb_free");
+  return nullptr;
+}
+
+// upload(ctx, dptr, typedArray[, byteOffset]): whole TypedArray -> device.
+napi_value Upload(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 3)) return nullptr;
+  wgb_ctx *ctx = ctx_of(env, a.v[0]);
+  if (!ctx) return nullptr;
+  void *dptr, *host;
+  size_t bytes;
+  if (!get_ptr(env, a.v[1], &dptr) || !get_typed(env, a.v[2], &host, &bytes)) return nullptr;
+  int64_t off = 0;
+  if (a.n > 3 && !get_i64(env, a.v[3], &off)) return nullptr;
+  WGB_OK_OR_THROW(wgb_memcpy_h2d(ctx, (char *)dptr + off, host, bytes), "wgb_memcpy_h2d");
+  return nullptr;
+}
+
+// download(ctx, dptr, typedArray[, byteOffset]): device -> whole TypedArray.
+napi_value Download(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 3)) return nullptr;
+  wgb_ctx *ctx = ctx_of(env, a.v[0]);
+  if (!ctx) return nullptr;
+  void *dptr, *host;
+  size_t bytes;
+  if (!get_ptr(env, a.v[1], &dptr) || !get_typed(env, a.v[2], &host, &bytes)) return nullptr;
+  int64_t off = 0;
+  if (a.n > 3 && !get_i64(env, a.v[3], &off)) return nullptr;
+  WGB_OK_OR_THROW(wgb_memcpy_d2h(ctx, host, (const char *)dptr + off, bytes), "wgb_memcpy_d2h");
+  return nullptr;
+}
+
+// ---- level 3 ---------------------------------------------------------------
+
+// gemm(kind, ctx, uplo, transA, transB, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc)
+// kind: 0 sgemm, 1 sgemmtr, 2 dgemm.
+napi_value Gemm(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 16)) return nullptr;
+  int kind, uplo, ta, tb;
+  int64_t m, n, k, lda, ldb, ldc;
+  double alpha, beta;
+  void *A, *B, *C;
+  if (!get_i32(env, a.v[0], &kind)) return nullptr;
+  wgb_ctx *ctx = ctx_of(env, a.v[1]);
+  if (!ctx) return nullptr;
+  if (!get_i32(env, a.v[2], &uplo) || !get_i32(env, a.v[3], &ta) || !get_i32(env, a.v[4], &tb) ||
+      !get_i64(env, a.v[5], &m) || !get_i64(env, a.v[6], &n) || !get_i64(env, a.v[7], &k) ||
+      !get_f64(env, a.v[8], &alpha) || !get_ptr(env, a.v[9], &A) || !get_i64(env, a.v[10], &lda) ||
+      !get_ptr(env, a.v[11], &B) || !get_i64(env, a.v[12], &ldb) || !get_f64(env, a.v[13], &beta) ||
+      !get_ptr(env, a.v[14], &C) || !get_i64(env, a.v[15], &ldc))
+    return nullptr;
+  if (kind == 0) {
+    WGB_OK_OR_THROW(wgb_sgemm(ctx, ta, tb, m, n, k, (float)alpha, (const float *)A, lda,
+                              (const float *)B, ldb, (float)beta, (float *)C, ldc), "wgb_sgemm");
+  } else if (kind == 1) {
+    WGB_OK_OR_THROW(wgb_sgemmtr(ctx, uplo, ta, tb, m, n, k, (float)alpha, (const float *)A, lda,
+                                (const float *)B, ldb, (float)beta, (float *)C, ldc), "wgb_sgemmtr");
+  } else {
+    WGB_OK_OR_THROW(wgb_dgemm(ctx, ta, tb, m, n, k, alpha, (const double *)A, lda,
+                              (const double *)B, ldb, beta, (double *)C, ldc), "wgb_dgemm");
+  }
+  return nullptr;
+}
+
+// ssyrk(ctx, uplo, trans, n, k, alpha, A, lda, beta, C, ldc)
+napi_value Ssyrk(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 11)) return nullptr;
+  wgb_ctx *ctx = ctx_of(env, a.v[0]);
+  if (!ctx) return nullptr;
+  int uplo, trans;
+  int64_t n, k, lda, ldc;
+  double alpha, beta;
+  void *A, *C;
+  if (!get_i32(env, a.v[1], &uplo) || !get_i32(env, a.v[2], &trans) || !get_i64(env, a.v[3], &n) ||
+      !get_i64(env, a.v[4], &k) || !get_f64(env, a.v[5], &alpha) || !get_ptr(env, a.v[6], &A) ||
+      !get_i64(env, a.v[7], &lda) || !get_f64(env, a.v[8], &beta) || !get_ptr(env, a.v[9], &C) ||
+      !get_i64(env, a.v[10], &ldc))
+    return nullptr;
+  WGB_OK_OR_THROW(wgb_ssyrk(ctx, uplo, trans, n, k, (float)alpha, (const float *)A, lda,
+                            (float)beta, (float *)C, ldc), "wgb_ssyrk");
+  return nullptr;
+}
+
+// ---- level 1 ---------------------------------------------------------------
+
+// reduce(kind, ctx, n, x, incx[, y, incy]) -> number; kind: 0 sdot, 1 sasum,
+// 2 snrm2, 3 isamax.
+napi_value Reduce(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 5)) return nullptr;
+  int kind;
+  if (!get_i32(env, a.v[0], &kind)) return nullptr;
+  wgb_ctx *ctx = ctx_of(env, a.v[1]);
+  if (!ctx) return nullptr;
+  int64_t n, incx, incy = 1;
+  void *x, *y = nullptr;
+  if (!get_i64(env, a.v[2], &n) || !get_ptr(env, a.v[3], &x) || !get_i64(env, a.v[4], &incx))
+    return nullptr;
+  if (kind == 0) {
+    if (a.n < 7) {
+      napi_throw_type_error(env, nullptr, "wgblas_hip addon: sdot needs y and incy");
+      return nullptr;
+    }
+    if (!get_ptr(env, a.v[5], &y) || !get_i64(env, a.v[6], &incy)) return nullptr;
+  }
+  float r = 0;
+  int64_t idx = -1;
+  switch (kind) {
+    case 0: WGB_OK_OR_THROW(wgb_sdot(ctx, n, (const float *)x, incx, (const float *)y, incy, &r), "wgb_sdot"); break;
+    case 1: WGB_OK_OR_THROW(wgb_sasum(ctx, n, (const float *)x, incx, &r), "wgb_sasum"); break;
+    case 2: WGB_OK_OR_THROW(wgb_snrm2(ctx, n, (const float *)x, incx, &r), "wgb_snrm2"); break;
+    default: WGB_OK_OR_THROW(wgb_isamax(ctx, n, (const float *)x, incx, &idx), "wgb_isamax"); return num(env, (double)idx);
+  }
+  return num(env, (double)r);
+}
+
+napi_value ModuleInit(napi_env env, napi_value exports) {
+  struct Fn {
+    const char *name;
+    napi_callback cb;
+  } fns[] = {
+      {"deviceCount", DeviceCount}, {"init", Init}, {"destroy", Destroy},
+      {"deviceName", DeviceName}, {"setTiming", SetTiming}, {"lastTimeMs", LastTimeMs},
+      {"synchronize", Synchronize}, {"malloc", Malloc}, {"free", Free},
+      {"upload", Upload}, {"download", Download}, {"gemm", Gemm},
+      {"ssyrk", Ssyrk}, {"reduce", Reduce},
+  };
+  for (const Fn &f : fns) {
+    napi_value v;
+    if (napi_create_function(env, f.name, NAPI_AUTO_LENGTH, f.cb, nullptr, &v) != napi_ok ||
+        napi_set_named_property(env, exports, f.name, v) != napi_ok)
+      return nullptr;
+  }
+  return exports;
+}
+
+}  // namespace
+
+NAPI_MODULE(wgblas_hip, ModuleInit)

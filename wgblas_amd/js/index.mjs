@@ -1,0 +1,15 @@
+// wgblas's public API for the hot path, on HIP (the routine set of
+// index.mjs in wgblas limited to the GEMM family and the level-1
+// reductions, plus the device, residency and seeded-input helpers).
+export { init, cleanup, gpuName, HipDevice } from "./src/init.mjs";
+export { GpuVector } from "./src/classes/GpuVector.mjs";
+export { GpuMatrix } from "./src/classes/GpuMatrix.mjs";
+export { randomFloat32Array, randomFloat64Array } from "./src/random.mjs";
+export { sgemm } from "./src/sgemm.mjs";
+export { sgemmtr } from "./src/sgemmtr.mjs";
+export { ssyrk } from "./src/ssyrk.mjs";
+export { dgemm } from "./src/dgemm.mjs";
+export { sdot } from "./src/sdot.mjs";
+export { sasum } from "./src/sasum.mjs";
+export { snrm2 } from "./src/snrm2.mjs";
+export { isamax } from "./src/isamax.mjs";

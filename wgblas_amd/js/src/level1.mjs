@@ -1,0 +1,73 @@
+// Shared checks and execution of the level-1 reductions, in wgblas's order
+// and with its messages (src/sdot/sdot.mjs:22-48, src/sasum/sasum.mjs,
+// src/snrm2/snrm2.mjs:21-31, src/isamax/isamax.mjs:21-34).
+import { GpuVector } from "./classes/GpuVector.mjs";
+import { requireGpuDevice, requireSameDevice } from "./device.mjs";
+import { lastGpuTimeMs } from "./init.mjs";
+import { native } from "./native.mjs";
+
+export const KIND = { sdot: 0, sasum: 1, snrm2: 2, isamax: 3 };
+
+/** One-vector routines (sasum, snrm2, isamax). Returns the result value. */
+export function reduceOne(routine, device, n, x, incx, emptyValue) {
+  const xIsGpu = x instanceof GpuVector;
+  requireGpuDevice(device);
+  requireSameDevice(device, routine, { x });
+  if (!Number.isInteger(n) || !Number.isInteger(incx)) throw new Error("n and incx must be integers.");
+  if (incx <= 0) throw new Error("incx must be positive.");
+  if (!xIsGpu && !(x instanceof Float32Array)) throw new Error("x must be a Float32Array or GpuVector.");
+  if (n <= 0) return { value: emptyValue };
+  if (x.length < (n - 1) * incx + 1)
+    throw new Error("x does not have enough elements for the given n and incx.");
+  return run(device, [x], (ctx, p) => native().reduce(KIND[routine], ctx, n, p[0], incx));
+}
+
+/** sdot's two-vector form. */
+export function reduceDot(device, n, x, incx, y, incy) {
+  const xIsGpu = x instanceof GpuVector;
+  const yIsGpu = y instanceof GpuVector;
+  requireGpuDevice(device);
+  requireSameDevice(device, "sdot", { x, y });
+  if (!Number.isInteger(n) || !Number.isInteger(incx) || !Number.isInteger(incy))
+    throw new Error("n, incx, and incy must be integers.");
+  if (incx <= 0 || incy <= 0) throw new Error("incx and incy must be positive.");
+  if (!xIsGpu && !(x instanceof Float32Array)) throw new Error("x must be a Float32Array or GpuVector.");
+  if (!yIsGpu && !(y instanceof Float32Array)) throw new Error("y must be a Float32Array or GpuVector.");
+  if (xIsGpu !== yIsGpu)
+    throw new Error("x and y must be the same type (both Float32Array or both GpuVector).");
+  if (n <= 0) return { value: 0 };
+  if (x.length < (n - 1) * incx + 1)
+    throw new Error("x does not have enough elements for the given n and incx.");
+  if (y.length < (n - 1) * incy + 1)
+    throw new Error("y does not have enough elements for the given n and incy.");
+  return run(device, [x, y], (ctx, p) => native().reduce(KIND.sdot, ctx, n, p[0], incx, p[1], incy));
+}
+
+// Host arrays go to temporary device buffers (freed before returning);
+// GpuVectors are read in place. The scalar result comes back to the host.
+function run(device, vectors, call) {
+  const nat = native();
+  const ctx = device.ctx();
+  const temps = [];
+  try {
+    const ptrs = vectors.map((v) => {
+      if (v instanceof GpuVector) return v._buf;
+      const p = nat.malloc(ctx, v.byteLength);
+      temps.push(p);
+      nat.upload(ctx, p, v);
+      return p;
+    });
+    const value = call(ctx, ptrs);
+    return { value, gpuTimeMs: lastGpuTimeMs(device) };
+  } finally {
+    for (const p of temps) nat.free(ctx, p);
+  }
+}
+
+/** { [key]: value } plus gpuTimeMs when the device is in benchmark mode. */
+export function shape(key, r) {
+  const out = {};
+  out[key] = r.value;
+  if (r.gpuTimeMs !== undefined) out.gpuTimeMs = r.gpuTimeMs;
+  return out;
+}

@@ -234,6 +234,60 @@ def bench_components(ctx, ev, quick):
     return comps
 
 
+def run_only(ctx, name, reps):
+    """One workload alone, `reps` launches, for counter runs (rocprofv3
+    --pmc): copy (1 GiB device-to-device, the traffic calibration),
+    sgemm_8192 (NN), dgemm_4096, ssyrk_8192, sdot / sasum / snrm2 / isamax
+    at n = 2^28."""
+    from wgblas_amd import LOWER, NO_TRANS, TRANS
+
+    if name == "copy":
+        n = 1 << 28
+        a, b = ctx.empty(n, np.float32), ctx.empty(n, np.float32)
+        for _ in range(reps):
+            ctx.lib.wgb_memcpy_d2d(ctx.handle, b.ptr, a.ptr, 4 * n)
+        ctx.synchronize()
+        return {"bytes_read": 4 * n, "bytes_written": 4 * n}
+    if name == "sgemm_8192":
+        n = 8192
+        buf = ctx.empty(3 * n * n, np.float32)
+        ctx.fill_uniform(buf, -1.0, 1.0, 2)
+        for _ in range(reps):
+            ctx.sgemm(NO_TRANS, NO_TRANS, n, n, n, 1.5, buf.offset(0), n, buf.offset(n * n), n, 0.5,
+                      buf.offset(2 * n * n), n)
+        ctx.synchronize()
+        return {"algorithmic_bytes": 4 * 4 * n * n}
+    if name == "dgemm_4096":
+        n = 4096
+        buf = ctx.empty(3 * n * n, np.float64)
+        ctx.fill_uniform(buf, -1.0, 1.0, 3)
+        for _ in range(reps):
+            ctx.dgemm(NO_TRANS, TRANS, n, n, n, 1.0, buf.offset(0), n, buf.offset(n * n), n, 1.0,
+                      buf.offset(2 * n * n), n)
+        ctx.synchronize()
+        return {"algorithmic_bytes": 8 * 4 * n * n}
+    if name == "ssyrk_8192":
+        n, k = 8192, 4096
+        dA, dC = ctx.empty(n * k, np.float32), ctx.empty(n * n, np.float32)
+        ctx.fill_normal(dA, 4)
+        ctx.fill_uniform(dC, -1.0, 1.0, 5)
+        for _ in range(reps):
+            ctx.ssyrk(LOWER, NO_TRANS, n, k, 1.0, dA, n, 0.25, dC, n)
+        ctx.synchronize()
+        return {"algorithmic_bytes": 4 * (n * k + n * (n + 1))}
+    n = 1 << 28
+    dx, dy = ctx.empty(n, np.float32), ctx.empty(n, np.float32)
+    ctx.fill_normal(dx, 1)
+    ctx.fill_normal(dy, 2)
+    out, iout = ctx.empty(4, np.float32), ctx.empty(1, np.int64)
+    fns = {"sdot": lambda: ctx.sdot_dev(n, dx, 1, dy, 1, out), "sasum": lambda: ctx.sasum_dev(n, dx, 1, out),
+           "snrm2": lambda: ctx.snrm2_dev(n, dx, 1, out), "isamax": lambda: ctx.isamax_dev(n, dx, 1, iout)}
+    for _ in range(reps):
+        fns[name]()
+    ctx.synchronize()
+    return {"algorithmic_bytes": (8 if name == "sdot" else 4) * n}
+
+
 def cpu_baseline(budget_s=12.0):
     """The oracle's fp32 restatement of the reference's per-element order
     (oracle/oracle.c orc_sgemm_wgsl), one host thread, on a bounded sample of
@@ -267,6 +321,10 @@ def main():
     ap.add_argument("--quick", action="store_true", help="fewer repetitions for the components")
     ap.add_argument("--no-components", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", default=None,
+                    help="run one workload alone (copy, sgemm_8192, dgemm_4096, ssyrk_8192, "
+                         "sdot, sasum, snrm2, isamax) for counter collection")
+    ap.add_argument("--reps", type=int, default=3)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
@@ -277,6 +335,11 @@ def main():
     from wgblas_amd import Context
 
     ctx = Context(0)
+    if args.only:
+        info = run_only(ctx, args.only, args.reps)
+        ctx.close()
+        print(json.dumps({"only": args.only, "reps": args.reps, **info}))
+        return 0
     ev = HipEvents(ctx.stream)
     name, arch = ctx.name()
     ms, flops, launch_ms, mean_launch = bench_gemm_headline(ctx, ev, args.steps, args.warmup)

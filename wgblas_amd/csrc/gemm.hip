@@ -280,6 +280,41 @@ __device__ __forceinline__ void fetch_operands(const T *stage, int wrow, int kc,
   }
 }
 
+// Fetches the MFMA operands of step s of one 16-k chunk for MB 16-row
+// blocks: out[b] = operand of block b. Same data as fetch_operands, issued
+// step by step so only one step's operands are live (used where register
+// pressure, not LDS instruction count, limits occupancy).
+template <typename T, int BT, bool KC, int MB>
+__device__ __forceinline__ void fetch_step(const T *stage, int wrow, int kc, int s, int lane,
+                                           T (&out)[MB]) {
+  constexpr int VW = Ty<T>::VW;
+  constexpr int BK = 128 / (int)sizeof(T);
+  constexpr int LDK = BK + VW;
+  constexpr int LDM = BT;
+  constexpr int RW = MB < VW ? MB : VW;
+  const int g = lane >> 4, i16 = lane & 15;
+  if (KC) {
+#pragma unroll
+    for (int b = 0; b < MB; ++b) out[b] = stage[(wrow + 16 * b + i16) * LDK + kc + 4 * g + s];
+  } else {
+#pragma unroll
+    for (int h = 0; h < MB / RW; ++h) {
+      const T *p = stage + (kc + 4 * g + s) * LDM + wrow + 16 * RW * h + RW * i16;
+      if (RW == 4) {
+        typedef typename Ty<T>::v4 V4;
+        V4 v = *reinterpret_cast<const V4 *>(p);
+#pragma unroll
+        for (int c = 0; c < RW; ++c) out[h * RW + c] = v[c];
+      } else {
+        typedef typename Ty<T>::v2 V2;
+        V2 v = *reinterpret_cast<const V2 *>(p);
+#pragma unroll
+        for (int c = 0; c < RW; ++c) out[h * RW + c] = v[c];
+      }
+    }
+  }
+}
+
 // Row inside the wave tile held by lane `lane` for MFMA block b and
 // accumulator register q.
 template <typename T, bool KC, int MB>
@@ -300,8 +335,16 @@ __device__ __forceinline__ int out_col(int b, int lane) {
   return 16 * RW * (b / RW) + RW * i16 + (b % RW);
 }
 
+// fp64 fetches operands per MFMA step and is held to two waves per SIMD
+// (256 registers): its 128 accumulator registers leave no room for a whole
+// chunk of operands at that occupancy. fp32 fetches a chunk at a time.
+template <typename T>
+struct KernelPolicy {
+  static constexpr bool kPerStep = sizeof(T) == 8;
+};
+
 template <typename T, int BT, bool AKC, bool BKC, bool VEC>
-__global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs<T> p) {
+__global__ __launch_bounds__(kThreads, sizeof(T) == 8 ? 2 : 1) void gemm_kernel(GemmArgs<T> p) {
   typedef typename Ty<T>::acc Acc;
   typedef typename Ty<T>::v16 V;
   constexpr int VW = Ty<T>::VW;
@@ -361,15 +404,28 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs<T> p) {
     const T *Bs = As + SA::ELEMS;
 #pragma unroll
     for (int kc = 0; kc < BK; kc += 16) {
-      T a[4][MB], b[4][MB];
-      fetch_operands<T, BT, AKC, MB>(As, wm, kc, lane, a);
-      fetch_operands<T, BT, BKC, MB>(Bs, wn, kc, lane, b);
+      if (KernelPolicy<T>::kPerStep) {
 #pragma unroll
-      for (int s = 0; s < 4; ++s)
+        for (int s = 0; s < 4; ++s) {
+          T a[MB], b[MB];
+          fetch_step<T, BT, AKC, MB>(As, wm, kc, s, lane, a);
+          fetch_step<T, BT, BKC, MB>(Bs, wn, kc, s, lane, b);
 #pragma unroll
-        for (int i = 0; i < MB; ++i)
+          for (int i = 0; i < MB; ++i)
 #pragma unroll
-          for (int j = 0; j < MB; ++j) acc[i][j] = Ty<T>::mfma(a[s][i], b[s][j], acc[i][j]);
+            for (int j = 0; j < MB; ++j) acc[i][j] = Ty<T>::mfma(a[i], b[j], acc[i][j]);
+        }
+      } else {
+        T a[4][MB], b[4][MB];
+        fetch_operands<T, BT, AKC, MB>(As, wm, kc, lane, a);
+        fetch_operands<T, BT, BKC, MB>(Bs, wn, kc, lane, b);
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+          for (int i = 0; i < MB; ++i)
+#pragma unroll
+            for (int j = 0; j < MB; ++j) acc[i][j] = Ty<T>::mfma(a[s][i], b[s][j], acc[i][j]);
+      }
     }
     if (more) {
       T *next = smem + ((kt + 1) & 1) * STAGE;

@@ -4,19 +4,20 @@
 // workgroups of 64 threads grid-stride over x with four accumulators each,
 // then a single workgroup folds the 128 partials (src/sdot/sdot.mjs:86-92,
 // src/shaders/sdot.wgsl, src/shaders/reduction/sum.wgsl). This file keeps the
-// two-pass structure and its determinism, but sizes pass 1 for MI355X's HBM:
+// two-stage structure and its determinism, sized for MI355X's HBM:
 //
-//  * pass 1 uses G = min(2048, ceil(n / 4096)) blocks of 256 threads, each
+//  * stage 1 uses G = min(2048, ceil(n / 4096)) blocks of 256 threads, each
 //    reading one contiguous range of x (and y); G and the ranges depend only
 //    on n, so the summation order (and the result) is the same on every run
 //    and every device;
 //  * unit-stride, 16-byte-aligned operands are read with 16-byte
-//    non-temporal loads, eight in flight per lane per input; other strides
-//    read one element per lane;
+//    non-temporal loads, eight in flight per lane per input; strides 2..4
+//    read their span the same way and keep every incx-th element; other
+//    strides read one element per lane;
 //  * a block folds its lanes with 64-lane shuffles, then its four waves in
-//    LDS, in a fixed order, and writes one partial;
-//  * pass 2 (one block) folds the G partials in a fixed order and, for snrm2
-//    and isamax, applies the final combine.
+//    LDS, in a fixed order, and stores one partial;
+//  * stage 2 (one block, a second launch) folds the G partials in a fixed
+//    order and applies the final combine (snrm2) or index pick (isamax).
 //
 // The per-element arithmetic follows the WGSL kernels: f32 accumulation,
 // snrm2's big/medium/small classification with the same power-of-two
@@ -75,6 +76,8 @@ struct SdotOp {
   __device__ static Partial identity() { return 0.0f; }
   __device__ static Partial merge(Partial a, Partial b) { return a + b; }
   __device__ static Partial shfl(Partial a, int off) { return __shfl_xor(a, off, 64); }
+  typedef float Result;
+  __device__ static Result result(Partial p) { return p; }
 };
 
 struct SasumOp {
@@ -93,6 +96,8 @@ struct SasumOp {
   __device__ static Partial identity() { return 0.0f; }
   __device__ static Partial merge(Partial a, Partial b) { return a + b; }
   __device__ static Partial shfl(Partial a, int off) { return __shfl_xor(a, off, 64); }
+  typedef float Result;
+  __device__ static Result result(Partial p) { return p; }
 };
 
 // snrm2: (big, medium, small) sums of scaled squares.
@@ -113,22 +118,19 @@ __device__ __forceinline__ void nrm_accum(Nrm &s, float v) {
   s.sml = sml ? fmaf(ys, ys, s.sml) : s.sml;
 }
 
-// True when |v| is outside the medium band and not zero (zero adds nothing
-// to whichever sum it lands in, so it can take the medium fast path).
-__device__ __forceinline__ bool nrm_odd(float v) {
-  float ax = fabsf(v);
-  return !(ax <= kTbig) || (ax < kTsml && ax != 0.0f);
-}
-
 struct Snrm2Op {
   static constexpr int NIN = 1;
   typedef Nrm State;
   typedef v4f Partial;  // (big, medium, small, 0)
   __device__ static State init() { return Nrm{0.f, 0.f, 0.f}; }
   __device__ static void add4(State &s, v4f a, v4f, int64_t) {
-    // Whole-wave fast path: when no lane holds an element outside the
-    // medium band, the four squares go straight into the medium sum.
-    bool odd = nrm_odd(a.x) || nrm_odd(a.y) || nrm_odd(a.z) || nrm_odd(a.w);
+    // Whole-wave fast path: when every lane's four |x| lie in
+    // [TSML, TBIG], the squares go straight into the medium sum. (min/max
+    // skip NaN, which then takes the fast path into the medium sum, exactly
+    // where the classification puts it.)
+    const float hi = fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w)));
+    const float lo = fminf(fminf(fabsf(a.x), fabsf(a.y)), fminf(fabsf(a.z), fabsf(a.w)));
+    const bool odd = !(hi <= kTbig) || lo < kTsml;
     if (__any(odd)) {
       nrm_accum(s, a.x);
       nrm_accum(s, a.y);
@@ -148,6 +150,8 @@ struct Snrm2Op {
   __device__ static Partial shfl(Partial a, int off) {
     return v4f{__shfl_xor(a.x, off, 64), __shfl_xor(a.y, off, 64), __shfl_xor(a.z, off, 64), 0.f};
   }
+  typedef float Result;
+  __device__ static Result result(Partial p);  // LAPACK combine, defined below
 };
 
 // isamax: (max |x|, its first index). A lane visits its elements in
@@ -174,10 +178,15 @@ struct IsamaxOp {
   typedef AmaxPartial Partial;
   __device__ static State init() { return AmaxPartial{-1.0f, 0.f, 0}; }
   __device__ static void add4(State &s, v4f a, v4f, int64_t i) {
-    amax_step(s, a.x, i);
-    amax_step(s, a.y, i + 1);
-    amax_step(s, a.z, i + 2);
-    amax_step(s, a.w, i + 3);
+    // max|x| of the four first (v_max ignores a NaN operand, so NaN never
+    // wins); only a vector that beats the running best is searched, for
+    // its first element equal to that max.
+    const float m = fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w)));
+    if (m > s.val) {
+      const int c = fabsf(a.x) == m ? 0 : fabsf(a.y) == m ? 1 : fabsf(a.z) == m ? 2 : 3;
+      s.val = m;
+      s.idx = i + c;
+    }
   }
   __device__ static void add1(State &s, float a, float, int64_t i, int) { amax_step(s, a, i); }
   __device__ static Partial finish(State s) { return s; }
@@ -188,6 +197,8 @@ struct IsamaxOp {
   __device__ static Partial shfl(Partial a, int off) {
     return AmaxPartial{__shfl_xor(a.val, off, 64), 0.f, __shfl_xor(a.idx, off, 64)};
   }
+  typedef int64_t Result;
+  __device__ static Result result(Partial p) { return p.idx; }
 };
 
 // ---- block merge (fixed order) --------------------------------------------
@@ -218,12 +229,21 @@ __device__ __forceinline__ void chunk_of(int64_t total, int64_t &beg, int64_t &e
   if (beg > end) beg = end;
 }
 
-// Pass 1 over unit-stride, 16-byte-aligned operands: 16-byte non-temporal
-// loads, kUnroll of them in flight per lane per input.
+// A block's partial goes to its slot; stage 2 (fold_kernel) folds them.
+// (Folding in the last block of the same launch needs an agent-scope
+// release per block, which writes back the XCD's L2: measured ~90 us per
+// 2048-block launch on MI355X, far more than the second launch costs.)
 template <class Op>
-__global__ __launch_bounds__(kThreads) void pass1_vec(const float *__restrict__ x,
-                                                      const float *__restrict__ y, int64_t n,
-                                                      typename Op::Partial *__restrict__ partials) {
+__device__ __forceinline__ void finish(typename Op::Partial p, typename Op::Partial *partials) {
+  if (threadIdx.x == 0) partials[blockIdx.x] = p;
+}
+
+// Unit-stride, 16-byte-aligned operands: 16-byte non-temporal loads,
+// kUnroll of them in flight per lane per input.
+template <class Op>
+__global__ __launch_bounds__(kThreads) void reduce_vec(const float *__restrict__ x,
+                                                       const float *__restrict__ y, int64_t n,
+                                                       typename Op::Partial *__restrict__ partials) {
   const v4f *x4 = reinterpret_cast<const v4f *>(x);
   const v4f *y4 = reinterpret_cast<const v4f *>(y);
   const int64_t n4 = n >> 2;
@@ -248,17 +268,62 @@ __global__ __launch_bounds__(kThreads) void pass1_vec(const float *__restrict__ 
   // The n % 4 trailing elements follow the last block's range.
   if (blockIdx.x == gridDim.x - 1 && threadIdx.x == 0)
     for (int64_t i = n4 * 4; i < n; ++i) Op::add1(s, x[i], Op::NIN == 2 ? y[i] : 0.f, i, 0);
-  typename Op::Partial p = block_merge<Op>(Op::finish(s));
-  if (threadIdx.x == 0) partials[blockIdx.x] = p;
+  finish<Op>(block_merge<Op>(Op::finish(s)), partials);
 }
 
-// Pass 1 for any positive stride (and misaligned unit stride): one element
-// per lane per step, kUnroll steps in flight.
+// Small constant strides (incx == incy == INC, 2..4): read the whole span
+// [0, (n-1)*INC] with the same coalesced 16-byte loads and keep every
+// INC-th element. The span's lines are fetched either way, so this trades
+// nothing in HBM bytes for far fewer, wider load instructions.
+template <class Op, int INC>
+__global__ __launch_bounds__(kThreads) void reduce_span(const float *__restrict__ x,
+                                                        const float *__restrict__ y, int64_t n,
+                                                        typename Op::Partial *__restrict__ partials) {
+  const v4f *x4 = reinterpret_cast<const v4f *>(x);
+  const v4f *y4 = reinterpret_cast<const v4f *>(y);
+  const uint32_t span = (uint32_t)((n - 1) * INC + 1);  // host checks span < 2^31
+  const int64_t n4 = span >> 2;
+  int64_t beg, end;
+  chunk_of(n4, beg, end);
+  typename Op::State s = Op::init();
+  uint32_t q = (uint32_t)(beg + threadIdx.x);
+  for (; q + (kUnroll - 1) * kThreads < (uint32_t)end; q += kUnroll * kThreads) {
+    v4f a[kUnroll], b[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      a[u] = nt_load(x4 + q + u * kThreads);
+      b[u] = Op::NIN == 2 ? nt_load(y4 + q + u * kThreads) : a[u];
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const uint32_t e = 4 * (q + u * kThreads) + c;
+        if (e % INC == 0) Op::add1(s, a[u][c], b[u][c], e / INC, c);
+      }
+  }
+  for (; q < (uint32_t)end; q += kThreads) {
+    v4f a = x4[q];
+    v4f b = Op::NIN == 2 ? y4[q] : a;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint32_t e = 4 * q + c;
+      if (e % INC == 0) Op::add1(s, a[c], b[c], e / INC, c);
+    }
+  }
+  if (blockIdx.x == gridDim.x - 1 && threadIdx.x == 0)
+    for (uint32_t e = (uint32_t)n4 * 4; e < span; ++e)
+      if (e % INC == 0) Op::add1(s, x[e], Op::NIN == 2 ? y[e] : 0.f, e / INC, 0);
+  finish<Op>(block_merge<Op>(Op::finish(s)), partials);
+}
+
+// Any positive strides (and misaligned unit stride): one element per lane
+// per step, kUnroll steps in flight.
 template <class Op>
-__global__ __launch_bounds__(kThreads) void pass1_strided(const float *__restrict__ x, int64_t incx,
-                                                          const float *__restrict__ y, int64_t incy,
-                                                          int64_t n,
-                                                          typename Op::Partial *__restrict__ partials) {
+__global__ __launch_bounds__(kThreads) void reduce_strided(const float *__restrict__ x, int64_t incx,
+                                                           const float *__restrict__ y, int64_t incy,
+                                                           int64_t n,
+                                                           typename Op::Partial *__restrict__ partials) {
   int64_t beg, end;
   chunk_of(n, beg, end);
   typename Op::State s = Op::init();
@@ -274,24 +339,26 @@ __global__ __launch_bounds__(kThreads) void pass1_strided(const float *__restric
     for (int u = 0; u < kUnroll; ++u) Op::add1(s, a[u], b[u], i + u * kThreads, u & 3);
   }
   for (; i < end; i += kThreads) Op::add1(s, x[i * incx], Op::NIN == 2 ? y[i * incy] : 0.f, i, 0);
-  typename Op::Partial p = block_merge<Op>(Op::finish(s));
-  if (threadIdx.x == 0) partials[blockIdx.x] = p;
+  finish<Op>(block_merge<Op>(Op::finish(s)), partials);
 }
 
-// Pass 2: one block folds the G partials in a fixed order.
+// Stage 2: one block folds the G partials in a fixed order (each thread
+// issues all of its loads before folding them) and writes the result.
 template <class Op>
-__device__ __forceinline__ typename Op::Partial fold_partials(const typename Op::Partial *partials,
-                                                              int G) {
-  typename Op::Partial p = Op::identity();
-  for (int i = threadIdx.x; i < G; i += kThreads) p = Op::merge(p, partials[i]);
-  return block_merge<Op>(p);
-}
-
-template <class Op>
-__global__ __launch_bounds__(kThreads) void sum_pass2(const float *__restrict__ partials, int G,
-                                                      float *__restrict__ out) {
-  float p = fold_partials<Op>(partials, G);
-  if (threadIdx.x == 0) *out = p;
+__global__ __launch_bounds__(kThreads) void fold_kernel(const typename Op::Partial *__restrict__ partials,
+                                                        int G, typename Op::Result *__restrict__ out) {
+  constexpr int kPer = wgb::kMaxReduceBlocks / kThreads;
+  typename Op::Partial v[kPer];
+#pragma unroll
+  for (int r = 0; r < kPer; ++r) {
+    const int i = threadIdx.x + r * kThreads;
+    v[r] = i < G ? partials[i] : Op::identity();
+  }
+  typename Op::Partial p = v[0];
+#pragma unroll
+  for (int r = 1; r < kPer; ++r) p = Op::merge(p, v[r]);
+  p = block_merge<Op>(p);
+  if (threadIdx.x == 0) *out = Op::result(p);
 }
 
 // v * 2^e by editing the exponent field, as scaledSum.wgsl's ldexpBits does:
@@ -338,17 +405,7 @@ __device__ float nrm_combine(float abig, float amed, float asml) {
   return scl * sqrtf(sumsq);
 }
 
-__global__ __launch_bounds__(kThreads) void snrm2_pass2(const v4f *__restrict__ partials, int G,
-                                                        float *__restrict__ out) {
-  v4f p = fold_partials<Snrm2Op>(partials, G);
-  if (threadIdx.x == 0) *out = nrm_combine(p.x, p.y, p.z);
-}
-
-__global__ __launch_bounds__(kThreads) void isamax_pass2(const AmaxPartial *__restrict__ partials,
-                                                         int G, int64_t *__restrict__ out) {
-  AmaxPartial p = fold_partials<IsamaxOp>(partials, G);
-  if (threadIdx.x == 0) *out = p.idx;
-}
+__device__ Snrm2Op::Result Snrm2Op::result(Partial p) { return nrm_combine(p.x, p.y, p.z); }
 
 // Writes the n <= 0 answer of a `_dev` call with a kernel rather than a
 // memset, so the call stays safe to capture in a HIP graph.
@@ -368,56 +425,50 @@ int check_vec(int64_t n, const float *x, int64_t incx, const char *xname, const 
 
 void *partials_of(wgb_ctx *ctx) { return ctx->scratch; }
 void *result_slot(wgb_ctx *ctx) { return (char *)ctx->scratch + (size_t)wgb::kMaxReduceBlocks * 16; }
-
+// Stage 1 (the read pass) and stage 2 (the fold), two launches on the stream.
 template <class Op>
-void launch_pass1(wgb_ctx *ctx, int G, int64_t n, const float *x, int64_t incx, const float *y,
-                  int64_t incy, typename Op::Partial *part) {
-  bool vec = incx == 1 && aligned16(x) && (Op::NIN == 1 || (incy == 1 && aligned16(y)));
-  if (vec)
-    pass1_vec<Op><<<G, kThreads, 0, ctx->stream>>>(x, y, n, part);
-  else
-    pass1_strided<Op><<<G, kThreads, 0, ctx->stream>>>(x, incx, y, incy, n, part);
+int launch_reduce(wgb_ctx *ctx, int64_t n, const float *x, int64_t incx, const float *y,
+                  int64_t incy, typename Op::Result *d_out, const char *what) {
+  const int G = reduce_blocks(n);
+  auto *part = (typename Op::Partial *)partials_of(ctx);
+  int Gl = G;
+  const bool same = Op::NIN == 1 || (incy == incx && aligned16(y));
+  const int64_t span = (n - 1) * incx + 1;
+  if (incx == 1 && aligned16(x) && same) {
+    reduce_vec<Op><<<G, kThreads, 0, ctx->stream>>>(x, y, n, part);
+  } else if (incx >= 2 && incx <= 4 && aligned16(x) && same && span < ((int64_t)1 << 31)) {
+    // G from the span, not n: each block reads a span range.
+    Gl = reduce_blocks(span);
+    if (incx == 2)
+      reduce_span<Op, 2><<<Gl, kThreads, 0, ctx->stream>>>(x, y, n, part);
+    else if (incx == 3)
+      reduce_span<Op, 3><<<Gl, kThreads, 0, ctx->stream>>>(x, y, n, part);
+    else
+      reduce_span<Op, 4><<<Gl, kThreads, 0, ctx->stream>>>(x, y, n, part);
+  } else {
+    reduce_strided<Op><<<G, kThreads, 0, ctx->stream>>>(x, incx, y, incy, n, part);
+  }
+  WGB_CHECK_LAUNCH(what);
+  fold_kernel<Op><<<1, kThreads, 0, ctx->stream>>>(part, Gl, d_out);
+  WGB_CHECK_LAUNCH(what);
+  return WGB_OK;
 }
 
 int launch_sdot(wgb_ctx *ctx, int64_t n, const float *x, int64_t incx, const float *y,
                 int64_t incy, float *d_out) {
-  int G = reduce_blocks(n);
-  float *part = (float *)partials_of(ctx);
-  launch_pass1<SdotOp>(ctx, G, n, x, incx, y, incy, part);
-  WGB_CHECK_LAUNCH("sdot pass 1");
-  sum_pass2<SdotOp><<<1, kThreads, 0, ctx->stream>>>(part, G, d_out);
-  WGB_CHECK_LAUNCH("sdot pass 2");
-  return WGB_OK;
+  return launch_reduce<SdotOp>(ctx, n, x, incx, y, incy, d_out, "sdot");
 }
 
 int launch_sasum(wgb_ctx *ctx, int64_t n, const float *x, int64_t incx, float *d_out) {
-  int G = reduce_blocks(n);
-  float *part = (float *)partials_of(ctx);
-  launch_pass1<SasumOp>(ctx, G, n, x, incx, x, incx, part);
-  WGB_CHECK_LAUNCH("sasum pass 1");
-  sum_pass2<SasumOp><<<1, kThreads, 0, ctx->stream>>>(part, G, d_out);
-  WGB_CHECK_LAUNCH("sasum pass 2");
-  return WGB_OK;
+  return launch_reduce<SasumOp>(ctx, n, x, incx, x, incx, d_out, "sasum");
 }
 
 int launch_snrm2(wgb_ctx *ctx, int64_t n, const float *x, int64_t incx, float *d_out) {
-  int G = reduce_blocks(n);
-  v4f *part = (v4f *)partials_of(ctx);
-  launch_pass1<Snrm2Op>(ctx, G, n, x, incx, x, incx, part);
-  WGB_CHECK_LAUNCH("snrm2 pass 1");
-  snrm2_pass2<<<1, kThreads, 0, ctx->stream>>>(part, G, d_out);
-  WGB_CHECK_LAUNCH("snrm2 pass 2");
-  return WGB_OK;
+  return launch_reduce<Snrm2Op>(ctx, n, x, incx, x, incx, d_out, "snrm2");
 }
 
 int launch_isamax(wgb_ctx *ctx, int64_t n, const float *x, int64_t incx, int64_t *d_out) {
-  int G = reduce_blocks(n);
-  AmaxPartial *part = (AmaxPartial *)partials_of(ctx);
-  launch_pass1<IsamaxOp>(ctx, G, n, x, incx, x, incx, part);
-  WGB_CHECK_LAUNCH("isamax pass 1");
-  isamax_pass2<<<1, kThreads, 0, ctx->stream>>>(part, G, d_out);
-  WGB_CHECK_LAUNCH("isamax pass 2");
-  return WGB_OK;
+  return launch_reduce<IsamaxOp>(ctx, n, x, incx, x, incx, d_out, "isamax");
 }
 
 // Copies a device scalar into the context's pinned slot and waits for it.

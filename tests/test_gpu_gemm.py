@@ -149,6 +149,43 @@ def test_beta_zero_ignores_nan_in_c(ctx):
     assert np.all(np.isfinite(got))
 
 
+@pytest.mark.parametrize("variant", ["ldc_pad4", "c_misaligned", "beta0_nan"])
+@pytest.mark.parametrize("ta", [0, 1])
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("shape", [(1024, 768, 96), (2048, 2304, 40)])  # small / large tier
+def test_epilogue_paths(ctx, variant, ta, dtype, shape):
+    """Whole-vector C epilogue (ldc multiple of the vector width, C 16-byte
+    aligned) against the element-wise one (C one element off alignment), with
+    ld padding kept bit-identical and beta == 0 never reading C."""
+    m, n, k = shape
+    ldc = m + 4
+    gen = orc.random_f64 if dtype == np.float64 else orc.random_f32
+    lda = k if ta else m
+    A = gen(lda * (m if ta else k), -1, 1, 41)
+    B = gen(k * n, -1, 1, 42)
+    C = gen(ldc * n, -1, 1, 43)
+    beta = 0.5
+    if variant == "beta0_nan":
+        C[::7] = np.nan
+        beta = 0.0
+    shift = 1 if variant == "c_misaligned" else 0
+    dA, dB = ctx.upload(A), ctx.upload(B)
+    dC = ctx.upload(np.concatenate([np.zeros(shift, dtype), C]))
+    call = ctx.dgemm if dtype == np.float64 else ctx.sgemm
+    call(ta, 0, m, n, k, 1.25, dA, lda, dB, k, beta, dC.offset(shift), ldc)
+    got = dC.to_host()[shift:]
+    for d in (dA, dB, dC):
+        d.free()
+    C0 = np.where(np.isnan(C), 0.0, C).astype(np.float64) if beta == 0.0 else C.astype(np.float64)
+    ref, absdot = orc.gemm_ld(0, ta, 0, m, n, k, 1.25, A.astype(np.float64), lda,
+                              B.astype(np.float64), k, beta, C0, ldc)
+    fac = gemm_forward_factor(got, ref, absdot, C0, m, n, k, 1.25, beta, ldc, 0,
+                              dd=dtype == np.float64)
+    assert fac <= 1.0, f"forward factor {fac}"
+    keep = untouched_mask(m, n, ldc, n, 0)
+    assert bits_equal(got[keep], C[keep]), "ld padding of C changed"
+
+
 @pytest.mark.parametrize("mn", [(100, 100), (150, 70), (70, 150)])
 @pytest.mark.parametrize("uplo", [1, 2])
 @pytest.mark.parametrize("ta", [0, 1])

@@ -14,7 +14,9 @@
 // buffered, in the orientation it has in memory so the global->LDS path is
 // plain 16-byte copies:
 //   * k-contiguous operands (op(A) with A transposed, op(B) with B not
-//     transposed) are stored [row][k] with a 16-byte row pad;
+//     transposed) are stored [row][k], 128-byte rows whose eight 16-byte
+//     chunks are XOR-swizzled by row (kc_swz) so that both the stores and
+//     the 16-row operand reads touch every LDS bank once;
 //   * mn-contiguous operands (A not transposed, B transposed) are stored
 //     [k][row].
 // MFMA operand fetch from either layout is one 16-byte (or 8-byte) LDS read
@@ -93,7 +95,8 @@ struct GemmArgs {
   T *C;
   int64_t ldc;
   int tiles_m, tiles_n, ntiles;
-  int uplo;  // 0 = full C, WGB_LOWER, WGB_UPPER
+  int uplo;   // 0 = full C, WGB_LOWER, WGB_UPPER
+  int c_vec;  // ldc % VW == 0 and C 16-byte aligned: whole-vector C access
 };
 
 constexpr int kThreads = 256;
@@ -149,8 +152,18 @@ __device__ inline void tile_of(int w, int ntiles, int tiles_m, int tiles_n, int 
   }
 }
 
+// Chunk position of 16-byte chunk c of staged row r in the [row][k] layout
+// is c ^ kc_swz(r). A ds_write_b128 phase (8 lanes) fills one 128-byte row;
+// a ds_read_b128 phase (16 lanes) reads one chunk of 16 consecutive rows.
+// Measured on MI355X (SQ_LDS_BANK_CONFLICT, one wave per block, every
+// 16-lane phase of the read pattern): the key r & 7 keeps both conflict-free,
+// while a 16-byte row pad, or a key that also folds in row bit 3, costs a
+// second cycle on every read.
+__device__ __forceinline__ int kc_swz(int row) { return row & 7; }
+
 // Global -> register -> LDS staging of one operand's BT x BK tile.
-// KC: k-contiguous in memory, staged [row][k] (row stride BK + VW).
+// KC: k-contiguous in memory, staged [row][k] (row stride BK, chunks
+//     swizzled by kc_swz).
 // !KC: row-contiguous in memory, staged [k][row] (row stride BT).
 template <typename T, int BT, bool KC, bool VEC>
 struct Stager {
@@ -160,7 +173,7 @@ struct Stager {
   static constexpr int LOADS = BT / 32;      // 16-byte vectors per thread
   static constexpr int VPK = BT / VW;        // vectors per k-row (!KC)
   static constexpr int KROWS = kThreads / VPK;  // k-rows per load step (!KC)
-  static constexpr int LDK = BK + VW;
+  static constexpr int LDK = BK;
   static constexpr int LDM = BT;
   static constexpr int ELEMS = KC ? BT * LDK : BK * LDM;
 
@@ -184,7 +197,7 @@ struct Stager {
       base = P + (row0 + row) * ld + kv * VW;
       r_step = 32 * ld;
       k_step = BK;
-      lds_off = row * LDK + kv * VW;
+      lds_off = row * LDK + (kv ^ kc_swz(row)) * VW;  // kc_swz(row + 32 r) == kc_swz(row)
       lds_r_step = 32 * LDK;
     } else {
       int mv = t % VPK, kk = t / VPK;
@@ -248,16 +261,30 @@ __device__ __forceinline__ void fetch_operands(const T *stage, int wrow, int kc,
   typedef typename Ty<T>::v4 V4;
   constexpr int VW = Ty<T>::VW;
   constexpr int BK = 128 / (int)sizeof(T);
-  constexpr int LDK = BK + VW;
+  constexpr int LDK = BK;
   constexpr int LDM = BT;
   constexpr int RW = MB < VW ? MB : VW;
   const int g = lane >> 4, i16 = lane & 15;
   if (KC) {
+    // wrow is a multiple of 16, so the row key is kc_swz(i16); the 4 k of
+    // lane group g are 4 / VW whole chunks.
+    const int key = kc_swz(i16);
 #pragma unroll
     for (int b = 0; b < MB; ++b) {
-      V4 v = *reinterpret_cast<const V4 *>(stage + (wrow + 16 * b + i16) * LDK + kc + 4 * g);
+      const T *row = stage + (wrow + 16 * b + i16) * LDK;
+      if (VW == 4) {
+        V4 v = *reinterpret_cast<const V4 *>(row + ((((kc + 4 * g) / VW) ^ key) * VW));
 #pragma unroll
-      for (int s = 0; s < 4; ++s) out[s][b] = v[s];
+        for (int s = 0; s < 4; ++s) out[s][b] = v[s];
+      } else {
+        typedef typename Ty<T>::v2 V2;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          V2 v = *reinterpret_cast<const V2 *>(row + ((((kc + 4 * g) / VW + h) ^ key) * VW));
+          out[2 * h][b] = v[0];
+          out[2 * h + 1][b] = v[1];
+        }
+      }
     }
   } else {
 #pragma unroll
@@ -289,13 +316,15 @@ __device__ __forceinline__ void fetch_step(const T *stage, int wrow, int kc, int
                                            T (&out)[MB]) {
   constexpr int VW = Ty<T>::VW;
   constexpr int BK = 128 / (int)sizeof(T);
-  constexpr int LDK = BK + VW;
+  constexpr int LDK = BK;
   constexpr int LDM = BT;
   constexpr int RW = MB < VW ? MB : VW;
   const int g = lane >> 4, i16 = lane & 15;
   if (KC) {
+    const int kk = kc + 4 * g + s;
+    const int off = (((kk / VW) ^ kc_swz(i16)) * VW) + kk % VW;
 #pragma unroll
-    for (int b = 0; b < MB; ++b) out[b] = stage[(wrow + 16 * b + i16) * LDK + kc + 4 * g + s];
+    for (int b = 0; b < MB; ++b) out[b] = stage[(wrow + 16 * b + i16) * LDK + off];
   } else {
 #pragma unroll
     for (int h = 0; h < MB / RW; ++h) {
@@ -333,6 +362,86 @@ __device__ __forceinline__ int out_col(int b, int lane) {
   const int i16 = lane & 15;
   if (KC) return 16 * b + i16;
   return 16 * RW * (b / RW) + RW * i16 + (b % RW);
+}
+
+// Epilogue of a whole interior tile with C accessed in vectors (ldc a
+// multiple of the vector width, C 16-byte aligned). Every lane holds runs of
+// consecutive C rows in one column:
+//   * A mn-contiguous: blocks i = RW h + c (c = 0..RW-1) of register q sit at
+//     rows 16 RW h + RW drow(g, q) + c, a run of RW rows;
+//   * A k-contiguous, fp32: registers q = 0..3 of block i sit at rows
+//     16 i + 4 g + q, a run of 4 rows.
+// (fp64 with A k-contiguous holds no runs: drow interleaves; it keeps the
+// scalar path.) All C loads of a batch are issued before any store.
+template <typename T, bool AKC, bool BKC, int MB>
+__device__ __forceinline__ void epilogue_vec(const GemmArgs<T> &p,
+                                             const typename Ty<T>::acc (&acc)[MB][MB],
+                                             int64_t row0, int64_t col0, int lane) {
+  constexpr int VW = Ty<T>::VW;
+  constexpr int RW = MB < VW ? MB : VW;
+  const int g = lane >> 4;
+  const T alpha = p.alpha, beta = p.beta;
+  if constexpr (!AKC) {
+    typedef T VN __attribute__((ext_vector_type(RW)));
+    // fp32 keeps every column block in flight at once; fp64 (accumulators
+    // in VGPRs) goes one column block at a time.
+    constexpr int JB = sizeof(T) == 4 ? MB : 1;
+#pragma unroll
+    for (int j0 = 0; j0 < MB; j0 += JB) {
+      VN cv[JB][MB / RW][4];
+      T *cp[JB][MB / RW][4];
+#pragma unroll
+      for (int jj = 0; jj < JB; ++jj) {
+        const int64_t col = col0 + out_col<BKC, MB, VW>(j0 + jj, lane);
+#pragma unroll
+        for (int h = 0; h < MB / RW; ++h)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            cp[jj][h][q] = p.C + (row0 + 16 * RW * h + RW * Ty<T>::drow(g, q)) + col * p.ldc;
+            if (beta != (T)0) cv[jj][h][q] = *reinterpret_cast<const VN *>(cp[jj][h][q]);
+          }
+      }
+#pragma unroll
+      for (int jj = 0; jj < JB; ++jj)
+#pragma unroll
+        for (int h = 0; h < MB / RW; ++h)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            VN v;
+#pragma unroll
+            for (int c = 0; c < RW; ++c) {
+              T x = alpha * acc[h * RW + c][j0 + jj][q];
+              v[c] = beta != (T)0 ? fma(beta, cv[jj][h][q][c], x) : x;
+            }
+            *reinterpret_cast<VN *>(cp[jj][h][q]) = v;
+          }
+    }
+  } else {
+    static_assert(sizeof(T) == 4, "vector epilogue with k-contiguous A is fp32 only");
+    typedef typename Ty<T>::v4 V4;
+    V4 cv[MB][MB];
+    T *cp[MB][MB];
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+#pragma unroll
+      for (int j = 0; j < MB; ++j) {
+        const int64_t col = col0 + out_col<BKC, MB, VW>(j, lane);
+        cp[i][j] = p.C + (row0 + 16 * i + 4 * g) + col * p.ldc;
+        if (beta != (T)0) cv[i][j] = *reinterpret_cast<const V4 *>(cp[i][j]);
+      }
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+#pragma unroll
+      for (int j = 0; j < MB; ++j) {
+        V4 v;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          T x = alpha * acc[i][j][q];
+          v[q] = beta != (T)0 ? fma(beta, cv[i][j][q], x) : x;
+        }
+        *reinterpret_cast<V4 *>(cp[i][j]) = v;
+      }
+  }
 }
 
 // fp64 fetches operands per MFMA step and is held to two waves per SIMD
@@ -387,24 +496,24 @@ __global__ __launch_bounds__(kThreads, sizeof(T) == 8 ? 2 : 1) void gemm_kernel(
   }
   sa.store(smem, ra);
   sb.store(smem + SA::ELEMS, rb);
-  __syncthreads();
 
-  for (int kt = 0; kt < nkt; ++kt) {
-    const bool more = kt + 1 < nkt;
-    if (more) {
-      if (kt + 1 < nkt_full) {
-        sa.template load<false>(ra, kt + 1);
-        sb.template load<false>(rb, kt + 1);
-      } else {
-        sa.template load<true>(ra, kt + 1);
-        sb.template load<true>(rb, kt + 1);
+  if constexpr (KernelPolicy<T>::kPerStep) {
+    __syncthreads();
+    for (int kt = 0; kt < nkt; ++kt) {
+      const bool more = kt + 1 < nkt;
+      if (more) {
+        if (kt + 1 < nkt_full) {
+          sa.template load<false>(ra, kt + 1);
+          sb.template load<false>(rb, kt + 1);
+        } else {
+          sa.template load<true>(ra, kt + 1);
+          sb.template load<true>(rb, kt + 1);
+        }
       }
-    }
-    const T *As = smem + (kt & 1) * STAGE;
-    const T *Bs = As + SA::ELEMS;
+      const T *As = smem + (kt & 1) * STAGE;
+      const T *Bs = As + SA::ELEMS;
 #pragma unroll
-    for (int kc = 0; kc < BK; kc += 16) {
-      if (KernelPolicy<T>::kPerStep) {
+      for (int kc = 0; kc < BK; kc += 16) {
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
           T a[MB], b[MB];
@@ -415,30 +524,90 @@ __global__ __launch_bounds__(kThreads, sizeof(T) == 8 ? 2 : 1) void gemm_kernel(
 #pragma unroll
             for (int j = 0; j < MB; ++j) acc[i][j] = Ty<T>::mfma(a[i], b[j], acc[i][j]);
         }
+      }
+      if (more) {
+        T *next = smem + ((kt + 1) & 1) * STAGE;
+        sa.store(next, ra);
+        sb.store(next + SA::ELEMS, rb);
+      }
+      __syncthreads();
+    }
+  } else {
+    // Two 16-k chunks per k-tile, software pipelined so that LDS reads and
+    // global loads are in flight under MFMAs. On entry to iteration kt:
+    // X = chunk 0 of tile kt (registers), R = tile kt+1 (registers, loaded
+    // one iteration earlier), tile kt in LDS buffer kt&1.
+    //   1. LDS reads of chunk 1 of tile kt into Y
+    //   2. MFMAs on X
+    //   3. R -> LDS buffer (kt+1)&1; global loads of tile kt+2 into R
+    //   4. barrier: every wave has finished reading buffer kt&1 (chunk 0
+    //      at the end of kt-1, chunk 1 in step 1, both waited for) and has
+    //      written tile kt+1, so buffer kt&1 may be refilled in kt+1
+    //   5. LDS reads of chunk 0 of tile kt+1 into X
+    //   6. MFMAs on Y
+    static_assert(BK == 32, "the pipelined fp32 loop assumes two 16-k chunks per k-tile");
+    if (1 < nkt) {
+      if (1 < nkt_full) {
+        sa.template load<false>(ra, 1);
+        sb.template load<false>(rb, 1);
       } else {
-        T a[4][MB], b[4][MB];
-        fetch_operands<T, BT, AKC, MB>(As, wm, kc, lane, a);
-        fetch_operands<T, BT, BKC, MB>(Bs, wn, kc, lane, b);
-#pragma unroll
-        for (int s = 0; s < 4; ++s)
-#pragma unroll
-          for (int i = 0; i < MB; ++i)
-#pragma unroll
-            for (int j = 0; j < MB; ++j) acc[i][j] = Ty<T>::mfma(a[s][i], b[s][j], acc[i][j]);
+        sa.template load<true>(ra, 1);
+        sb.template load<true>(rb, 1);
       }
     }
-    if (more) {
-      T *next = smem + ((kt + 1) & 1) * STAGE;
-      sa.store(next, ra);
-      sb.store(next + SA::ELEMS, rb);
-    }
     __syncthreads();
+    T x[4][MB], y[4][MB], xb[4][MB], yb[4][MB];
+    fetch_operands<T, BT, AKC, MB>(smem, wm, 0, lane, x);
+    fetch_operands<T, BT, BKC, MB>(smem + SA::ELEMS, wn, 0, lane, xb);
+    for (int kt = 0; kt < nkt; ++kt) {
+      const bool more = kt + 1 < nkt;
+      const T *As = smem + (kt & 1) * STAGE;
+      fetch_operands<T, BT, AKC, MB>(As, wm, 16, lane, y);
+      fetch_operands<T, BT, BKC, MB>(As + SA::ELEMS, wn, 16, lane, yb);
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+#pragma unroll
+          for (int j = 0; j < MB; ++j) acc[i][j] = Ty<T>::mfma(x[s][i], xb[s][j], acc[i][j]);
+      T *next = smem + ((kt + 1) & 1) * STAGE;
+      if (more) {
+        sa.store(next, ra);
+        sb.store(next + SA::ELEMS, rb);
+        if (kt + 2 < nkt) {
+          if (kt + 2 < nkt_full) {
+            sa.template load<false>(ra, kt + 2);
+            sb.template load<false>(rb, kt + 2);
+          } else {
+            sa.template load<true>(ra, kt + 2);
+            sb.template load<true>(rb, kt + 2);
+          }
+        }
+      }
+      __syncthreads();
+      if (more) {
+        fetch_operands<T, BT, AKC, MB>(next, wm, 0, lane, x);
+        fetch_operands<T, BT, BKC, MB>(next + SA::ELEMS, wn, 0, lane, xb);
+      }
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+#pragma unroll
+          for (int j = 0; j < MB; ++j) acc[i][j] = Ty<T>::mfma(y[s][i], yb[s][j], acc[i][j]);
+    }
   }
 
   // Epilogue: C = alpha*acc + beta*C on the tile's in-range (and, for
   // sgemmtr/ssyrk, in-triangle) elements.
   const T alpha = p.alpha, beta = p.beta;
   const bool tri_diag = p.uplo != 0 && tm == tn;
+  if constexpr (!AKC || sizeof(T) == 4) {
+    if (interior && !tri_diag && p.c_vec) {
+      epilogue_vec<T, AKC, BKC, MB>(p, acc, m0 + wm, n0 + wn, lane);
+      return;
+    }
+  }
 #pragma unroll
   for (int i = 0; i < MB; ++i) {
 #pragma unroll
@@ -560,6 +729,7 @@ int gemm_run(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64_t 
   a.ldc = ldc;
   a.uplo = uplo;
   const int VW = Ty<T>::VW;
+  a.c_vec = (ldc % VW == 0) && aligned16(C);
   const bool akc = transA == WGB_TRANS;
   const bool bkc = transB == WGB_NO_TRANS;
   const bool vec = (lda % VW == 0) && (ldb % VW == 0) && aligned16(A) && aligned16(B);

@@ -85,3 +85,50 @@ def bits_equal(a, b):
     if a.dtype == np.float32:
         return np.array_equal(a.view(np.uint32), b.view(np.uint32))
     return np.array_equal(a.view(np.uint64), b.view(np.uint64))
+
+
+def cm_view(flat, rows, cols, ld):
+    """Column-major (rows x cols, leading dimension ld) view of a flat array."""
+    need = cols * ld
+    buf = flat if flat.size >= need else np.concatenate([flat, np.zeros(need - flat.size, flat.dtype)])
+    return buf[:need].reshape(cols, ld).T[:rows, :]
+
+
+def op(M, trans):
+    return M.T if trans else M
+
+
+def check_gemm_props(C, C0, opA, opB, alpha, beta, k, eps=EPS32, kterm=1, cterm=1.0, rows=(),
+                     cols=(), seed=0, uplo=0):
+    """C, C0: m x n views; opA m x k; opB k x n (any float dtype)."""
+    m, n = C.shape
+    rng = np.random.default_rng(seed)
+    A64 = np.asarray(opA, np.float64)
+    B64 = np.asarray(opB, np.float64)
+    rows = sorted(set([0, 1, m - 1] + list(rows) + [int(r) for r in rng.integers(0, m, 8)]))
+    cols = sorted(set([0, 1, n - 1] + list(cols) + [int(c) for c in rng.integers(0, n, 8)]))
+    worst = 0.0
+    for sel_r, sel_c in ((rows, slice(None)), (slice(None), cols)):
+        exact = alpha * (A64[sel_r, :] @ B64[:, sel_c]) + beta * np.asarray(C0[sel_r, sel_c], np.float64)
+        absd = np.abs(A64[sel_r, :]) @ np.abs(B64[:, sel_c])
+        bound = eps * ((k + kterm) * abs(alpha) * absd + cterm * abs(beta) * np.abs(np.asarray(C0[sel_r, sel_c], np.float64)))
+        got = np.asarray(C[sel_r, sel_c], np.float64)
+        if uplo:
+            i = np.arange(m)[sel_r][:, None] if not isinstance(sel_r, slice) else np.arange(m)[:, None]
+            j = np.arange(n)[sel_c][None, :] if not isinstance(sel_c, slice) else np.arange(n)[None, :]
+            mask = (i >= j) if uplo == 1 else (i <= j)
+            err = np.where(mask, np.abs(got - exact), 0.0)
+        else:
+            err = np.abs(got - exact)
+        assert np.all(err <= bound), f"forward factor {np.max(err / np.where(bound > 0, bound, 1))}"
+        worst = max(worst, float(np.max(err / np.where(bound > 0, bound, np.inf))))
+    if uplo == 0:
+        for t in range(2):
+            x = rng.choice([-1.0, 1.0], size=n)
+            lhs = np.asarray(C, np.float64) @ x
+            rhs = alpha * (A64 @ (B64 @ x)) + beta * (np.asarray(C0, np.float64) @ x)
+            tol = eps * ((k + kterm) * abs(alpha) * (np.abs(A64) @ (np.abs(B64) @ np.abs(x)))
+                         + cterm * abs(beta) * (np.abs(np.asarray(C0, np.float64)) @ np.abs(x)))
+            tol += 1e-12 * (np.abs(lhs) + np.abs(rhs))
+            assert np.all(np.abs(lhs - rhs) <= tol), "Freivalds projection exceeds the summed bound"
+    return worst

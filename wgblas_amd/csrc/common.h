@@ -22,6 +22,10 @@ struct wgb_ctx {
   // by a result slot. Stream order makes reuse across calls safe.
   void *scratch = nullptr;
   size_t scratch_bytes = 0;
+  // GEMM split-k workspace: partial tiles of the launch's last, partly
+  // filled round (grown on demand, reused in stream order).
+  void *gemm_ws = nullptr;
+  size_t gemm_ws_bytes = 0;
   // Pinned host slot the host-result reductions copy their scalar into.
   void *host_result = nullptr;
   char name[256] = {0};

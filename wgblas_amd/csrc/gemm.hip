@@ -97,6 +97,12 @@ struct GemmArgs {
   int tiles_m, tiles_n, ntiles;
   int uplo;   // 0 = full C, WGB_LOWER, WGB_UPPER
   int c_vec;  // ldc % VW == 0 and C 16-byte aligned: whole-vector C access
+  // Split-k tail: logical tiles [nregular, ntiles) are computed as `splits`
+  // k-ranges of kt_split k-tiles each; unit u = (tile - nregular) * splits +
+  // split writes its raw BT x BT partial (column-major, ld BT) to ws + u BT^2
+  // and split_fixup adds them. nregular == ntiles: no split.
+  int nregular, splits, kt_split;
+  T *ws;
 };
 
 constexpr int kThreads = 256;
@@ -130,13 +136,18 @@ __device__ inline void triangle_decode(int L, int cols, int &r, int &c) {
   }
 }
 
-__device__ inline void tile_of(int w, int ntiles, int tiles_m, int tiles_n, int uplo, int &tm,
-                               int &tn) {
-  // XCD-aware remap: workgroup w runs on XCD w % 8; give each XCD a
-  // contiguous run of logical tiles.
+// XCD-aware remap of workgroup w of a grid of n: the hardware deals
+// workgroups round-robin over the 8 XCDs (w % 8); give each XCD a contiguous
+// run of logical tiles so its L2 sees shared A and B panels.
+__device__ inline int xcd_remap(int w, int n) {
   int x = w % kXcds, j = w / kXcds;
-  int q = ntiles / kXcds, r = ntiles % kXcds;
-  int L = x * q + (x < r ? x : r) + j;
+  int q = n / kXcds, r = n % kXcds;
+  return x * q + (x < r ? x : r) + j;
+}
+
+// Logical tile L -> (tile row, tile col): row-major over the triangle for
+// sgemmtr/ssyrk, otherwise groups of kGroupM tile-rows walked column-wise.
+__device__ inline void logical_tile(int L, int tiles_m, int tiles_n, int uplo, int &tm, int &tn) {
   if (uplo == WGB_LOWER) {
     triangle_decode(L, tiles_n, tm, tn);
   } else if (uplo == WGB_UPPER) {
@@ -211,6 +222,12 @@ struct Stager {
     }
   }
 
+  // Moves the tile origin to k-tile kt0 (split-k ranges).
+  __device__ void advance(int kt0) {
+    base += (int64_t)kt0 * k_step;
+    K -= (int64_t)kt0 * BK;
+  }
+
   __device__ static V load_n(const T *p, int64_t nvalid) {
     V v;
 #pragma unroll
@@ -220,10 +237,11 @@ struct Stager {
 
   __device__ static V load_full(const T *p) {
     if (VEC) return *reinterpret_cast<const V *>(p);
-    V v;
-#pragma unroll
-    for (int c = 0; c < VW; ++c) v[c] = p[c];
-    return v;
+    // Only element-aligned (ld not a multiple of VW, or a misaligned base):
+    // CDNA multi-dword global loads need dword alignment only, so this is
+    // still a single 16-byte load.
+    typedef T VU __attribute__((ext_vector_type(VW), aligned(sizeof(T))));
+    return *reinterpret_cast<const VU *>(p);
   }
 
   template <bool GUARD>
@@ -465,20 +483,36 @@ __global__ __launch_bounds__(kThreads, sizeof(T) == 8 ? 2 : 1) void gemm_kernel(
   constexpr int STAGE = SA::ELEMS + SB::ELEMS;
   __shared__ __attribute__((aligned(16))) T smem[2 * STAGE];
 
-  int tm, tn;
-  tile_of(blockIdx.x, p.ntiles, p.tiles_m, p.tiles_n, p.uplo, tm, tn);
+  // Block -> tile and k-range: the first nregular blocks take whole tiles
+  // (XCD-remapped), the rest are split-k units of the tail tiles.
+  int tm, tn, unit = -1, kt0 = 0;
+  const int nkt_all = (int)((p.k + BK - 1) / BK);
+  int nkt = nkt_all;
+  if ((int)blockIdx.x < p.nregular) {
+    logical_tile(xcd_remap(blockIdx.x, p.nregular), p.tiles_m, p.tiles_n, p.uplo, tm, tn);
+  } else {
+    unit = (int)blockIdx.x - p.nregular;
+    logical_tile(p.nregular + unit / p.splits, p.tiles_m, p.tiles_n, p.uplo, tm, tn);
+    kt0 = (unit % p.splits) * p.kt_split;
+    nkt = nkt_all - kt0 < p.kt_split ? nkt_all - kt0 : p.kt_split;
+  }
+  // (nkt >= 1: k > 0 here, and the host never plans an empty split; an
+  // explicit nkt check costs the fp32 loop ~60 VGPRs of scheduling freedom.)
   if (tm < 0 || tn < 0 || tm >= p.tiles_m || tn >= p.tiles_n) return;  // block-uniform
   const int64_t m0 = (int64_t)tm * BT, n0 = (int64_t)tn * BT;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int wm = (wave & 1) * WT, wn = (wave >> 1) * WT;
 
+  // k-tiles are counted from kt0 below: the stagers start at k = kt0 BK and
+  // see K - kt0 BK columns.
   SA sa;
   SB sb;
   sa.init(p.A, p.lda, m0, t, p.m, p.k);
   sb.init(p.B, p.ldb, n0, t, p.n, p.k);
+  sa.advance(kt0);
+  sb.advance(kt0);
   const bool interior = (m0 + BT <= p.m) && (n0 + BT <= p.n);
-  const int nkt = (int)((p.k + BK - 1) / BK);
-  const int nkt_full = interior ? (int)(p.k / BK) : 0;
+  const int nkt_full = interior ? (int)(p.k / BK) - kt0 : 0;
 
   Acc acc[MB][MB];
 #pragma unroll
@@ -600,6 +634,29 @@ __global__ __launch_bounds__(kThreads, sizeof(T) == 8 ? 2 : 1) void gemm_kernel(
 
   // Epilogue: C = alpha*acc + beta*C on the tile's in-range (and, for
   // sgemmtr/ssyrk, in-triangle) elements.
+  if (unit >= 0) {
+    // Split-k unit: raw partial sums of the whole BT x BT tile (rows and
+    // columns past m, n hold zeros from the zero-filled operand loads).
+    T *slice = p.ws + (int64_t)unit * BT * BT;
+    if constexpr (!AKC || sizeof(T) == 4) {
+      GemmArgs<T> q = p;
+      q.C = slice;
+      q.ldc = BT;
+      q.alpha = (T)1;
+      q.beta = (T)0;
+      epilogue_vec<T, AKC, BKC, MB>(q, acc, wm, wn, lane);
+    } else {
+#pragma unroll
+      for (int i = 0; i < MB; ++i)
+#pragma unroll
+        for (int j = 0; j < MB; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            slice[(wm + out_row<T, AKC, MB>(i, q, lane)) +
+                  (int64_t)(wn + out_col<BKC, MB, VW>(j, lane)) * BT] = acc[i][j][q];
+    }
+    return;
+  }
   const T alpha = p.alpha, beta = p.beta;
   const bool tri_diag = p.uplo != 0 && tm == tn;
   if constexpr (!AKC || sizeof(T) == 4) {
@@ -644,30 +701,114 @@ __global__ void scale_kernel(int64_t m, int64_t n, T beta, T *C, int64_t ldc, in
   }
 }
 
-template <typename T, int BT, bool AKC, bool BKC, bool VEC>
-void launch_one(const GemmArgs<T> &a, hipStream_t s) {
-  gemm_kernel<T, BT, AKC, BKC, VEC><<<a.ntiles, kThreads, 0, s>>>(a);
+// Split-k fixup: C = alpha * (sum over splits, in split order) + beta * C on
+// the in-range, in-triangle elements of the tail tiles. One block per tile
+// column, one thread per tile row.
+template <typename T, int BT>
+__global__ __launch_bounds__(BT) void split_fixup(GemmArgs<T> p) {
+  const int tile = (int)blockIdx.x / BT, cl = (int)blockIdx.x % BT, rl = (int)threadIdx.x;
+  int tm, tn;
+  logical_tile(p.nregular + tile, p.tiles_m, p.tiles_n, p.uplo, tm, tn);
+  const int64_t row = (int64_t)tm * BT + rl, col = (int64_t)tn * BT + cl;
+  if (row >= p.m || col >= p.n) return;
+  if (p.uplo == WGB_LOWER && row < col) return;
+  if (p.uplo == WGB_UPPER && row > col) return;
+  const T *src = p.ws + (int64_t)tile * p.splits * BT * BT + (int64_t)cl * BT + rl;
+  T sum = src[0];
+  for (int s = 1; s < p.splits; ++s) sum += src[(int64_t)s * BT * BT];
+  T *cp = p.C + row + col * p.ldc;
+  T v = p.alpha * sum;
+  if (p.beta != (T)0) v = fma(p.beta, *cp, v);
+  *cp = v;
 }
 
+template <typename T>
+using KernelFn = void (*)(GemmArgs<T>);
+
 template <typename T, int BT>
-void launch_tier(const GemmArgs<T> &a, bool akc, bool bkc, bool vec, hipStream_t s) {
+KernelFn<T> pick_kernel(bool akc, bool bkc, bool vec) {
   if (vec) {
-    if (akc) {
-      if (bkc) launch_one<T, BT, true, true, true>(a, s);
-      else launch_one<T, BT, true, false, true>(a, s);
-    } else {
-      if (bkc) launch_one<T, BT, false, true, true>(a, s);
-      else launch_one<T, BT, false, false, true>(a, s);
-    }
-  } else {
-    if (akc) {
-      if (bkc) launch_one<T, BT, true, true, false>(a, s);
-      else launch_one<T, BT, true, false, false>(a, s);
-    } else {
-      if (bkc) launch_one<T, BT, false, true, false>(a, s);
-      else launch_one<T, BT, false, false, false>(a, s);
+    if (akc) return bkc ? gemm_kernel<T, BT, true, true, true> : gemm_kernel<T, BT, true, false, true>;
+    return bkc ? gemm_kernel<T, BT, false, true, true> : gemm_kernel<T, BT, false, false, true>;
+  }
+  if (akc) return bkc ? gemm_kernel<T, BT, true, true, false> : gemm_kernel<T, BT, true, false, false>;
+  return bkc ? gemm_kernel<T, BT, false, true, false> : gemm_kernel<T, BT, false, false, false>;
+}
+
+// Resident blocks per CU of one kernel instantiation (LDS and registers),
+// cached per (tier, operand layout) slot; 0 = not yet queried.
+template <typename T, int BT>
+int blocks_per_cu(KernelFn<T> fn, int slot) {
+  static int cache[8] = {0};
+  if (cache[slot] == 0) {
+    int nb = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, reinterpret_cast<const void *>(fn),
+                                                     kThreads, 0) != hipSuccess || nb < 1)
+      nb = 1;
+    cache[slot] = nb;
+  }
+  return cache[slot];
+}
+
+// Grows the context's split-k workspace to at least `bytes`. The stream is
+// drained first: an earlier launch may still read the old buffer.
+int ensure_workspace(wgb_ctx *ctx, size_t bytes) {
+  if (ctx->gemm_ws_bytes >= bytes) return WGB_OK;
+  const size_t round = (size_t)16 << 20;
+  bytes = (bytes + round - 1) / round * round;
+  WGB_CHECK_HIP(hipStreamSynchronize(ctx->stream));
+  if (ctx->gemm_ws) WGB_CHECK_HIP(hipFree(ctx->gemm_ws));
+  ctx->gemm_ws = nullptr;
+  ctx->gemm_ws_bytes = 0;
+  if (hipMalloc(&ctx->gemm_ws, bytes) != hipSuccess) {
+    (void)hipGetLastError();
+    ctx->gemm_ws = nullptr;
+    return wgb::fail(WGB_ERR_ALLOC, "hipMalloc of the GEMM split-k workspace failed");
+  }
+  ctx->gemm_ws_bytes = bytes;
+  return WGB_OK;
+}
+
+// Launches one GEMM on a BT tier. Tiles fill `slots` = CUs x resident blocks
+// per round; when the last round is at most half full, its tiles are split
+// along k into up to 16 units (at least 4 k-tiles each) so the last round is
+// as full as the rest, and split_fixup combines the partials in split order.
+template <typename T, int BT>
+int launch_tier(wgb_ctx *ctx, GemmArgs<T> &a, bool akc, bool bkc, bool vec) {
+  constexpr int BK = 128 / (int)sizeof(T);
+  KernelFn<T> fn = pick_kernel<T, BT>(akc, bkc, vec);
+  const int64_t cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
+  const int64_t slots = cus * blocks_per_cu<T, BT>(fn, (akc ? 4 : 0) + (bkc ? 2 : 0) + (vec ? 1 : 0));
+  const int64_t nkt = (a.k + BK - 1) / BK;
+  a.nregular = a.ntiles;
+  a.splits = 1;
+  a.kt_split = (int)nkt;
+  a.ws = nullptr;
+  const int64_t rem = a.ntiles % slots;
+  if (rem > 0 && 2 * rem <= slots) {
+    int64_t S = slots / rem;
+    if (S > 16) S = 16;
+    if (S > nkt / 4) S = nkt / 4;
+    if (S >= 2) {
+      const int64_t kts = (nkt + S - 1) / S;
+      S = (nkt + kts - 1) / kts;  // every split non-empty
+      int st = ensure_workspace(ctx, (size_t)(rem * S) * BT * BT * sizeof(T));
+      if (st) return st;
+      a.nregular = (int)(a.ntiles - rem);
+      a.splits = (int)S;
+      a.kt_split = (int)kts;
+      a.ws = static_cast<T *>(ctx->gemm_ws);
     }
   }
+  const int64_t grid = a.nregular + (int64_t)(a.ntiles - a.nregular) * a.splits;
+  void *args[] = {&a};
+  WGB_CHECK_HIP(hipLaunchKernel(reinterpret_cast<const void *>(fn), dim3((unsigned)grid),
+                                dim3(kThreads), args, 0, ctx->stream));
+  if (a.splits > 1) {
+    split_fixup<T, BT><<<(unsigned)((a.ntiles - a.nregular) * BT), BT, 0, ctx->stream>>>(a);
+    WGB_CHECK_LAUNCH("split_fixup");
+  }
+  return WGB_OK;
 }
 
 bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
@@ -751,10 +892,9 @@ int gemm_run(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64_t 
   a.tiles_m = (int)tmn;
   a.tiles_n = (int)tnn;
   a.ntiles = (int)ntiles;
-  if (bt == 128)
-    launch_tier<T, 128>(a, akc, bkc, vec, ctx->stream);
-  else
-    launch_tier<T, 64>(a, akc, bkc, vec, ctx->stream);
+  int st = bt == 128 ? launch_tier<T, 128>(ctx, a, akc, bkc, vec)
+                     : launch_tier<T, 64>(ctx, a, akc, bkc, vec);
+  if (st) return st;
   WGB_CHECK_LAUNCH("gemm_kernel");
   wgb::timing_end(ctx);
   return WGB_OK;

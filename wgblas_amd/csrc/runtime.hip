@@ -108,6 +108,7 @@ extern "C" int wgb_destroy(wgb_ctx *ctx) {
   (void)hipSetDevice(ctx->device);
   if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
   if (ctx->scratch) (void)hipFree(ctx->scratch);
+  if (ctx->gemm_ws) (void)hipFree(ctx->gemm_ws);
   if (ctx->host_result) (void)hipHostFree(ctx->host_result);
   if (ctx->ev_start) (void)hipEventDestroy(ctx->ev_start);
   if (ctx->ev_stop) (void)hipEventDestroy(ctx->ev_stop);

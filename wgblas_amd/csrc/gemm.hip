@@ -106,6 +106,11 @@ struct GemmArgs {
 };
 
 constexpr int kThreads = 256;
+// Instruction classes of __builtin_amdgcn_sched_group_barrier.
+constexpr int kSchedMfma = 0x008;
+constexpr int kSchedVmemRead = 0x020;
+constexpr int kSchedDsRead = 0x100;
+constexpr int kSchedDsWrite = 0x200;
 constexpr int kGroupM = 8;
 constexpr int kXcds = 8;
 
@@ -470,8 +475,12 @@ struct KernelPolicy {
   static constexpr bool kPerStep = sizeof(T) == 8;
 };
 
+// fp64 and the fp32 kernels with one k-contiguous and one mn-contiguous
+// operand are held to 256 registers (two waves per SIMD) explicitly; the
+// other fp32 kernels fit on their own with accumulators in AGPRs, which
+// measured faster for them.
 template <typename T, int BT, bool AKC, bool BKC, bool VEC>
-__global__ __launch_bounds__(kThreads, sizeof(T) == 8 ? 2 : 1) void gemm_kernel(GemmArgs<T> p) {
+__global__ __launch_bounds__(kThreads, (sizeof(T) == 8 || AKC != BKC) ? 2 : 1) void gemm_kernel(GemmArgs<T> p) {
   typedef typename Ty<T>::acc Acc;
   typedef typename Ty<T>::v16 V;
   constexpr int VW = Ty<T>::VW;
@@ -593,7 +602,56 @@ __global__ __launch_bounds__(kThreads, sizeof(T) == 8 ? 2 : 1) void gemm_kernel(
     T x[4][MB], y[4][MB], xb[4][MB], yb[4][MB];
     fetch_operands<T, BT, AKC, MB>(smem, wm, 0, lane, x);
     fetch_operands<T, BT, BKC, MB>(smem + SA::ELEMS, wn, 0, lane, xb);
-    for (int kt = 0; kt < nkt; ++kt) {
+    // Steady state (both next tiles exist and are whole): the same steps
+    // without branches, with the chunk-1 reads, the LDS stores and the
+    // global loads spread among the chunk-0 MFMAs (sched_group_barrier:
+    // 1 MFMA per read, 3 per store, 2 per global load) so that no wave sits
+    // in a long non-MFMA stretch while the other wave on its SIMD is in one
+    // too. Measured +5-8% over leaving the order to the scheduler.
+    int kt = 0;
+    const int nsteady = (nkt < nkt_full ? nkt : nkt_full) - 2;
+    for (; kt < nsteady; ++kt) {
+      const T *As = smem + (kt & 1) * STAGE;
+      T *next = smem + ((kt + 1) & 1) * STAGE;
+      fetch_operands<T, BT, AKC, MB>(As, wm, 16, lane, y);
+      fetch_operands<T, BT, BKC, MB>(As + SA::ELEMS, wn, 16, lane, yb);
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+#pragma unroll
+          for (int j = 0; j < MB; ++j) acc[i][j] = Ty<T>::mfma(x[s][i], xb[s][j], acc[i][j]);
+      sa.store(next, ra);
+      sb.store(next + SA::ELEMS, rb);
+      sa.template load<false>(ra, kt + 2);
+      sb.template load<false>(rb, kt + 2);
+#pragma unroll
+      for (int g = 0; g < 2 * MB; ++g) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+      }
+#pragma unroll
+      for (int g = 0; g < SA::LOADS + SB::LOADS; ++g) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 3, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedDsWrite, 1, 0);
+      }
+#pragma unroll
+      for (int g = 0; g < SA::LOADS + SB::LOADS; ++g) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedVmemRead, 1, 0);
+      }
+      __syncthreads();
+      fetch_operands<T, BT, AKC, MB>(next, wm, 0, lane, x);
+      fetch_operands<T, BT, BKC, MB>(next + SA::ELEMS, wn, 0, lane, xb);
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+#pragma unroll
+          for (int j = 0; j < MB; ++j) acc[i][j] = Ty<T>::mfma(y[s][i], yb[s][j], acc[i][j]);
+    }
+    // The last two k-tiles (and every k-tile of edge tiles): guarded loads.
+    for (; kt < nkt; ++kt) {
       const bool more = kt + 1 < nkt;
       const T *As = smem + (kt & 1) * STAGE;
       fetch_operands<T, BT, AKC, MB>(As, wm, 16, lane, y);

@@ -105,8 +105,10 @@ def check_gemm_props(C, C0, opA, opB, alpha, beta, k, eps=EPS32, kterm=1, cterm=
     rng = np.random.default_rng(seed)
     A64 = np.asarray(opA, np.float64)
     B64 = np.asarray(opB, np.float64)
-    rows = sorted(set([0, 1, m - 1] + list(rows) + [int(r) for r in rng.integers(0, m, 8)]))
-    cols = sorted(set([0, 1, n - 1] + list(cols) + [int(c) for c in rng.integers(0, n, 8)]))
+    rows = sorted(r for r in set([0, 1, m - 1] + list(rows) + [int(r) for r in rng.integers(0, m, 8)])
+                  if r < m)
+    cols = sorted(c for c in set([0, 1, n - 1] + list(cols) + [int(c) for c in rng.integers(0, n, 8)])
+                  if c < n)
     worst = 0.0
     for sel_r, sel_c in ((rows, slice(None)), (slice(None), cols)):
         exact = alpha * (A64[sel_r, :] @ B64[:, sel_c]) + beta * np.asarray(C0[sel_r, sel_c], np.float64)
@@ -132,3 +134,44 @@ def check_gemm_props(C, C0, opA, opB, alpha, beta, k, eps=EPS32, kterm=1, cterm=
             tol += 1e-12 * (np.abs(lhs) + np.abs(rhs))
             assert np.all(np.abs(lhs - rhs) <= tol), "Freivalds projection exceeds the summed bound"
     return worst
+
+
+def run_gemm_props_case(ctx, kind, uplo, ta, tb, m, n, k, alpha, beta, ldc_pad=3, seed=11,
+                        lda_pad=0, ldb_pad=0):
+    """Runs sgemm / sgemmtr / ssyrk / dgemm through the C ABI on device-seeded
+    inputs and checks the result with check_gemm_props (sampled rows and
+    columns plus a Freivalds projection) and bit checks of what must stay."""
+    dt = np.float64 if kind == "dgemm" else np.float32
+    a_rows, a_cols = (k, m) if ta else (m, k)
+    if kind == "ssyrk":
+        tb = 1 - ta
+        b_rows, b_cols = a_rows, a_cols
+    else:
+        b_rows, b_cols = (n, k) if tb else (k, n)
+    lda, ldb, ldc = a_rows + lda_pad, b_rows + ldb_pad, m + ldc_pad
+    sa, sb, sc = lda * a_cols, ldb * b_cols, ldc * n
+    buf = ctx.empty(sa + sb + sc, dt)
+    ctx.fill_uniform(buf, -1.0, 1.0, seed)
+    host = buf.to_host()
+    A, C0 = host[:sa], host[sa + sb:]
+    B = A if kind == "ssyrk" else host[sa:sa + sb]
+    pa, pb, pc = buf.offset(0), buf.offset(sa), buf.offset(sa + sb)
+    if kind == "dgemm":
+        ctx.dgemm(ta, tb, m, n, k, alpha, pa, lda, pb, ldb, beta, pc, ldc)
+    elif kind == "ssyrk":
+        ctx.ssyrk(uplo, ta, n, k, alpha, pa, lda, beta, pc, ldc)
+    elif uplo:
+        ctx.sgemmtr(uplo, ta, tb, m, n, k, alpha, pa, lda, pb, ldb, beta, pc, ldc)
+    else:
+        ctx.sgemm(ta, tb, m, n, k, alpha, pa, lda, pb, ldb, beta, pc, ldc)
+    C = buf.to_host()[sa + sb:]
+    buf.free()
+    keep = untouched_mask(m, n, ldc, n, uplo)
+    assert bits_equal(C[keep], C0[keep]), "C changed outside its m x n part / triangle"
+    Am = op(cm_view(A, a_rows, a_cols, lda), ta)
+    Bm = op(cm_view(B, b_rows, b_cols, ldb), tb)
+    edges = (0, 63, 64, 127, 128, 255, 256, m - 1, n - 1)
+    kw = dict(eps=EPS_DD, kterm=2, cterm=3.0) if kind == "dgemm" else {}
+    check_gemm_props(cm_view(C, m, n, ldc), cm_view(C0, m, n, ldc), Am, Bm, alpha, beta, k,
+                     rows=tuple(r for r in edges if r < m), cols=tuple(c for c in edges if c < n),
+                     seed=seed, uplo=uplo, **kw)

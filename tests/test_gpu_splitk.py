@@ -10,48 +10,11 @@ by sampled rows and columns against a float64 product under the reference's
 forward-error bound plus a Freivalds projection over all of C, and whatever
 the call must not touch (ld padding, the other triangle) is bit-checked.
 """
-import numpy as np
 import pytest
 
-from tests.helpers import EPS_DD, bits_equal, check_gemm_props, cm_view, op, untouched_mask
+from tests.helpers import run_gemm_props_case as run_case
 
 pytestmark = pytest.mark.gpu
-
-
-def run_case(ctx, kind, uplo, ta, tb, m, n, k, alpha, beta, ldc_pad=3, seed=11):
-    dt = np.float64 if kind == "dgemm" else np.float32
-    a_rows, a_cols = (k, m) if ta else (m, k)
-    if kind == "ssyrk":
-        tb = 1 - ta
-        b_rows, b_cols = a_rows, a_cols
-    else:
-        b_rows, b_cols = (n, k) if tb else (k, n)
-    lda, ldb, ldc = a_rows, b_rows, m + ldc_pad
-    sa, sb, sc = lda * a_cols, ldb * b_cols, ldc * n
-    buf = ctx.empty(sa + sb + sc, dt)
-    ctx.fill_uniform(buf, -1.0, 1.0, seed)
-    host = buf.to_host()
-    A, C0 = host[:sa], host[sa + sb:]
-    B = A if kind == "ssyrk" else host[sa:sa + sb]
-    pa, pb, pc = buf.offset(0), buf.offset(sa), buf.offset(sa + sb)
-    if kind == "dgemm":
-        ctx.dgemm(ta, tb, m, n, k, alpha, pa, lda, pb, ldb, beta, pc, ldc)
-    elif kind == "ssyrk":
-        ctx.ssyrk(uplo, ta, n, k, alpha, pa, lda, beta, pc, ldc)
-    elif uplo:
-        ctx.sgemmtr(uplo, ta, tb, m, n, k, alpha, pa, lda, pb, ldb, beta, pc, ldc)
-    else:
-        ctx.sgemm(ta, tb, m, n, k, alpha, pa, lda, pb, ldb, beta, pc, ldc)
-    C = buf.to_host()[sa + sb:]
-    buf.free()
-    keep = untouched_mask(m, n, ldc, n, uplo)
-    assert bits_equal(C[keep], C0[keep]), "C changed outside its m x n part / triangle"
-    Am = op(cm_view(A, a_rows, a_cols, lda), ta)
-    Bm = op(cm_view(B, b_rows, b_cols, ldb), tb)
-    edges = (0, 127, 128, 255, 256, min(m, n) - 1)
-    kw = dict(eps=EPS_DD, kterm=2, cterm=3.0) if kind == "dgemm" else {}
-    check_gemm_props(cm_view(C, m, n, ldc), cm_view(C0, m, n, ldc), Am, Bm, alpha, beta, k,
-                     rows=edges, cols=edges, seed=seed, uplo=uplo, **kw)
 
 
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])

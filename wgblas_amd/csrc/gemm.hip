@@ -48,6 +48,7 @@
 #include "common.h"
 
 #include <cmath>
+#include <type_traits>
 
 namespace {
 
@@ -97,6 +98,7 @@ struct GemmArgs {
   int tiles_m, tiles_n, ntiles;
   int uplo;   // 0 = full C, WGB_LOWER, WGB_UPPER
   int c_vec;  // ldc % VW == 0 and C 16-byte aligned: whole-vector C access
+  int edge_ok;  // edge tiles may take the EDGE loads (mn-contiguous ld >= VW - 1)
   // Split-k tail: logical tiles [nregular, ntiles) are computed as `splits`
   // k-ranges of kt_split k-tiles each; unit u = (tile - nregular) * splits +
   // split writes its raw BT x BT partial (column-major, ld BT) to ws + u BT^2
@@ -201,6 +203,17 @@ struct Stager {
   int64_t row_first;  // KC: global row of r = 0;   !KC: first global row of the vector
   int k_first;        // KC: k offset of the vector; !KC: k-row of r = 0
   int64_t rows_total, K;
+  // Edge tiles (set by init_edge), on whole k-tiles that are not the last
+  // one: a lane whose rows are past rows_total (KC: load steps r >= nvr;
+  // MC: vok false) reads at fb instead, row rows_total-1 of the same k. An
+  // MC vector that is only partly in range reads up to VW-1 elements past
+  // the end of its column, i.e. inside the next column (the k-tile is not the
+  // last one). Values read for rows past rows_total only reach C rows /
+  // columns that are never written, so they need not be zero, only be read
+  // from inside the matrix.
+  const T *fb;
+  int nvr;
+  bool vok;
 
   __device__ void init(const T *P, int64_t ld, int64_t row0, int t, int64_t rows_total_,
                        int64_t K_) {
@@ -233,6 +246,19 @@ struct Stager {
     K -= (int64_t)kt0 * BK;
   }
 
+  // Edge-tile fields (after init and advance): see the members above.
+  __device__ void init_edge() {
+    const int64_t valid = rows_total - row_first;  // rows of this thread in range (may be <= 0)
+    if (KC) {
+      const int64_t n = valid <= 0 ? 0 : (valid + 31) / 32;
+      nvr = (int)(n < LOADS ? n : LOADS);
+      fb = base + (rows_total - 1 - row_first) * (r_step / 32);
+    } else {
+      vok = valid > 0;
+      fb = base + (rows_total - 1 - row_first);
+    }
+  }
+
   __device__ static V load_n(const T *p, int64_t nvalid) {
     V v;
 #pragma unroll
@@ -249,14 +275,20 @@ struct Stager {
     return *reinterpret_cast<const VU *>(p);
   }
 
-  template <bool GUARD>
+  // GUARD: k-tile past the end of K (element guards on rows and k);
+  // otherwise a whole k-tile, with EDGE for tiles that cross rows_total.
+  template <bool GUARD, bool EDGE = false>
   __device__ void load(V (&regs)[LOADS], int kt) const {
     const T *p = base + (int64_t)kt * k_step;
 #pragma unroll
     for (int r = 0; r < LOADS; ++r) {
       const T *q = p + r * r_step;
-      if (!GUARD) {
+      if (!GUARD && !EDGE) {
         regs[r] = load_full(q);
+      } else if (!GUARD && KC) {
+        regs[r] = load_full(r < nvr ? q : fb + (int64_t)kt * k_step);
+      } else if (!GUARD) {
+        regs[r] = load_full(vok ? q : fb + (int64_t)kt * k_step + r * r_step);
       } else if (KC) {
         int64_t row = row_first + 32 * r;
         int64_t nv = K - ((int64_t)kt * BK + k_first);
@@ -521,7 +553,7 @@ __global__ __launch_bounds__(kThreads, (sizeof(T) == 8 || AKC != BKC) ? 2 : 1) v
   sa.advance(kt0);
   sb.advance(kt0);
   const bool interior = (m0 + BT <= p.m) && (n0 + BT <= p.n);
-  const int nkt_full = interior ? (int)(p.k / BK) - kt0 : 0;
+  const int nkt_full = (int)(p.k / BK) - kt0;  // whole k-tiles from kt0
 
   Acc acc[MB][MB];
 #pragma unroll
@@ -529,166 +561,192 @@ __global__ __launch_bounds__(kThreads, (sizeof(T) == 8 || AKC != BKC) ? 2 : 1) v
 #pragma unroll
     for (int j = 0; j < MB; ++j) acc[i][j] = Acc(0);
 
-  V ra[SA::LOADS], rb[SB::LOADS];
-  if (0 < nkt_full) {
-    sa.template load<false>(ra, 0);
-    sb.template load<false>(rb, 0);
-  } else {
-    sa.template load<true>(ra, 0);
-    sb.template load<true>(rb, 0);
-  }
-  sa.store(smem, ra);
-  sb.store(smem + SA::ELEMS, rb);
+  // Main loop, instantiated once for interior tiles and once for edge tiles
+  // (rows past m or columns past n: whole k-tiles take the EDGE loads).
+  auto mainloop = [&](auto edge_tag) {
+    constexpr bool EDGE = decltype(edge_tag)::value;
+    if constexpr (EDGE) {
+      sa.init_edge();
+      sb.init_edge();
+    }
+    // Whole k-tiles taking unguarded (or EDGE) loads; an edge tile's last
+    // whole k-tile is guarded too (EDGE reads may run past a column end).
+    const int nkt_whole = EDGE ? (p.edge_ok ? nkt_full - 1 : 0) : nkt_full;
+    V ra[SA::LOADS], rb[SB::LOADS];
+    if (0 < nkt_whole) {
+      sa.template load<false, EDGE>(ra, 0);
+      sb.template load<false, EDGE>(rb, 0);
+    } else {
+      sa.template load<true>(ra, 0);
+      sb.template load<true>(rb, 0);
+    }
+    sa.store(smem, ra);
+    sb.store(smem + SA::ELEMS, rb);
 
-  if constexpr (KernelPolicy<T>::kPerStep) {
-    __syncthreads();
-    for (int kt = 0; kt < nkt; ++kt) {
-      const bool more = kt + 1 < nkt;
-      if (more) {
-        if (kt + 1 < nkt_full) {
-          sa.template load<false>(ra, kt + 1);
-          sb.template load<false>(rb, kt + 1);
-        } else {
-          sa.template load<true>(ra, kt + 1);
-          sb.template load<true>(rb, kt + 1);
-        }
-      }
-      const T *As = smem + (kt & 1) * STAGE;
-      const T *Bs = As + SA::ELEMS;
-#pragma unroll
-      for (int kc = 0; kc < BK; kc += 16) {
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          T a[MB], b[MB];
-          fetch_step<T, BT, AKC, MB>(As, wm, kc, s, lane, a);
-          fetch_step<T, BT, BKC, MB>(Bs, wn, kc, s, lane, b);
-#pragma unroll
-          for (int i = 0; i < MB; ++i)
-#pragma unroll
-            for (int j = 0; j < MB; ++j) acc[i][j] = Ty<T>::mfma(a[i], b[j], acc[i][j]);
-        }
-      }
-      if (more) {
-        T *next = smem + ((kt + 1) & 1) * STAGE;
-        sa.store(next, ra);
-        sb.store(next + SA::ELEMS, rb);
-      }
+    if constexpr (KernelPolicy<T>::kPerStep) {
       __syncthreads();
-    }
-  } else {
-    // Two 16-k chunks per k-tile, software pipelined so that LDS reads and
-    // global loads are in flight under MFMAs. On entry to iteration kt:
-    // X = chunk 0 of tile kt (registers), R = tile kt+1 (registers, loaded
-    // one iteration earlier), tile kt in LDS buffer kt&1.
-    //   1. LDS reads of chunk 1 of tile kt into Y
-    //   2. MFMAs on X
-    //   3. R -> LDS buffer (kt+1)&1; global loads of tile kt+2 into R
-    //   4. barrier: every wave has finished reading buffer kt&1 (chunk 0
-    //      at the end of kt-1, chunk 1 in step 1, both waited for) and has
-    //      written tile kt+1, so buffer kt&1 may be refilled in kt+1
-    //   5. LDS reads of chunk 0 of tile kt+1 into X
-    //   6. MFMAs on Y
-    static_assert(BK == 32, "the pipelined fp32 loop assumes two 16-k chunks per k-tile");
-    if (1 < nkt) {
-      if (1 < nkt_full) {
-        sa.template load<false>(ra, 1);
-        sb.template load<false>(rb, 1);
-      } else {
-        sa.template load<true>(ra, 1);
-        sb.template load<true>(rb, 1);
-      }
-    }
-    __syncthreads();
-    T x[4][MB], y[4][MB], xb[4][MB], yb[4][MB];
-    fetch_operands<T, BT, AKC, MB>(smem, wm, 0, lane, x);
-    fetch_operands<T, BT, BKC, MB>(smem + SA::ELEMS, wn, 0, lane, xb);
-    // Steady state (both next tiles exist and are whole): the same steps
-    // without branches, with the chunk-1 reads, the LDS stores and the
-    // global loads spread among the chunk-0 MFMAs (sched_group_barrier:
-    // 1 MFMA per read, 3 per store, 2 per global load) so that no wave sits
-    // in a long non-MFMA stretch while the other wave on its SIMD is in one
-    // too. Measured +5-8% over leaving the order to the scheduler.
-    int kt = 0;
-    const int nsteady = (nkt < nkt_full ? nkt : nkt_full) - 2;
-    for (; kt < nsteady; ++kt) {
-      const T *As = smem + (kt & 1) * STAGE;
-      T *next = smem + ((kt + 1) & 1) * STAGE;
-      fetch_operands<T, BT, AKC, MB>(As, wm, 16, lane, y);
-      fetch_operands<T, BT, BKC, MB>(As + SA::ELEMS, wn, 16, lane, yb);
-#pragma unroll
-      for (int s = 0; s < 4; ++s)
-#pragma unroll
-        for (int i = 0; i < MB; ++i)
-#pragma unroll
-          for (int j = 0; j < MB; ++j) acc[i][j] = Ty<T>::mfma(x[s][i], xb[s][j], acc[i][j]);
-      sa.store(next, ra);
-      sb.store(next + SA::ELEMS, rb);
-      sa.template load<false>(ra, kt + 2);
-      sb.template load<false>(rb, kt + 2);
-#pragma unroll
-      for (int g = 0; g < 2 * MB; ++g) {
-        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
-      }
-#pragma unroll
-      for (int g = 0; g < SA::LOADS + SB::LOADS; ++g) {
-        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 3, 0);
-        __builtin_amdgcn_sched_group_barrier(kSchedDsWrite, 1, 0);
-      }
-#pragma unroll
-      for (int g = 0; g < SA::LOADS + SB::LOADS; ++g) {
-        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2, 0);
-        __builtin_amdgcn_sched_group_barrier(kSchedVmemRead, 1, 0);
-      }
-      __syncthreads();
-      fetch_operands<T, BT, AKC, MB>(next, wm, 0, lane, x);
-      fetch_operands<T, BT, BKC, MB>(next + SA::ELEMS, wn, 0, lane, xb);
-#pragma unroll
-      for (int s = 0; s < 4; ++s)
-#pragma unroll
-        for (int i = 0; i < MB; ++i)
-#pragma unroll
-          for (int j = 0; j < MB; ++j) acc[i][j] = Ty<T>::mfma(y[s][i], yb[s][j], acc[i][j]);
-    }
-    // The last two k-tiles (and every k-tile of edge tiles): guarded loads.
-    for (; kt < nkt; ++kt) {
-      const bool more = kt + 1 < nkt;
-      const T *As = smem + (kt & 1) * STAGE;
-      fetch_operands<T, BT, AKC, MB>(As, wm, 16, lane, y);
-      fetch_operands<T, BT, BKC, MB>(As + SA::ELEMS, wn, 16, lane, yb);
-#pragma unroll
-      for (int s = 0; s < 4; ++s)
-#pragma unroll
-        for (int i = 0; i < MB; ++i)
-#pragma unroll
-          for (int j = 0; j < MB; ++j) acc[i][j] = Ty<T>::mfma(x[s][i], xb[s][j], acc[i][j]);
-      T *next = smem + ((kt + 1) & 1) * STAGE;
-      if (more) {
-        sa.store(next, ra);
-        sb.store(next + SA::ELEMS, rb);
-        if (kt + 2 < nkt) {
-          if (kt + 2 < nkt_full) {
-            sa.template load<false>(ra, kt + 2);
-            sb.template load<false>(rb, kt + 2);
+      for (int kt = 0; kt < nkt; ++kt) {
+        const bool more = kt + 1 < nkt;
+        if (more) {
+          if (kt + 1 < nkt_whole) {
+            sa.template load<false, EDGE>(ra, kt + 1);
+            sb.template load<false, EDGE>(rb, kt + 1);
           } else {
-            sa.template load<true>(ra, kt + 2);
-            sb.template load<true>(rb, kt + 2);
+            sa.template load<true>(ra, kt + 1);
+            sb.template load<true>(rb, kt + 1);
           }
         }
+        const T *As = smem + (kt & 1) * STAGE;
+        const T *Bs = As + SA::ELEMS;
+  #pragma unroll
+        for (int kc = 0; kc < BK; kc += 16) {
+  #pragma unroll
+          for (int s = 0; s < 4; ++s) {
+            T a[MB], b[MB];
+            fetch_step<T, BT, AKC, MB>(As, wm, kc, s, lane, a);
+            fetch_step<T, BT, BKC, MB>(Bs, wn, kc, s, lane, b);
+  #pragma unroll
+            for (int i = 0; i < MB; ++i)
+  #pragma unroll
+              for (int j = 0; j < MB; ++j) acc[i][j] = Ty<T>::mfma(a[i], b[j], acc[i][j]);
+          }
+        }
+        if (more) {
+          T *next = smem + ((kt + 1) & 1) * STAGE;
+          sa.store(next, ra);
+          sb.store(next + SA::ELEMS, rb);
+        }
+        __syncthreads();
+      }
+    } else {
+      // Two 16-k chunks per k-tile, software pipelined so that LDS reads and
+      // global loads are in flight under MFMAs. On entry to iteration kt:
+      // X = chunk 0 of tile kt (registers), R = tile kt+1 (registers, loaded
+      // one iteration earlier), tile kt in LDS buffer kt&1.
+      //   1. LDS reads of chunk 1 of tile kt into Y
+      //   2. MFMAs on X
+      //   3. R -> LDS buffer (kt+1)&1; global loads of tile kt+2 into R
+      //   4. barrier: every wave has finished reading buffer kt&1 (chunk 0
+      //      at the end of kt-1, chunk 1 in step 1, both waited for) and has
+      //      written tile kt+1, so buffer kt&1 may be refilled in kt+1
+      //   5. LDS reads of chunk 0 of tile kt+1 into X
+      //   6. MFMAs on Y
+      static_assert(BK == 32, "the pipelined fp32 loop assumes two 16-k chunks per k-tile");
+      if (1 < nkt) {
+        if (1 < nkt_whole) {
+          sa.template load<false, EDGE>(ra, 1);
+          sb.template load<false, EDGE>(rb, 1);
+        } else {
+          sa.template load<true>(ra, 1);
+          sb.template load<true>(rb, 1);
+        }
       }
       __syncthreads();
-      if (more) {
+      T x[4][MB], y[4][MB], xb[4][MB], yb[4][MB];
+      fetch_operands<T, BT, AKC, MB>(smem, wm, 0, lane, x);
+      fetch_operands<T, BT, BKC, MB>(smem + SA::ELEMS, wn, 0, lane, xb);
+      // Steady state (both next tiles exist and are whole): the same steps
+      // without branches, with the chunk-1 reads, the LDS stores and the
+      // global loads spread among the chunk-0 MFMAs (sched_group_barrier:
+      // 1 MFMA per read, 3 per store, 2 per global load) so that no wave sits
+      // in a long non-MFMA stretch while the other wave on its SIMD is in one
+      // too. Measured +5-8% over leaving the order to the scheduler.
+      int kt = 0;
+      const int nsteady = (nkt < nkt_whole ? nkt : nkt_whole) - 2;
+      for (; kt < nsteady; ++kt) {
+        const T *As = smem + (kt & 1) * STAGE;
+        T *next = smem + ((kt + 1) & 1) * STAGE;
+        fetch_operands<T, BT, AKC, MB>(As, wm, 16, lane, y);
+        fetch_operands<T, BT, BKC, MB>(As + SA::ELEMS, wn, 16, lane, yb);
+  #pragma unroll
+        for (int s = 0; s < 4; ++s)
+  #pragma unroll
+          for (int i = 0; i < MB; ++i)
+  #pragma unroll
+            for (int j = 0; j < MB; ++j) acc[i][j] = Ty<T>::mfma(x[s][i], xb[s][j], acc[i][j]);
+        // Stores then loads, operand by operand; with A mn-contiguous and B
+        // k-contiguous (NN), B's eight-rows-per-instruction loads go first
+        // (measured +3-5% for NN, neutral to slightly negative elsewhere).
+        if constexpr (BKC && !AKC) {
+          sb.store(next + SA::ELEMS, rb);
+          sa.store(next, ra);
+          sb.template load<false, EDGE>(rb, kt + 2);
+          sa.template load<false, EDGE>(ra, kt + 2);
+        } else {
+          sa.store(next, ra);
+          sb.store(next + SA::ELEMS, rb);
+          sa.template load<false, EDGE>(ra, kt + 2);
+          sb.template load<false, EDGE>(rb, kt + 2);
+        }
+  #pragma unroll
+        for (int g = 0; g < 2 * MB; ++g) {
+          __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+        }
+  #pragma unroll
+        for (int g = 0; g < SA::LOADS + SB::LOADS; ++g) {
+          __builtin_amdgcn_sched_group_barrier(kSchedMfma, 3, 0);
+          __builtin_amdgcn_sched_group_barrier(kSchedDsWrite, 1, 0);
+        }
+  #pragma unroll
+        for (int g = 0; g < SA::LOADS + SB::LOADS; ++g) {
+          __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2, 0);
+          __builtin_amdgcn_sched_group_barrier(kSchedVmemRead, 1, 0);
+        }
+        __syncthreads();
         fetch_operands<T, BT, AKC, MB>(next, wm, 0, lane, x);
         fetch_operands<T, BT, BKC, MB>(next + SA::ELEMS, wn, 0, lane, xb);
+  #pragma unroll
+        for (int s = 0; s < 4; ++s)
+  #pragma unroll
+          for (int i = 0; i < MB; ++i)
+  #pragma unroll
+            for (int j = 0; j < MB; ++j) acc[i][j] = Ty<T>::mfma(y[s][i], yb[s][j], acc[i][j]);
       }
-#pragma unroll
-      for (int s = 0; s < 4; ++s)
-#pragma unroll
-        for (int i = 0; i < MB; ++i)
-#pragma unroll
-          for (int j = 0; j < MB; ++j) acc[i][j] = Ty<T>::mfma(y[s][i], yb[s][j], acc[i][j]);
+      // The last two k-tiles (and every k-tile of edge tiles): guarded loads.
+      for (; kt < nkt; ++kt) {
+        const bool more = kt + 1 < nkt;
+        const T *As = smem + (kt & 1) * STAGE;
+        fetch_operands<T, BT, AKC, MB>(As, wm, 16, lane, y);
+        fetch_operands<T, BT, BKC, MB>(As + SA::ELEMS, wn, 16, lane, yb);
+  #pragma unroll
+        for (int s = 0; s < 4; ++s)
+  #pragma unroll
+          for (int i = 0; i < MB; ++i)
+  #pragma unroll
+            for (int j = 0; j < MB; ++j) acc[i][j] = Ty<T>::mfma(x[s][i], xb[s][j], acc[i][j]);
+        T *next = smem + ((kt + 1) & 1) * STAGE;
+        if (more) {
+          sa.store(next, ra);
+          sb.store(next + SA::ELEMS, rb);
+          if (kt + 2 < nkt) {
+            if (kt + 2 < nkt_whole) {
+              sa.template load<false, EDGE>(ra, kt + 2);
+              sb.template load<false, EDGE>(rb, kt + 2);
+            } else {
+              sa.template load<true>(ra, kt + 2);
+              sb.template load<true>(rb, kt + 2);
+            }
+          }
+        }
+        __syncthreads();
+        if (more) {
+          fetch_operands<T, BT, AKC, MB>(next, wm, 0, lane, x);
+          fetch_operands<T, BT, BKC, MB>(next + SA::ELEMS, wn, 0, lane, xb);
+        }
+  #pragma unroll
+        for (int s = 0; s < 4; ++s)
+  #pragma unroll
+          for (int i = 0; i < MB; ++i)
+  #pragma unroll
+            for (int j = 0; j < MB; ++j) acc[i][j] = Ty<T>::mfma(y[s][i], yb[s][j], acc[i][j]);
+      }
     }
-  }
+  };
+  if (interior)
+    mainloop(std::integral_constant<bool, false>{});
+  else
+    mainloop(std::integral_constant<bool, true>{});
 
   // Epilogue: C = alpha*acc + beta*C on the tile's in-range (and, for
   // sgemmtr/ssyrk, in-triangle) elements.
@@ -929,6 +987,10 @@ int gemm_run(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64_t 
   a.uplo = uplo;
   const int VW = Ty<T>::VW;
   a.c_vec = (ldc % VW == 0) && aligned16(C);
+  // An EDGE load of an mn-contiguous operand reads at most column kk+1's
+  // first VW-2 elements past column kk's end (kk <= K-2): inside the matrix
+  // when ld >= VW - 1.
+  a.edge_ok = !(transA == WGB_NO_TRANS && lda < VW - 1) && !(transB == WGB_TRANS && ldb < VW - 1);
   const bool akc = transA == WGB_TRANS;
   const bool bkc = transB == WGB_NO_TRANS;
   const bool vec = (lda % VW == 0) && (ldb % VW == 0) && aligned16(A) && aligned16(B);

@@ -4,13 +4,12 @@ Edge tiles stream their whole k-tiles with clamped addresses: a lane whose
 rows lie past m (or n) reads a row of the matrix that is in range, and an
 mn-contiguous vector that is only partly in range reads into the next
 column; those values reach only C rows / columns that are never written. The
-last whole k-tile and a partial k-tile take element guards. Leading
-dimensions below the vector width minus one (where a partial vector could
-reach past the matrix) keep the guarded path throughout. These shapes cover
-both tiers, every operand layout, ld padding, the ld = 3 boundary, the
-guarded fallback, triangles and fp64; each result is checked by sampled rows
-and columns under the forward-error bound, a Freivalds projection and bit
-checks of what must stay untouched.
+last whole k-tile and a partial k-tile take element guards (their address
+bounds are modelled on the CPU in test_gemm_edge_model.py). These shapes
+cover both tiers, every operand layout, ld padding, leading dimensions of 1-3
+(vectors that overrun their column), triangles and fp64; each result is
+checked by sampled rows and columns under the forward-error bound, a
+Freivalds projection and bit checks of what must stay untouched.
 """
 import pytest
 
@@ -35,11 +34,11 @@ def test_sgemm_edge_tiles_padded_ld(ctx, ta, tb):
 
 
 @pytest.mark.parametrize("shape,ta,tb", [
-    ((2, 300, 500), 0, 0),    # A mn-contiguous with lda = 2: guarded edge path
-    ((3, 300, 500), 0, 1),    # lda = 3 = vector width - 1: clamped edge path
+    ((2, 300, 500), 0, 0),    # A mn-contiguous with lda = 2
+    ((3, 300, 500), 0, 1),    # lda = 3
     ((300, 3, 500), 0, 1),    # B transposed, ldb = 3
-    ((300, 2, 500), 1, 1),    # B transposed, ldb = 2: guarded
-    ((1, 1, 600), 0, 0),
+    ((300, 2, 500), 1, 1),    # B transposed, ldb = 2
+    ((1, 1, 600), 0, 0),      # every vector overruns its column
 ])
 def test_sgemm_thin_edges(ctx, shape, ta, tb):
     m, n, k = shape

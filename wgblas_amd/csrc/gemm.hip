@@ -98,7 +98,6 @@ struct GemmArgs {
   int tiles_m, tiles_n, ntiles;
   int uplo;   // 0 = full C, WGB_LOWER, WGB_UPPER
   int c_vec;  // ldc % VW == 0 and C 16-byte aligned: whole-vector C access
-  int edge_ok;  // edge tiles may take the EDGE loads (mn-contiguous ld >= VW - 1)
   // Split-k tail: logical tiles [nregular, ntiles) are computed as `splits`
   // k-ranges of kt_split k-tiles each; unit u = (tile - nregular) * splits +
   // split writes its raw BT x BT partial (column-major, ld BT) to ws + u BT^2
@@ -207,8 +206,9 @@ struct Stager {
   // one: a lane whose rows are past rows_total (KC: load steps r >= nvr;
   // MC: vok false) reads at fb instead, row rows_total-1 of the same k. An
   // MC vector that is only partly in range reads up to VW-1 elements past
-  // the end of its column, i.e. inside the next column (the k-tile is not the
-  // last one). Values read for rows past rows_total only reach C rows /
+  // the end of its column; at least BK more columns of the matrix follow
+  // (the last whole k-tile is not read this way), so the read stays inside
+  // it for any ld. Values read for rows past rows_total only reach C rows /
   // columns that are never written, so they need not be zero, only be read
   // from inside the matrix.
   const T *fb;
@@ -571,7 +571,7 @@ __global__ __launch_bounds__(kThreads, (sizeof(T) == 8 || AKC != BKC) ? 2 : 1) v
     }
     // Whole k-tiles taking unguarded (or EDGE) loads; an edge tile's last
     // whole k-tile is guarded too (EDGE reads may run past a column end).
-    const int nkt_whole = EDGE ? (p.edge_ok ? nkt_full - 1 : 0) : nkt_full;
+    const int nkt_whole = EDGE ? nkt_full - 1 : nkt_full;
     V ra[SA::LOADS], rb[SB::LOADS];
     if (0 < nkt_whole) {
       sa.template load<false, EDGE>(ra, 0);
@@ -987,10 +987,6 @@ int gemm_run(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64_t 
   a.uplo = uplo;
   const int VW = Ty<T>::VW;
   a.c_vec = (ldc % VW == 0) && aligned16(C);
-  // An EDGE load of an mn-contiguous operand reads at most column kk+1's
-  // first VW-2 elements past column kk's end (kk <= K-2): inside the matrix
-  // when ld >= VW - 1.
-  a.edge_ok = !(transA == WGB_NO_TRANS && lda < VW - 1) && !(transB == WGB_TRANS && ldb < VW - 1);
   const bool akc = transA == WGB_TRANS;
   const bool bkc = transB == WGB_NO_TRANS;
   const bool vec = (lda % VW == 0) && (ldb % VW == 0) && aligned16(A) && aligned16(B);

@@ -197,6 +197,16 @@ def bench_components(ctx, ev, quick):
     fl = float(n) * (n + 1) * k
     comps["ssyrk_8192x4096_x10"] = {"ms_per_call": ms, "tflops": fl / ms / 1e9,
                                     "frac_fp32_peak": fl / ms / 1e-3 / PEAK_FP32}
+    # the same configuration through sgemmtr (lower, op(A) = A, op(B) = A^T)
+    g = lambda: ctx.sgemmtr(LOWER, NO_TRANS, TRANS, n, n, k, 1.0, dA, n, dA, n, 0.25, dC, n)
+    g()
+    ctx.synchronize()
+    ev.start()
+    for _ in range(10):
+        g()
+    ms = ev.stop_ms() / 10
+    comps["sgemmtr_8192x4096_x10"] = {"ms_per_call": ms, "tflops": fl / ms / 1e9,
+                                      "frac_fp32_peak": fl / ms / 1e-3 / PEAK_FP32}
     dA.free()
     dC.free()
 

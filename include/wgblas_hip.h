@@ -152,6 +152,23 @@ int wgb_dgemm(wgb_ctx *ctx, int transA, int transB, int64_t m, int64_t n,
               const double *B, int64_t ldb, double beta, double *C,
               int64_t ldc);
 
+/* Native-FP64 dgemmtr: dgemm's operation on the uplo triangle of the m-by-n
+ * C only, with dgemm's quick return. Replaces dgemmtr
+ * (src/dgemmtr/dgemmtr.mjs:25-328, which runs dgemm_small with its triangle
+ * mask). */
+int wgb_dgemmtr(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m,
+                int64_t n, int64_t k, double alpha, const double *A,
+                int64_t lda, const double *B, int64_t ldb, double beta,
+                double *C, int64_t ldc);
+
+/* Native-FP64 dsyrk: C <- alpha*op(A)*op(A)^T + beta*C on the uplo triangle
+ * of the n-by-n C, with dgemm's quick return; A is read once for both
+ * operands. Replaces dsyrk (src/dsyrk/dsyrk.mjs:28-305, which copies A into
+ * a second buffer). */
+int wgb_dsyrk(wgb_ctx *ctx, int uplo, int trans, int64_t n, int64_t k,
+              double alpha, const double *A, int64_t lda, double beta,
+              double *C, int64_t ldc);
+
 /* ---- level 1 reductions --------------------------------------------------- */
 /* n <= 0 returns 0 (index -1) without touching the device. incx, incy must be
  * positive. The host-result forms block until the value is on the host; the

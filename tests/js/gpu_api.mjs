@@ -81,6 +81,7 @@ const call = {
   sgemm: (a) => wg.sgemm(device, a.transA, a.transB, a.m, a.n, a.k, a.alpha, a.A, a.lda, a.B, a.ldb, a.beta, a.C, a.ldc, a.layout),
   sgemmtr: (a) => wg.sgemmtr(device, a.uplo, a.transA, a.transB, a.m, a.n, a.k, a.alpha, a.A, a.lda, a.B, a.ldb, a.beta, a.C, a.ldc, a.layout),
   dgemm: (a) => wg.dgemm(device, a.transA, a.transB, a.m, a.n, a.k, a.alpha, a.A, a.lda, a.B, a.ldb, a.beta, a.C, a.ldc, a.layout),
+  dgemmtr: (a) => wg.dgemmtr(device, a.uplo, a.transA, a.transB, a.m, a.n, a.k, a.alpha, a.A, a.lda, a.B, a.ldb, a.beta, a.C, a.ldc, a.layout),
 };
 
 const exactEqual = (got, want, label) => {
@@ -146,15 +147,15 @@ test("init / gpuName / cleanup", async () => {
 });
 
 // ------------------------------------------------------------- fixtures
-for (const routine of ["sgemm", "sgemmtr", "dgemm"]) {
-  const Arr = routine === "dgemm" ? Float64Array : Float32Array;
+for (const routine of ["sgemm", "sgemmtr", "dgemm", "dgemmtr"]) {
+  const Arr = routine.startsWith("d") ? Float64Array : Float32Array;
   for (const file of [`${routine}.edge-cases`, `${routine}.edge-cases-column-major`]) {
     for (const c of fixture(file)) {
       test(`${routine} ${file.includes("column") ? "cm" : "rm"}: ${c.label}`, async () => {
         const a = gemmArgs(c, Arr);
         const want = refGemm(a).out;
         const got = await call[routine](a);
-        if (routine === "dgemm" && (a.alpha === 0 || a.k === 0) && a.beta === 1) {
+        if (routine.startsWith("d") && (a.alpha === 0 || a.k === 0) && a.beta === 1) {
           assert(got.C === a.C, "quick return hands back the same C");
           return;
         }
@@ -165,17 +166,24 @@ for (const routine of ["sgemm", "sgemmtr", "dgemm"]) {
   }
 }
 
-for (const file of ["ssyrk.edge-cases", "ssyrk.edge-cases-column-major"]) {
-  for (const c of fixture(file)) {
-    test(`ssyrk ${file.includes("column") ? "cm" : "rm"}: ${c.label}`, async () => {
-      const layout = c.layout || "row-major";
-      const A = new Float32Array(c.A);
-      const C = new Float32Array(c.C);
-      const transB = c.trans === "no-transpose" ? "transpose" : "no-transpose";
-      const want = refGemm({ uplo: c.uplo, transA: c.trans, transB, m: c.n, n: c.n, k: c.k, alpha: c.alpha, A, lda: c.lda, B: A, ldb: c.lda, beta: c.beta, C, ldc: c.ldc, layout }).out;
-      const got = await wg.ssyrk(device, c.uplo, c.trans, c.n, c.k, c.alpha, A, c.lda, c.beta, C, c.ldc, layout);
-      exactEqual(got.C, want, c.label);
-    });
+for (const routine of ["ssyrk", "dsyrk"]) {
+  const Arr = routine === "dsyrk" ? Float64Array : Float32Array;
+  for (const file of [`${routine}.edge-cases`, `${routine}.edge-cases-column-major`]) {
+    for (const c of fixture(file)) {
+      test(`${routine} ${file.includes("column") ? "cm" : "rm"}: ${c.label}`, async () => {
+        const layout = c.layout || "row-major";
+        const A = new Arr(c.A);
+        const C = new Arr(c.C);
+        const transB = c.trans === "no-transpose" ? "transpose" : "no-transpose";
+        const got = await wg[routine](device, c.uplo, c.trans, c.n, c.k, c.alpha, A, c.lda, c.beta, C, c.ldc, layout);
+        if (routine === "dsyrk" && (c.alpha === 0 || c.k === 0) && c.beta === 1) {
+          assert(got.C === C, "quick return hands back the same C");
+          return;
+        }
+        const want = refGemm({ uplo: c.uplo, transA: c.trans, transB, m: c.n, n: c.n, k: c.k, alpha: c.alpha, A, lda: c.lda, B: A, ldb: c.lda, beta: c.beta, C, ldc: c.ldc, layout }).out;
+        exactEqual(got.C, want, c.label);
+      });
+    }
   }
 }
 
@@ -326,6 +334,43 @@ test("dgemm: random 150x133x77 within the double-double bound, all layouts/trans
           C: wg.randomFloat64Array(M * N, -1, 1, 5), ldc: cm ? M : N };
         checkGemm((await call.dgemm(a)).C, a, true);
       }
+});
+
+test("dgemmtr / dsyrk: random within the double-double bound, resident and host", async () => {
+  for (const layout of ["row-major", "column-major"])
+    for (const uplo of ["lower", "upper"]) {
+      const cm = layout === "column-major";
+      const M = 140;
+      const N = 95;
+      const K = 70;
+      const a = { uplo, transA: "no-transpose", transB: "transpose", m: M, n: N, k: K, alpha: 1.25, beta: -0.5, layout,
+        A: wg.randomFloat64Array(M * K, -1, 1, 7), lda: cm ? M : K,
+        B: wg.randomFloat64Array(N * K, -1, 1, 8), ldb: cm ? N : K,
+        C: wg.randomFloat64Array(M * N, -1, 1, 9), ldc: cm ? M : N };
+      checkGemm((await call.dgemmtr(a)).C, a, true);
+      checkGemm(await residentGemm("dgemmtr", a, Float64Array), a, true);
+      for (const trans of ["no-transpose", "transpose"]) {
+        const n = 130;
+        const k = 40;
+        const [aR, aC] = trans === "no-transpose" ? [n, k] : [k, n];
+        const lda = cm ? aR : aC;
+        const A = wg.randomFloat64Array(aR * aC, -1, 1, 10);
+        const C = wg.randomFloat64Array(n * n, -1, 1, 11);
+        const transB = trans === "no-transpose" ? "transpose" : "no-transpose";
+        const s = { uplo, transA: trans, transB, m: n, n, k, alpha: 1, beta: 0.25, A, lda, B: A, ldb: lda, C, ldc: n, layout };
+        checkGemm((await wg.dsyrk(device, uplo, trans, n, k, 1, A, lda, 0.25, C, n, layout)).C, s, true);
+        const gA = wg.GpuMatrix.from(device, A, aR, aC, lda, layout);
+        const gC = wg.GpuMatrix.from(device, C, n, n, n, layout);
+        try {
+          const r = await wg.dsyrk(device, uplo, trans, n, k, 1, gA, lda, 0.25, gC, n);
+          assertEqual(Object.keys(r).length, 0, "resident call returns {}");
+          checkGemm(await gC.read(), s, true);
+        } finally {
+          gA.destroy();
+          gC.destroy();
+        }
+      }
+    }
 });
 
 test("GpuMatrix.read strips lda padding; GpuVector round trip", async () => {

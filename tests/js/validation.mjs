@@ -198,6 +198,31 @@ async function main() {
     C: Object.assign({}, loadParam("C"), { dependsOn: ["n", "ldc"] }),
     ldc: loadParam("ld"),
   }, (a) => wg.ssyrk(a.device, a.uplo, a.trans, a.n, a.k, a.alpha, a.A, a.lda, a.beta, a.C, a.ldc, a.layout), device);
+  register("dgemmtr", Object.assign({ uplo: loadParam("uplo") }, gemmSpecs(true)),
+    (a) => wg.dgemmtr(a.device, a.uplo, a.transA, a.transB, a.m, a.n, a.k, a.alpha, a.A, a.lda, a.B, a.ldb, a.beta, a.C, a.ldc, a.layout), device);
+  // dsyrk: wgblas's tests/dsyrk/src/test.dsyrk.js composition (A64 with the
+  // level-3 edge/invalid cases in f64 wording plus the wrong-dtype GpuMatrix).
+  const A64 = loadParam("A64");
+  register("dsyrk", {
+    device: loadParam("device"),
+    uplo: loadParam("uplo"),
+    trans: loadParam("trans"),
+    layout: loadParam("layout"),
+    n: nWithNegative("must be non-negative"),
+    k: loadParam("k"),
+    alpha: loadParam("alpha"),
+    beta: loadParam("beta"),
+    A: Object.assign({}, A64, {
+      edge: A["level-3"].edge,
+      invalid: A["level-3"].invalid
+        .map((e) => Object.assign({}, e, { error: e.error.replace("Float32Array", "Float64Array") }))
+        .concat(A64.invalid.filter((e) => e.scenario === "wrongDtypeGpuMatrix")),
+      dependsOn: ["n", "k", "lda", "trans"],
+    }),
+    lda: loadParam("ld"),
+    C: Object.assign({}, loadParam("C64"), { dependsOn: ["n", "ldc"] }),
+    ldc: loadParam("ld"),
+  }, (a) => wg.dsyrk(a.device, a.uplo, a.trans, a.n, a.k, a.alpha, a.A, a.lda, a.beta, a.C, a.ldc, a.layout), device);
   register("sdot", {
     device: loadParam("device"), n: loadParam("n"), incx: loadParam("incx"), incy: loadParam("incy"),
     x: loadParam("x"), y: loadParam("y"),

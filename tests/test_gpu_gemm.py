@@ -21,8 +21,11 @@ def run_gemm(ctx, uplo, ta, tb, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc, dt
     dA = ctx.upload(np.asarray(A, dtype) if np.size(A) else np.zeros(1, dtype))
     dB = dA if syrk else ctx.upload(np.asarray(B, dtype) if np.size(B) else np.zeros(1, dtype))
     dC = ctx.upload(np.asarray(C, dtype))
-    if dtype == np.float64:
-        assert uplo == 0
+    if dtype == np.float64 and syrk:
+        ctx.dsyrk(uplo, ta, n, k, alpha, dA, lda, beta, dC, ldc)
+    elif dtype == np.float64 and uplo:
+        ctx.dgemmtr(uplo, ta, tb, m, n, k, alpha, dA, lda, dB, ldb, beta, dC, ldc)
+    elif dtype == np.float64:
         ctx.dgemm(ta, tb, m, n, k, alpha, dA, lda, dB, ldb, beta, dC, ldc)
     elif syrk:
         ctx.ssyrk(uplo, ta, n, k, alpha, dA, lda, beta, dC, ldc)
@@ -58,28 +61,32 @@ def check_case(ctx, uplo, ta, tb, m, n, k, alpha, beta, lda, ldb, ldc, seeds=(0,
 
 
 # ---------------------------------------------------------------- fixtures
-@pytest.mark.parametrize("routine", ["sgemm", "sgemmtr", "dgemm"])
+@pytest.mark.parametrize("routine", ["sgemm", "sgemmtr", "dgemm", "dgemmtr"])
 @pytest.mark.parametrize("cm", [False, True])
 def test_edge_cases_exact(ctx, routine, cm):
-    dtype = np.float64 if routine == "dgemm" else np.float32
+    dtype = np.float64 if routine.startswith("d") else np.float32
     for case in refcases.load(routine, cm):
         call = refcases.gemm_call(case, dtype)
         uplo, ta, tb, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc = call
-        if routine == "dgemm" and (alpha == 0 or k == 0) and beta == 1:
+        if routine.startswith("d") and (alpha == 0 or k == 0) and beta == 1:
             continue  # quick return: C is the caller's own buffer, untouched
         got = run_gemm(ctx, uplo, ta, tb, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc, dtype)
         want = refcases.numpy_gemm(*call).astype(dtype)
         assert np.array_equal(got, want), case["label"]
 
 
+@pytest.mark.parametrize("routine", ["ssyrk", "dsyrk"])
 @pytest.mark.parametrize("cm", [False, True])
-def test_ssyrk_edge_cases_exact(ctx, cm):
-    for case in refcases.load("ssyrk", cm):
-        uplo, trans, n, k, alpha, A, lda, beta, C, ldc = refcases.syrk_call(case)
+def test_syrk_edge_cases_exact(ctx, routine, cm):
+    dtype = np.float64 if routine == "dsyrk" else np.float32
+    for case in refcases.load(routine, cm):
+        uplo, trans, n, k, alpha, A, lda, beta, C, ldc = refcases.syrk_call(case, dtype)
+        if routine == "dsyrk" and (alpha == 0 or k == 0) and beta == 1:
+            continue  # quick return
         got = run_gemm(ctx, uplo, trans, 0, n, n, k, alpha, A, lda, None, lda, beta, C, ldc,
-                       syrk=True)
+                       dtype=dtype, syrk=True)
         want = refcases.numpy_gemm(uplo, trans, 1 - trans, n, n, k, alpha, A, lda, A, lda, beta,
-                                   C, ldc).astype(np.float32)
+                                   C, ldc).astype(dtype)
         assert np.array_equal(got, want), case["label"]
 
 

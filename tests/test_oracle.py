@@ -232,7 +232,7 @@ def test_sgemm_edge_cases_hand_values():
         assert np.array_equal(out32, np.array(want, np.float32)), case["label"]
 
 
-@pytest.mark.parametrize("routine", ["sgemm", "dgemm", "sgemmtr"])
+@pytest.mark.parametrize("routine", ["sgemm", "dgemm", "sgemmtr", "dgemmtr"])
 @pytest.mark.parametrize("cm", [False, True])
 def test_gemm_edge_cases_match_numpy(routine, cm):
     for case in refcases.load(routine, cm):
@@ -240,13 +240,14 @@ def test_gemm_edge_cases_match_numpy(routine, cm):
         want = refcases.numpy_gemm(*call)
         out, _ = orc.gemm_ld(*call)
         assert np.array_equal(out, want), case["label"]
-        if routine != "dgemm":
+        if not routine.startswith("d"):
             assert np.array_equal(orc.sgemm_wgsl(*call), want.astype(np.float32)), case["label"]
 
 
+@pytest.mark.parametrize("routine", ["ssyrk", "dsyrk"])
 @pytest.mark.parametrize("cm", [False, True])
-def test_ssyrk_edge_cases_match_numpy(cm):
-    for case in refcases.load("ssyrk", cm):
+def test_syrk_edge_cases_match_numpy(routine, cm):
+    for case in refcases.load(routine, cm):
         uplo, trans, n, k, alpha, A, lda, beta, C, ldc = refcases.syrk_call(case, np.float64)
         call = (uplo, trans, 1 - trans, n, n, k, alpha, A, lda, A, lda, beta, C, ldc)
         want = refcases.numpy_gemm(*call)

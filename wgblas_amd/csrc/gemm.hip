@@ -1059,3 +1059,27 @@ extern "C" int wgb_dgemm(wgb_ctx *ctx, int transA, int transB, int64_t m, int64_
   if ((alpha == 0.0 || k == 0) && beta == 1.0) return WGB_OK;
   return gemm_run<double>(ctx, 0, transA, transB, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc);
 }
+
+extern "C" int wgb_dgemmtr(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64_t n,
+                           int64_t k, double alpha, const double *A, int64_t lda, const double *B,
+                           int64_t ldb, double beta, double *C, int64_t ldc) {
+  int st = wgb::enter(ctx);
+  if (st) return st;
+  if ((st = check_gemm_args(uplo, true, transA, transB, m, n, k, A, lda, B, ldb, C, ldc))) return st;
+  // dgemm's quick return (src/dgemmtr/dgemmtr.mjs:189).
+  if ((alpha == 0.0 || k == 0) && beta == 1.0) return WGB_OK;
+  return gemm_run<double>(ctx, uplo, transA, transB, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc);
+}
+
+extern "C" int wgb_dsyrk(wgb_ctx *ctx, int uplo, int trans, int64_t n, int64_t k, double alpha,
+                         const double *A, int64_t lda, double beta, double *C, int64_t ldc) {
+  int st = wgb::enter(ctx);
+  if (st) return st;
+  if (trans != WGB_NO_TRANS && trans != WGB_TRANS)
+    return wgb::fail(WGB_ERR_INVALID_VALUE, "trans must be WGB_NO_TRANS or WGB_TRANS");
+  const int transB = trans == WGB_NO_TRANS ? WGB_TRANS : WGB_NO_TRANS;
+  if ((st = check_gemm_args(uplo, true, trans, transB, n, n, k, A, lda, A, lda, C, ldc))) return st;
+  // dgemm's quick return (src/dsyrk/dsyrk.mjs:142).
+  if ((alpha == 0.0 || k == 0) && beta == 1.0) return WGB_OK;
+  return gemm_run<double>(ctx, uplo, trans, transB, n, n, k, alpha, A, lda, A, lda, beta, C, ldc);
+}

@@ -267,7 +267,7 @@ napi_value Download(napi_env env, napi_callback_info info) {
 // ---- level 3 ---------------------------------------------------------------
 
 // gemm(kind, ctx, uplo, transA, transB, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc)
-// kind: 0 sgemm, 1 sgemmtr, 2 dgemm.
+// kind: 0 sgemm, 1 sgemmtr, 2 dgemm, 3 dgemmtr.
 napi_value Gemm(napi_env env, napi_callback_info info) {
   Args a;
   if (!get_args(env, info, a, 16)) return nullptr;
@@ -290,14 +290,18 @@ napi_value Gemm(napi_env env, napi_callback_info info) {
   } else if (kind == 1) {
     WGB_OK_OR_THROW(wgb_sgemmtr(ctx, uplo, ta, tb, m, n, k, (float)alpha, (const float *)A, lda,
                                 (const float *)B, ldb, (float)beta, (float *)C, ldc), "wgb_sgemmtr");
-  } else {
+  } else if (kind == 2) {
     WGB_OK_OR_THROW(wgb_dgemm(ctx, ta, tb, m, n, k, alpha, (const double *)A, lda,
                               (const double *)B, ldb, beta, (double *)C, ldc), "wgb_dgemm");
+  } else {
+    WGB_OK_OR_THROW(wgb_dgemmtr(ctx, uplo, ta, tb, m, n, k, alpha, (const double *)A, lda,
+                                (const double *)B, ldb, beta, (double *)C, ldc), "wgb_dgemmtr");
   }
   return nullptr;
 }
 
-// ssyrk(ctx, uplo, trans, n, k, alpha, A, lda, beta, C, ldc)
+// syrk(ctx, uplo, trans, n, k, alpha, A, lda, beta, C, ldc[, f64]): ssyrk, or
+// dsyrk when the optional twelfth argument is true.
 napi_value Ssyrk(napi_env env, napi_callback_info info) {
   Args a;
   if (!get_args(env, info, a, 11)) return nullptr;
@@ -312,8 +316,15 @@ napi_value Ssyrk(napi_env env, napi_callback_info info) {
       !get_i64(env, a.v[7], &lda) || !get_f64(env, a.v[8], &beta) || !get_ptr(env, a.v[9], &C) ||
       !get_i64(env, a.v[10], &ldc))
     return nullptr;
-  WGB_OK_OR_THROW(wgb_ssyrk(ctx, uplo, trans, n, k, (float)alpha, (const float *)A, lda,
-                            (float)beta, (float *)C, ldc), "wgb_ssyrk");
+  bool f64 = false;
+  if (a.n > 11 && napi_get_value_bool(env, a.v[11], &f64) != napi_ok) f64 = false;
+  if (f64) {
+    WGB_OK_OR_THROW(wgb_dsyrk(ctx, uplo, trans, n, k, alpha, (const double *)A, lda, beta,
+                              (double *)C, ldc), "wgb_dsyrk");
+  } else {
+    WGB_OK_OR_THROW(wgb_ssyrk(ctx, uplo, trans, n, k, (float)alpha, (const float *)A, lda,
+                              (float)beta, (float *)C, ldc), "wgb_ssyrk");
+  }
   return nullptr;
 }
 

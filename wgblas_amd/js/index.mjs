@@ -9,6 +9,8 @@ export { sgemm } from "./src/sgemm.mjs";
 export { sgemmtr } from "./src/sgemmtr.mjs";
 export { ssyrk } from "./src/ssyrk.mjs";
 export { dgemm } from "./src/dgemm.mjs";
+export { dgemmtr } from "./src/dgemmtr.mjs";
+export { dsyrk } from "./src/dsyrk.mjs";
 export { sdot } from "./src/sdot.mjs";
 export { sasum } from "./src/sasum.mjs";
 export { snrm2 } from "./src/snrm2.mjs";

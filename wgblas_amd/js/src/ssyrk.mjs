@@ -11,10 +11,23 @@ import { native } from "./native.mjs";
 
 export async function ssyrk(device, uplo, trans, n, k, alpha, A, lda, beta, C, ldc,
                             layout = "row-major") {
+  return syrk("ssyrk", device, uplo, trans, n, k, alpha, A, lda, beta, C, ldc, layout);
+}
+
+/**
+ * ssyrk / dsyrk body (routine "ssyrk" or "dsyrk"): wgblas's checks in its
+ * order, then the column-major mapping and one device call. dsyrk adds the
+ * f64 dtype checks and dgemm's quick return (src/dsyrk/dsyrk.mjs:60-142).
+ * Throws synchronously; the async wrappers turn that into a rejection.
+ */
+export function syrk(routine, device, uplo, trans, n, k, alpha, A, lda, beta, C, ldc, layout) {
+  const f64 = routine === "dsyrk";
+  const arr = f64 ? Float64Array : Float32Array;
+  const arrName = f64 ? "Float64Array" : "Float32Array";
   const AIsGpu = A instanceof GpuMatrix;
   const CIsGpu = C instanceof GpuMatrix;
   requireGpuDevice(device);
-  requireSameDevice(device, "ssyrk", { A, C });
+  requireSameDevice(device, routine, { A, C });
   checkUplo(uplo);
   checkTrans("trans", trans);
   checkLayout(layout);
@@ -22,8 +35,12 @@ export async function ssyrk(device, uplo, trans, n, k, alpha, A, lda, beta, C, l
   checkScalar("beta", beta);
   for (const v of [n, k, lda, ldc])
     if (!Number.isInteger(v)) throw new Error("n, k, lda, and ldc must be integers.");
-  if (!AIsGpu && !(A instanceof Float32Array)) throw new Error("A must be a Float32Array or GpuMatrix.");
-  if (!CIsGpu && !(C instanceof Float32Array)) throw new Error("C must be a Float32Array or GpuMatrix.");
+  if (!AIsGpu && !(A instanceof arr)) throw new Error(`A must be a ${arrName} or GpuMatrix.`);
+  if (!CIsGpu && !(C instanceof arr)) throw new Error(`C must be a ${arrName} or GpuMatrix.`);
+  if (f64 && AIsGpu && A.dtype !== Float64Array)
+    throw new Error("A must be a Float64Array-backed GpuMatrix.");
+  if (f64 && CIsGpu && C.dtype !== Float64Array)
+    throw new Error("C must be a Float64Array-backed GpuMatrix.");
   if (AIsGpu && !CIsGpu) throw new Error("C must be a GpuMatrix when A is a GpuMatrix.");
   if (CIsGpu && !AIsGpu) throw new Error("A must be a GpuMatrix when C is a GpuMatrix.");
   if (n < 0 || k < 0) throw new Error("n and k must be non-negative.");
@@ -45,7 +62,8 @@ export async function ssyrk(device, uplo, trans, n, k, alpha, A, lda, beta, C, l
   const t = (trans === "transpose") !== (layoutA !== "column-major") ? TRANS : NO_TRANS;
   let u = UPLO[uplo];
   if (layoutC !== "column-major") u = u === 1 ? 2 : 1;
-  return execute(device, [A], C, CIsGpu, Float32Array, (ctx, p, pC) =>
-    native().ssyrk(ctx, u, t, n, k, alpha, p[0], lda, beta, pC, ldc),
+  if (f64 && (alpha === 0 || k === 0) && beta === 1) return CIsGpu ? {} : { C };
+  return execute(device, [A], C, CIsGpu, arr, (ctx, p, pC) =>
+    native().ssyrk(ctx, u, t, n, k, alpha, p[0], lda, beta, pC, ldc, f64),
   );
 }

@@ -47,6 +47,10 @@ _SIGNATURES = {
                   _i64],
     "wgb_dgemm": [_ptr, C.c_int, C.c_int, _i64, _i64, _i64, C.c_double, _ptr, _i64, _ptr, _i64,
                   C.c_double, _ptr, _i64],
+    "wgb_dgemmtr": [_ptr, C.c_int, C.c_int, C.c_int, _i64, _i64, _i64, C.c_double, _ptr, _i64,
+                    _ptr, _i64, C.c_double, _ptr, _i64],
+    "wgb_dsyrk": [_ptr, C.c_int, C.c_int, _i64, _i64, C.c_double, _ptr, _i64, C.c_double, _ptr,
+                  _i64],
     "wgb_sdot": [_ptr, _i64, _ptr, _i64, _ptr, _i64, C.POINTER(C.c_float)],
     "wgb_sdot_dev": [_ptr, _i64, _ptr, _i64, _ptr, _i64, _ptr],
     "wgb_sasum": [_ptr, _i64, _ptr, _i64, C.POINTER(C.c_float)],
@@ -236,6 +240,14 @@ class Context:
     def dgemm(self, transA, transB, m, n, k, alpha, A, lda, B, ldb, beta, C_, ldc):
         _check(self.lib.wgb_dgemm(self.handle, transA, transB, m, n, k, alpha, _p(A), lda,
                                   _p(B), ldb, beta, _p(C_), ldc), "wgb_dgemm")
+
+    def dgemmtr(self, uplo, transA, transB, m, n, k, alpha, A, lda, B, ldb, beta, C_, ldc):
+        _check(self.lib.wgb_dgemmtr(self.handle, uplo, transA, transB, m, n, k, alpha, _p(A),
+                                    lda, _p(B), ldb, beta, _p(C_), ldc), "wgb_dgemmtr")
+
+    def dsyrk(self, uplo, trans, n, k, alpha, A, lda, beta, C_, ldc):
+        _check(self.lib.wgb_dsyrk(self.handle, uplo, trans, n, k, alpha, _p(A), lda, beta,
+                                  _p(C_), ldc), "wgb_dsyrk")
 
     # ---- level 1 ----
     def sdot(self, n, x, incx, y, incy):

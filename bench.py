@@ -15,7 +15,9 @@ Also reported under "components", each timed the same way: sgemm 512^3
 (config 1), the ragged sgemm 8191 x 8193 x 4097 with ld = 1 (mod 64)
 (config 3), dgemm 4096^3 N/T alpha = beta = 1 (config 4), ssyrk lower
 n = 8192, k = 4096, 10 chained resident calls (config 5), and sdot / sasum /
-snrm2 / isamax at n = 2^28 plus the incx = 3, n = 2^26 variants (config 2).
+snrm2 / isamax at n = 2^28 plus the incx = 3, n = 2^26 variants (config 2),
+sgemmtr on config 5's operands, and ddot / dasum / dnrm2 / idamax at n = 2^27
+(the same bytes as config 2's fp32 vectors).
 
 `roofline` is for the headline kernel: algorithmic flops per launch (2mnk)
 over the mean launch duration measured with events around each launch,
@@ -239,6 +241,26 @@ def bench_components(ctx, ev, quick):
         comps[f"{name}_2^26_incx3"] = {"ms": ms, "GB/s_useful": useful,
                                        "GB/s_span": 3 * useful,
                                        "frac_hbm_peak_span": 3 * useful * 1e9 / PEAK_HBM}
+    dx.free()
+    dy.free()
+
+    # the fp64 reductions over the same bytes: n = 2^27 doubles
+    n = 1 << 27
+    dx, dy = ctx.empty(n, np.float64), ctx.empty(n, np.float64)
+    ctx.fill_normal(dx, 1)
+    ctx.fill_normal(dy, 2)
+    out = ctx.empty(4, np.float64)
+    red = {
+        "ddot": (lambda nn: ctx.ddot_dev(nn, dx, 1, dy, 1, out), 16),
+        "dasum": (lambda nn: ctx.dasum_dev(nn, dx, 1, out), 8),
+        "dnrm2": (lambda nn: ctx.dnrm2_dev(nn, dx, 1, out), 8),
+        "idamax": (lambda nn: ctx.idamax_dev(nn, dx, 1, iout), 8),
+    }
+    for name, (fn, bpe) in red.items():
+        fn(n)
+        ms = per_launch_ms(ctx, lambda: fn(n), lreps)
+        gbs = bpe * n / ms / 1e6
+        comps[f"{name}_2^27"] = {"ms": ms, "GB/s": gbs, "frac_hbm_peak": gbs * 1e9 / PEAK_HBM}
     dx.free()
     dy.free()
     return comps

@@ -206,6 +206,30 @@ int wgb_isamax(wgb_ctx *ctx, int64_t n, const float *x, int64_t incx,
 int wgb_isamax_dev(wgb_ctx *ctx, int64_t n, const float *x, int64_t incx,
                    int64_t *d_result);
 
+/* The fp64 reductions, accumulated in native float64 with the same rules as
+ * their fp32 counterparts (wgblas computes them in double-double:
+ * src/shaders/{ddot,dasum,dnrm2,idamax}.wgsl, src/shaders/reduction/*F64.wgsl).
+ * ddot replaces src/ddot/ddot.mjs:19-174; dasum src/dasum/dasum.mjs:18-138;
+ * dnrm2 src/dnrm2/dnrm2.mjs:22-149 (Blue's algorithm with LAPACK 3.10's
+ * dnrm2 thresholds for IEEE double; NaN gives NaN, Inf gives Inf); idamax
+ * src/idamax/idamax.mjs:18-152 (isamax's NaN and tie rules, n <= 0 -> -1). */
+int wgb_ddot(wgb_ctx *ctx, int64_t n, const double *x, int64_t incx,
+             const double *y, int64_t incy, double *result);
+int wgb_ddot_dev(wgb_ctx *ctx, int64_t n, const double *x, int64_t incx,
+                 const double *y, int64_t incy, double *d_result);
+int wgb_dasum(wgb_ctx *ctx, int64_t n, const double *x, int64_t incx,
+              double *result);
+int wgb_dasum_dev(wgb_ctx *ctx, int64_t n, const double *x, int64_t incx,
+                  double *d_result);
+int wgb_dnrm2(wgb_ctx *ctx, int64_t n, const double *x, int64_t incx,
+              double *result);
+int wgb_dnrm2_dev(wgb_ctx *ctx, int64_t n, const double *x, int64_t incx,
+                  double *d_result);
+int wgb_idamax(wgb_ctx *ctx, int64_t n, const double *x, int64_t incx,
+               int64_t *result);
+int wgb_idamax_dev(wgb_ctx *ctx, int64_t n, const double *x, int64_t incx,
+                   int64_t *d_result);
+
 #ifdef __cplusplus
 }
 #endif

@@ -368,6 +368,56 @@ int64_t orc_isamax_brute(int64_t n, const float *x, int64_t incx) {
   return best;
 }
 
+/* fp64 level 1 (src/ddot/ddot.mjs, src/dasum/dasum.mjs, src/dnrm2/dnrm2.mjs,
+ * src/idamax/idamax.mjs): the reference's tests compare with stdlib's f64
+ * routines under eps = 2^-48 bounds (tests/ddot/helpers.js,
+ * tests/dnrm2/helpers.js) or exactly (idamax); these long-double sums are
+ * the exact values those bounds are taken around. */
+double orc_ddot_ld(int64_t n, const double *x, int64_t incx, const double *y, int64_t incy,
+                   double *sum_abs) {
+  long double s = 0, a = 0;
+  for (int64_t i = 0; i < n; ++i) {
+    long double p = (long double)x[i * incx] * (long double)y[i * incy];
+    s += p;
+    a += fabsl(p);
+  }
+  if (sum_abs) *sum_abs = (double)a;
+  return (double)s;
+}
+
+double orc_dasum_ld(int64_t n, const double *x, int64_t incx) {
+  long double a = 0;
+  for (int64_t i = 0; i < n; ++i) a += fabsl((long double)x[i * incx]);
+  return (double)a;
+}
+
+/* long double squares cannot overflow for double inputs (|x|^2 <= 2^2048 is
+ * far below long double's 2^16384), so no scaling is needed here. */
+double orc_dnrm2_ld(int64_t n, const double *x, int64_t incx) {
+  long double s = 0;
+  for (int64_t i = 0; i < n; ++i) {
+    long double v = (long double)x[i * incx];
+    s += v * v;
+  }
+  return (double)sqrtl(s);
+}
+
+/* idamax: isamax's rules on doubles (src/idamax/idamax.mjs:34-36,
+ * tests/idamax/src/test.idamax.js:97-126). */
+int64_t orc_idamax_brute(int64_t n, const double *x, int64_t incx) {
+  if (n <= 0) return -1;
+  int64_t best = 0;
+  double bv = -1.0;
+  for (int64_t i = 0; i < n; ++i) {
+    double v = fabs(x[i * incx]);
+    if (v > bv) {
+      bv = v;
+      best = i;
+    }
+  }
+  return best;
+}
+
 /* op(M)[r][c] of a column-major matrix with leading dimension ld. */
 static inline double op_elem(const double *M, int64_t ld, int trans, int64_t r, int64_t c) {
   return trans ? M[c + r * ld] : M[r + c * ld];

@@ -29,6 +29,10 @@ _SIG = {
     "orc_sum_abs_ld": (C.c_double, [_i64, _f32p, _i64]),
     "orc_nrm2_ld": (C.c_double, [_i64, _f32p, _i64]),
     "orc_isamax_brute": (_i64, [_i64, _f32p, _i64]),
+    "orc_ddot_ld": (C.c_double, [_i64, _f64p, _i64, _f64p, _i64, _f64p]),
+    "orc_dasum_ld": (C.c_double, [_i64, _f64p, _i64]),
+    "orc_dnrm2_ld": (C.c_double, [_i64, _f64p, _i64]),
+    "orc_idamax_brute": (_i64, [_i64, _f64p, _i64]),
     "orc_gemm_ld": (None, [C.c_int, C.c_int, C.c_int, _i64, _i64, _i64, C.c_double, _f64p, _i64,
                            _f64p, _i64, C.c_double, _f64p, _i64, _f64p, _i64, _f64p]),
     "orc_sgemm_wgsl": (None, [C.c_int, C.c_int, C.c_int, _i64, _i64, _i64, C.c_float, _f32p, _i64,
@@ -132,6 +136,30 @@ def nrm2_ld(n, x, incx):
 def isamax_brute(n, x, incx):
     x, xp = _f32(x)
     return int(lib().orc_isamax_brute(n, xp, incx))
+
+
+def ddot_ld(n, x, incx, y, incy):
+    """(sum x*y, sum |x*y|) of float64 vectors in long double."""
+    x, xp = _f64(x)
+    y, yp = _f64(y)
+    a = C.c_double(0)
+    s = lib().orc_ddot_ld(n, xp, incx, yp, incy, C.byref(a))
+    return s, a.value
+
+
+def dasum_ld(n, x, incx):
+    x, xp = _f64(x)
+    return lib().orc_dasum_ld(n, xp, incx)
+
+
+def dnrm2_ld(n, x, incx):
+    x, xp = _f64(x)
+    return lib().orc_dnrm2_ld(n, xp, incx)
+
+
+def idamax_brute(n, x, incx):
+    x, xp = _f64(x)
+    return int(lib().orc_idamax_brute(n, xp, incx))
 
 
 # ---- level 3 (column-major flat arrays) ----

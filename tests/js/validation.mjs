@@ -27,7 +27,7 @@ function loadParam(name) {
 }
 
 // The Float64Array variant of a float32 spec: same cases, f64 wording, and a
-// GpuMatrix-of-the-wrong-dtype case for matrix specs.
+// GpuMatrix / GpuVector-of-the-wrong-dtype case for matrix / vector specs.
 function derive64(base) {
   const isArray = base.type !== "float";
   const isMatrix = (base.dependsOn || []).some((d) => d.startsWith("ld"));
@@ -35,6 +35,8 @@ function derive64(base) {
     Object.assign({}, e, { error: typeof e.error === "string" ? e.error.replace("Float32Array", "Float64Array") : e.error }));
   if (base.type === "float32array" && isMatrix)
     invalid.push({ scenario: "wrongDtypeGpuMatrix", error: "must be a Float64Array-backed GpuMatrix", label: "GpuMatrix of Float32Array" });
+  if (base.type === "float32array" && !isMatrix)
+    invalid.push({ scenario: "wrongDtypeGpuVector", error: "must be a Float64Array-backed GpuVector", label: "GpuVector of Float32Array" });
   return Object.assign({}, base, { type: isArray ? "float64array" : "float64", invalid });
 }
 
@@ -78,6 +80,8 @@ function resolve(entry, name, spec, baselines, device) {
       const data = new Float32Array(16).fill(1);
       return wg.GpuMatrix.from(device, data, 2, 2, 2, baselines.layout || "row-major");
     }
+    if (entry.scenario === "wrongDtypeGpuVector")
+      return wg.GpuVector.from(device, new Float32Array(minLength(spec.dependsOn, baselines)).fill(1));
     const len = minLength(spec.dependsOn, baselines);
     const Ctor = ctorOf(spec.type);
     if (entry.scenario === "minimal") return new Ctor(len).fill(1);
@@ -114,14 +118,14 @@ function register(routine, specs, call, device) {
   const baselines = baselinesOf(specs, device);
   for (const [name, spec] of Object.entries(specs)) {
     for (const entry of spec.invalid || []) {
-      if (!GPU && entry.scenario === "wrongDtypeGpuMatrix") continue;
+      if (!GPU && /^wrongDtype/.test(entry.scenario || "")) continue;
       test(`${routine} ${name} invalid: ${entry.label || JSON.stringify(entry)}`, async () => {
         const args = Object.assign({}, baselines);
         args[name] = resolve(entry, name, spec, baselines, device);
         try {
           await assertRejects(() => call(args), entry.error);
         } finally {
-          if (args[name] instanceof wg.GpuMatrix) args[name].destroy();
+          if (args[name] instanceof wg.GpuMatrix || args[name] instanceof wg.GpuVector) args[name].destroy();
         }
       });
     }
@@ -229,6 +233,15 @@ async function main() {
   }, (a) => wg.sdot(a.device, a.n, a.x, a.incx, a.y, a.incy), device);
   for (const r of ["sasum", "snrm2", "isamax"])
     register(r, { device: loadParam("device"), n: loadParam("n"), incx: loadParam("incx"), x: loadParam("x") },
+      (a) => wg[r](a.device, a.n, a.x, a.incx), device);
+  // fp64 level 1: wgblas's tests/{ddot,dasum,dnrm2,idamax}/src/test.*.js
+  // compositions (x64 / y64 derived from the f32 specs).
+  register("ddot", {
+    device: loadParam("device"), n: loadParam("n"), incx: loadParam("incx"), incy: loadParam("incy"),
+    x: loadParam("x64"), y: loadParam("y64"),
+  }, (a) => wg.ddot(a.device, a.n, a.x, a.incx, a.y, a.incy), device);
+  for (const r of ["dasum", "dnrm2", "idamax"])
+    register(r, { device: loadParam("device"), n: loadParam("n"), incx: loadParam("incx"), x: loadParam("x64") },
       (a) => wg[r](a.device, a.n, a.x, a.incx), device);
   await run();
   if (GPU) wg.cleanup();

@@ -300,3 +300,80 @@ def test_sgemm_k0_is_beta_c_bit_exact():
     C = orc.random_f32(16, -5, 5, 300)
     out32 = orc.sgemm_wgsl(0, 0, 1, 4, 4, 0, 1.5, np.zeros(3), 4, np.zeros(3), 4, 0.5, C, 4)
     assert np.array_equal(out32, (np.float32(0.5) * C).astype(np.float32))
+
+
+# ---- fp64 level 1 (ddot / dasum / dnrm2 / idamax) --------------------------
+from fractions import Fraction  # noqa: E402
+
+
+def _exact(values):
+    return sum((Fraction(v) for v in values), Fraction(0))
+
+
+def _ulps64(a, b):
+    if a == b:
+        return 0
+    ia = np.array(a, np.float64).view(np.int64)
+    ib = np.array(b, np.float64).view(np.int64)
+    return abs(int(ia) - int(ib))
+
+
+def test_ddot_dasum_edge_cases_against_exact_rationals():
+    # Fixtures: wgblas tests/{ddot,dasum}/edge-cases.json, against the exact
+    # rational result of the double inputs: the long-double sums must be
+    # within their own precision (n 2^-63 sum|x y|, plus the final rounding).
+    for c in refcases.load("ddot"):
+        x, y = np.array(c["x"], np.float64), np.array(c["y"], np.float64)
+        terms = [Fraction(float(x[i * c["incx"]])) * Fraction(float(y[i * c["incy"]])) for i in range(c["n"])]
+        exact = sum(terms, Fraction(0))
+        got, sum_abs = orc.ddot_ld(c["n"], x, c["incx"], y, c["incy"])
+        tol = c["n"] * 2.0 ** -63 * sum_abs + 2.0 ** -53 * abs(float(exact))
+        assert abs(Fraction(got) - exact) <= Fraction(tol), c["label"]
+    for c in refcases.load("dasum"):
+        x = np.array(c["x"], np.float64)
+        want = float(_exact(abs(float(x[i * c["incx"]])) for i in range(c["n"])))
+        assert _ulps64(orc.dasum_ld(c["n"], x, c["incx"]), want) <= 1, c["label"]
+
+
+DNRM2_EXPECT = [5.0, 5.0, 1.0, 0.0, 5.0, 5.0, 3e19, None, math.sqrt(3.0) * 1e-20, None]
+IDAMAX_EXPECT = [0, 0, 1, 1, 0, 3, 0, 1, 0, 1, 1, 1]
+
+
+def test_dnrm2_idamax_edge_cases_hand_values():
+    for c, want in zip(refcases.load("dnrm2"), DNRM2_EXPECT):
+        x = np.array(c["x"], np.float64)
+        got = orc.dnrm2_ld(c["n"], x, c["incx"])
+        if want is None:  # sqrt of the exact sum of squares
+            want = math.sqrt(float(_exact(Fraction(float(x[i * c["incx"]])) ** 2 for i in range(c["n"]))))
+        assert _ulps64(got, want) <= 1, c["label"]
+    for c, want in zip(refcases.load("idamax"), IDAMAX_EXPECT):
+        assert orc.idamax_brute(c["n"], np.array(c["x"], np.float64), c["incx"]) == want, c["label"]
+
+
+def test_idamax_nan_rules_and_fp64_specials():
+    # tests/idamax/src/test.idamax.js:97-144
+    run = lambda a: orc.idamax_brute(len(a), np.array(a, np.float64), 1)
+    N, I = np.nan, np.inf
+    assert run([1, N, 7, 3]) == 2 and run([1, 2, 3, N]) == 2
+    assert run([N, N, N, N]) == 0
+    assert run([N, 5, 2, 3]) == 1 and run([N, I, 2, 3]) == 1
+    assert run([1, I, 2, 3]) == 1 and run([1, -I, 2, 3]) == 1
+    assert orc.idamax_brute(0, np.zeros(1), 1) == -1
+    # native f64 range: 1e300 < 1e301 (the reference's double-double reads both as Inf)
+    assert run([1e300, 1e301, 5]) == 1
+    assert math.isinf(orc.dnrm2_ld(3, np.array([1.0, I, 2.0]), 1))
+    assert math.isnan(orc.dnrm2_ld(3, np.array([1.0, I, N]), 1))
+    assert orc.dnrm2_ld(2, np.array([3e300, 4e300]), 1) == 5e300
+
+
+def test_fp64_oracles_agree_with_numpy_on_random_vectors():
+    rng = np.random.default_rng(11)
+    for n, inc in ((1, 1), (50, 1), (1000, 3), (4097, 2)):
+        x = rng.standard_normal((n - 1) * inc + 1)
+        y = rng.standard_normal((n - 1) * inc + 1)
+        xs, ys = x[::inc][:n], y[::inc][:n]
+        s, a = orc.ddot_ld(n, x, inc, y, inc)
+        assert abs(s - float(np.dot(xs, ys))) <= 4 * n * 2.0 ** -53 * a
+        assert abs(orc.dasum_ld(n, x, inc) - float(np.sum(np.abs(xs)))) <= 4 * n * 2.0 ** -53 * np.sum(np.abs(xs))
+        assert abs(orc.dnrm2_ld(n, x, inc) - float(np.linalg.norm(xs))) <= 4 * n * 2.0 ** -53 * np.linalg.norm(xs)
+        assert orc.idamax_brute(n, x, inc) == int(np.argmax(np.abs(xs)))

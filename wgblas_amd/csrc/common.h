@@ -48,7 +48,7 @@ void timing_end(wgb_ctx *ctx);
 // Largest number of first-pass blocks a reduction may use; the scratch
 // buffer is sized for this many 16-byte partials plus the result slot.
 constexpr int kMaxReduceBlocks = 2048;
-constexpr size_t kScratchBytes = (size_t)kMaxReduceBlocks * 16 + 256;
+constexpr size_t kScratchBytes = (size_t)kMaxReduceBlocks * 32 + 256;  // 32-byte partial slots + result
 
 }  // namespace wgb
 

@@ -331,7 +331,7 @@ napi_value Ssyrk(napi_env env, napi_callback_info info) {
 // ---- level 1 ---------------------------------------------------------------
 
 // reduce(kind, ctx, n, x, incx[, y, incy]) -> number; kind: 0 sdot, 1 sasum,
-// 2 snrm2, 3 isamax.
+// 2 snrm2, 3 isamax, 4 ddot, 5 dasum, 6 dnrm2, 7 idamax.
 napi_value Reduce(napi_env env, napi_callback_info info) {
   Args a;
   if (!get_args(env, info, a, 5)) return nullptr;
@@ -343,20 +343,26 @@ napi_value Reduce(napi_env env, napi_callback_info info) {
   void *x, *y = nullptr;
   if (!get_i64(env, a.v[2], &n) || !get_ptr(env, a.v[3], &x) || !get_i64(env, a.v[4], &incx))
     return nullptr;
-  if (kind == 0) {
+  if (kind == 0 || kind == 4) {
     if (a.n < 7) {
-      napi_throw_type_error(env, nullptr, "wgblas_hip addon: sdot needs y and incy");
+      napi_throw_type_error(env, nullptr, "wgblas_hip addon: sdot / ddot need y and incy");
       return nullptr;
     }
     if (!get_ptr(env, a.v[5], &y) || !get_i64(env, a.v[6], &incy)) return nullptr;
   }
   float r = 0;
+  double d = 0;
   int64_t idx = -1;
+  const double *xd = (const double *)x;
   switch (kind) {
     case 0: WGB_OK_OR_THROW(wgb_sdot(ctx, n, (const float *)x, incx, (const float *)y, incy, &r), "wgb_sdot"); break;
     case 1: WGB_OK_OR_THROW(wgb_sasum(ctx, n, (const float *)x, incx, &r), "wgb_sasum"); break;
     case 2: WGB_OK_OR_THROW(wgb_snrm2(ctx, n, (const float *)x, incx, &r), "wgb_snrm2"); break;
-    default: WGB_OK_OR_THROW(wgb_isamax(ctx, n, (const float *)x, incx, &idx), "wgb_isamax"); return num(env, (double)idx);
+    case 3: WGB_OK_OR_THROW(wgb_isamax(ctx, n, (const float *)x, incx, &idx), "wgb_isamax"); return num(env, (double)idx);
+    case 4: WGB_OK_OR_THROW(wgb_ddot(ctx, n, xd, incx, (const double *)y, incy, &d), "wgb_ddot"); return num(env, d);
+    case 5: WGB_OK_OR_THROW(wgb_dasum(ctx, n, xd, incx, &d), "wgb_dasum"); return num(env, d);
+    case 6: WGB_OK_OR_THROW(wgb_dnrm2(ctx, n, xd, incx, &d), "wgb_dnrm2"); return num(env, d);
+    default: WGB_OK_OR_THROW(wgb_idamax(ctx, n, xd, incx, &idx), "wgb_idamax"); return num(env, (double)idx);
   }
   return num(env, (double)r);
 }

@@ -1,4 +1,5 @@
-// Level-1 reductions: sdot, sasum, snrm2, isamax.
+// Level-1 reductions: sdot, sasum, snrm2, isamax and their native-fp64
+// counterparts ddot, dasum, dnrm2, idamax.
 //
 // wgblas runs each of these as two compute passes on one encoder: 128
 // workgroups of 64 threads grid-stride over x with four accumulators each,
@@ -24,12 +25,32 @@
 // thresholds and scales (src/shaders/snrm2.wgsl:33-51), LAPACK 3.10's combine
 // (src/shaders/reduction/scaledSum.wgsl:50-101), and isamax's strict '>'
 // with a -1 sentinel and lower-index tie break (src/shaders/isamax.wgsl:28-80,
-// src/shaders/reduction/argmax.wgsl).
+// src/shaders/reduction/argmax.wgsl). The fp64 routines (wgblas emulates
+// them in double-double: src/shaders/{ddot,dasum,dnrm2,idamax}.wgsl,
+// reduction/*F64.wgsl) accumulate in native f64 with the same rules; dnrm2
+// uses Blue's algorithm with LAPACK 3.10's dnrm2 thresholds for IEEE double
+// (wgblas moves them to fit double-double's f32 exponent range).
 #include "common.h"
 
 namespace {
 
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef double v2d __attribute__((ext_vector_type(2)));
+typedef double v4d __attribute__((ext_vector_type(4)));
+
+// The 16-byte vector of an element type: W elements.
+template <typename T>
+struct Vec16;
+template <>
+struct Vec16<float> {
+  typedef v4f type;
+  static constexpr int W = 4;
+};
+template <>
+struct Vec16<double> {
+  typedef v2d type;
+  static constexpr int W = 2;
+};
 
 constexpr int kThreads = 256;
 constexpr int kUnroll = 8;
@@ -41,6 +62,17 @@ constexpr float kTbig = 0x1p50f;
 constexpr float kSsml = 0x1p75f;
 constexpr float kSbig = 0x1p-76f;
 constexpr int kSbigSqExp = -152;  // log2(SBIG^2)
+
+// dnrm2 thresholds and scales for IEEE double, LAPACK 3.10's dnrm2
+// (la_constants: tsml = 2^ceil((minexp-1)/2), tbig = 2^floor((maxexp-digits+1)/2),
+// ssml = 2^-floor((minexp-digits)/2), sbig = 2^-ceil((maxexp+digits-1)/2)).
+constexpr double kDTsml = 0x1p-511;
+constexpr double kDTbig = 0x1p486;
+constexpr double kDSsml = 0x1p537;
+constexpr double kDSbig = 0x1p-538;
+
+// Partial slots in the context scratch (the largest Partial is dnrm2's).
+constexpr size_t kPartialBytes = 32;
 
 int reduce_blocks(int64_t n) {
   int64_t g = (n + kElemsPerBlockMin - 1) / kElemsPerBlockMin;
@@ -54,18 +86,21 @@ bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 // ---- the four reductions as accumulate / merge policies -------------------
 //
 // State: what one lane accumulates. Partial: what a block (and pass 2)
-// merges. add4 takes four consecutive elements starting at element index
-// `i`; add1 takes one element, `c` (0..3) naming an accumulation chain the
-// policy may use for ILP.
+// merges. addv takes one 16-byte vector (W consecutive elements starting at
+// element index `i`); add1 takes one element, `c` naming an accumulation
+// chain the policy may use for ILP (taken modulo its chain count).
 
 __device__ __forceinline__ v4f nt_load(const v4f *p) { return __builtin_nontemporal_load(p); }
+__device__ __forceinline__ v2d nt_load(const v2d *p) { return __builtin_nontemporal_load(p); }
 
 struct SdotOp {
+  typedef float Elem;
+  typedef v4f V;
   static constexpr int NIN = 2;
   typedef v4f State;
   typedef float Partial;
   __device__ static State init() { return v4f{0.f, 0.f, 0.f, 0.f}; }
-  __device__ static void add4(State &s, v4f a, v4f b, int64_t) {
+  __device__ static void addv(State &s, v4f a, v4f b, int64_t) {
     s.x = fmaf(a.x, b.x, s.x);
     s.y = fmaf(a.y, b.y, s.y);
     s.z = fmaf(a.z, b.z, s.z);
@@ -81,11 +116,13 @@ struct SdotOp {
 };
 
 struct SasumOp {
+  typedef float Elem;
+  typedef v4f V;
   static constexpr int NIN = 1;
   typedef v4f State;
   typedef float Partial;
   __device__ static State init() { return v4f{0.f, 0.f, 0.f, 0.f}; }
-  __device__ static void add4(State &s, v4f a, v4f, int64_t) {
+  __device__ static void addv(State &s, v4f a, v4f, int64_t) {
     s.x += fabsf(a.x);
     s.y += fabsf(a.y);
     s.z += fabsf(a.z);
@@ -119,11 +156,13 @@ __device__ __forceinline__ void nrm_accum(Nrm &s, float v) {
 }
 
 struct Snrm2Op {
+  typedef float Elem;
+  typedef v4f V;
   static constexpr int NIN = 1;
   typedef Nrm State;
   typedef v4f Partial;  // (big, medium, small, 0)
   __device__ static State init() { return Nrm{0.f, 0.f, 0.f}; }
-  __device__ static void add4(State &s, v4f a, v4f, int64_t) {
+  __device__ static void addv(State &s, v4f a, v4f, int64_t) {
     // Whole-wave fast path: when every lane's four |x| lie in
     // [TSML, TBIG], the squares go straight into the medium sum. (min/max
     // skip NaN, which then takes the fast path into the medium sum, exactly
@@ -173,11 +212,13 @@ __device__ __forceinline__ void amax_step(AmaxPartial &s, float v, int64_t i) {
 }
 
 struct IsamaxOp {
+  typedef float Elem;
+  typedef v4f V;
   static constexpr int NIN = 1;
   typedef AmaxPartial State;
   typedef AmaxPartial Partial;
   __device__ static State init() { return AmaxPartial{-1.0f, 0.f, 0}; }
-  __device__ static void add4(State &s, v4f a, v4f, int64_t i) {
+  __device__ static void addv(State &s, v4f a, v4f, int64_t i) {
     // max|x| of the four first (v_max ignores a NaN operand, so NaN never
     // wins); only a vector that beats the running best is searched, for
     // its first element equal to that max.
@@ -196,6 +237,139 @@ struct IsamaxOp {
   }
   __device__ static Partial shfl(Partial a, int off) {
     return AmaxPartial{__shfl_xor(a.val, off, 64), 0.f, __shfl_xor(a.idx, off, 64)};
+  }
+  typedef int64_t Result;
+  __device__ static Result result(Partial p) { return p.idx; }
+};
+
+// ---- fp64 policies ---------------------------------------------------------
+
+struct DdotOp {
+  typedef double Elem;
+  typedef v2d V;
+  static constexpr int NIN = 2;
+  typedef v2d State;
+  typedef double Partial;
+  __device__ static State init() { return v2d{0.0, 0.0}; }
+  __device__ static void addv(State &s, v2d a, v2d b, int64_t) {
+    s.x = fma(a.x, b.x, s.x);
+    s.y = fma(a.y, b.y, s.y);
+  }
+  __device__ static void add1(State &s, double a, double b, int64_t, int c) {
+    s[c & 1] = fma(a, b, s[c & 1]);
+  }
+  __device__ static Partial finish(State s) { return s.x + s.y; }
+  __device__ static Partial identity() { return 0.0; }
+  __device__ static Partial merge(Partial a, Partial b) { return a + b; }
+  __device__ static Partial shfl(Partial a, int off) { return __shfl_xor(a, off, 64); }
+  typedef double Result;
+  __device__ static Result result(Partial p) { return p; }
+};
+
+struct DasumOp {
+  typedef double Elem;
+  typedef v2d V;
+  static constexpr int NIN = 1;
+  typedef v2d State;
+  typedef double Partial;
+  __device__ static State init() { return v2d{0.0, 0.0}; }
+  __device__ static void addv(State &s, v2d a, v2d, int64_t) {
+    s.x += fabs(a.x);
+    s.y += fabs(a.y);
+  }
+  __device__ static void add1(State &s, double a, double, int64_t, int c) { s[c & 1] += fabs(a); }
+  __device__ static Partial finish(State s) { return s.x + s.y; }
+  __device__ static Partial identity() { return 0.0; }
+  __device__ static Partial merge(Partial a, Partial b) { return a + b; }
+  __device__ static Partial shfl(Partial a, int off) { return __shfl_xor(a, off, 64); }
+  typedef double Result;
+  __device__ static Result result(Partial p) { return p; }
+};
+
+struct NrmD {
+  double big, med, sml;
+};
+
+// dnrm2's classification, as nrm_accum with LAPACK's double constants: NaN
+// fails both tests and lands in medium; Inf lands in big.
+__device__ __forceinline__ void nrmd_accum(NrmD &s, double v) {
+  double ax = fabs(v);
+  bool big = ax > kDTbig;
+  bool sml = ax < kDTsml;
+  double yb = ax * kDSbig;
+  double ys = ax * kDSsml;
+  s.big = big ? fma(yb, yb, s.big) : s.big;
+  s.med = (big || sml) ? s.med : fma(ax, ax, s.med);
+  s.sml = sml ? fma(ys, ys, s.sml) : s.sml;
+}
+
+struct Dnrm2Op {
+  typedef double Elem;
+  typedef v2d V;
+  static constexpr int NIN = 1;
+  typedef NrmD State;
+  typedef v4d Partial;  // (big, medium, small, 0)
+  __device__ static State init() { return NrmD{0.0, 0.0, 0.0}; }
+  __device__ static void addv(State &s, v2d a, v2d, int64_t) {
+    // Whole-wave fast path as in snrm2 (min/max skip NaN, which then goes
+    // to the medium sum, where the classification puts it).
+    const double hi = fmax(fabs(a.x), fabs(a.y));
+    const double lo = fmin(fabs(a.x), fabs(a.y));
+    const bool odd = !(hi <= kDTbig) || lo < kDTsml;
+    if (__any(odd)) {
+      nrmd_accum(s, a.x);
+      nrmd_accum(s, a.y);
+    } else {
+      s.med = fma(a.x, a.x, s.med);
+      s.med = fma(a.y, a.y, s.med);
+    }
+  }
+  __device__ static void add1(State &s, double a, double, int64_t, int) { nrmd_accum(s, a); }
+  __device__ static Partial finish(State s) { return v4d{s.big, s.med, s.sml, 0.0}; }
+  __device__ static Partial identity() { return v4d{0.0, 0.0, 0.0, 0.0}; }
+  __device__ static Partial merge(Partial a, Partial b) { return a + b; }
+  __device__ static Partial shfl(Partial a, int off) {
+    return v4d{__shfl_xor(a.x, off, 64), __shfl_xor(a.y, off, 64), __shfl_xor(a.z, off, 64), 0.0};
+  }
+  typedef double Result;
+  __device__ static Result result(Partial p);  // LAPACK combine, defined below
+};
+
+struct AmaxPartialD {
+  double val;
+  int64_t idx;
+};
+
+// idamax: isamax's rules on doubles (strict '>', -1 sentinel, NaN never
+// selected, lower index on ties).
+struct IdamaxOp {
+  typedef double Elem;
+  typedef v2d V;
+  static constexpr int NIN = 1;
+  typedef AmaxPartialD State;
+  typedef AmaxPartialD Partial;
+  __device__ static State init() { return AmaxPartialD{-1.0, 0}; }
+  __device__ static void addv(State &s, v2d a, v2d, int64_t i) {
+    const double m = fmax(fabs(a.x), fabs(a.y));
+    if (m > s.val) {
+      s.idx = i + (fabs(a.x) == m ? 0 : 1);
+      s.val = m;
+    }
+  }
+  __device__ static void add1(State &s, double a, double, int64_t i, int) {
+    const double ax = fabs(a);
+    if (ax > s.val) {
+      s.val = ax;
+      s.idx = i;
+    }
+  }
+  __device__ static Partial finish(State s) { return s; }
+  __device__ static Partial identity() { return AmaxPartialD{-1.0, 0}; }
+  __device__ static Partial merge(Partial a, Partial b) {
+    return (b.val > a.val || (b.val == a.val && b.idx < a.idx)) ? b : a;
+  }
+  __device__ static Partial shfl(Partial a, int off) {
+    return AmaxPartialD{__shfl_xor(a.val, off, 64), __shfl_xor(a.idx, off, 64)};
   }
   typedef int64_t Result;
   __device__ static Result result(Partial p) { return p.idx; }
@@ -241,33 +415,36 @@ __device__ __forceinline__ void finish(typename Op::Partial p, typename Op::Part
 // Unit-stride, 16-byte-aligned operands: 16-byte non-temporal loads,
 // kUnroll of them in flight per lane per input.
 template <class Op>
-__global__ __launch_bounds__(kThreads) void reduce_vec(const float *__restrict__ x,
-                                                       const float *__restrict__ y, int64_t n,
+__global__ __launch_bounds__(kThreads) void reduce_vec(const typename Op::Elem *__restrict__ x,
+                                                       const typename Op::Elem *__restrict__ y, int64_t n,
                                                        typename Op::Partial *__restrict__ partials) {
-  const v4f *x4 = reinterpret_cast<const v4f *>(x);
-  const v4f *y4 = reinterpret_cast<const v4f *>(y);
-  const int64_t n4 = n >> 2;
+  typedef typename Op::V V;
+  constexpr int W = Vec16<typename Op::Elem>::W;
+  const V *xv = reinterpret_cast<const V *>(x);
+  const V *yv = reinterpret_cast<const V *>(y);
+  const int64_t nv = n / W;
   int64_t beg, end;
-  chunk_of(n4, beg, end);
+  chunk_of(nv, beg, end);
   typename Op::State s = Op::init();
   int64_t q = beg + threadIdx.x;
   for (; q + (kUnroll - 1) * kThreads < end; q += kUnroll * kThreads) {
-    v4f a[kUnroll], b[kUnroll];
+    V a[kUnroll], b[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      a[u] = nt_load(x4 + q + u * kThreads);
-      b[u] = Op::NIN == 2 ? nt_load(y4 + q + u * kThreads) : a[u];
+      a[u] = nt_load(xv + q + u * kThreads);
+      b[u] = Op::NIN == 2 ? nt_load(yv + q + u * kThreads) : a[u];
     }
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) Op::add4(s, a[u], b[u], 4 * (q + u * kThreads));
+    for (int u = 0; u < kUnroll; ++u) Op::addv(s, a[u], b[u], W * (q + u * kThreads));
   }
   for (; q < end; q += kThreads) {
-    v4f a = x4[q];
-    Op::add4(s, a, Op::NIN == 2 ? y4[q] : a, 4 * q);
+    V a = xv[q];
+    Op::addv(s, a, Op::NIN == 2 ? yv[q] : a, W * q);
   }
-  // The n % 4 trailing elements follow the last block's range.
+  // The n % W trailing elements follow the last block's range.
   if (blockIdx.x == gridDim.x - 1 && threadIdx.x == 0)
-    for (int64_t i = n4 * 4; i < n; ++i) Op::add1(s, x[i], Op::NIN == 2 ? y[i] : 0.f, i, 0);
+    for (int64_t i = nv * W; i < n; ++i)
+      Op::add1(s, x[i], Op::NIN == 2 ? y[i] : (typename Op::Elem)0, i, 0);
   finish<Op>(block_merge<Op>(Op::finish(s)), partials);
 }
 
@@ -276,69 +453,73 @@ __global__ __launch_bounds__(kThreads) void reduce_vec(const float *__restrict__
 // INC-th element. The span's lines are fetched either way, so this trades
 // nothing in HBM bytes for far fewer, wider load instructions.
 template <class Op, int INC>
-__global__ __launch_bounds__(kThreads) void reduce_span(const float *__restrict__ x,
-                                                        const float *__restrict__ y, int64_t n,
+__global__ __launch_bounds__(kThreads) void reduce_span(const typename Op::Elem *__restrict__ x,
+                                                        const typename Op::Elem *__restrict__ y, int64_t n,
                                                         typename Op::Partial *__restrict__ partials) {
-  const v4f *x4 = reinterpret_cast<const v4f *>(x);
-  const v4f *y4 = reinterpret_cast<const v4f *>(y);
+  typedef typename Op::V V;
+  constexpr int W = Vec16<typename Op::Elem>::W;
+  const V *xv = reinterpret_cast<const V *>(x);
+  const V *yv = reinterpret_cast<const V *>(y);
   const uint32_t span = (uint32_t)((n - 1) * INC + 1);  // host checks span < 2^31
-  const int64_t n4 = span >> 2;
+  const int64_t nv = span / W;
   int64_t beg, end;
-  chunk_of(n4, beg, end);
+  chunk_of(nv, beg, end);
   typename Op::State s = Op::init();
   uint32_t q = (uint32_t)(beg + threadIdx.x);
   for (; q + (kUnroll - 1) * kThreads < (uint32_t)end; q += kUnroll * kThreads) {
-    v4f a[kUnroll], b[kUnroll];
+    V a[kUnroll], b[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      a[u] = nt_load(x4 + q + u * kThreads);
-      b[u] = Op::NIN == 2 ? nt_load(y4 + q + u * kThreads) : a[u];
+      a[u] = nt_load(xv + q + u * kThreads);
+      b[u] = Op::NIN == 2 ? nt_load(yv + q + u * kThreads) : a[u];
     }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u)
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const uint32_t e = 4 * (q + u * kThreads) + c;
+      for (int c = 0; c < W; ++c) {
+        const uint32_t e = W * (q + u * kThreads) + c;
         if (e % INC == 0) Op::add1(s, a[u][c], b[u][c], e / INC, c);
       }
   }
   for (; q < (uint32_t)end; q += kThreads) {
-    v4f a = x4[q];
-    v4f b = Op::NIN == 2 ? y4[q] : a;
+    V a = xv[q];
+    V b = Op::NIN == 2 ? yv[q] : a;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const uint32_t e = 4 * q + c;
+    for (int c = 0; c < W; ++c) {
+      const uint32_t e = W * q + c;
       if (e % INC == 0) Op::add1(s, a[c], b[c], e / INC, c);
     }
   }
   if (blockIdx.x == gridDim.x - 1 && threadIdx.x == 0)
-    for (uint32_t e = (uint32_t)n4 * 4; e < span; ++e)
-      if (e % INC == 0) Op::add1(s, x[e], Op::NIN == 2 ? y[e] : 0.f, e / INC, 0);
+    for (uint32_t e = (uint32_t)nv * W; e < span; ++e)
+      if (e % INC == 0) Op::add1(s, x[e], Op::NIN == 2 ? y[e] : (typename Op::Elem)0, e / INC, 0);
   finish<Op>(block_merge<Op>(Op::finish(s)), partials);
 }
 
 // Any positive strides (and misaligned unit stride): one element per lane
 // per step, kUnroll steps in flight.
 template <class Op>
-__global__ __launch_bounds__(kThreads) void reduce_strided(const float *__restrict__ x, int64_t incx,
-                                                           const float *__restrict__ y, int64_t incy,
-                                                           int64_t n,
+__global__ __launch_bounds__(kThreads) void reduce_strided(const typename Op::Elem *__restrict__ x,
+                                                           int64_t incx,
+                                                           const typename Op::Elem *__restrict__ y,
+                                                           int64_t incy, int64_t n,
                                                            typename Op::Partial *__restrict__ partials) {
+  typedef typename Op::Elem T;
   int64_t beg, end;
   chunk_of(n, beg, end);
   typename Op::State s = Op::init();
   int64_t i = beg + threadIdx.x;
   for (; i + (kUnroll - 1) * kThreads < end; i += kUnroll * kThreads) {
-    float a[kUnroll], b[kUnroll];
+    T a[kUnroll], b[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       a[u] = x[(i + u * kThreads) * incx];
-      b[u] = Op::NIN == 2 ? y[(i + u * kThreads) * incy] : 0.f;
+      b[u] = Op::NIN == 2 ? y[(i + u * kThreads) * incy] : (T)0;
     }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) Op::add1(s, a[u], b[u], i + u * kThreads, u & 3);
   }
-  for (; i < end; i += kThreads) Op::add1(s, x[i * incx], Op::NIN == 2 ? y[i * incy] : 0.f, i, 0);
+  for (; i < end; i += kThreads) Op::add1(s, x[i * incx], Op::NIN == 2 ? y[i * incy] : (T)0, i, 0);
   finish<Op>(block_merge<Op>(Op::finish(s)), partials);
 }
 
@@ -407,6 +588,32 @@ __device__ float nrm_combine(float abig, float amed, float asml) {
 
 __device__ Snrm2Op::Result Snrm2Op::result(Partial p) { return nrm_combine(p.x, p.y, p.z); }
 
+// LAPACK 3.10's dnrm2 combine of the three sums (a NaN medium sum gives NaN
+// first, as snrm2's; an Inf lands in the big sum and gives Inf).
+__device__ double nrmd_combine(double abig, double amed, double asml) {
+  if (isnan(amed)) return amed;
+  double scl = 1.0, sumsq = amed;
+  if (abig > 0.0) {
+    if (amed > 0.0) abig = abig + (amed * kDSbig) * kDSbig;
+    scl = 1.0 / kDSbig;
+    sumsq = abig;
+  } else if (asml > 0.0) {
+    if (amed > 0.0) {
+      amed = sqrt(amed);
+      asml = sqrt(asml) / kDSsml;
+      double ymax = fmax(asml, amed), ymin = fmin(asml, amed);
+      double q = ymin / ymax;
+      sumsq = ymax * ymax * (1.0 + q * q);
+    } else {
+      scl = 1.0 / kDSsml;
+      sumsq = asml;
+    }
+  }
+  return scl * sqrt(sumsq);
+}
+
+__device__ Dnrm2Op::Result Dnrm2Op::result(Partial p) { return nrmd_combine(p.x, p.y, p.z); }
+
 // Writes the n <= 0 answer of a `_dev` call with a kernel rather than a
 // memset, so the call stays safe to capture in a HIP graph.
 template <typename T>
@@ -416,7 +623,8 @@ __global__ void set_value(T *out, T v) {
 
 // ---- host side -------------------------------------------------------------
 
-int check_vec(int64_t n, const float *x, int64_t incx, const char *xname, const char *incname) {
+template <typename T>
+int check_vec(int64_t n, const T *x, int64_t incx, const char *xname, const char *incname) {
   if (incx <= 0)
     return wgb::fail(WGB_ERR_INVALID_VALUE, std::string(incname) + " must be positive");
   if (n > 0 && !x) return wgb::fail(WGB_ERR_INVALID_VALUE, std::string(xname) + " is null");
@@ -424,11 +632,16 @@ int check_vec(int64_t n, const float *x, int64_t incx, const char *xname, const 
 }
 
 void *partials_of(wgb_ctx *ctx) { return ctx->scratch; }
-void *result_slot(wgb_ctx *ctx) { return (char *)ctx->scratch + (size_t)wgb::kMaxReduceBlocks * 16; }
+void *result_slot(wgb_ctx *ctx) {
+  return (char *)ctx->scratch + (size_t)wgb::kMaxReduceBlocks * kPartialBytes;
+}
+
 // Stage 1 (the read pass) and stage 2 (the fold), two launches on the stream.
 template <class Op>
-int launch_reduce(wgb_ctx *ctx, int64_t n, const float *x, int64_t incx, const float *y,
-                  int64_t incy, typename Op::Result *d_out, const char *what) {
+int launch_reduce(wgb_ctx *ctx, int64_t n, const typename Op::Elem *x, int64_t incx,
+                  const typename Op::Elem *y, int64_t incy, typename Op::Result *d_out,
+                  const char *what) {
+  static_assert(sizeof(typename Op::Partial) <= kPartialBytes, "partial slot too small");
   const int G = reduce_blocks(n);
   auto *part = (typename Op::Partial *)partials_of(ctx);
   int Gl = G;
@@ -454,23 +667,6 @@ int launch_reduce(wgb_ctx *ctx, int64_t n, const float *x, int64_t incx, const f
   return WGB_OK;
 }
 
-int launch_sdot(wgb_ctx *ctx, int64_t n, const float *x, int64_t incx, const float *y,
-                int64_t incy, float *d_out) {
-  return launch_reduce<SdotOp>(ctx, n, x, incx, y, incy, d_out, "sdot");
-}
-
-int launch_sasum(wgb_ctx *ctx, int64_t n, const float *x, int64_t incx, float *d_out) {
-  return launch_reduce<SasumOp>(ctx, n, x, incx, x, incx, d_out, "sasum");
-}
-
-int launch_snrm2(wgb_ctx *ctx, int64_t n, const float *x, int64_t incx, float *d_out) {
-  return launch_reduce<Snrm2Op>(ctx, n, x, incx, x, incx, d_out, "snrm2");
-}
-
-int launch_isamax(wgb_ctx *ctx, int64_t n, const float *x, int64_t incx, int64_t *d_out) {
-  return launch_reduce<IsamaxOp>(ctx, n, x, incx, x, incx, d_out, "isamax");
-}
-
 // Copies a device scalar into the context's pinned slot and waits for it.
 template <typename T>
 int fetch_scalar(wgb_ctx *ctx, const T *d_src, T *host_dst) {
@@ -481,131 +677,133 @@ int fetch_scalar(wgb_ctx *ctx, const T *d_src, T *host_dst) {
   return WGB_OK;
 }
 
-}  // namespace
-
-extern "C" int wgb_sdot_dev(wgb_ctx *ctx, int64_t n, const float *x, int64_t incx, const float *y,
-                            int64_t incy, float *d_result) {
+// The `_dev` form: result written to device memory, n <= 0 gives `empty`
+// (set by a kernel, so the call stays graph-capturable). y == nullptr for
+// the one-vector routines.
+template <class Op>
+int reduce_to_device(wgb_ctx *ctx, int64_t n, const typename Op::Elem *x, int64_t incx,
+                     const typename Op::Elem *y, int64_t incy, typename Op::Result *d_result,
+                     typename Op::Result empty, const char *what) {
   int st = wgb::enter(ctx);
   if (st) return st;
   if ((st = check_vec(n, x, incx, "x", "incx"))) return st;
-  if ((st = check_vec(n, y, incy, "y", "incy"))) return st;
+  if (Op::NIN == 2 && (st = check_vec(n, y, incy, "y", "incy"))) return st;
   if (!d_result) return wgb::fail(WGB_ERR_INVALID_VALUE, "d_result is null");
+  if (Op::NIN == 1) {
+    y = x;
+    incy = incx;
+  }
   wgb::timing_begin(ctx);
   if (n <= 0)
-    set_value<<<1, 1, 0, ctx->stream>>>(d_result, 0.0f);
-  else if ((st = launch_sdot(ctx, n, x, incx, y, incy, d_result)))
+    set_value<<<1, 1, 0, ctx->stream>>>(d_result, empty);
+  else if ((st = launch_reduce<Op>(ctx, n, x, incx, y, incy, d_result, what)))
     return st;
   wgb::timing_end(ctx);
   return WGB_OK;
+}
+
+// The host-result form: n <= 0 returns `empty` without touching the device.
+template <class Op>
+int reduce_to_host(wgb_ctx *ctx, int64_t n, const typename Op::Elem *x, int64_t incx,
+                   const typename Op::Elem *y, int64_t incy, typename Op::Result *result,
+                   typename Op::Result empty, const char *what) {
+  int st = wgb::enter(ctx);
+  if (st) return st;
+  if ((st = check_vec(n, x, incx, "x", "incx"))) return st;
+  if (Op::NIN == 2 && (st = check_vec(n, y, incy, "y", "incy"))) return st;
+  if (!result) return wgb::fail(WGB_ERR_INVALID_VALUE, "result is null");
+  if (n <= 0) {
+    *result = empty;
+    return WGB_OK;
+  }
+  if (Op::NIN == 1) {
+    y = x;
+    incy = incx;
+  }
+  auto *slot = (typename Op::Result *)result_slot(ctx);
+  wgb::timing_begin(ctx);
+  if ((st = launch_reduce<Op>(ctx, n, x, incx, y, incy, slot, what))) return st;
+  wgb::timing_end(ctx);
+  return fetch_scalar(ctx, slot, result);
+}
+
+}  // namespace
+
+// ---- fp32 ---------------------------------------------------------------
+
+extern "C" int wgb_sdot_dev(wgb_ctx *ctx, int64_t n, const float *x, int64_t incx, const float *y,
+                            int64_t incy, float *d_result) {
+  return reduce_to_device<SdotOp>(ctx, n, x, incx, y, incy, d_result, 0.0f, "sdot");
 }
 
 extern "C" int wgb_sdot(wgb_ctx *ctx, int64_t n, const float *x, int64_t incx, const float *y,
                         int64_t incy, float *result) {
-  int st = wgb::enter(ctx);
-  if (st) return st;
-  if ((st = check_vec(n, x, incx, "x", "incx"))) return st;
-  if ((st = check_vec(n, y, incy, "y", "incy"))) return st;
-  if (!result) return wgb::fail(WGB_ERR_INVALID_VALUE, "result is null");
-  if (n <= 0) {
-    *result = 0.0f;
-    return WGB_OK;
-  }
-  float *slot = (float *)result_slot(ctx);
-  wgb::timing_begin(ctx);
-  if ((st = launch_sdot(ctx, n, x, incx, y, incy, slot))) return st;
-  wgb::timing_end(ctx);
-  return fetch_scalar(ctx, slot, result);
+  return reduce_to_host<SdotOp>(ctx, n, x, incx, y, incy, result, 0.0f, "sdot");
 }
 
 extern "C" int wgb_sasum_dev(wgb_ctx *ctx, int64_t n, const float *x, int64_t incx,
                              float *d_result) {
-  int st = wgb::enter(ctx);
-  if (st) return st;
-  if ((st = check_vec(n, x, incx, "x", "incx"))) return st;
-  if (!d_result) return wgb::fail(WGB_ERR_INVALID_VALUE, "d_result is null");
-  wgb::timing_begin(ctx);
-  if (n <= 0)
-    set_value<<<1, 1, 0, ctx->stream>>>(d_result, 0.0f);
-  else if ((st = launch_sasum(ctx, n, x, incx, d_result)))
-    return st;
-  wgb::timing_end(ctx);
-  return WGB_OK;
+  return reduce_to_device<SasumOp>(ctx, n, x, incx, nullptr, 0, d_result, 0.0f, "sasum");
 }
 
 extern "C" int wgb_sasum(wgb_ctx *ctx, int64_t n, const float *x, int64_t incx, float *result) {
-  int st = wgb::enter(ctx);
-  if (st) return st;
-  if ((st = check_vec(n, x, incx, "x", "incx"))) return st;
-  if (!result) return wgb::fail(WGB_ERR_INVALID_VALUE, "result is null");
-  if (n <= 0) {
-    *result = 0.0f;
-    return WGB_OK;
-  }
-  float *slot = (float *)result_slot(ctx);
-  wgb::timing_begin(ctx);
-  if ((st = launch_sasum(ctx, n, x, incx, slot))) return st;
-  wgb::timing_end(ctx);
-  return fetch_scalar(ctx, slot, result);
+  return reduce_to_host<SasumOp>(ctx, n, x, incx, nullptr, 0, result, 0.0f, "sasum");
 }
 
 extern "C" int wgb_snrm2_dev(wgb_ctx *ctx, int64_t n, const float *x, int64_t incx,
                              float *d_result) {
-  int st = wgb::enter(ctx);
-  if (st) return st;
-  if ((st = check_vec(n, x, incx, "x", "incx"))) return st;
-  if (!d_result) return wgb::fail(WGB_ERR_INVALID_VALUE, "d_result is null");
-  wgb::timing_begin(ctx);
-  if (n <= 0)
-    set_value<<<1, 1, 0, ctx->stream>>>(d_result, 0.0f);
-  else if ((st = launch_snrm2(ctx, n, x, incx, d_result)))
-    return st;
-  wgb::timing_end(ctx);
-  return WGB_OK;
+  return reduce_to_device<Snrm2Op>(ctx, n, x, incx, nullptr, 0, d_result, 0.0f, "snrm2");
 }
 
 extern "C" int wgb_snrm2(wgb_ctx *ctx, int64_t n, const float *x, int64_t incx, float *result) {
-  int st = wgb::enter(ctx);
-  if (st) return st;
-  if ((st = check_vec(n, x, incx, "x", "incx"))) return st;
-  if (!result) return wgb::fail(WGB_ERR_INVALID_VALUE, "result is null");
-  if (n <= 0) {
-    *result = 0.0f;
-    return WGB_OK;
-  }
-  float *slot = (float *)result_slot(ctx);
-  wgb::timing_begin(ctx);
-  if ((st = launch_snrm2(ctx, n, x, incx, slot))) return st;
-  wgb::timing_end(ctx);
-  return fetch_scalar(ctx, slot, result);
+  return reduce_to_host<Snrm2Op>(ctx, n, x, incx, nullptr, 0, result, 0.0f, "snrm2");
 }
 
 extern "C" int wgb_isamax_dev(wgb_ctx *ctx, int64_t n, const float *x, int64_t incx,
                               int64_t *d_result) {
-  int st = wgb::enter(ctx);
-  if (st) return st;
-  if ((st = check_vec(n, x, incx, "x", "incx"))) return st;
-  if (!d_result) return wgb::fail(WGB_ERR_INVALID_VALUE, "d_result is null");
-  wgb::timing_begin(ctx);
-  if (n <= 0)
-    set_value<<<1, 1, 0, ctx->stream>>>(d_result, (int64_t)-1);
-  else if ((st = launch_isamax(ctx, n, x, incx, d_result)))
-    return st;
-  wgb::timing_end(ctx);
-  return WGB_OK;
+  return reduce_to_device<IsamaxOp>(ctx, n, x, incx, nullptr, 0, d_result, (int64_t)-1, "isamax");
 }
 
 extern "C" int wgb_isamax(wgb_ctx *ctx, int64_t n, const float *x, int64_t incx, int64_t *result) {
-  int st = wgb::enter(ctx);
-  if (st) return st;
-  if ((st = check_vec(n, x, incx, "x", "incx"))) return st;
-  if (!result) return wgb::fail(WGB_ERR_INVALID_VALUE, "result is null");
-  if (n <= 0) {
-    *result = -1;
-    return WGB_OK;
-  }
-  int64_t *slot = (int64_t *)result_slot(ctx);
-  wgb::timing_begin(ctx);
-  if ((st = launch_isamax(ctx, n, x, incx, slot))) return st;
-  wgb::timing_end(ctx);
-  return fetch_scalar(ctx, slot, result);
+  return reduce_to_host<IsamaxOp>(ctx, n, x, incx, nullptr, 0, result, (int64_t)-1, "isamax");
+}
+
+// ---- fp64 ---------------------------------------------------------------
+
+extern "C" int wgb_ddot_dev(wgb_ctx *ctx, int64_t n, const double *x, int64_t incx,
+                            const double *y, int64_t incy, double *d_result) {
+  return reduce_to_device<DdotOp>(ctx, n, x, incx, y, incy, d_result, 0.0, "ddot");
+}
+
+extern "C" int wgb_ddot(wgb_ctx *ctx, int64_t n, const double *x, int64_t incx, const double *y,
+                        int64_t incy, double *result) {
+  return reduce_to_host<DdotOp>(ctx, n, x, incx, y, incy, result, 0.0, "ddot");
+}
+
+extern "C" int wgb_dasum_dev(wgb_ctx *ctx, int64_t n, const double *x, int64_t incx,
+                             double *d_result) {
+  return reduce_to_device<DasumOp>(ctx, n, x, incx, nullptr, 0, d_result, 0.0, "dasum");
+}
+
+extern "C" int wgb_dasum(wgb_ctx *ctx, int64_t n, const double *x, int64_t incx, double *result) {
+  return reduce_to_host<DasumOp>(ctx, n, x, incx, nullptr, 0, result, 0.0, "dasum");
+}
+
+extern "C" int wgb_dnrm2_dev(wgb_ctx *ctx, int64_t n, const double *x, int64_t incx,
+                             double *d_result) {
+  return reduce_to_device<Dnrm2Op>(ctx, n, x, incx, nullptr, 0, d_result, 0.0, "dnrm2");
+}
+
+extern "C" int wgb_dnrm2(wgb_ctx *ctx, int64_t n, const double *x, int64_t incx, double *result) {
+  return reduce_to_host<Dnrm2Op>(ctx, n, x, incx, nullptr, 0, result, 0.0, "dnrm2");
+}
+
+extern "C" int wgb_idamax_dev(wgb_ctx *ctx, int64_t n, const double *x, int64_t incx,
+                              int64_t *d_result) {
+  return reduce_to_device<IdamaxOp>(ctx, n, x, incx, nullptr, 0, d_result, (int64_t)-1, "idamax");
+}
+
+extern "C" int wgb_idamax(wgb_ctx *ctx, int64_t n, const double *x, int64_t incx,
+                          int64_t *result) {
+  return reduce_to_host<IdamaxOp>(ctx, n, x, incx, nullptr, 0, result, (int64_t)-1, "idamax");
 }

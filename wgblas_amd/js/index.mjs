@@ -15,3 +15,7 @@ export { sdot } from "./src/sdot.mjs";
 export { sasum } from "./src/sasum.mjs";
 export { snrm2 } from "./src/snrm2.mjs";
 export { isamax } from "./src/isamax.mjs";
+export { ddot } from "./src/ddot.mjs";
+export { dasum } from "./src/dasum.mjs";
+export { dnrm2 } from "./src/dnrm2.mjs";
+export { idamax } from "./src/idamax.mjs";

@@ -59,6 +59,14 @@ _SIGNATURES = {
     "wgb_snrm2_dev": [_ptr, _i64, _ptr, _i64, _ptr],
     "wgb_isamax": [_ptr, _i64, _ptr, _i64, C.POINTER(_i64)],
     "wgb_isamax_dev": [_ptr, _i64, _ptr, _i64, _ptr],
+    "wgb_ddot": [_ptr, _i64, _ptr, _i64, _ptr, _i64, C.POINTER(C.c_double)],
+    "wgb_ddot_dev": [_ptr, _i64, _ptr, _i64, _ptr, _i64, _ptr],
+    "wgb_dasum": [_ptr, _i64, _ptr, _i64, C.POINTER(C.c_double)],
+    "wgb_dasum_dev": [_ptr, _i64, _ptr, _i64, _ptr],
+    "wgb_dnrm2": [_ptr, _i64, _ptr, _i64, C.POINTER(C.c_double)],
+    "wgb_dnrm2_dev": [_ptr, _i64, _ptr, _i64, _ptr],
+    "wgb_idamax": [_ptr, _i64, _ptr, _i64, C.POINTER(_i64)],
+    "wgb_idamax_dev": [_ptr, _i64, _ptr, _i64, _ptr],
 }
 _RESTYPES = {
     "wgb_stream": _ptr,
@@ -283,6 +291,41 @@ class Context:
 
     def isamax_dev(self, n, x, incx, out):
         _check(self.lib.wgb_isamax_dev(self.handle, n, _p(x), incx, _p(out)), "wgb_isamax_dev")
+
+    # ---- fp64 level 1 ----
+    def ddot(self, n, x, incx, y, incy):
+        r = C.c_double(0)
+        _check(self.lib.wgb_ddot(self.handle, n, _p(x), incx, _p(y), incy, C.byref(r)),
+               "wgb_ddot")
+        return float(r.value)
+
+    def ddot_dev(self, n, x, incx, y, incy, out):
+        _check(self.lib.wgb_ddot_dev(self.handle, n, _p(x), incx, _p(y), incy, _p(out)),
+               "wgb_ddot_dev")
+
+    def dasum(self, n, x, incx):
+        r = C.c_double(0)
+        _check(self.lib.wgb_dasum(self.handle, n, _p(x), incx, C.byref(r)), "wgb_dasum")
+        return float(r.value)
+
+    def dasum_dev(self, n, x, incx, out):
+        _check(self.lib.wgb_dasum_dev(self.handle, n, _p(x), incx, _p(out)), "wgb_dasum_dev")
+
+    def dnrm2(self, n, x, incx):
+        r = C.c_double(0)
+        _check(self.lib.wgb_dnrm2(self.handle, n, _p(x), incx, C.byref(r)), "wgb_dnrm2")
+        return float(r.value)
+
+    def dnrm2_dev(self, n, x, incx, out):
+        _check(self.lib.wgb_dnrm2_dev(self.handle, n, _p(x), incx, _p(out)), "wgb_dnrm2_dev")
+
+    def idamax(self, n, x, incx):
+        r = _i64(0)
+        _check(self.lib.wgb_idamax(self.handle, n, _p(x), incx, C.byref(r)), "wgb_idamax")
+        return int(r.value)
+
+    def idamax_dev(self, n, x, incx, out):
+        _check(self.lib.wgb_idamax_dev(self.handle, n, _p(x), incx, _p(out)), "wgb_idamax_dev")
 
 
 def _p(x):

@@ -17,7 +17,8 @@ Also reported under "components", each timed the same way: sgemm 512^3
 n = 8192, k = 4096, 10 chained resident calls (config 5), and sdot / sasum /
 snrm2 / isamax at n = 2^28 plus the incx = 3, n = 2^26 variants (config 2),
 sgemmtr on config 5's operands, and ddot / dasum / dnrm2 / idamax at n = 2^27
-(the same bytes as config 2's fp32 vectors).
+(the same bytes as config 2's fp32 vectors; uniform[-1, 1) inputs, seeds 1
+and 2, as wgblas's randomFloat64Array).
 
 `roofline` is for the headline kernel: algorithmic flops per launch (2mnk)
 over the mean launch duration measured with events around each launch,
@@ -247,8 +248,8 @@ def bench_components(ctx, ev, quick):
     # the fp64 reductions over the same bytes: n = 2^27 doubles
     n = 1 << 27
     dx, dy = ctx.empty(n, np.float64), ctx.empty(n, np.float64)
-    ctx.fill_normal(dx, 1)
-    ctx.fill_normal(dy, 2)
+    ctx.fill_uniform(dx, -1.0, 1.0, 1)
+    ctx.fill_uniform(dy, -1.0, 1.0, 2)
     out = ctx.empty(4, np.float64)
     red = {
         "ddot": (lambda nn: ctx.ddot_dev(nn, dx, 1, dy, 1, out), 16),

@@ -236,6 +236,87 @@ test("level 1: n <= 0 and NaN rules", async () => {
   assert(Number.isNaN((await wg.snrm2(device, big.length, big, 1)).nrm2));
 });
 
+// fp64 level 1 (tests/{ddot,dasum,dnrm2,idamax}/): the reference's bounds
+// around float64 sums (ddot n 2^-48 sum|xy|, dasum 64 ULP by a relative
+// 64 * 2^-52, dnrm2 10 * 2^-48 relative), idamax exact
+const IDAMAX_EXPECT = [0, 0, 1, 1, 0, 3, 0, 1, 0, 1, 1, 1];
+const D_KEY = { ddot: "dot", dasum: "asum", dnrm2: "nrm2", idamax: "index" };
+function refD(routine, c) {
+  let s = 0;
+  let a = 0;
+  for (let i = 0; i < c.n; i++) {
+    const xv = c.x[i * c.incx];
+    if (routine === "ddot") {
+      s += xv * c.y[i * c.incy];
+      a += Math.abs(xv * c.y[i * c.incy]);
+    } else if (routine === "dasum") s += Math.abs(xv);
+    else s = Math.hypot(s, xv);
+  }
+  if (routine === "ddot") return { want: s, tol: c.n * 2 ** -48 * a };
+  if (routine === "dasum") return { want: s, tol: 64 * 2 ** -52 * s };
+  return { want: s, tol: 10 * 2 ** -48 * s };
+}
+for (const routine of Object.keys(D_KEY)) {
+  fixture(`${routine}.edge-cases`).forEach((c, i) => {
+    test(`${routine}: ${c.label}`, async () => {
+      const x = new Float64Array(c.x);
+      const args = routine === "ddot" ? [c.n, x, c.incx, new Float64Array(c.y), c.incy] : [c.n, x, c.incx];
+      const check = (got, how) => {
+        if (routine === "idamax") return assertEqual(got, IDAMAX_EXPECT[i], how);
+        const { want, tol } = refD(routine, c);
+        assert(Math.abs(got - want) <= tol, `${how}: ${got} vs ${want}`);
+      };
+      check((await wg[routine](device, ...args))[D_KEY[routine]], "host arrays");
+      const gx = wg.GpuVector.from(device, x);
+      const gy = routine === "ddot" ? wg.GpuVector.from(device, new Float64Array(c.y)) : null;
+      try {
+        const res = routine === "ddot" ? await wg.ddot(device, c.n, gx, c.incx, gy, c.incy)
+          : await wg[routine](device, c.n, gx, c.incx);
+        check(res[D_KEY[routine]], "GpuVector");
+      } finally {
+        gx.destroy();
+        if (gy) gy.destroy();
+      }
+    });
+  });
+}
+
+test("fp64 level 1: n <= 0, NaN rules, f64 range, long strided vectors", async () => {
+  const x = wg.randomFloat64Array(8, -1, 1, 300);
+  assertEqual((await wg.ddot(device, 0, x, 1, x, 1)).dot, 0);
+  assertEqual((await wg.dasum(device, 0, x, 1)).asum, 0);
+  assertEqual((await wg.dnrm2(device, 0, x, 1)).nrm2, 0);
+  assertEqual((await wg.idamax(device, 0, x, 1)).index, -1);
+  const N = NaN;
+  const I = Infinity;
+  for (const [arr, want] of [[[1, N, 7, 3], 2], [[N, N, N, N], 0], [[N, I, 2, 3], 1], [[1, -I, 2, 3], 1],
+    [[1e300, 1e301, 5, 1], 1]])
+    assertEqual((await wg.idamax(device, 4, new Float64Array(arr), 1)).index, want, JSON.stringify(arr));
+  assertEqual((await wg.dnrm2(device, 2, new Float64Array([3e300, 4e300]), 1)).nrm2, 5e300);
+  const n = 100003;
+  const inc = 3;
+  const v = wg.randomFloat64Array((n - 1) * inc + 1, -1, 1, 17);
+  const w = wg.randomFloat64Array((n - 1) * inc + 1, -1, 1, 18);
+  const c = { n, x: v, y: w, incx: inc, incy: inc };
+  const gv = wg.GpuVector.from(device, v);
+  const gw = wg.GpuVector.from(device, w);
+  try {
+    for (const routine of ["ddot", "dasum", "dnrm2"]) {
+      const res = routine === "ddot" ? await wg.ddot(device, n, gv, inc, gw, inc) : await wg[routine](device, n, gv, inc);
+      const { want, tol } = refD(routine, c);
+      // long sums: the float64 reference itself carries n 2^-53 relative error
+      const slack = routine === "ddot" ? 0 : n * 2 ** -53 * want;
+      assert(Math.abs(res[D_KEY[routine]] - want) <= tol + slack, `${routine}: ${res[D_KEY[routine]]} vs ${want}`);
+    }
+    let best = 0;
+    for (let i = 1; i < n; i++) if (Math.abs(v[i * inc]) > Math.abs(v[best * inc])) best = i;
+    assertEqual((await wg.idamax(device, n, gv, inc)).index, best);
+  } finally {
+    gv.destroy();
+    gw.destroy();
+  }
+});
+
 // ------------------------------------------------------------ regressions
 for (const layout of ["row-major", "column-major"])
   for (const transA of ["no-transpose", "transpose"])

@@ -41,6 +41,11 @@ typedef enum wgb_status {
 enum { WGB_NO_TRANS = 0, WGB_TRANS = 1 };
 /* uplo arguments: wgblas's 'lower' / 'upper' strings (column-major frame). */
 enum { WGB_LOWER = 1, WGB_UPPER = 2 };
+/* side of the symmetric / triangular operand in ssymm, strmm, strsm */
+enum { WGB_LEFT = 1, WGB_RIGHT = 2 };
+/* diagonal of the triangular operand in strmm, strsm (WGB_UNIT: taken as 1,
+ * never read) */
+enum { WGB_NON_UNIT = 0, WGB_UNIT = 1 };
 
 typedef struct wgb_ctx wgb_ctx;
 
@@ -168,6 +173,43 @@ int wgb_dgemmtr(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m,
 int wgb_dsyrk(wgb_ctx *ctx, int uplo, int trans, int64_t n, int64_t k,
               double alpha, const double *A, int64_t lda, double beta,
               double *C, int64_t ldc);
+
+/* C <- alpha*op(A)*op(B)^T + alpha*op(B)*op(A)^T + beta*C on the uplo
+ * triangle of the n-by-n C; op(X) is n-by-k (trans == WGB_NO_TRANS) or X^T
+ * for a k-by-n X, the same trans for A and B. Two triangle GEMM launches, the
+ * second with beta = 1, as wgblas runs it; alpha == 0 or k == 0 is
+ * C <- beta*C on the triangle without reading A or B.
+ * Replaces ssyr2k (src/ssyr2k/ssyr2k.mjs:27-301). */
+int wgb_ssyr2k(wgb_ctx *ctx, int uplo, int trans, int64_t n, int64_t k,
+               float alpha, const float *A, int64_t lda, const float *B,
+               int64_t ldb, float beta, float *C, int64_t ldc);
+
+/* C <- alpha*A*B + beta*C (side WGB_LEFT, A m-by-m) or alpha*B*A + beta*C
+ * (WGB_RIGHT, A n-by-n); A symmetric, only its uplo triangle is read.
+ * C and B are m-by-n. alpha == 0 reads neither A nor B.
+ * Replaces ssymm (src/ssymm/ssymm.mjs:30-318: symmetrize.wgsl, then sgemm). */
+int wgb_ssymm(wgb_ctx *ctx, int side, int uplo, int64_t m, int64_t n,
+              float alpha, const float *A, int64_t lda, const float *B,
+              int64_t ldb, float beta, float *C, int64_t ldc);
+
+/* B <- alpha*op(A)*B (WGB_LEFT, A m-by-m) or alpha*B*op(A) (WGB_RIGHT,
+ * A n-by-n); A triangular (uplo triangle read; diag WGB_UNIT takes its
+ * diagonal as 1 without reading it). B is m-by-n, overwritten in place;
+ * its ld padding is untouched. alpha == 0 sets B to zero without reading A
+ * or B. Replaces strmm (src/strmm/strmm.mjs:30-344: triangularize.wgsl,
+ * then sgemm with its k band). */
+int wgb_strmm(wgb_ctx *ctx, int side, int uplo, int transA, int diag,
+              int64_t m, int64_t n, float alpha, const float *A, int64_t lda,
+              float *B, int64_t ldb);
+
+/* Solves op(A)*X = alpha*B (WGB_LEFT, A m-by-m) or X*op(A) = alpha*B
+ * (WGB_RIGHT, A n-by-n) for X, overwriting the m-by-n B; A triangular as in
+ * wgb_strmm. Substitution on diagonal blocks of order <= 64, GEMM updates in
+ * between; no explicit inverse. alpha == 0 sets B to zero without reading A
+ * or B. Replaces strsm (src/strsm/strsm.mjs:148-583). */
+int wgb_strsm(wgb_ctx *ctx, int side, int uplo, int transA, int diag,
+              int64_t m, int64_t n, float alpha, const float *A, int64_t lda,
+              float *B, int64_t ldb);
 
 /* ---- level 1 reductions --------------------------------------------------- */
 /* n <= 0 returns 0 (index -1) without touching the device. incx, incy must be

@@ -484,3 +484,170 @@ void orc_sgemm_wgsl(int uplo, int transA, int transB, int64_t m, int64_t n, int6
     }
   }
 }
+
+/* ---- level 3 on the GEMM (src/{ssyr2k,ssymm,strmm,strsm}) ----------------
+ * The reference's tests compare with stdlib's ssyr2k/ssymm/strmm/strsm
+ * (reference BLAS ports) under forward-error bounds (tests/ssyr2k/helpers.js,
+ * tests/ssymm/helpers.js, tests/strmm/helpers.js) or a backward residual
+ * (tests/strsm/helpers.js). These restate the mathematics in long double:
+ * the exact values the bounds are taken around. Matrices are column-major
+ * with leading dimensions; sides and diag as in include/wgblas_hip.h
+ * (side 1 left / 2 right, uplo 1 lower / 2 upper, diag 1 unit). */
+
+/* C <- alpha*(op(A) op(B)^T + op(B) op(A)^T) + beta*C on the uplo triangle
+ * (src/ssyr2k/ssyr2k.mjs:25-26); op(X) is n x k (X n x k stored, trans 0) or
+ * X^T. alpha == 0 reads neither A nor B, beta == 0 never reads C.
+ * absdot1/absdot2 (may be NULL) get sum_p |op(A)[i,p] op(B)[j,p]| and
+ * sum_p |op(B)[i,p] op(A)[j,p]|. Elements outside the triangle keep C. */
+void orc_ssyr2k_ld(int uplo, int trans, int64_t n, int64_t k, double alpha, const double *A,
+                   int64_t lda, const double *B, int64_t ldb, double beta, const double *C,
+                   int64_t ldc, double *out, double *absdot1, double *absdot2) {
+  for (int64_t j = 0; j < n; ++j)
+    for (int64_t i = 0; i < n; ++i) {
+      int64_t o = i + j * ldc;
+      int in_tri = uplo == 1 ? i >= j : i <= j;
+      if (absdot1) absdot1[o] = 0.0;
+      if (absdot2) absdot2[o] = 0.0;
+      if (!in_tri) {
+        out[o] = C[o];
+        continue;
+      }
+      long double s = 0, a1 = 0, a2 = 0;
+      if (alpha != 0.0)
+        for (int64_t p = 0; p < k; ++p) {
+          /* op(X)[r, p] = X[r + p*ld] (trans 0) or X[p + r*ld] */
+          long double ai = trans ? A[p + i * lda] : A[i + p * lda];
+          long double aj = trans ? A[p + j * lda] : A[j + p * lda];
+          long double bi = trans ? B[p + i * ldb] : B[i + p * ldb];
+          long double bj = trans ? B[p + j * ldb] : B[j + p * ldb];
+          s += ai * bj + bi * aj;
+          a1 += fabsl(ai * bj);
+          a2 += fabsl(bi * aj);
+        }
+      long double v = (long double)alpha * s;
+      if (beta != 0.0) v += (long double)beta * C[o];
+      out[o] = (double)v;
+      if (absdot1) absdot1[o] = (double)a1;
+      if (absdot2) absdot2[o] = (double)a2;
+    }
+}
+
+/* The symmetric matrix whose uplo triangle A stores, element (i, k)
+ * (src/shaders/symmetrize.wgsl). */
+static inline long double sym_elem(const double *A, int64_t lda, int uplo, int64_t i, int64_t k) {
+  int stored = uplo == 1 ? i >= k : i <= k;
+  return stored ? A[i + k * lda] : A[k + i * lda];
+}
+
+/* C <- alpha*S*B + beta*C (side 1) or alpha*B*S + beta*C (side 2), S the
+ * symmetric matrix of A's uplo triangle; C, B m x n (src/ssymm/ssymm.mjs:
+ * 27-29). alpha == 0 reads neither A nor B, beta == 0 never reads C. absdot
+ * (may be NULL) gets sum_p |S B| terms. */
+void orc_ssymm_ld(int side, int uplo, int64_t m, int64_t n, double alpha, const double *A,
+                  int64_t lda, const double *B, int64_t ldb, double beta, const double *C,
+                  int64_t ldc, double *out, double *absdot) {
+  int64_t order = side == 1 ? m : n;
+  for (int64_t j = 0; j < n; ++j)
+    for (int64_t i = 0; i < m; ++i) {
+      long double s = 0, a = 0;
+      if (alpha != 0.0)
+        for (int64_t p = 0; p < order; ++p) {
+          long double t = side == 1 ? sym_elem(A, lda, uplo, i, p) * (long double)B[p + j * ldb]
+                                    : (long double)B[i + p * ldb] * sym_elem(A, lda, uplo, p, j);
+          s += t;
+          a += fabsl(t);
+        }
+      long double v = (long double)alpha * s;
+      if (beta != 0.0) v += (long double)beta * C[i + j * ldc];
+      out[i + j * ldc] = (double)v;
+      if (absdot) absdot[i + j * ldc] = (double)a;
+    }
+}
+
+/* op(A)[i, k] of a triangular A: the uplo triangle of A (or of A^T), the
+ * diagonal taken as 1 for a unit triangle; *inside is 0 outside the
+ * triangle (the structural zeros the sums below skip). */
+static inline long double tri_elem(const double *A, int64_t lda, int uplo, int trans, int unit,
+                                   int64_t i, int64_t k, int *inside) {
+  if (i == k) {
+    *inside = 1;
+    return unit ? 1.0L : (long double)A[i + i * lda];
+  }
+  /* op(A) lower iff (uplo lower) != trans */
+  int op_lower = (uplo == 1) != (trans != 0);
+  *inside = op_lower ? i > k : i < k;
+  if (!*inside) return 0.0L;
+  return trans ? A[k + i * lda] : A[i + k * lda];
+}
+
+/* B <- alpha*op(A)*B (side 1) or alpha*B*op(A) (side 2), A triangular
+ * (src/strmm/strmm.mjs:27-29); the sums run over the triangle only, as
+ * reference BLAS's loops do. alpha == 0 gives zeros without reading A or B.
+ * out has B's layout (ldb); its padding is copied from B. absdot (may be
+ * NULL) gets sum_p |op(A) B| terms. */
+void orc_strmm_ld(int side, int uplo, int trans, int unit, int64_t m, int64_t n, double alpha,
+                  const double *A, int64_t lda, const double *B, int64_t ldb, double *out,
+                  double *absdot) {
+  int64_t order = side == 1 ? m : n;
+  for (int64_t j = 0; j < n; ++j)
+    for (int64_t i = 0; i < m; ++i) {
+      long double s = 0, a = 0;
+      if (alpha != 0.0)
+        for (int64_t p = 0; p < order; ++p) {
+          int inside;
+          long double t;
+          if (side == 1) {
+            long double e = tri_elem(A, lda, uplo, trans, unit, i, p, &inside);
+            if (!inside) continue;
+            t = e * (long double)B[p + j * ldb];
+          } else {
+            long double e = tri_elem(A, lda, uplo, trans, unit, p, j, &inside);
+            if (!inside) continue;
+            t = (long double)B[i + p * ldb] * e;
+          }
+          s += t;
+          a += fabsl(t);
+        }
+      out[i + j * ldb] = (double)((long double)alpha * s);
+      if (absdot) absdot[i + j * ldb] = (double)a;
+    }
+}
+
+/* Solves op(A) X = alpha B (side 1) or X op(A) = alpha B (side 2) by
+ * substitution in long double (src/strsm/strsm.mjs:148-151). out holds B on
+ * entry (ldb) and X on return; padding untouched. Per right-hand side the
+ * unknowns go in dependency order, each x = (alpha b - sum of the solved
+ * terms in its row) / diagonal, with no zero skipping (as wgblas's strsm).
+ * alpha == 0 gives zeros without reading A or B. */
+void orc_strsm_ld(int side, int uplo, int trans, int unit, int64_t m, int64_t n, double alpha,
+                  const double *A, int64_t lda, double *out, int64_t ldb) {
+  int64_t order = side == 1 ? m : n, nrhs = side == 1 ? n : m;
+  int op_lower = (uplo == 1) != (trans != 0);
+  /* left: unknown i of rhs r is X[i, r], coupled by op(A)[i, k]; forward iff
+   * op(A) lower. right: unknown i of rhs r is X[r, i], coupled by
+   * op(A)[k, i]; forward iff op(A) upper. */
+  int forward = side == 1 ? op_lower : !op_lower;
+  for (int64_t r = 0; r < nrhs; ++r) {
+    for (int64_t q = 0; q < order; ++q) {
+      int64_t i = forward ? q : order - 1 - q;
+      double *xi = side == 1 ? &out[i + r * ldb] : &out[r + i * ldb];
+      if (alpha == 0.0) {
+        *xi = 0.0;
+        continue;
+      }
+      long double s = (long double)alpha * (long double)*xi;
+      for (int64_t qq = 0; qq < q; ++qq) {
+        int64_t k = forward ? qq : order - 1 - qq;
+        int inside;
+        long double c = side == 1 ? tri_elem(A, lda, uplo, trans, unit, i, k, &inside)
+                                  : tri_elem(A, lda, uplo, trans, unit, k, i, &inside);
+        if (!inside) continue;
+        long double xk = side == 1 ? out[k + r * ldb] : out[r + k * ldb];
+        s -= c * xk;
+      }
+      int inside;
+      long double d = tri_elem(A, lda, uplo, trans, unit, i, i, &inside);
+      *xi = (double)(s / d);
+    }
+  }
+}

@@ -37,6 +37,14 @@ _SIG = {
                            _f64p, _i64, C.c_double, _f64p, _i64, _f64p, _i64, _f64p]),
     "orc_sgemm_wgsl": (None, [C.c_int, C.c_int, C.c_int, _i64, _i64, _i64, C.c_float, _f32p, _i64,
                               _f32p, _i64, C.c_float, _f32p, _i64]),
+    "orc_ssyr2k_ld": (None, [C.c_int, C.c_int, _i64, _i64, C.c_double, _f64p, _i64, _f64p, _i64,
+                             C.c_double, _f64p, _i64, _f64p, _f64p, _f64p]),
+    "orc_ssymm_ld": (None, [C.c_int, C.c_int, _i64, _i64, C.c_double, _f64p, _i64, _f64p, _i64,
+                            C.c_double, _f64p, _i64, _f64p, _f64p]),
+    "orc_strmm_ld": (None, [C.c_int, C.c_int, C.c_int, C.c_int, _i64, _i64, C.c_double, _f64p,
+                            _i64, _f64p, _i64, _f64p, _f64p]),
+    "orc_strsm_ld": (None, [C.c_int, C.c_int, C.c_int, C.c_int, _i64, _i64, C.c_double, _f64p,
+                            _i64, _f64p, _i64]),
 }
 
 _lib = None
@@ -184,4 +192,54 @@ def sgemm_wgsl(uplo, transA, transB, m, n, k, alpha, A, lda, B, ldb, beta, Cin, 
     out = np.array(Cin, dtype=np.float32, copy=True)
     lib().orc_sgemm_wgsl(uplo, transA, transB, m, n, k, alpha, Ap, lda, Bp, ldb, beta,
                          out.ctypes.data_as(_f32p), ldc)
+    return out
+
+
+def ssyr2k_ld(uplo, trans, n, k, alpha, A, lda, B, ldb, beta, Cin, ldc):
+    """Returns (out, absdot1, absdot2), (ldc*n)-long column-major: out holds
+    alpha*(op(A)op(B)^T + op(B)op(A)^T) + beta*C on the uplo triangle (long
+    double), C elsewhere; absdot1 / absdot2 the two products' sum_p |a*b|."""
+    A, Ap = _f64(A if A is not None and len(A) else np.zeros(1))
+    B, Bp = _f64(B if B is not None and len(B) else np.zeros(1))
+    Cin, Cp = _f64(Cin)
+    out = Cin.copy()
+    a1, a2 = np.zeros_like(Cin), np.zeros_like(Cin)
+    lib().orc_ssyr2k_ld(uplo, trans, n, k, alpha, Ap, lda, Bp, ldb, beta, Cp, ldc,
+                        out.ctypes.data_as(_f64p), a1.ctypes.data_as(_f64p),
+                        a2.ctypes.data_as(_f64p))
+    return out, a1, a2
+
+
+def ssymm_ld(side, uplo, m, n, alpha, A, lda, B, ldb, beta, Cin, ldc):
+    """Returns (out, absdot): alpha*S*B + beta*C (side 1) or alpha*B*S +
+    beta*C (side 2), S the symmetric matrix of A's uplo triangle."""
+    A, Ap = _f64(A)
+    B, Bp = _f64(B)
+    Cin, Cp = _f64(Cin)
+    out = Cin.copy()
+    ad = np.zeros_like(Cin)
+    lib().orc_ssymm_ld(side, uplo, m, n, alpha, Ap, lda, Bp, ldb, beta, Cp, ldc,
+                       out.ctypes.data_as(_f64p), ad.ctypes.data_as(_f64p))
+    return out, ad
+
+
+def strmm_ld(side, uplo, trans, unit, m, n, alpha, A, lda, B, ldb):
+    """Returns (out, absdot): alpha*op(A)*B (side 1) or alpha*B*op(A) (side
+    2) over A's triangle, in B's layout (padding copied from B)."""
+    A, Ap = _f64(A)
+    B, Bp = _f64(B)
+    out = B.copy()
+    ad = np.zeros_like(B)
+    lib().orc_strmm_ld(side, uplo, trans, unit, m, n, alpha, Ap, lda, Bp, ldb,
+                       out.ctypes.data_as(_f64p), ad.ctypes.data_as(_f64p))
+    return out, ad
+
+
+def strsm_ld(side, uplo, trans, unit, m, n, alpha, A, lda, B, ldb):
+    """X with op(A) X = alpha B (side 1) or X op(A) = alpha B (side 2), in B's
+    layout (padding copied from B), by long-double substitution."""
+    A, Ap = _f64(A)
+    out = np.array(B, dtype=np.float64, copy=True)
+    lib().orc_strsm_ld(side, uplo, trans, unit, m, n, alpha, Ap, lda,
+                       out.ctypes.data_as(_f64p), ldb)
     return out

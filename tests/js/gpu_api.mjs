@@ -236,6 +236,242 @@ test("level 1: n <= 0 and NaN rules", async () => {
   assert(Number.isNaN((await wg.snrm2(device, big.length, big, 1)).nrm2));
 });
 
+// level 3 on the GEMM (tests/{ssyr2k,ssymm,strmm,strsm}/): double-precision
+// triple loops here; ssyr2k / ssymm / strmm within the reference's forward
+// bounds, strsm by its backward residual (tests/strsm/helpers.js).
+const el = (M, ld, layout, r, c) => (layout === "column-major" ? M[c * ld + r] : M[r * ld + c]);
+const symEl = (A, lda, layout, uplo, r, c) =>
+  (uplo === "lower" ? c <= r : c >= r) ? el(A, lda, layout, r, c) : el(A, lda, layout, c, r);
+function triEl(A, lda, layout, uplo, transA, diag, r, c) {
+  if (r === c) return diag === "unit" ? 1 : el(A, lda, layout, r, r);
+  const lowerOp = (uplo === "lower") !== (transA === "transpose");
+  if (lowerOp ? c > r : c < r) return 0;
+  return transA === "transpose" ? el(A, lda, layout, c, r) : el(A, lda, layout, r, c);
+}
+
+// Expected output buffer and per-element bound of a level-3 call `a`.
+function refLevel3(routine, a) {
+  const layout = a.layout || "row-major";
+  const out = Float64Array.from(routine === "strmm" ? a.B : a.C);
+  const bound = new Float64Array(out.length);
+  const eps = 2 ** -23;
+  const rows = routine === "ssyr2k" ? a.n : a.m;
+  const cols = a.n;
+  for (let i = 0; i < rows; i++)
+    for (let j = 0; j < cols; j++) {
+      let s = 0;
+      let d = 0;
+      let coef;
+      if (routine === "ssyr2k") {
+        if (!inTri(a.uplo, i, j)) continue;
+        const t = a.trans;
+        for (let p = 0; p < a.k; p++) {
+          const v = opElem(a.A, a.lda, layout, t, i, p) * opElem(a.B, a.ldb, layout, t, j, p) +
+            opElem(a.B, a.ldb, layout, t, i, p) * opElem(a.A, a.lda, layout, t, j, p);
+          s += v;
+          d += Math.abs(opElem(a.A, a.lda, layout, t, i, p) * opElem(a.B, a.ldb, layout, t, j, p)) +
+            Math.abs(opElem(a.B, a.ldb, layout, t, i, p) * opElem(a.A, a.lda, layout, t, j, p));
+        }
+        coef = a.k + 3;
+      } else {
+        const order = a.side === "left" ? a.m : a.n;
+        for (let p = 0; p < order; p++) {
+          let v;
+          if (routine === "ssymm")
+            v = a.side === "left" ? symEl(a.A, a.lda, layout, a.uplo, i, p) * el(a.B, a.ldb, layout, p, j)
+              : el(a.B, a.ldb, layout, i, p) * symEl(a.A, a.lda, layout, a.uplo, p, j);
+          else
+            v = a.side === "left" ? triEl(a.A, a.lda, layout, a.uplo, a.transA, a.diag, i, p) * el(a.B, a.ldb, layout, p, j)
+              : el(a.B, a.ldb, layout, i, p) * triEl(a.A, a.lda, layout, a.uplo, a.transA, a.diag, p, j);
+          s += v;
+          d += Math.abs(v);
+        }
+        coef = order + 1;
+      }
+      const ld = routine === "strmm" ? a.ldb : a.ldc;
+      const idx = cIndex(ld, layout, i, j);
+      const cin = routine === "strmm" ? 0 : a.C[idx];
+      out[idx] = (a.alpha === 0 ? 0 : a.alpha * s) + (routine === "strmm" || a.beta === 0 ? 0 : a.beta * cin);
+      bound[idx] = eps * (coef * Math.abs(a.alpha) * d + (routine === "strmm" ? 0 : 3 * Math.abs(a.beta) * Math.abs(cin)));
+      bound[idx] += 1e-300;  // marks the element as computed
+    }
+  return { out, bound };
+}
+
+function checkLevel3(routine, got, a) {
+  const { out, bound } = refLevel3(routine, a);
+  const orig = routine === "strmm" ? a.B : a.C;
+  for (let i = 0; i < out.length; i++) {
+    if (bound[i] === 0) assert(Object.is(got[i], orig[i]), `${routine}: element ${i} outside the output changed`);
+    else assert(Math.abs(got[i] - out[i]) <= bound[i], `${routine}: element ${i} = ${got[i]}, want ${out[i]}`);
+  }
+}
+
+function trsmResidual(X, a) {
+  const layout = a.layout || "row-major";
+  const order = a.side === "left" ? a.m : a.n;
+  let worst = 0;
+  for (let i = 0; i < a.m; i++)
+    for (let j = 0; j < a.n; j++) {
+      let acc = 0;
+      let d = 0;
+      for (let k = 0; k < order; k++) {
+        const [av, xv] = a.side === "left"
+          ? [triEl(a.A, a.lda, layout, a.uplo, a.transA, a.diag, i, k), el(X, a.ldb, layout, k, j)]
+          : [triEl(a.A, a.lda, layout, a.uplo, a.transA, a.diag, k, j), el(X, a.ldb, layout, i, k)];
+        acc += av * xv;
+        d += Math.abs(av * xv);
+      }
+      const rhs = a.alpha === 0 ? 0 : a.alpha * el(a.B, a.ldb, layout, i, j);
+      const bound = 2 ** -23 * (order + 1) * d;
+      const err = Math.abs(acc - rhs);
+      const f = bound === 0 ? (err === 0 ? 0 : Infinity) : err / bound;
+      if (!(f <= worst)) worst = f;
+    }
+  return worst;
+}
+
+const level3Call = {
+  ssyr2k: (a) => wg.ssyr2k(device, a.uplo, a.trans, a.n, a.k, a.alpha, a.A, a.lda, a.B, a.ldb, a.beta, a.C, a.ldc, a.layout),
+  ssymm: (a) => wg.ssymm(device, a.side, a.uplo, a.m, a.n, a.alpha, a.A, a.lda, a.B, a.ldb, a.beta, a.C, a.ldc, a.layout),
+  strmm: (a) => wg.strmm(device, a.side, a.uplo, a.transA, a.diag, a.m, a.n, a.alpha, a.A, a.lda, a.B, a.ldb, a.layout),
+  strsm: (a) => wg.strsm(device, a.side, a.uplo, a.transA, a.diag, a.m, a.n, a.alpha, a.A, a.lda, a.B, a.ldb, a.layout),
+};
+
+// GpuMatrix forms of a level-3 call's operands (shapes as wgblas's
+// gpustorage tests build them) and the output read back with its ld.
+async function residentLevel3(routine, a) {
+  const layout = a.layout || "row-major";
+  const mats = {};
+  const shape = (name) => {
+    if (routine === "ssyr2k") {
+      if (name === "C") return [a.n, a.n, a.ldc];
+      const ld = name === "A" ? a.lda : a.ldb;
+      return a.trans === "no-transpose" ? [a.n, a.k, ld] : [a.k, a.n, ld];
+    }
+    if (name === "A") {
+      const order = a.side === "left" ? a.m : a.n;
+      return [order, order, a.lda];
+    }
+    return [a.m, a.n, name === "B" ? a.ldb : a.ldc];
+  };
+  const names = routine === "strmm" || routine === "strsm" ? ["A", "B"] : ["A", "B", "C"];
+  const outName = routine === "strmm" || routine === "strsm" ? "B" : "C";
+  try {
+    for (const nm of names) {
+      const [r, c, ld] = shape(nm);
+      const outer = layout === "column-major" ? c : r;
+      const padded = new Float32Array(Math.max(outer * ld, a[nm].length));
+      padded.set(a[nm]);
+      mats[nm] = wg.GpuMatrix.from(device, padded, r, c, ld, layout);
+    }
+    const res = await level3Call[routine](Object.assign({}, a, mats));
+    assertEqual(Object.keys(res).length, 0, "resident call returns {}");
+    const [r, c, ld] = shape(outName);
+    const dense = await mats[outName].read();
+    const inner = layout === "column-major" ? r : c;
+    const outer = layout === "column-major" ? c : r;
+    const raw = Float32Array.from(a[outName]);
+    for (let o = 0; o < outer; o++) raw.set(dense.subarray(o * inner, o * inner + inner), o * ld);
+    return raw;
+  } finally {
+    for (const nm of Object.keys(mats)) mats[nm].destroy();
+  }
+}
+
+const f32 = (c, names) => {
+  const a = Object.assign({}, c);
+  for (const nm of names) a[nm] = new Float32Array(c[nm]);
+  a.layout = c.layout || "row-major";
+  return a;
+};
+
+for (const routine of ["ssyr2k", "ssymm", "strmm", "strsm"]) {
+  for (const file of [`${routine}.edge-cases`, `${routine}.edge-cases-column-major`]) {
+    for (const c of fixture(file)) {
+      test(`${routine} ${file.includes("column") ? "cm" : "rm"}: ${c.label}`, async () => {
+        const a = f32(c, routine === "strmm" || routine === "strsm" ? ["A", "B"] : ["A", "B", "C"]);
+        const key = routine === "strmm" || routine === "strsm" ? "B" : "C";
+        const host = (await level3Call[routine](a))[key];
+        const resident = await residentLevel3(routine, a);
+        for (const got of [host, resident]) {
+          if (routine === "strsm") assert(trsmResidual(got, a) <= 1, `${c.label}: residual`);
+          else checkLevel3(routine, got, a);
+        }
+      });
+    }
+  }
+}
+
+test("level 3: multi-tile, mixed GpuMatrix layouts, alpha = 0, strsm many blocks", async () => {
+  // ssyr2k with A row-major and B column-major GpuMatrix operands
+  const n = 150;
+  const k = 9;
+  const A = wg.randomFloat32Array(n * k, -1, 1, 71);
+  const B = wg.randomFloat32Array(n * k, -1, 1, 72);
+  const C = wg.randomFloat32Array(n * n, -1, 1, 73);
+  const gA = wg.GpuMatrix.from(device, A, n, k, k, "row-major");
+  const gB = wg.GpuMatrix.from(device, B, n, k, n, "column-major");
+  const gC = wg.GpuMatrix.from(device, C, n, n, n, "row-major");
+  try {
+    await wg.ssyr2k(device, "lower", "no-transpose", n, k, 1.5, gA, k, gB, n, 0.5, gC, n);
+    const got = await gC.read();
+    for (let i = 0; i < n; i++)
+      for (let j = 0; j < n; j++) {
+        if (j > i) {
+          assert(Object.is(got[i * n + j], C[i * n + j]), "upper triangle untouched");
+          continue;
+        }
+        let s = 0;
+        let d = 0;
+        for (let p = 0; p < k; p++) {
+          const v1 = A[i * k + p] * B[p * n + j];
+          const v2 = B[p * n + i] * A[j * k + p];
+          s += v1 + v2;
+          d += Math.abs(v1) + Math.abs(v2);
+        }
+        const want = 1.5 * s + 0.5 * C[i * n + j];
+        assert(Math.abs(got[i * n + j] - want) <= 2 ** -23 * ((k + 3) * 1.5 * d + 1.5 * Math.abs(C[i * n + j])),
+          `ssyr2k mixed layouts (${i}, ${j})`);
+      }
+  } finally {
+    gA.destroy();
+    gB.destroy();
+    gC.destroy();
+  }
+  // ssymm / strmm multi-tile in both layouts (tests/ssymm/src/test.ssymm.js:236-297)
+  for (const layout of ["row-major", "column-major"])
+    for (const side of ["left", "right"]) {
+      const N = 400;
+      const other = 72;
+      const m = side === "left" ? N : other;
+      const nn = side === "left" ? other : N;
+      const ld = (layout === "column-major" ? m : nn) + 4;
+      const outer = layout === "column-major" ? nn : m;
+      const a = { side, uplo: "upper", m, n: nn, alpha: 1.5, beta: 0.5, layout, transA: "transpose", diag: "unit",
+        A: wg.randomFloat32Array(N * N, -1, 1, 91), lda: N, B: wg.randomFloat32Array(outer * ld, -1, 1, 92), ldb: ld,
+        C: wg.randomFloat32Array(outer * ld, -1, 1, 93), ldc: ld };
+      checkLevel3("ssymm", (await level3Call.ssymm(a)).C, a);
+      checkLevel3("strmm", (await level3Call.strmm(a)).B, a);
+    }
+  // alpha = 0: strmm / strsm give zeros without reading NaN / Inf
+  const z = { side: "left", uplo: "lower", transA: "no-transpose", diag: "non-unit", m: 7, n: 7, alpha: 0,
+    A: wg.randomFloat32Array(49, -1, 1, 1), lda: 7, B: wg.randomFloat32Array(49, -1, 1, 2), ldb: 7, layout: "row-major" };
+  z.A[3 * 7 + 1] = NaN;
+  z.B[2 * 7 + 3] = Infinity;
+  for (const r of ["strmm", "strsm"]) {
+    const got = (await level3Call[r](z)).B;
+    assert(got.every((v) => Object.is(v, 0)), `${r} alpha = 0 writes +0`);
+  }
+  // strsm across several diagonal blocks, resident, column-major with padding
+  const N = 600;
+  const A2 = wg.randomFloat32Array(N * N, -1 / N, 1 / N, 121);
+  for (let i = 0; i < N; i++) A2[i * N + i] = 2;
+  const s = { side: "right", uplo: "lower", transA: "transpose", diag: "non-unit", m: 200, n: N, alpha: 1.5,
+    A: A2, lda: N, B: wg.randomFloat32Array(N * 204, -1, 1, 122), ldb: 204, layout: "column-major" };
+  assert(trsmResidual(await residentLevel3("strsm", s), s) <= 1, "strsm 600 resident residual");
+});
+
 // fp64 level 1 (tests/{ddot,dasum,dnrm2,idamax}/): the reference's bounds
 // around float64 sums (ddot n 2^-48 sum|xy|, dasum 64 ULP by a relative
 // 64 * 2^-52, dnrm2 10 * 2^-48 relative), idamax exact

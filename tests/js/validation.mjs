@@ -59,6 +59,10 @@ function matrixShape(dependsOn, dims) {
     const noTrans = (dims[transKey] || "no-transpose") === "no-transpose";
     return noTrans ? { outer: rows, inner: cols } : { outer: cols, inner: rows };
   }
+  if (deps.has("side")) {
+    const order = (dims.side || "left") === "left" ? dims.m : dims.n;
+    return { outer: order, inner: order };
+  }
   if (deps.has("m") && deps.has("n")) return cm ? { outer: dims.n, inner: dims.m } : { outer: dims.m, inner: dims.n };
   if (deps.has("n")) return { outer: dims.n, inner: dims.n };
   return null;
@@ -227,6 +231,59 @@ async function main() {
     C: Object.assign({}, loadParam("C64"), { dependsOn: ["n", "ldc"] }),
     ldc: loadParam("ld"),
   }, (a) => wg.dsyrk(a.device, a.uplo, a.trans, a.n, a.k, a.alpha, a.A, a.lda, a.beta, a.C, a.ldc, a.layout), device);
+  // level 3 on the GEMM: wgblas's tests/{ssyr2k,ssymm,strmm,strsm}/src/test.*.js
+  // compositions.
+  register("ssyr2k", {
+    device: loadParam("device"),
+    uplo: loadParam("uplo"),
+    trans: loadParam("trans"),
+    layout: loadParam("layout"),
+    n: nWithNegative("must be non-negative"),
+    k: loadParam("k"),
+    alpha: loadParam("alpha"),
+    beta: loadParam("beta"),
+    A: Object.assign({}, A, A["level-3"], { dependsOn: ["n", "k", "lda", "trans"] }),
+    lda: loadParam("ld"),
+    B: Object.assign({}, loadParam("B"), { dependsOn: ["n", "k", "ldb", "trans"] }),
+    ldb: loadParam("ld"),
+    C: Object.assign({}, loadParam("C"), { dependsOn: ["n", "ldc"] }),
+    ldc: loadParam("ld"),
+  }, (a) => wg.ssyr2k(a.device, a.uplo, a.trans, a.n, a.k, a.alpha, a.A, a.lda, a.B, a.ldb, a.beta, a.C, a.ldc,
+    a.layout), device);
+  register("ssymm", {
+    device: loadParam("device"),
+    side: loadParam("side"),
+    uplo: loadParam("uplo"),
+    layout: loadParam("layout"),
+    m: Object.assign({}, loadParam("m"), { baseline: 2 }),
+    n: nWithNegative("must be non-negative"),
+    alpha: loadParam("alpha"),
+    beta: loadParam("beta"),
+    A: Object.assign({}, A, { dependsOn: ["m", "n", "lda", "side"] }),
+    lda: loadParam("ld"),
+    B: Object.assign({}, loadParam("B"), { dependsOn: ["m", "n", "ldb"] }),
+    ldb: loadParam("ld"),
+    C: loadParam("C"),
+    ldc: loadParam("ld"),
+  }, (a) => wg.ssymm(a.device, a.side, a.uplo, a.m, a.n, a.alpha, a.A, a.lda, a.B, a.ldb, a.beta, a.C, a.ldc,
+    a.layout), device);
+  for (const r of ["strmm", "strsm"])
+    register(r, {
+      device: loadParam("device"),
+      side: loadParam("side"),
+      uplo: loadParam("uplo"),
+      transA: loadParam("trans"),
+      diag: loadParam("diag"),
+      layout: loadParam("layout"),
+      m: Object.assign({}, loadParam("m"), { baseline: 2 }),
+      n: nWithNegative("must be non-negative"),
+      alpha: loadParam("alpha"),
+      A: Object.assign({}, A, { dependsOn: ["m", "n", "lda", "side"] }),
+      lda: loadParam("ld"),
+      B: Object.assign({}, loadParam("B"), { dependsOn: ["m", "n", "ldb"] }),
+      ldb: loadParam("ld"),
+    }, (a) => wg[r](a.device, a.side, a.uplo, a.transA, a.diag, a.m, a.n, a.alpha, a.A, a.lda, a.B, a.ldb,
+      a.layout), device);
   register("sdot", {
     device: loadParam("device"), n: loadParam("n"), incx: loadParam("incx"), incy: loadParam("incy"),
     x: loadParam("x"), y: loadParam("y"),

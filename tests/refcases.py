@@ -83,3 +83,124 @@ def numpy_gemm(uplo, ta, tb, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc):
     idx = (i + j * ldc)[mask]
     out[idx] = res[mask]
     return out
+
+
+SIDE = {"left": 1, "right": 2}
+DIAG = {"non-unit": 0, "unit": 1}
+
+
+def syr2k_call(case, dtype=np.float32):
+    """Column-major (uplo, trans, n, k, alpha, A, lda, B, ldb, beta, C, ldc)
+    for ssyr2k: a row-major operand read column-major is its transpose
+    (trans flips); the result is symmetric, so a row-major C is the other
+    triangle."""
+    layout = case.get("layout", "row-major")
+    uplo, trans = UPLO[case["uplo"]], TRANS[case["trans"]]
+    A, B, C = (np.array(case[x], dtype) for x in "ABC")
+    if layout != "column-major":
+        uplo, trans = flip_uplo(uplo), 1 - trans
+    return (uplo, trans, case["n"], case["k"], case["alpha"], A, case["lda"], B, case["ldb"],
+            case["beta"], C, case["ldc"])
+
+
+def symm_call(case, dtype=np.float32):
+    """Column-major (side, uplo, m, n, alpha, A, lda, B, ldb, beta, C, ldc)
+    for ssymm: row-major C = S B is column-major C^T = B^T S (side flips, m
+    and n swap) and A read column-major stores the other triangle."""
+    layout = case.get("layout", "row-major")
+    side, uplo = SIDE[case["side"]], UPLO[case["uplo"]]
+    m, n = case["m"], case["n"]
+    A, B, C = (np.array(case[x], dtype) for x in "ABC")
+    if layout != "column-major":
+        side, uplo, m, n = 3 - side, flip_uplo(uplo), n, m
+    return (side, uplo, m, n, case["alpha"], A, case["lda"], B, case["ldb"], case["beta"], C,
+            case["ldc"])
+
+
+def tri_call(case, dtype=np.float32):
+    """Column-major (side, uplo, trans, unit, m, n, alpha, A, lda, B, ldb) for
+    strmm / strsm: row-major B = op(A) B is column-major B^T = B^T op(A)^T;
+    A read column-major is A^T, so side and uplo flip while trans stays."""
+    layout = case.get("layout", "row-major")
+    side, uplo = SIDE[case["side"]], UPLO[case["uplo"]]
+    trans, unit = TRANS[case["transA"]], DIAG[case["diag"]]
+    m, n = case["m"], case["n"]
+    A, B = np.array(case["A"], dtype), np.array(case["B"], dtype)
+    if layout != "column-major":
+        side, uplo, m, n = 3 - side, flip_uplo(uplo), n, m
+    return (side, uplo, trans, unit, m, n, case["alpha"], A, case["lda"], B, case["ldb"])
+
+
+def put(out, vals, ld):
+    """Writes the dense rows x cols `vals` into the column-major buffer out."""
+    rows, cols = vals.shape
+    i = np.arange(rows)[:, None]
+    j = np.arange(cols)[None, :]
+    out[(i + j * ld).ravel()] = vals.ravel()
+    return out
+
+
+def numpy_syr2k(uplo, trans, n, k, alpha, A, lda, B, ldb, beta, C, ldc):
+    opA = dense_op(A, n, k, lda, trans)
+    opB = dense_op(B, n, k, ldb, trans)
+    prod = opA @ opB.T + opB @ opA.T if alpha != 0 else np.zeros((n, n))
+    cij = dense_op(C, n, n, ldc, 0)
+    res = alpha * prod + (beta * cij if beta != 0 else 0.0)
+    out = np.array(C, np.float64, copy=True)
+    i = np.arange(n)[:, None]
+    j = np.arange(n)[None, :]
+    mask = (i >= j) if uplo == 1 else (i <= j)
+    out[(i + j * ldc)[mask]] = res[mask]
+    return out
+
+
+def dense_sym(A, order, lda, uplo):
+    """The symmetric matrix whose uplo triangle A stores."""
+    full = dense_op(A, order, order, lda, 0)
+    tri = np.tril(full) if uplo == 1 else np.triu(full)
+    return tri + tri.T - np.diag(np.diag(full))
+
+
+def dense_tri(A, order, lda, uplo, trans, unit):
+    """op(A) of a triangular A: its uplo triangle, zeros elsewhere, unit
+    diagonal when unit."""
+    full = dense_op(A, order, order, lda, 0)
+    tri = np.tril(full) if uplo == 1 else np.triu(full)
+    if unit:
+        np.fill_diagonal(tri, 1.0)
+    return tri.T if trans else tri
+
+
+def numpy_symm(side, uplo, m, n, alpha, A, lda, B, ldb, beta, C, ldc):
+    order = m if side == 1 else n
+    S = dense_sym(A, order, lda, uplo)
+    Bd = dense_op(B, m, n, ldb, 0)
+    prod = (S @ Bd if side == 1 else Bd @ S) if alpha != 0 else np.zeros((m, n))
+    res = alpha * prod + (beta * dense_op(C, m, n, ldc, 0) if beta != 0 else 0.0)
+    return put(np.array(C, np.float64, copy=True), res, ldc)
+
+
+def numpy_trmm(side, uplo, trans, unit, m, n, alpha, A, lda, B, ldb):
+    order = m if side == 1 else n
+    T = dense_tri(A, order, lda, uplo, trans, unit)
+    Bd = dense_op(B, m, n, ldb, 0)
+    res = alpha * (T @ Bd if side == 1 else Bd @ T) if alpha != 0 else np.zeros((m, n))
+    return put(np.array(B, np.float64, copy=True), res, ldb)
+
+
+def scipy_trsm(side, uplo, trans, unit, m, n, alpha, A, lda, B, ldb):
+    """X of op(A) X = alpha B / X op(A) = alpha B by scipy.linalg.solve_triangular."""
+    from scipy.linalg import solve_triangular
+
+    order = m if side == 1 else n
+    full = dense_op(A, order, order, lda, 0)
+    Bd = alpha * dense_op(B, m, n, ldb, 0)
+    if alpha == 0:
+        X = np.zeros((m, n))
+    elif side == 1:
+        X = solve_triangular(full, Bd, trans=trans, lower=uplo == 1, unit_diagonal=bool(unit))
+    else:
+        # X op(A) = B  <=>  op(A)^T X^T = B^T
+        X = solve_triangular(full, Bd.T, trans=1 - trans, lower=uplo == 1,
+                             unit_diagonal=bool(unit)).T
+    return put(np.array(B, np.float64, copy=True), X, ldb)

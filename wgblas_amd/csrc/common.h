@@ -26,6 +26,10 @@ struct wgb_ctx {
   // filled round (grown on demand, reused in stream order).
   void *gemm_ws = nullptr;
   size_t gemm_ws_bytes = 0;
+  // Level-3 operand workspace: ssymm's symmetrized A, strmm's masked A and
+  // its copy of B (grown on demand, reused in stream order).
+  void *op_ws = nullptr;
+  size_t op_ws_bytes = 0;
   // Pinned host slot the host-result reductions copy their scalar into.
   void *host_result = nullptr;
   char name[256] = {0};
@@ -46,9 +50,22 @@ void timing_begin(wgb_ctx *ctx);
 void timing_end(wgb_ctx *ctx);
 
 // Largest number of first-pass blocks a reduction may use; the scratch
-// buffer is sized for this many 16-byte partials plus the result slot.
+// buffer is sized for this many 32-byte partials plus the result slot.
 constexpr int kMaxReduceBlocks = 2048;
 constexpr size_t kScratchBytes = (size_t)kMaxReduceBlocks * 32 + 256;  // 32-byte partial slots + result
+
+// GEMM k-band: which operand is triangular (zero outside its triangle).
+enum { kBandNone = 0, kBandALower = 1, kBandAUpper = 2, kBandBLower = 3, kBandBUpper = 4 };
+
+// One fp32 GEMM on ctx's stream, C = alpha op(A) op(B) + beta C on the uplo
+// part of C (0 = all), without argument checks or timing events.
+int gemm_f32(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64_t n, int64_t k,
+             float alpha, const float *A, int64_t lda, const float *B, int64_t ldb, float beta,
+             float *C, int64_t ldc, int band);
+// The GEMM entry points' argument checks.
+int check_gemm(int uplo, bool want_uplo, int transA, int transB, int64_t m, int64_t n, int64_t k,
+               const void *A, int64_t lda, const void *B, int64_t ldb, const void *C,
+               int64_t ldc);
 
 }  // namespace wgb
 

@@ -98,6 +98,9 @@ struct GemmArgs {
   int tiles_m, tiles_n, ntiles;
   int uplo;   // 0 = full C, WGB_LOWER, WGB_UPPER
   int c_vec;  // ldc % VW == 0 and C 16-byte aligned: whole-vector C access
+  // wgb::kBand*: one operand is triangular (zero outside its triangle), so a
+  // tile only needs the k-tiles its nonzero band reaches (never split).
+  int band;
   // Split-k tail: logical tiles [nregular, ntiles) are computed as `splits`
   // k-ranges of kt_split k-tiles each; unit u = (tile - nregular) * splits +
   // split writes its raw BT x BT partial (column-major, ld BT) to ws + u BT^2
@@ -531,6 +534,17 @@ __global__ __launch_bounds__(kThreads, (sizeof(T) == 8 || AKC != BKC) ? 2 : 1) v
   int nkt = nkt_all;
   if ((int)blockIdx.x < p.nregular) {
     logical_tile(xcd_remap(blockIdx.x, p.nregular), p.tiles_m, p.tiles_n, p.uplo, tm, tn);
+    if (p.band != wgb::kBandNone) {
+      // op(A) lower: k < m0 + BT; op(A) upper: k >= m0; op(B) lower
+      // (nonzero for k >= j): k >= n0; op(B) upper: k < n0 + BT.
+      constexpr int TK = BT / BK;
+      const int lo = p.band == wgb::kBandAUpper ? tm * TK : p.band == wgb::kBandBLower ? tn * TK : 0;
+      int hi = p.band == wgb::kBandALower ? (tm + 1) * TK
+                                          : p.band == wgb::kBandBUpper ? (tn + 1) * TK : nkt_all;
+      if (hi > nkt_all) hi = nkt_all;
+      kt0 = lo;
+      nkt = hi - lo;
+    }
   } else {
     unit = (int)blockIdx.x - p.nregular;
     logical_tile(p.nregular + unit / p.splits, p.tiles_m, p.tiles_n, p.uplo, tm, tn);
@@ -901,7 +915,7 @@ int launch_tier(wgb_ctx *ctx, GemmArgs<T> &a, bool akc, bool bkc, bool vec) {
   a.kt_split = (int)nkt;
   a.ws = nullptr;
   const int64_t rem = a.ntiles % slots;
-  if (rem > 0 && 2 * rem <= slots) {
+  if (a.band == wgb::kBandNone && rem > 0 && 2 * rem <= slots) {
     int64_t S = slots / rem;
     if (S > 16) S = 16;
     if (S > nkt / 4) S = nkt / 4;
@@ -957,19 +971,18 @@ int check_gemm_args(int uplo, bool want_uplo, int transA, int transB, int64_t m,
   return WGB_OK;
 }
 
+// Enqueues one GEMM (no argument checks, no timing events).
 template <typename T>
-int gemm_run(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64_t n, int64_t k,
-             T alpha, const T *A, int64_t lda, const T *B, int64_t ldb, T beta, T *C,
-             int64_t ldc) {
+int gemm_launch(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64_t n, int64_t k,
+                T alpha, const T *A, int64_t lda, const T *B, int64_t ldb, T beta, T *C,
+                int64_t ldc, int band) {
   if (m == 0 || n == 0) return WGB_OK;
-  wgb::timing_begin(ctx);
   if (alpha == (T)0 || k == 0) {
     dim3 block(256);
     int64_t gx = (m + 255) / 256;
     dim3 grid((unsigned)(gx > 1024 ? 1024 : gx), (unsigned)(n > 65535 ? 65535 : n));
     scale_kernel<T><<<grid, block, 0, ctx->stream>>>(m, n, beta, C, ldc, uplo);
     WGB_CHECK_LAUNCH("scale_kernel");
-    wgb::timing_end(ctx);
     return WGB_OK;
   }
   GemmArgs<T> a;
@@ -985,6 +998,7 @@ int gemm_run(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64_t 
   a.C = C;
   a.ldc = ldc;
   a.uplo = uplo;
+  a.band = band;
   const int VW = Ty<T>::VW;
   a.c_vec = (ldc % VW == 0) && aligned16(C);
   const bool akc = transA == WGB_TRANS;
@@ -1012,11 +1026,40 @@ int gemm_run(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64_t 
                      : launch_tier<T, 64>(ctx, a, akc, bkc, vec);
   if (st) return st;
   WGB_CHECK_LAUNCH("gemm_kernel");
+  return WGB_OK;
+}
+
+template <typename T>
+int gemm_run(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64_t n, int64_t k,
+             T alpha, const T *A, int64_t lda, const T *B, int64_t ldb, T beta, T *C,
+             int64_t ldc) {
+  if (m == 0 || n == 0) return WGB_OK;
+  wgb::timing_begin(ctx);
+  int st = gemm_launch<T>(ctx, uplo, transA, transB, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc,
+                          wgb::kBandNone);
+  if (st) return st;
   wgb::timing_end(ctx);
   return WGB_OK;
 }
 
 }  // namespace
+
+namespace wgb {
+
+int gemm_f32(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64_t n, int64_t k,
+             float alpha, const float *A, int64_t lda, const float *B, int64_t ldb, float beta,
+             float *C, int64_t ldc, int band) {
+  return gemm_launch<float>(ctx, uplo, transA, transB, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc,
+                            band);
+}
+
+int check_gemm(int uplo, bool want_uplo, int transA, int transB, int64_t m, int64_t n, int64_t k,
+               const void *A, int64_t lda, const void *B, int64_t ldb, const void *C,
+               int64_t ldc) {
+  return check_gemm_args(uplo, want_uplo, transA, transB, m, n, k, A, lda, B, ldb, C, ldc);
+}
+
+}  // namespace wgb
 
 extern "C" int wgb_sgemm(wgb_ctx *ctx, int transA, int transB, int64_t m, int64_t n, int64_t k,
                          float alpha, const float *A, int64_t lda, const float *B, int64_t ldb,

@@ -1,0 +1,400 @@
+// The level-3 routines that run on the GEMM kernel: ssyr2k, ssymm, strmm,
+// strsm (wgblas src/{ssyr2k,ssymm,strmm,strsm}/*.mjs).
+//
+// ssyr2k: two triangle GEMM launches, the second with beta = 1.
+// ssymm: the symmetric operand is expanded into a dense workspace copy
+//   (LDS-tiled, coalesced both ways), then one GEMM.
+// strmm: A's triangle is copied with zeros elsewhere, B is copied (the GEMM
+//   cannot read and write B at once), then one GEMM whose tiles only run the
+//   k-tiles the triangle reaches (about half the flops of a dense product).
+// strsm: recursive halving of the triangular dimension. Diagonal blocks of
+//   order <= 64 are solved by substitution, one wave per 64 right-hand sides
+//   with the unknowns in registers; the off-diagonal updates are GEMMs that
+//   read the solved rows of B and write other rows of B in place (disjoint
+//   memory), so strsm needs no workspace and no explicit inverse.
+#include "common.h"
+
+#include <hip/hip_runtime.h>
+
+#include "wgblas_hip.h"
+
+namespace {
+
+using wgb::fail;
+
+constexpr int kTile = 64;  // symmetrize tile (64 x 64)
+constexpr int kLeaf = 64;  // order of strsm's substitution blocks
+
+int64_t imax(int64_t a, int64_t b) { return a > b ? a : b; }
+int64_t round4(int64_t v) { return (v + 3) / 4 * 4; }
+
+// Grows the context's operand workspace to at least `bytes`. The stream is
+// drained first: an earlier launch may still read the old buffer.
+int ensure_op_workspace(wgb_ctx *ctx, size_t bytes) {
+  if (ctx->op_ws_bytes >= bytes) return WGB_OK;
+  const size_t round = (size_t)16 << 20;
+  bytes = (bytes + round - 1) / round * round;
+  WGB_CHECK_HIP(hipStreamSynchronize(ctx->stream));
+  if (ctx->op_ws) WGB_CHECK_HIP(hipFree(ctx->op_ws));
+  ctx->op_ws = nullptr;
+  ctx->op_ws_bytes = 0;
+  if (hipMalloc(&ctx->op_ws, bytes) != hipSuccess) {
+    (void)hipGetLastError();
+    ctx->op_ws = nullptr;
+    return fail(WGB_ERR_ALLOC, "hipMalloc of the level-3 operand workspace failed");
+  }
+  ctx->op_ws_bytes = bytes;
+  return WGB_OK;
+}
+
+// W (order x order, column-major, ld ldw) <- the symmetric matrix whose uplo
+// triangle A holds (src/shaders/symmetrize.wgsl). Block (bi, bj) writes W's
+// 64 x 64 tile (bi, bj): a tile inside the stored triangle copies A's tile,
+// a tile in the other triangle reads the mirrored tile (bj, bi) and
+// transposes it through LDS, a diagonal tile takes each element from
+// whichever of (i, j), (j, i) is stored. 256 threads = 64 rows x 4 column
+// phases, so every wave reads and writes 256 contiguous bytes of a column.
+__global__ __launch_bounds__(256) void symmetrize_kernel(int64_t order, const float *__restrict__ A,
+                                                         int64_t lda, int uplo,
+                                                         float *__restrict__ W, int64_t ldw) {
+  __shared__ float s[kTile][kTile + 1];  // s[col][row] of the source tile
+  const int bi = blockIdx.x, bj = blockIdx.y;
+  const bool lower = uplo == WGB_LOWER;
+  const bool diag = bi == bj;
+  const bool stored = lower ? bi > bj : bi < bj;
+  const int si = (stored || diag) ? bi : bj, sj = (stored || diag) ? bj : bi;
+  const int r = threadIdx.x & 63, ph = threadIdx.x >> 6;
+  const int64_t srow = (int64_t)si * kTile + r;
+  for (int c = ph; c < kTile; c += 4) {
+    const int64_t scol = (int64_t)sj * kTile + c;
+    s[c][r] = (srow < order && scol < order) ? A[srow + scol * lda] : 0.f;
+  }
+  __syncthreads();
+  const int64_t row = (int64_t)bi * kTile + r;
+  if (row >= order) return;
+  for (int c = ph; c < kTile; c += 4) {
+    const int64_t col = (int64_t)bj * kTile + c;
+    if (col >= order) break;
+    float v;
+    if (stored)
+      v = s[c][r];
+    else if (!diag)
+      v = s[r][c];  // W(row, col) = A(col, row), element (c, r) of tile (bj, bi)
+    else
+      v = (lower ? r >= c : r <= c) ? s[c][r] : s[r][c];
+    W[row + col * ldw] = v;
+  }
+}
+
+// W <- A's uplo triangle, zero elsewhere, ones on the diagonal for a unit
+// triangle (src/shaders/triangularize.wgsl builds op(A); W keeps A's own
+// orientation and the GEMM applies transA).
+__global__ __launch_bounds__(256) void triangle_copy_kernel(int64_t order,
+                                                            const float *__restrict__ A,
+                                                            int64_t lda, int uplo, int unit,
+                                                            float *__restrict__ W, int64_t ldw) {
+  const int64_t row = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (row >= order) return;
+  const bool lower = uplo == WGB_LOWER;
+  for (int64_t col = blockIdx.y; col < order; col += gridDim.y) {
+    float v;
+    if (row == col)
+      v = unit ? 1.f : A[row + col * lda];
+    else
+      v = (lower ? row > col : row < col) ? A[row + col * lda] : 0.f;
+    W[row + col * ldw] = v;
+  }
+}
+
+// Substitution solve of one diagonal block, in the solve frame: for every
+// right-hand side v, M x = alpha v with M lower triangular of order nb <= 64.
+// Frame element (i, k) of M is Ablk[ia(i) mi + ia(k) mk] and element i of
+// right-hand side r is Bblk[ia(i) vi + r vr], where ia(i) = nb-1-i for an
+// upper system solved backward (rev) and i otherwise; the solution
+// overwrites v. One wave per 64 right-hand sides: lane r holds its 64
+// unknowns in registers, M sits in LDS (column k contiguous, read as
+// broadcasts). Column-oriented order, as wgblas's strsm_small.wgsl and
+// reference BLAS: x_k /= M(k,k), then x_i -= M(i,k) x_k for i > k; alpha is
+// applied as v is read. VI1: the frame index is B's contiguous one (left
+// side).
+template <bool VI1>
+__global__ __launch_bounds__(64) void trsm_leaf_kernel(int nb, int64_t nrhs,
+                                                       const float *__restrict__ Ablk, int64_t mi,
+                                                       int64_t mk, int rev, int unit,
+                                                       float *__restrict__ Bblk, int64_t vi,
+                                                       int64_t vr, float alpha) {
+  __shared__ __attribute__((aligned(16))) float Ms[kLeaf * kLeaf];  // Ms[k*64 + i] = M(i, k)
+  __shared__ float Xs[kLeaf][kLeaf + 1];                            // Xs[rhs][i]
+  const int lane = threadIdx.x;
+  const int64_t rhs0 = (int64_t)blockIdx.x * kLeaf;
+  for (int e = lane; e < kLeaf * kLeaf; e += kLeaf) {
+    const int i = e & (kLeaf - 1), k = e / kLeaf;
+    float v = 0.f;
+    if (i < nb && k <= i) {
+      const int ii = rev ? nb - 1 - i : i, kk = rev ? nb - 1 - k : k;
+      v = (i == k && unit) ? 1.f : Ablk[ii * mi + kk * mk];
+    } else if (i == k) {
+      v = 1.f;  // padding rows past nb: unit diagonal, fed only by zeros
+    }
+    Ms[e] = v;
+  }
+  // v is staged through Xs[rhs][i] with coalesced loads: along the frame
+  // index when it is B's contiguous one (VI1), else along the right-hand
+  // sides.
+  if constexpr (VI1) {
+    for (int c = 0; c < kLeaf; ++c) {
+      const int64_t rc = rhs0 + c;
+      Xs[c][lane] = (lane < nb && rc < nrhs) ? Bblk[(rev ? nb - 1 - lane : lane) + rc * vr] : 0.f;
+    }
+  } else {
+    const int64_t r = rhs0 + lane;
+    for (int i = 0; i < kLeaf; ++i)
+      Xs[lane][i] = (i < nb && r < nrhs) ? Bblk[(rev ? nb - 1 - i : i) * vi + r] : 0.f;
+  }
+  __syncthreads();
+  float x[kLeaf];
+#pragma unroll
+  for (int i = 0; i < kLeaf; ++i) x[i] = alpha * Xs[lane][i];
+#pragma unroll
+  for (int k = 0; k < kLeaf; ++k) {
+    x[k] = x[k] / Ms[k * kLeaf + k];
+#pragma unroll
+    for (int i = k + 1; i < kLeaf; ++i) x[i] = fmaf(-Ms[k * kLeaf + i], x[k], x[i]);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < kLeaf; ++i) Xs[lane][i] = x[i];
+  __syncthreads();
+  if constexpr (VI1) {
+    for (int c = 0; c < kLeaf; ++c) {
+      const int64_t rc = rhs0 + c;
+      if (lane < nb && rc < nrhs) Bblk[(rev ? nb - 1 - lane : lane) + rc * vr] = Xs[c][lane];
+    }
+  } else {
+    const int64_t r = rhs0 + lane;
+    if (r < nrhs)
+      for (int i = 0; i < nb; ++i) Bblk[(rev ? nb - 1 - i : i) * vi + r] = Xs[lane][i];
+  }
+}
+
+// strsm in the solve frame: frame index = B's row (left side) or column
+// (right side); M = op(A) (left) or op(A)^T (right), lower when the solve
+// runs forward.
+struct Trsm {
+  wgb_ctx *ctx;
+  bool left, trans, unit, forward;
+  int64_t m, n;
+  float alpha;
+  const float *A;
+  int64_t lda;
+  float *B;
+  int64_t ldb;
+};
+
+int trsm_leaf(const Trsm &p, int64_t lo, int64_t nb, float alpha) {
+  const bool m_is_a = p.left != p.trans;  // M is A itself, else A^T
+  const float *Ablk = p.A + lo + lo * p.lda;
+  const int64_t mi = m_is_a ? 1 : p.lda, mk = m_is_a ? p.lda : 1;
+  const int64_t nrhs = p.left ? p.n : p.m;
+  const int64_t grid = (nrhs + kLeaf - 1) / kLeaf;
+  const int rev = p.forward ? 0 : 1;
+  if (p.left)
+    trsm_leaf_kernel<true><<<(unsigned)grid, kLeaf, 0, p.ctx->stream>>>(
+        (int)nb, nrhs, Ablk, mi, mk, rev, p.unit, p.B + lo, 1, p.ldb, alpha);
+  else
+    trsm_leaf_kernel<false><<<(unsigned)grid, kLeaf, 0, p.ctx->stream>>>(
+        (int)nb, nrhs, Ablk, mi, mk, rev, p.unit, p.B + lo * p.ldb, p.ldb, 1, alpha);
+  WGB_CHECK_LAUNCH("trsm_leaf_kernel");
+  return WGB_OK;
+}
+
+// Frame rows [b, b+nbr) <- beta * themselves - M[b.., a..] X[a.., :], X the
+// solved frame rows [a, a+nar). Left: B[b,:] = beta B[b,:] - op(A)[b,a] B[a,:];
+// right: B[:,b] = beta B[:,b] - B[:,a] op(A)[a,b]. Both read rows / columns
+// of B disjoint from the ones they write.
+int trsm_update(const Trsm &p, int64_t a, int64_t nar, int64_t b, int64_t nbr, float beta) {
+  const int t = p.trans ? WGB_TRANS : WGB_NO_TRANS;
+  if (p.left) {
+    const float *Ap = p.trans ? p.A + a + b * p.lda : p.A + b + a * p.lda;
+    return wgb::gemm_f32(p.ctx, 0, t, WGB_NO_TRANS, nbr, p.n, nar, -1.f, Ap, p.lda, p.B + a, p.ldb,
+                         beta, p.B + b, p.ldb, wgb::kBandNone);
+  }
+  const float *Ap = p.trans ? p.A + b + a * p.lda : p.A + a + b * p.lda;
+  return wgb::gemm_f32(p.ctx, 0, WGB_NO_TRANS, t, p.m, nbr, nar, -1.f, p.B + a * p.ldb, p.ldb, Ap,
+                       p.lda, beta, p.B + b * p.ldb, p.ldb, wgb::kBandNone);
+}
+
+// Solves frame rows [lo, hi); `scaled`: those rows of B already carry alpha.
+// The first half in solve order is solved, the second half is updated with
+// it (beta = alpha folds the scaling into that GEMM), then solved.
+int trsm_solve(const Trsm &p, int64_t lo, int64_t hi, bool scaled) {
+  const int64_t size = hi - lo;
+  if (size <= kLeaf) return trsm_leaf(p, lo, size, scaled ? 1.f : p.alpha);
+  const int64_t mid = lo + (size / 2 + kLeaf - 1) / kLeaf * kLeaf;
+  const int64_t a0 = p.forward ? lo : mid, a1 = p.forward ? mid : hi;
+  const int64_t b0 = p.forward ? mid : lo, b1 = p.forward ? hi : mid;
+  int st = trsm_solve(p, a0, a1, scaled);
+  if (st) return st;
+  if ((st = trsm_update(p, a0, a1 - a0, b0, b1 - b0, scaled ? 1.f : p.alpha))) return st;
+  return trsm_solve(p, b0, b1, true);
+}
+
+// B <- 0 over its m x n part, reading nothing.
+int zero_b(wgb_ctx *ctx, int64_t m, int64_t n, float *B, int64_t ldb) {
+  return wgb::gemm_f32(ctx, 0, WGB_NO_TRANS, WGB_NO_TRANS, m, n, 0, 0.f, nullptr, 1, nullptr, 1,
+                       0.f, B, ldb, wgb::kBandNone);
+}
+
+int check_tri(int side, int uplo, int transA, int diag, int64_t m, int64_t n, const void *A,
+              int64_t lda, const void *B, int64_t ldb) {
+  if (side != WGB_LEFT && side != WGB_RIGHT)
+    return fail(WGB_ERR_INVALID_VALUE, "side must be WGB_LEFT or WGB_RIGHT");
+  if (uplo != WGB_LOWER && uplo != WGB_UPPER)
+    return fail(WGB_ERR_INVALID_VALUE, "uplo must be WGB_LOWER or WGB_UPPER");
+  if (transA != WGB_NO_TRANS && transA != WGB_TRANS)
+    return fail(WGB_ERR_INVALID_VALUE, "transA must be WGB_NO_TRANS or WGB_TRANS");
+  if (diag != WGB_NON_UNIT && diag != WGB_UNIT)
+    return fail(WGB_ERR_INVALID_VALUE, "diag must be WGB_NON_UNIT or WGB_UNIT");
+  if (m < 0 || n < 0) return fail(WGB_ERR_INVALID_VALUE, "m and n must be non-negative");
+  if (m > INT32_MAX || n > INT32_MAX) return fail(WGB_ERR_INVALID_VALUE, "m and n must be below 2^31");
+  const int64_t order = side == WGB_LEFT ? m : n;
+  if (lda < imax(1, order)) return fail(WGB_ERR_INVALID_VALUE, "lda must be >= max(1, order of A)");
+  if (ldb < imax(1, m)) return fail(WGB_ERR_INVALID_VALUE, "ldb must be >= max(1, m)");
+  if (m > 0 && n > 0 && (!A || !B)) return fail(WGB_ERR_INVALID_VALUE, "A or B is null");
+  return WGB_OK;
+}
+
+}  // namespace
+
+extern "C" int wgb_ssyr2k(wgb_ctx *ctx, int uplo, int trans, int64_t n, int64_t k, float alpha,
+                          const float *A, int64_t lda, const float *B, int64_t ldb, float beta,
+                          float *C, int64_t ldc) {
+  int st = wgb::enter(ctx);
+  if (st) return st;
+  if (trans != WGB_NO_TRANS && trans != WGB_TRANS)
+    return fail(WGB_ERR_INVALID_VALUE, "trans must be WGB_NO_TRANS or WGB_TRANS");
+  const int tB = trans == WGB_NO_TRANS ? WGB_TRANS : WGB_NO_TRANS;
+  if ((st = wgb::check_gemm(uplo, true, trans, tB, n, n, k, A, lda, B, ldb, C, ldc))) return st;
+  if (n == 0) return WGB_OK;
+  wgb::timing_begin(ctx);
+  // pass 1: alpha op(A) op(B)^T + beta C; pass 2: alpha op(B) op(A)^T + C
+  // (src/ssyr2k/ssyr2k.mjs:206-262)
+  if ((st = wgb::gemm_f32(ctx, uplo, trans, tB, n, n, k, alpha, A, lda, B, ldb, beta, C, ldc,
+                          wgb::kBandNone)))
+    return st;
+  if (alpha != 0.f && k != 0 &&
+      (st = wgb::gemm_f32(ctx, uplo, trans, tB, n, n, k, alpha, B, ldb, A, lda, 1.f, C, ldc,
+                          wgb::kBandNone)))
+    return st;
+  wgb::timing_end(ctx);
+  return WGB_OK;
+}
+
+extern "C" int wgb_ssymm(wgb_ctx *ctx, int side, int uplo, int64_t m, int64_t n, float alpha,
+                         const float *A, int64_t lda, const float *B, int64_t ldb, float beta,
+                         float *C, int64_t ldc) {
+  int st = wgb::enter(ctx);
+  if (st) return st;
+  if (side != WGB_LEFT && side != WGB_RIGHT)
+    return fail(WGB_ERR_INVALID_VALUE, "side must be WGB_LEFT or WGB_RIGHT");
+  if (uplo != WGB_LOWER && uplo != WGB_UPPER)
+    return fail(WGB_ERR_INVALID_VALUE, "uplo must be WGB_LOWER or WGB_UPPER");
+  if (m < 0 || n < 0) return fail(WGB_ERR_INVALID_VALUE, "m and n must be non-negative");
+  if (m > INT32_MAX || n > INT32_MAX) return fail(WGB_ERR_INVALID_VALUE, "m and n must be below 2^31");
+  const int64_t order = side == WGB_LEFT ? m : n;
+  if (lda < imax(1, order)) return fail(WGB_ERR_INVALID_VALUE, "lda must be >= max(1, order of A)");
+  if (ldb < imax(1, m)) return fail(WGB_ERR_INVALID_VALUE, "ldb must be >= max(1, m)");
+  if (ldc < imax(1, m)) return fail(WGB_ERR_INVALID_VALUE, "ldc must be >= max(1, m)");
+  if (m == 0 || n == 0) return WGB_OK;
+  if (!C || (alpha != 0.f && (!A || !B))) return fail(WGB_ERR_INVALID_VALUE, "A, B or C is null");
+  wgb::timing_begin(ctx);
+  if (alpha == 0.f) {
+    // C <- beta C, reading neither A nor B
+    st = wgb::gemm_f32(ctx, 0, WGB_NO_TRANS, WGB_NO_TRANS, m, n, 0, 0.f, nullptr, 1, nullptr, 1,
+                       beta, C, ldc, wgb::kBandNone);
+  } else {
+    const int64_t ldw = round4(order);
+    if ((st = ensure_op_workspace(ctx, (size_t)ldw * order * sizeof(float)))) return st;
+    float *W = static_cast<float *>(ctx->op_ws);
+    const int64_t tiles = (order + kTile - 1) / kTile;
+    symmetrize_kernel<<<dim3((unsigned)tiles, (unsigned)tiles), 256, 0, ctx->stream>>>(order, A, lda,
+                                                                                      uplo, W, ldw);
+    WGB_CHECK_LAUNCH("symmetrize_kernel");
+    st = side == WGB_LEFT
+             ? wgb::gemm_f32(ctx, 0, WGB_NO_TRANS, WGB_NO_TRANS, m, n, m, alpha, W, ldw, B, ldb,
+                             beta, C, ldc, wgb::kBandNone)
+             : wgb::gemm_f32(ctx, 0, WGB_NO_TRANS, WGB_NO_TRANS, m, n, n, alpha, B, ldb, W, ldw,
+                             beta, C, ldc, wgb::kBandNone);
+  }
+  if (st) return st;
+  wgb::timing_end(ctx);
+  return WGB_OK;
+}
+
+extern "C" int wgb_strmm(wgb_ctx *ctx, int side, int uplo, int transA, int diag, int64_t m,
+                         int64_t n, float alpha, const float *A, int64_t lda, float *B,
+                         int64_t ldb) {
+  int st = wgb::enter(ctx);
+  if (st) return st;
+  if ((st = check_tri(side, uplo, transA, diag, m, n, A, lda, B, ldb))) return st;
+  if (m == 0 || n == 0) return WGB_OK;
+  wgb::timing_begin(ctx);
+  if (alpha == 0.f) {
+    st = zero_b(ctx, m, n, B, ldb);
+  } else {
+    const bool left = side == WGB_LEFT;
+    const int64_t order = left ? m : n;
+    const int64_t ldw = round4(order), ldbc = round4(m);
+    if ((st = ensure_op_workspace(ctx, (size_t)(ldw * order + ldbc * n) * sizeof(float)))) return st;
+    float *W = static_cast<float *>(ctx->op_ws);
+    float *Bc = W + ldw * order;  // 16-byte aligned: ldw is a multiple of 4
+    const int64_t gy = order < 65535 ? order : 65535;
+    triangle_copy_kernel<<<dim3((unsigned)((order + 255) / 256), (unsigned)gy), 256, 0,
+                           ctx->stream>>>(order, A, lda, uplo, diag == WGB_UNIT, W, ldw);
+    WGB_CHECK_LAUNCH("triangle_copy_kernel");
+    WGB_CHECK_HIP(hipMemcpy2DAsync(Bc, (size_t)ldbc * sizeof(float), B, (size_t)ldb * sizeof(float),
+                                   (size_t)m * sizeof(float), (size_t)n, hipMemcpyDeviceToDevice,
+                                   ctx->stream));
+    const bool op_lower = (uplo == WGB_LOWER) != (transA == WGB_TRANS);
+    st = left ? wgb::gemm_f32(ctx, 0, transA, WGB_NO_TRANS, m, n, m, alpha, W, ldw, Bc, ldbc, 0.f, B,
+                              ldb, op_lower ? wgb::kBandALower : wgb::kBandAUpper)
+              : wgb::gemm_f32(ctx, 0, WGB_NO_TRANS, transA, m, n, n, alpha, Bc, ldbc, W, ldw, 0.f, B,
+                              ldb, op_lower ? wgb::kBandBLower : wgb::kBandBUpper);
+  }
+  if (st) return st;
+  wgb::timing_end(ctx);
+  return WGB_OK;
+}
+
+extern "C" int wgb_strsm(wgb_ctx *ctx, int side, int uplo, int transA, int diag, int64_t m,
+                         int64_t n, float alpha, const float *A, int64_t lda, float *B,
+                         int64_t ldb) {
+  int st = wgb::enter(ctx);
+  if (st) return st;
+  if ((st = check_tri(side, uplo, transA, diag, m, n, A, lda, B, ldb))) return st;
+  if (m == 0 || n == 0) return WGB_OK;
+  wgb::timing_begin(ctx);
+  if (alpha == 0.f) {
+    // B becomes a literal zero, not 0 * B (src/strsm/strsm.mjs:424-430)
+    st = zero_b(ctx, m, n, B, ldb);
+  } else {
+    Trsm p;
+    p.ctx = ctx;
+    p.left = side == WGB_LEFT;
+    p.trans = transA == WGB_TRANS;
+    p.unit = diag == WGB_UNIT;
+    const bool op_lower = (uplo == WGB_LOWER) != p.trans;
+    p.forward = p.left ? op_lower : !op_lower;
+    p.m = m;
+    p.n = n;
+    p.alpha = alpha;
+    p.A = A;
+    p.lda = lda;
+    p.B = B;
+    p.ldb = ldb;
+    st = trsm_solve(p, 0, p.left ? m : n, false);
+  }
+  if (st) return st;
+  wgb::timing_end(ctx);
+  return WGB_OK;
+}

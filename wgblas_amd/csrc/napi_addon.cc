@@ -328,6 +328,73 @@ napi_value Ssyrk(napi_env env, napi_callback_info info) {
   return nullptr;
 }
 
+// ssyr2k(ctx, uplo, trans, n, k, alpha, A, lda, B, ldb, beta, C, ldc)
+napi_value Ssyr2k(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 13)) return nullptr;
+  wgb_ctx *ctx = ctx_of(env, a.v[0]);
+  if (!ctx) return nullptr;
+  int uplo, trans;
+  int64_t n, k, lda, ldb, ldc;
+  double alpha, beta;
+  void *A, *B, *C;
+  if (!get_i32(env, a.v[1], &uplo) || !get_i32(env, a.v[2], &trans) || !get_i64(env, a.v[3], &n) ||
+      !get_i64(env, a.v[4], &k) || !get_f64(env, a.v[5], &alpha) || !get_ptr(env, a.v[6], &A) ||
+      !get_i64(env, a.v[7], &lda) || !get_ptr(env, a.v[8], &B) || !get_i64(env, a.v[9], &ldb) ||
+      !get_f64(env, a.v[10], &beta) || !get_ptr(env, a.v[11], &C) || !get_i64(env, a.v[12], &ldc))
+    return nullptr;
+  WGB_OK_OR_THROW(wgb_ssyr2k(ctx, uplo, trans, n, k, (float)alpha, (const float *)A, lda,
+                             (const float *)B, ldb, (float)beta, (float *)C, ldc), "wgb_ssyr2k");
+  return nullptr;
+}
+
+// ssymm(ctx, side, uplo, m, n, alpha, A, lda, B, ldb, beta, C, ldc)
+napi_value Ssymm(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 13)) return nullptr;
+  wgb_ctx *ctx = ctx_of(env, a.v[0]);
+  if (!ctx) return nullptr;
+  int side, uplo;
+  int64_t m, n, lda, ldb, ldc;
+  double alpha, beta;
+  void *A, *B, *C;
+  if (!get_i32(env, a.v[1], &side) || !get_i32(env, a.v[2], &uplo) || !get_i64(env, a.v[3], &m) ||
+      !get_i64(env, a.v[4], &n) || !get_f64(env, a.v[5], &alpha) || !get_ptr(env, a.v[6], &A) ||
+      !get_i64(env, a.v[7], &lda) || !get_ptr(env, a.v[8], &B) || !get_i64(env, a.v[9], &ldb) ||
+      !get_f64(env, a.v[10], &beta) || !get_ptr(env, a.v[11], &C) || !get_i64(env, a.v[12], &ldc))
+    return nullptr;
+  WGB_OK_OR_THROW(wgb_ssymm(ctx, side, uplo, m, n, (float)alpha, (const float *)A, lda,
+                            (const float *)B, ldb, (float)beta, (float *)C, ldc), "wgb_ssymm");
+  return nullptr;
+}
+
+// tri(kind, ctx, side, uplo, transA, diag, m, n, alpha, A, lda, B, ldb);
+// kind: 0 strmm, 1 strsm.
+napi_value Tri(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 13)) return nullptr;
+  int kind, side, uplo, trans, diag;
+  if (!get_i32(env, a.v[0], &kind)) return nullptr;
+  wgb_ctx *ctx = ctx_of(env, a.v[1]);
+  if (!ctx) return nullptr;
+  int64_t m, n, lda, ldb;
+  double alpha;
+  void *A, *B;
+  if (!get_i32(env, a.v[2], &side) || !get_i32(env, a.v[3], &uplo) || !get_i32(env, a.v[4], &trans) ||
+      !get_i32(env, a.v[5], &diag) || !get_i64(env, a.v[6], &m) || !get_i64(env, a.v[7], &n) ||
+      !get_f64(env, a.v[8], &alpha) || !get_ptr(env, a.v[9], &A) || !get_i64(env, a.v[10], &lda) ||
+      !get_ptr(env, a.v[11], &B) || !get_i64(env, a.v[12], &ldb))
+    return nullptr;
+  if (kind == 0) {
+    WGB_OK_OR_THROW(wgb_strmm(ctx, side, uplo, trans, diag, m, n, (float)alpha, (const float *)A,
+                              lda, (float *)B, ldb), "wgb_strmm");
+  } else {
+    WGB_OK_OR_THROW(wgb_strsm(ctx, side, uplo, trans, diag, m, n, (float)alpha, (const float *)A,
+                              lda, (float *)B, ldb), "wgb_strsm");
+  }
+  return nullptr;
+}
+
 // ---- level 1 ---------------------------------------------------------------
 
 // reduce(kind, ctx, n, x, incx[, y, incy]) -> number; kind: 0 sdot, 1 sasum,
@@ -376,7 +443,8 @@ napi_value ModuleInit(napi_env env, napi_value exports) {
       {"deviceName", DeviceName}, {"setTiming", SetTiming}, {"lastTimeMs", LastTimeMs},
       {"synchronize", Synchronize}, {"malloc", Malloc}, {"free", Free},
       {"upload", Upload}, {"download", Download}, {"gemm", Gemm},
-      {"ssyrk", Ssyrk}, {"reduce", Reduce},
+      {"ssyrk", Ssyrk}, {"ssyr2k", Ssyr2k}, {"ssymm", Ssymm},
+      {"tri", Tri}, {"reduce", Reduce},
   };
   for (const Fn &f : fns) {
     napi_value v;

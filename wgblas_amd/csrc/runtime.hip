@@ -84,9 +84,16 @@ extern "C" int wgb_init(int device, wgb_ctx **out) {
   hipDeviceProp_t prop;
   hipError_t e = hipGetDeviceProperties(&prop, device);
   if (e == hipSuccess) {
-    std::snprintf(ctx->name, sizeof(ctx->name), "%s", prop.name);
     std::snprintf(ctx->arch, sizeof(ctx->arch), "%s", prop.gcnArchName);
     ctx->num_cus = prop.multiProcessorCount;
+    // the marketing name can be empty when the driver's id table lacks the
+    // part; fall back to the architecture and CU count
+    if (prop.name[0])
+      std::snprintf(ctx->name, sizeof(ctx->name), "%s", prop.name);
+    else
+      std::snprintf(ctx->name, sizeof(ctx->name), "AMD %.*s (%d CUs)",
+                    (int)std::strcspn(prop.gcnArchName, ":"), prop.gcnArchName,
+                    prop.multiProcessorCount);
   }
   if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
   if (e == hipSuccess) e = hipEventCreate(&ctx->ev_start);
@@ -109,6 +116,7 @@ extern "C" int wgb_destroy(wgb_ctx *ctx) {
   if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
   if (ctx->scratch) (void)hipFree(ctx->scratch);
   if (ctx->gemm_ws) (void)hipFree(ctx->gemm_ws);
+  if (ctx->op_ws) (void)hipFree(ctx->op_ws);
   if (ctx->host_result) (void)hipHostFree(ctx->host_result);
   if (ctx->ev_start) (void)hipEventDestroy(ctx->ev_start);
   if (ctx->ev_stop) (void)hipEventDestroy(ctx->ev_stop);

@@ -1,6 +1,7 @@
 // wgblas's public API for the hot path, on HIP (the routine set of
-// index.mjs in wgblas limited to the GEMM family and the level-1
-// reductions, plus the device, residency and seeded-input helpers).
+// index.mjs in wgblas limited to the GEMM family, the level-3 routines built
+// on it and the level-1 reductions, plus the device, residency and
+// seeded-input helpers).
 export { init, cleanup, gpuName, HipDevice } from "./src/init.mjs";
 export { GpuVector } from "./src/classes/GpuVector.mjs";
 export { GpuMatrix } from "./src/classes/GpuMatrix.mjs";
@@ -11,6 +12,10 @@ export { ssyrk } from "./src/ssyrk.mjs";
 export { dgemm } from "./src/dgemm.mjs";
 export { dgemmtr } from "./src/dgemmtr.mjs";
 export { dsyrk } from "./src/dsyrk.mjs";
+export { ssyr2k } from "./src/ssyr2k.mjs";
+export { ssymm } from "./src/ssymm.mjs";
+export { strmm } from "./src/strmm.mjs";
+export { strsm } from "./src/strsm.mjs";
 export { sdot } from "./src/sdot.mjs";
 export { sasum } from "./src/sasum.mjs";
 export { snrm2 } from "./src/snrm2.mjs";

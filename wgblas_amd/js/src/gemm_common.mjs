@@ -118,11 +118,12 @@ export function toColumnMajor(a, eff, uplo) {
 
 /**
  * Runs one device call. Host-array operands are copied to temporary device
- * buffers (freed before returning) and C is read back into a new typed array
- * (the input is not modified); GpuMatrix operands are used in place.
- * `launch(ctx, ptrA, ptrB, ptrC)` issues the call.
+ * buffers (freed before returning) and the output C is read back into a new
+ * typed array (the input is not modified), returned under `key` ("C", or
+ * "B" for strmm / strsm); GpuMatrix operands are used in place.
+ * `launch(ctx, ptrs, ptrC)` issues the call.
  */
-export function execute(device, operands, C, CIsGpu, arrayType, launch) {
+export function execute(device, operands, C, CIsGpu, arrayType, launch, key = "C") {
   const nat = native();
   const ctx = device.ctx();
   const temps = [];
@@ -148,7 +149,7 @@ export function execute(device, operands, C, CIsGpu, arrayType, launch) {
     if (CIsGpu) return t === undefined ? {} : { gpuTimeMs: t };
     const out = new arrayType(C.length);
     nat.download(ctx, pC, out);
-    return t === undefined ? { C: out } : { C: out, gpuTimeMs: t };
+    return t === undefined ? { [key]: out } : { [key]: out, gpuTimeMs: t };
   } finally {
     for (const p of temps) nat.free(ctx, p);
   }

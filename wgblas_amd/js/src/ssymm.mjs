@@ -1,0 +1,57 @@
+// ssymm: C <- alpha*A*B + beta*C (side 'left') or alpha*B*A + beta*C
+// ('right'), A symmetric with only its uplo triangle read (wgblas
+// src/ssymm/ssymm.mjs:30-318), on wgb_ssymm. Argument checks keep wgblas's
+// order and messages (ssymm.mjs:48-134).
+import { GpuMatrix } from "./classes/GpuMatrix.mjs";
+import { requireGpuDevice, requireSameDevice } from "./device.mjs";
+import { checkLayout, checkOperand, checkScalar, checkUplo, execute, UPLO } from "./gemm_common.mjs";
+import { checkSide, SIDE } from "./tri_common.mjs";
+import { native } from "./native.mjs";
+
+export async function ssymm(device, side, uplo, m, n, alpha, A, lda, B, ldb, beta, C, ldc,
+                            layout = "row-major") {
+  const AIsGpu = A instanceof GpuMatrix;
+  const BIsGpu = B instanceof GpuMatrix;
+  const CIsGpu = C instanceof GpuMatrix;
+  requireGpuDevice(device);
+  requireSameDevice(device, "ssymm", { A, B, C });
+  checkSide(side);
+  checkUplo(uplo);
+  checkLayout(layout);
+  checkScalar("alpha", alpha);
+  checkScalar("beta", beta);
+  for (const v of [m, n, lda, ldb, ldc])
+    if (!Number.isInteger(v)) throw new Error("m, n, lda, ldb, and ldc must be integers.");
+  if (!AIsGpu && !(A instanceof Float32Array)) throw new Error("A must be a Float32Array or GpuMatrix.");
+  if (!BIsGpu && !(B instanceof Float32Array)) throw new Error("B must be a Float32Array or GpuMatrix.");
+  if (!CIsGpu && !(C instanceof Float32Array)) throw new Error("C must be a Float32Array or GpuMatrix.");
+  if ((AIsGpu || BIsGpu) && !CIsGpu) throw new Error("C must be a GpuMatrix when A or B is a GpuMatrix.");
+  if (CIsGpu && (!AIsGpu || !BIsGpu)) throw new Error("A and B must be GpuMatrix when C is a GpuMatrix.");
+  if (m < 0 || n < 0) throw new Error("m and n must be non-negative.");
+  if (m === 0 || n === 0) return CIsGpu ? {} : { C };
+  const layoutA = AIsGpu ? A.layout : layout;
+  const layoutB = BIsGpu ? B.layout : layout;
+  const layoutC = CIsGpu ? C.layout : layout;
+  const order = side === "left" ? m : n;
+  if (lda < order) throw new Error("lda must be >= " + (side === "left" ? "m" : "n") + ".");
+  if (AIsGpu) {
+    if (lda !== A.lda) throw new Error("lda must match A.lda when A is a GpuMatrix.");
+    if (A.rows < order || A.cols < order) throw new Error("A is too small for the given m/n and side.");
+  } else if (A.length < (order - 1) * lda + order) {
+    throw new Error("A does not have enough elements for the given dimensions and lda.");
+  }
+  checkOperand(B, BIsGpu, layoutB, "no-transpose", m, n, ldb, { X: "B", ld: "ldb", dims: "m and n" });
+  checkOperand(C, CIsGpu, layoutC, "no-transpose", m, n, ldc, { X: "C", ld: "ldc", dims: "m and n" });
+  // The C ABI has no trans flag for B: B and C must share a storage order.
+  if (layoutB !== layoutC) throw new Error("B and C must have the same layout.");
+  // Column-major frame: a row-major A stores the other triangle of the same
+  // symmetric matrix; a row-major C = S B is the column-major C^T = B^T S.
+  let u = UPLO[uplo];
+  if (layoutA !== "column-major") u = u === 1 ? 2 : 1;
+  let s = SIDE[side];
+  let [mm, nn] = [m, n];
+  if (layoutC !== "column-major") [s, mm, nn] = [3 - s, n, m];
+  return execute(device, [A, B], C, CIsGpu, Float32Array, (ctx, p, pC) =>
+    native().ssymm(ctx, s, u, mm, nn, alpha, p[0], lda, p[1], ldb, beta, pC, ldc),
+  );
+}

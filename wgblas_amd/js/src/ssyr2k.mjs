@@ -1,0 +1,64 @@
+// ssyr2k: C <- alpha*op(A)*op(B)^T + alpha*op(B)*op(A)^T + beta*C on the uplo
+// triangle of the n x n C (wgblas src/ssyr2k/ssyr2k.mjs:27-301), on
+// wgb_ssyr2k (two triangle launches, the second with beta = 1, as wgblas).
+// Argument checks keep wgblas's order and messages (ssyr2k.mjs:45-133).
+import { GpuMatrix } from "./classes/GpuMatrix.mjs";
+import { requireGpuDevice, requireSameDevice } from "./device.mjs";
+import {
+  checkLayout, checkOperand, checkScalar, checkTrans, checkUplo, execute, TRANS, NO_TRANS, UPLO,
+} from "./gemm_common.mjs";
+import { native } from "./native.mjs";
+
+export async function ssyr2k(device, uplo, trans, n, k, alpha, A, lda, B, ldb, beta, C, ldc,
+                             layout = "row-major") {
+  const AIsGpu = A instanceof GpuMatrix;
+  const BIsGpu = B instanceof GpuMatrix;
+  const CIsGpu = C instanceof GpuMatrix;
+  requireGpuDevice(device);
+  requireSameDevice(device, "ssyr2k", { A, B, C });
+  checkUplo(uplo);
+  checkTrans("trans", trans);
+  checkLayout(layout);
+  checkScalar("alpha", alpha);
+  checkScalar("beta", beta);
+  for (const v of [n, k, lda, ldb, ldc])
+    if (!Number.isInteger(v)) throw new Error("n, k, lda, ldb, and ldc must be integers.");
+  if (!AIsGpu && !(A instanceof Float32Array)) throw new Error("A must be a Float32Array or GpuMatrix.");
+  if (!BIsGpu && !(B instanceof Float32Array)) throw new Error("B must be a Float32Array or GpuMatrix.");
+  if (!CIsGpu && !(C instanceof Float32Array)) throw new Error("C must be a Float32Array or GpuMatrix.");
+  if ((AIsGpu || BIsGpu) && !CIsGpu) throw new Error("C must be a GpuMatrix when A or B is a GpuMatrix.");
+  if (CIsGpu && (!AIsGpu || !BIsGpu)) throw new Error("A and B must be GpuMatrix when C is a GpuMatrix.");
+  if (n < 0 || k < 0) throw new Error("n and k must be non-negative.");
+  if (lda <= 0 || ldb <= 0 || ldc <= 0) throw new Error("lda, ldb, and ldc must be positive.");
+  if (n === 0) return CIsGpu ? {} : { C };
+  const layoutA = AIsGpu ? A.layout : layout;
+  const layoutB = BIsGpu ? B.layout : layout;
+  const layoutC = CIsGpu ? C.layout : layout;
+  checkOperand(A, AIsGpu, layoutA, trans, n, k, lda, { X: "A", ld: "lda", dims: "n, k, and trans" });
+  checkOperand(B, BIsGpu, layoutB, trans, n, k, ldb, { X: "B", ld: "ldb", dims: "n, k, and trans" });
+  if (ldc < n) throw new Error("ldc must be >= n.");
+  if (CIsGpu) {
+    if (ldc !== C.lda) throw new Error("ldc must match C.lda when C is a GpuMatrix.");
+    if (C.rows < n || C.cols < n) throw new Error("C is too small for the given n.");
+  } else if (C.length < (n - 1) * ldc + n) {
+    throw new Error("C does not have enough elements for the given dimensions and ldc.");
+  }
+  // Column-major frame: a row-major operand flips its own trans; the update
+  // is symmetric, so a row-major C is the other triangle.
+  const tA = (trans === "transpose") !== (layoutA !== "column-major") ? TRANS : NO_TRANS;
+  const tB = (trans === "transpose") !== (layoutB !== "column-major") ? TRANS : NO_TRANS;
+  let u = UPLO[uplo];
+  if (layoutC !== "column-major") u = u === 1 ? 2 : 1;
+  return execute(device, [A, B], C, CIsGpu, Float32Array, (ctx, p, pC) => {
+    const nat = native();
+    if (tA === tB) {
+      nat.ssyr2k(ctx, u, tA, n, k, alpha, p[0], lda, p[1], ldb, beta, pC, ldc);
+      return;
+    }
+    // A and B in different layouts (GpuMatrix operands): the same two
+    // triangle passes with a trans flag per operand.
+    nat.gemm(1, ctx, u, tA, 1 - tB, n, n, k, alpha, p[0], lda, p[1], ldb, beta, pC, ldc);
+    if (alpha !== 0 && k !== 0)
+      nat.gemm(1, ctx, u, tB, 1 - tA, n, n, k, alpha, p[1], ldb, p[0], lda, 1, pC, ldc);
+  });
+}

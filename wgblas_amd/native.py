@@ -15,6 +15,8 @@ LIB_PATH = os.path.join(_HERE, "lib", "libwgblas_hip.so")
 
 NO_TRANS, TRANS = 0, 1
 LOWER, UPPER = 1, 2
+LEFT, RIGHT = 1, 2
+NON_UNIT, UNIT = 0, 1
 
 _i64 = C.c_int64
 _ptr = C.c_void_p
@@ -51,6 +53,14 @@ _SIGNATURES = {
                     _ptr, _i64, C.c_double, _ptr, _i64],
     "wgb_dsyrk": [_ptr, C.c_int, C.c_int, _i64, _i64, C.c_double, _ptr, _i64, C.c_double, _ptr,
                   _i64],
+    "wgb_ssyr2k": [_ptr, C.c_int, C.c_int, _i64, _i64, C.c_float, _ptr, _i64, _ptr, _i64,
+                   C.c_float, _ptr, _i64],
+    "wgb_ssymm": [_ptr, C.c_int, C.c_int, _i64, _i64, C.c_float, _ptr, _i64, _ptr, _i64,
+                  C.c_float, _ptr, _i64],
+    "wgb_strmm": [_ptr, C.c_int, C.c_int, C.c_int, C.c_int, _i64, _i64, C.c_float, _ptr, _i64,
+                  _ptr, _i64],
+    "wgb_strsm": [_ptr, C.c_int, C.c_int, C.c_int, C.c_int, _i64, _i64, C.c_float, _ptr, _i64,
+                  _ptr, _i64],
     "wgb_sdot": [_ptr, _i64, _ptr, _i64, _ptr, _i64, C.POINTER(C.c_float)],
     "wgb_sdot_dev": [_ptr, _i64, _ptr, _i64, _ptr, _i64, _ptr],
     "wgb_sasum": [_ptr, _i64, _ptr, _i64, C.POINTER(C.c_float)],
@@ -256,6 +266,22 @@ class Context:
     def dsyrk(self, uplo, trans, n, k, alpha, A, lda, beta, C_, ldc):
         _check(self.lib.wgb_dsyrk(self.handle, uplo, trans, n, k, alpha, _p(A), lda, beta,
                                   _p(C_), ldc), "wgb_dsyrk")
+
+    def ssyr2k(self, uplo, trans, n, k, alpha, A, lda, B, ldb, beta, C_, ldc):
+        _check(self.lib.wgb_ssyr2k(self.handle, uplo, trans, n, k, alpha, _p(A), lda, _p(B), ldb,
+                                   beta, _p(C_), ldc), "wgb_ssyr2k")
+
+    def ssymm(self, side, uplo, m, n, alpha, A, lda, B, ldb, beta, C_, ldc):
+        _check(self.lib.wgb_ssymm(self.handle, side, uplo, m, n, alpha, _p(A), lda, _p(B), ldb,
+                                  beta, _p(C_), ldc), "wgb_ssymm")
+
+    def strmm(self, side, uplo, transA, diag, m, n, alpha, A, lda, B, ldb):
+        _check(self.lib.wgb_strmm(self.handle, side, uplo, transA, diag, m, n, alpha, _p(A), lda,
+                                  _p(B), ldb), "wgb_strmm")
+
+    def strsm(self, side, uplo, transA, diag, m, n, alpha, A, lda, B, ldb):
+        _check(self.lib.wgb_strsm(self.handle, side, uplo, transA, diag, m, n, alpha, _p(A), lda,
+                                  _p(B), ldb), "wgb_strsm")
 
     # ---- level 1 ----
     def sdot(self, n, x, incx, y, incy):

@@ -210,8 +210,20 @@ def bench_components(ctx, ev, quick):
     ms = ev.stop_ms() / 10
     comps["sgemmtr_8192x4096_x10"] = {"ms_per_call": ms, "tflops": fl / ms / 1e9,
                                       "frac_fp32_peak": fl / ms / 1e-3 / PEAK_FP32}
+    # ssyr2k on the same shape: B = a second n x k operand (2 n(n+1) k flops,
+    # wgblas's benchmarks/ssyr2k convention)
+    dB = ctx.empty(n * k, np.float32)
+    ctx.fill_normal(dB, 6)
+    h = lambda: ctx.ssyr2k(LOWER, NO_TRANS, n, k, 1.0, dA, n, dB, n, 0.25, dC, n)
+    h()
+    ms = per_launch_ms(ctx, h, reps)
+    fl = 2.0 * n * (n + 1) * k
+    comps["ssyr2k_8192x4096"] = {"ms": ms, "tflops": fl / ms / 1e9,
+                                 "frac_fp32_peak": fl / ms / 1e-3 / PEAK_FP32}
     dA.free()
+    dB.free()
     dC.free()
+    comps.update(bench_level3(ctx, reps))
 
     # config 2: reductions at n = 2^28 (normal seed 1 / 2, planted duplicate max)
     n = 1 << 28
@@ -267,6 +279,58 @@ def bench_components(ctx, ev, quick):
     return comps
 
 
+def bench_level3(ctx, reps):
+    """ssymm, strmm and strsm at order 8192 (left side, lower, no transpose),
+    strsm also at 4096 (the top of wgblas's benchmarks/strsm sizes).
+    `tflops` follows wgblas's benchmarks/<routine> flop conventions (ssymm
+    2mn*order + 2mn, strmm 2mn*order + mn, strsm mn*order); `frac_fp32_peak`
+    uses the arithmetic the routine must do (strmm: the triangle's
+    mn*order)."""
+    from wgblas_amd import LEFT, LOWER, NON_UNIT, NO_TRANS
+
+    comps = {}
+    n = 8192
+    dA = ctx.empty(n * n, np.float32)
+    dB = ctx.empty(n * n, np.float32)
+    dC = ctx.empty(n * n, np.float32)
+    ctx.fill_uniform(dA, -1.0, 1.0, 7)
+    ctx.fill_uniform(dB, -1.0, 1.0, 8)
+    ctx.fill_uniform(dC, -1.0, 1.0, 9)
+    f = lambda: ctx.ssymm(LEFT, LOWER, n, n, 1.0, dA, n, dB, n, 0.5, dC, n)
+    f()
+    ms = per_launch_ms(ctx, f, reps)
+    fl = 2.0 * n * n * n + 2.0 * n * n
+    comps["ssymm_8192"] = {"ms": ms, "tflops": fl / ms / 1e9, "frac_fp32_peak": fl / ms / 1e-3 / PEAK_FP32}
+    f = lambda: ctx.strmm(LEFT, LOWER, NO_TRANS, NON_UNIT, n, n, 1.0, dA, n, dB, n)
+    f()
+    ms = per_launch_ms(ctx, f, reps)
+    fl_ref, fl = 2.0 * n * n * n + 1.0 * n * n, 1.0 * n * n * n
+    comps["strmm_8192"] = {"ms": ms, "tflops": fl_ref / ms / 1e9, "tflops_triangle": fl / ms / 1e9,
+                           "frac_fp32_peak": fl / ms / 1e-3 / PEAK_FP32}
+    # strsm: a well-conditioned lower triangle (off-diagonals in [-1/n, 1/n),
+    # diagonal 2, as wgblas's tests build it); B is re-filled before each
+    # solve, outside the timed launch
+    for order in (4096, 8192):
+        ctx.fill_uniform(dA, -1.0 / order, 1.0 / order, 10)
+        diag = np.full(1, 2.0, np.float32)
+        for i in range(order):
+            ctx.h2d(dA.offset(i * order + i), diag)
+        fl = 1.0 * order * order * order
+        times = []
+        for _ in range(max(2, reps // 2)):
+            ctx.fill_uniform(dB, -1.0, 1.0, 11)
+            times.append(per_launch_ms(
+                ctx, lambda: ctx.strsm(LEFT, LOWER, NO_TRANS, NON_UNIT, order, order, 1.0, dA, order,
+                                       dB, order), 1))
+        ms = sorted(times)[len(times) // 2]
+        comps[f"strsm_{order}"] = {"ms": ms, "tflops": fl / ms / 1e9,
+                                   "frac_fp32_peak": fl / ms / 1e-3 / PEAK_FP32}
+    dA.free()
+    dB.free()
+    dC.free()
+    return comps
+
+
 def run_only(ctx, name, reps):
     """One workload alone, `reps` launches, for counter runs (rocprofv3
     --pmc): copy (1 GiB device-to-device, the traffic calibration),
@@ -308,6 +372,28 @@ def run_only(ctx, name, reps):
             ctx.ssyrk(LOWER, NO_TRANS, n, k, 1.0, dA, n, 0.25, dC, n)
         ctx.synchronize()
         return {"algorithmic_bytes": 4 * (n * k + n * (n + 1))}
+    if name in ("ssyr2k_8192", "ssymm_8192", "strmm_8192", "strsm_8192"):
+        from wgblas_amd import LEFT, NON_UNIT
+
+        n = 8192
+        dA, dB, dC = (ctx.empty(n * n, np.float32) for _ in range(3))
+        ctx.fill_uniform(dA, -1.0 / n, 1.0 / n, 10)
+        ctx.fill_uniform(dC, -1.0, 1.0, 9)
+        diag = np.full(1, 2.0, np.float32)
+        for i in range(n):
+            ctx.h2d(dA.offset(i * n + i), diag)
+        for _ in range(reps):
+            ctx.fill_uniform(dB, -1.0, 1.0, 11)
+            if name == "ssyr2k_8192":
+                ctx.ssyr2k(LOWER, NO_TRANS, n, n // 2, 1.0, dA, n, dB, n, 0.25, dC, n)
+            elif name == "ssymm_8192":
+                ctx.ssymm(LEFT, LOWER, n, n, 1.0, dA, n, dB, n, 0.5, dC, n)
+            elif name == "strmm_8192":
+                ctx.strmm(LEFT, LOWER, NO_TRANS, NON_UNIT, n, n, 1.0, dA, n, dB, n)
+            else:
+                ctx.strsm(LEFT, LOWER, NO_TRANS, NON_UNIT, n, n, 1.0, dA, n, dB, n)
+        ctx.synchronize()
+        return {"algorithmic_bytes": 4 * 3 * n * n}
     n = 1 << 28
     dx, dy = ctx.empty(n, np.float32), ctx.empty(n, np.float32)
     ctx.fill_normal(dx, 1)
@@ -356,7 +442,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default=None,
                     help="run one workload alone (copy, sgemm_8192, dgemm_4096, ssyrk_8192, "
-                         "sdot, sasum, snrm2, isamax) for counter collection")
+                         "ssyr2k_8192, ssymm_8192, strmm_8192, strsm_8192, sdot, sasum, snrm2, "
+                         "isamax) for counter and kernel-trace collection")
     ap.add_argument("--reps", type=int, default=3)
     args = ap.parse_args()
     if args.gpus != 1:

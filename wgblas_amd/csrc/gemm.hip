@@ -510,12 +510,11 @@ struct KernelPolicy {
   static constexpr bool kPerStep = sizeof(T) == 8;
 };
 
-// fp64 and the fp32 kernels with one k-contiguous and one mn-contiguous
-// operand are held to 256 registers (two waves per SIMD) explicitly; the
-// other fp32 kernels fit on their own with accumulators in AGPRs, which
-// measured faster for them.
+// One BT x BT tile (tm, tn) of C over k-tiles [kt0, kt0 + nkt): the main
+// loop and the epilogue (unit >= 0: a split-k unit's raw partial to ws).
 template <typename T, int BT, bool AKC, bool BKC, bool VEC>
-__global__ __launch_bounds__(kThreads, (sizeof(T) == 8 || AKC != BKC) ? 2 : 1) void gemm_kernel(GemmArgs<T> p) {
+__device__ __forceinline__ void gemm_tile(const GemmArgs<T> &p, int tm, int tn, int unit, int kt0,
+                                          int nkt, T *smem, const int t) {
   typedef typename Ty<T>::acc Acc;
   typedef typename Ty<T>::v16 V;
   constexpr int VW = Ty<T>::VW;
@@ -525,37 +524,10 @@ __global__ __launch_bounds__(kThreads, (sizeof(T) == 8 || AKC != BKC) ? 2 : 1) v
   typedef Stager<T, BT, AKC, VEC> SA;
   typedef Stager<T, BT, BKC, VEC> SB;
   constexpr int STAGE = SA::ELEMS + SB::ELEMS;
-  __shared__ __attribute__((aligned(16))) T smem[2 * STAGE];
-
-  // Block -> tile and k-range: the first nregular blocks take whole tiles
-  // (XCD-remapped), the rest are split-k units of the tail tiles.
-  int tm, tn, unit = -1, kt0 = 0;
   const int nkt_all = (int)((p.k + BK - 1) / BK);
-  int nkt = nkt_all;
-  if ((int)blockIdx.x < p.nregular) {
-    logical_tile(xcd_remap(blockIdx.x, p.nregular), p.tiles_m, p.tiles_n, p.uplo, tm, tn);
-    if (p.band != wgb::kBandNone) {
-      // op(A) lower: k < m0 + BT; op(A) upper: k >= m0; op(B) lower
-      // (nonzero for k >= j): k >= n0; op(B) upper: k < n0 + BT.
-      constexpr int TK = BT / BK;
-      const int lo = p.band == wgb::kBandAUpper ? tm * TK : p.band == wgb::kBandBLower ? tn * TK : 0;
-      int hi = p.band == wgb::kBandALower ? (tm + 1) * TK
-                                          : p.band == wgb::kBandBUpper ? (tn + 1) * TK : nkt_all;
-      if (hi > nkt_all) hi = nkt_all;
-      kt0 = lo;
-      nkt = hi - lo;
-    }
-  } else {
-    unit = (int)blockIdx.x - p.nregular;
-    logical_tile(p.nregular + unit / p.splits, p.tiles_m, p.tiles_n, p.uplo, tm, tn);
-    kt0 = (unit % p.splits) * p.kt_split;
-    nkt = nkt_all - kt0 < p.kt_split ? nkt_all - kt0 : p.kt_split;
-  }
-  // (nkt >= 1: k > 0 here, and the host never plans an empty split; an
-  // explicit nkt check costs the fp32 loop ~60 VGPRs of scheduling freedom.)
-  if (tm < 0 || tn < 0 || tm >= p.tiles_m || tn >= p.tiles_n) return;  // block-uniform
+  (void)nkt_all;
   const int64_t m0 = (int64_t)tm * BT, n0 = (int64_t)tn * BT;
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int lane = t & 63, wave = t >> 6;
   const int wm = (wave & 1) * WT, wn = (wave >> 1) * WT;
 
   // k-tiles are counted from kt0 below: the stagers start at k = kt0 BK and
@@ -816,6 +788,77 @@ __global__ __launch_bounds__(kThreads, (sizeof(T) == 8 || AKC != BKC) ? 2 : 1) v
   }
 }
 
+
+// fp64 and the fp32 kernels with one k-contiguous and one mn-contiguous
+// operand are held to 256 registers (two waves per SIMD) explicitly; the
+// other fp32 kernels fit on their own with accumulators in AGPRs, which
+// measured faster for them.
+//
+// PAIR (launches with a k band, p.band != kBandNone): a tile row's (or
+// column's) k range grows with its index, so block b takes the tile pair
+// (r, c) and (tiles-1-r, c) (columns for a band on op(B)) and every block
+// does the same work, whatever order the dispatcher fills the CUs in.
+template <typename T, int BT, bool AKC, bool BKC, bool VEC, bool PAIR>
+__global__ __launch_bounds__(kThreads, (sizeof(T) == 8 || AKC != BKC) ? 2 : 1) void gemm_kernel(GemmArgs<T> p) {
+  constexpr int BK = 128 / (int)sizeof(T);
+  typedef Stager<T, BT, AKC, VEC> SA;
+  typedef Stager<T, BT, BKC, VEC> SB;
+  constexpr int STAGE = SA::ELEMS + SB::ELEMS;
+  __shared__ __attribute__((aligned(16))) T smem[2 * STAGE];
+
+  if constexpr (!PAIR) {
+    // Block -> tile and k-range: the first nregular blocks take whole tiles
+    // (XCD-remapped), the rest are split-k units of the tail tiles.
+    int tm, tn, unit = -1, kt0 = 0;
+    const int nkt_all = (int)((p.k + BK - 1) / BK);
+    int nkt = nkt_all;
+    if ((int)blockIdx.x < p.nregular) {
+      logical_tile(xcd_remap(blockIdx.x, p.nregular), p.tiles_m, p.tiles_n, p.uplo, tm, tn);
+    } else {
+      unit = (int)blockIdx.x - p.nregular;
+      logical_tile(p.nregular + unit / p.splits, p.tiles_m, p.tiles_n, p.uplo, tm, tn);
+      kt0 = (unit % p.splits) * p.kt_split;
+      nkt = nkt_all - kt0 < p.kt_split ? nkt_all - kt0 : p.kt_split;
+    }
+    // (nkt >= 1: k > 0 here, and the host never plans an empty split; an
+    // explicit nkt check costs the fp32 loop ~60 VGPRs of scheduling freedom.)
+    if (tm < 0 || tn < 0 || tm >= p.tiles_m || tn >= p.tiles_n) return;  // block-uniform
+    gemm_tile<T, BT, AKC, BKC, VEC>(p, tm, tn, unit, kt0, nkt, smem, (int)threadIdx.x);
+  } else {
+    const int nkt_all = (int)((p.k + BK - 1) / BK);
+    const bool on_rows = p.band == wgb::kBandALower || p.band == wgb::kBandAUpper;
+    const int prs = on_rows ? (p.tiles_m + 1) / 2 : p.tiles_m;
+    const int pcs = on_rows ? p.tiles_n : (p.tiles_n + 1) / 2;
+    int pr, pc;
+    logical_tile(xcd_remap(blockIdx.x, p.nregular), prs, pcs, 0, pr, pc);
+#pragma unroll 1
+    for (int pass = 0; pass < 2; ++pass) {
+      int tm = pr, tn = pc;
+      if (pass == 1) {
+        if (on_rows)
+          tm = p.tiles_m - 1 - pr;
+        else
+          tn = p.tiles_n - 1 - pc;
+        if (tm == pr && tn == pc) break;  // the middle row / column of an odd count
+        __syncthreads();  // every wave is done with the first tile's LDS stages
+      }
+      // op(A) lower: k < m0 + BT; op(A) upper: k >= m0; op(B) lower
+      // (nonzero for k >= j): k >= n0; op(B) upper: k < n0 + BT.
+      constexpr int TK = BT / BK;
+      const int lo = p.band == wgb::kBandAUpper ? tm * TK : p.band == wgb::kBandBLower ? tn * TK : 0;
+      int hi = p.band == wgb::kBandALower ? (tm + 1) * TK
+                                          : p.band == wgb::kBandBUpper ? (tn + 1) * TK : nkt_all;
+      if (hi > nkt_all) hi = nkt_all;
+      // threadIdx.x passed through an empty asm each pass: the values the
+      // tile derives from it are recomputed per tile instead of being hoisted
+      // out of this loop and held in registers across both tiles.
+      int t = (int)threadIdx.x;
+      asm volatile("" : "+v"(t));
+      gemm_tile<T, BT, AKC, BKC, VEC>(p, tm, tn, -1, lo, hi - lo, smem, t);
+    }
+  }
+}
+
 // C <- beta*C (or 0 when beta == 0) on the uplo part of the m x n C: the
 // alpha == 0 / k == 0 path, which reads neither A nor B.
 template <typename T>
@@ -855,21 +898,30 @@ __global__ __launch_bounds__(BT) void split_fixup(GemmArgs<T> p) {
 template <typename T>
 using KernelFn = void (*)(GemmArgs<T>);
 
-template <typename T, int BT>
-KernelFn<T> pick_kernel(bool akc, bool bkc, bool vec) {
+template <typename T, int BT, bool PAIR>
+KernelFn<T> pick_layout(bool akc, bool bkc, bool vec) {
   if (vec) {
-    if (akc) return bkc ? gemm_kernel<T, BT, true, true, true> : gemm_kernel<T, BT, true, false, true>;
-    return bkc ? gemm_kernel<T, BT, false, true, true> : gemm_kernel<T, BT, false, false, true>;
+    if (akc) return bkc ? gemm_kernel<T, BT, true, true, true, PAIR> : gemm_kernel<T, BT, true, false, true, PAIR>;
+    return bkc ? gemm_kernel<T, BT, false, true, true, PAIR> : gemm_kernel<T, BT, false, false, true, PAIR>;
   }
-  if (akc) return bkc ? gemm_kernel<T, BT, true, true, false> : gemm_kernel<T, BT, true, false, false>;
-  return bkc ? gemm_kernel<T, BT, false, true, false> : gemm_kernel<T, BT, false, false, false>;
+  if (akc) return bkc ? gemm_kernel<T, BT, true, true, false, PAIR> : gemm_kernel<T, BT, true, false, false, PAIR>;
+  return bkc ? gemm_kernel<T, BT, false, true, false, PAIR> : gemm_kernel<T, BT, false, false, false, PAIR>;
+}
+
+// Banded (paired-tile) kernels exist for fp32 only: strmm is their caller.
+template <typename T, int BT>
+KernelFn<T> pick_kernel(bool akc, bool bkc, bool vec, bool pair) {
+  if constexpr (sizeof(T) == 4) {
+    if (pair) return pick_layout<T, BT, true>(akc, bkc, vec);
+  }
+  return pick_layout<T, BT, false>(akc, bkc, vec);
 }
 
 // Resident blocks per CU of one kernel instantiation (LDS and registers),
 // cached per (tier, operand layout) slot; 0 = not yet queried.
 template <typename T, int BT>
 int blocks_per_cu(KernelFn<T> fn, int slot) {
-  static int cache[8] = {0};
+  static int cache[16] = {0};
   if (cache[slot] == 0) {
     int nb = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, reinterpret_cast<const void *>(fn),
@@ -906,11 +958,18 @@ int ensure_workspace(wgb_ctx *ctx, size_t bytes) {
 template <typename T, int BT>
 int launch_tier(wgb_ctx *ctx, GemmArgs<T> &a, bool akc, bool bkc, bool vec) {
   constexpr int BK = 128 / (int)sizeof(T);
-  KernelFn<T> fn = pick_kernel<T, BT>(akc, bkc, vec);
+  const bool pair = sizeof(T) == 4 && a.band != wgb::kBandNone;
+  KernelFn<T> fn = pick_kernel<T, BT>(akc, bkc, vec, pair);
   const int64_t cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
-  const int64_t slots = cus * blocks_per_cu<T, BT>(fn, (akc ? 4 : 0) + (bkc ? 2 : 0) + (vec ? 1 : 0));
+  const int64_t slots =
+      cus * blocks_per_cu<T, BT>(fn, (pair ? 8 : 0) + (akc ? 4 : 0) + (bkc ? 2 : 0) + (vec ? 1 : 0));
   const int64_t nkt = (a.k + BK - 1) / BK;
   a.nregular = a.ntiles;
+  if (pair) {
+    // one block per tile pair (rows r and tiles_m-1-r, or columns), no split
+    const bool on_rows = a.band == wgb::kBandALower || a.band == wgb::kBandAUpper;
+    a.nregular = on_rows ? (a.tiles_m + 1) / 2 * a.tiles_n : a.tiles_m * ((a.tiles_n + 1) / 2);
+  }
   a.splits = 1;
   a.kt_split = (int)nkt;
   a.ws = nullptr;
@@ -930,7 +989,7 @@ int launch_tier(wgb_ctx *ctx, GemmArgs<T> &a, bool akc, bool bkc, bool vec) {
       a.ws = static_cast<T *>(ctx->gemm_ws);
     }
   }
-  const int64_t grid = a.nregular + (int64_t)(a.ntiles - a.nregular) * a.splits;
+  const int64_t grid = pair ? a.nregular : a.nregular + (int64_t)(a.ntiles - a.nregular) * a.splits;
   void *args[] = {&a};
   WGB_CHECK_HIP(hipLaunchKernel(reinterpret_cast<const void *>(fn), dim3((unsigned)grid),
                                 dim3(kThreads), args, 0, ctx->stream));

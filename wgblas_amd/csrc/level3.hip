@@ -8,8 +8,8 @@
 //   cannot read and write B at once), then one GEMM whose tiles only run the
 //   k-tiles the triangle reaches (about half the flops of a dense product).
 // strsm: recursive halving of the triangular dimension. Diagonal blocks of
-//   order <= 64 are solved by substitution, one wave per 64 right-hand sides
-//   with the unknowns in registers; the off-diagonal updates are GEMMs that
+//   order <= 64 are solved by substitution, one wave per right-hand side
+//   with a lane per unknown; the off-diagonal updates are GEMMs that
 //   read the solved rows of B and write other rows of B in place (disjoint
 //   memory), so strsm needs no workspace and no explicit inverse.
 #include "common.h"
@@ -23,7 +23,8 @@ namespace {
 using wgb::fail;
 
 constexpr int kTile = 64;  // symmetrize tile (64 x 64)
-constexpr int kLeaf = 64;  // order of strsm's substitution blocks
+constexpr int kLeaf = 64;       // order of strsm's substitution blocks
+constexpr int kLeafWaves = 16;  // right-hand sides (one wave each) per leaf block
 
 int64_t imax(int64_t a, int64_t b) { return a > b ? a : b; }
 int64_t round4(int64_t v) { return (v + 3) / 4 * 4; }
@@ -111,70 +112,55 @@ __global__ __launch_bounds__(256) void triangle_copy_kernel(int64_t order,
 // Frame element (i, k) of M is Ablk[ia(i) mi + ia(k) mk] and element i of
 // right-hand side r is Bblk[ia(i) vi + r vr], where ia(i) = nb-1-i for an
 // upper system solved backward (rev) and i otherwise; the solution
-// overwrites v. One wave per 64 right-hand sides: lane r holds its 64
-// unknowns in registers, M sits in LDS (column k contiguous, read as
-// broadcasts). Column-oriented order, as wgblas's strsm_small.wgsl and
-// reference BLAS: x_k /= M(k,k), then x_i -= M(i,k) x_k for i > k; alpha is
-// applied as v is read. VI1: the frame index is B's contiguous one (left
-// side).
-template <bool VI1>
-__global__ __launch_bounds__(64) void trsm_leaf_kernel(int nb, int64_t nrhs,
-                                                       const float *__restrict__ Ablk, int64_t mi,
-                                                       int64_t mk, int rev, int unit,
-                                                       float *__restrict__ Bblk, int64_t vi,
-                                                       int64_t vr, float alpha) {
-  __shared__ __attribute__((aligned(16))) float Ms[kLeaf * kLeaf];  // Ms[k*64 + i] = M(i, k)
-  __shared__ float Xs[kLeaf][kLeaf + 1];                            // Xs[rhs][i]
-  const int lane = threadIdx.x;
-  const int64_t rhs0 = (int64_t)blockIdx.x * kLeaf;
-  for (int e = lane; e < kLeaf * kLeaf; e += kLeaf) {
+// overwrites v. One wave per right-hand side, lane i owning unknown i and
+// row i of M (in registers, from the block's LDS copy): step k broadcasts
+// the finished x_k = v_k / M(k,k) with readlane and every later lane
+// subtracts M(i,k) x_k, the column-oriented order of wgblas's
+// strsm_small.wgsl and of reference BLAS, with no barrier inside the solve.
+// alpha is applied as v is read. Rows past nb are padding with a unit
+// diagonal; they never feed real rows.
+__global__ __launch_bounds__(64 * kLeafWaves) void trsm_leaf_kernel(
+    int nb, int64_t nrhs, const float *__restrict__ Ablk, int64_t mi, int64_t mk, int rev,
+    int unit, float *__restrict__ Bblk, int64_t vi, int64_t vr, float alpha) {
+  constexpr int kThreadsLeaf = 64 * kLeafWaves;
+  constexpr int kPer = kLeaf * kLeaf / kThreadsLeaf;
+  __shared__ float Ms[kLeaf][kLeaf + 1];  // Ms[i][k] = M(i, k), zero above the diagonal
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  float mv[kPer];
+#pragma unroll
+  for (int q = 0; q < kPer; ++q) {  // all loads in flight before the LDS stores
+    const int e = t + q * kThreadsLeaf;
     const int i = e & (kLeaf - 1), k = e / kLeaf;
     float v = 0.f;
     if (i < nb && k <= i) {
       const int ii = rev ? nb - 1 - i : i, kk = rev ? nb - 1 - k : k;
       v = (i == k && unit) ? 1.f : Ablk[ii * mi + kk * mk];
     } else if (i == k) {
-      v = 1.f;  // padding rows past nb: unit diagonal, fed only by zeros
+      v = 1.f;
     }
-    Ms[e] = v;
+    mv[q] = v;
   }
-  // v is staged through Xs[rhs][i] with coalesced loads: along the frame
-  // index when it is B's contiguous one (VI1), else along the right-hand
-  // sides.
-  if constexpr (VI1) {
-    for (int c = 0; c < kLeaf; ++c) {
-      const int64_t rc = rhs0 + c;
-      Xs[c][lane] = (lane < nb && rc < nrhs) ? Bblk[(rev ? nb - 1 - lane : lane) + rc * vr] : 0.f;
-    }
-  } else {
-    const int64_t r = rhs0 + lane;
-    for (int i = 0; i < kLeaf; ++i)
-      Xs[lane][i] = (i < nb && r < nrhs) ? Bblk[(rev ? nb - 1 - i : i) * vi + r] : 0.f;
-  }
-  __syncthreads();
-  float x[kLeaf];
 #pragma unroll
-  for (int i = 0; i < kLeaf; ++i) x[i] = alpha * Xs[lane][i];
+  for (int q = 0; q < kPer; ++q) {
+    const int e = t + q * kThreadsLeaf;
+    Ms[e & (kLeaf - 1)][e / kLeaf] = mv[q];
+  }
+  const int64_t r = (int64_t)blockIdx.x * kLeafWaves + wave;  // this wave's right-hand side
+  const bool live = r < nrhs && lane < nb;
+  const int64_t at = (int64_t)(rev ? nb - 1 - lane : lane) * vi + r * vr;
+  float b = live ? alpha * Bblk[at] : 0.f;
+  __syncthreads();
+  float row[kLeaf];
+#pragma unroll
+  for (int k = 0; k < kLeaf; ++k) row[k] = Ms[lane][k];
 #pragma unroll
   for (int k = 0; k < kLeaf; ++k) {
-    x[k] = x[k] / Ms[k * kLeaf + k];
-#pragma unroll
-    for (int i = k + 1; i < kLeaf; ++i) x[i] = fmaf(-Ms[k * kLeaf + i], x[k], x[i]);
+    const float bk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(b), k));
+    const float dk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(row[k]), k));
+    const float xk = bk / dk;
+    b = lane > k ? fmaf(-row[k], xk, b) : (lane == k ? xk : b);
   }
-  __syncthreads();
-#pragma unroll
-  for (int i = 0; i < kLeaf; ++i) Xs[lane][i] = x[i];
-  __syncthreads();
-  if constexpr (VI1) {
-    for (int c = 0; c < kLeaf; ++c) {
-      const int64_t rc = rhs0 + c;
-      if (lane < nb && rc < nrhs) Bblk[(rev ? nb - 1 - lane : lane) + rc * vr] = Xs[c][lane];
-    }
-  } else {
-    const int64_t r = rhs0 + lane;
-    if (r < nrhs)
-      for (int i = 0; i < nb; ++i) Bblk[(rev ? nb - 1 - i : i) * vi + r] = Xs[lane][i];
-  }
+  if (live) Bblk[at] = b;
 }
 
 // strsm in the solve frame: frame index = B's row (left side) or column
@@ -196,14 +182,14 @@ int trsm_leaf(const Trsm &p, int64_t lo, int64_t nb, float alpha) {
   const float *Ablk = p.A + lo + lo * p.lda;
   const int64_t mi = m_is_a ? 1 : p.lda, mk = m_is_a ? p.lda : 1;
   const int64_t nrhs = p.left ? p.n : p.m;
-  const int64_t grid = (nrhs + kLeaf - 1) / kLeaf;
+  const int64_t grid = (nrhs + kLeafWaves - 1) / kLeafWaves;
   const int rev = p.forward ? 0 : 1;
-  if (p.left)
-    trsm_leaf_kernel<true><<<(unsigned)grid, kLeaf, 0, p.ctx->stream>>>(
-        (int)nb, nrhs, Ablk, mi, mk, rev, p.unit, p.B + lo, 1, p.ldb, alpha);
-  else
-    trsm_leaf_kernel<false><<<(unsigned)grid, kLeaf, 0, p.ctx->stream>>>(
-        (int)nb, nrhs, Ablk, mi, mk, rev, p.unit, p.B + lo * p.ldb, p.ldb, 1, alpha);
+  // left: frame index = row of B (stride 1), right-hand side = column;
+  // right: frame index = column of B, right-hand side = row
+  float *Bblk = p.left ? p.B + lo : p.B + lo * p.ldb;
+  const int64_t vi = p.left ? 1 : p.ldb, vr = p.left ? p.ldb : 1;
+  trsm_leaf_kernel<<<(unsigned)grid, 64 * kLeafWaves, 0, p.ctx->stream>>>(
+      (int)nb, nrhs, Ablk, mi, mk, rev, p.unit, Bblk, vi, vr, alpha);
   WGB_CHECK_LAUNCH("trsm_leaf_kernel");
   return WGB_OK;
 }

@@ -8,8 +8,8 @@
 //   cannot read and write B at once), then one GEMM whose tiles only run the
 //   k-tiles the triangle reaches (about half the flops of a dense product).
 // strsm: recursive halving of the triangular dimension. Diagonal blocks of
-//   order <= 64 are solved by substitution, one wave per right-hand side
-//   with a lane per unknown; the off-diagonal updates are GEMMs that
+//   order <= 128 are solved by substitution, one lane per right-hand side,
+//   eight waves splitting its unknowns; the off-diagonal updates are GEMMs that
 //   read the solved rows of B and write other rows of B in place (disjoint
 //   memory), so strsm needs no workspace and no explicit inverse.
 #include "common.h"
@@ -23,8 +23,7 @@ namespace {
 using wgb::fail;
 
 constexpr int kTile = 64;  // symmetrize tile (64 x 64)
-constexpr int kLeaf = 64;       // order of strsm's substitution blocks
-constexpr int kLeafWaves = 16;  // right-hand sides (one wave each) per leaf block
+constexpr int kLeaf = 128;  // order of strsm's substitution blocks
 
 int64_t imax(int64_t a, int64_t b) { return a > b ? a : b; }
 int64_t round4(int64_t v) { return (v + 3) / 4 * 4; }
@@ -108,59 +107,145 @@ __global__ __launch_bounds__(256) void triangle_copy_kernel(int64_t order,
 }
 
 // Substitution solve of one diagonal block, in the solve frame: for every
-// right-hand side v, M x = alpha v with M lower triangular of order nb <= 64.
+// right-hand side v, M x = alpha v with M lower triangular of order nb <= NB.
 // Frame element (i, k) of M is Ablk[ia(i) mi + ia(k) mk] and element i of
 // right-hand side r is Bblk[ia(i) vi + r vr], where ia(i) = nb-1-i for an
 // upper system solved backward (rev) and i otherwise; the solution
-// overwrites v. One wave per right-hand side, lane i owning unknown i and
-// row i of M (in registers, from the block's LDS copy): step k broadcasts
-// the finished x_k = v_k / M(k,k) with readlane and every later lane
-// subtracts M(i,k) x_k, the column-oriented order of wgblas's
-// strsm_small.wgsl and of reference BLAS, with no barrier inside the solve.
-// alpha is applied as v is read. Rows past nb are padding with a unit
-// diagonal; they never feed real rows.
-__global__ __launch_bounds__(64 * kLeafWaves) void trsm_leaf_kernel(
-    int nb, int64_t nrhs, const float *__restrict__ Ablk, int64_t mi, int64_t mk, int rev,
-    int unit, float *__restrict__ Bblk, int64_t vi, int64_t vr, float alpha) {
-  constexpr int kThreadsLeaf = 64 * kLeafWaves;
-  constexpr int kPer = kLeaf * kLeaf / kThreadsLeaf;
-  __shared__ float Ms[kLeaf][kLeaf + 1];  // Ms[i][k] = M(i, k), zero above the diagonal
+// overwrites v.
+//
+// A block takes 64 right-hand sides, one per lane, and its NB / 16 waves
+// each own 16 consecutive rows of them in registers. Chunk c: wave c
+// substitutes through its rows (x_k *= 1/M(k,k), then x_i -= M(i,k) x_k for
+// its later rows: the column-oriented order of wgblas's strsm_small.wgsl and
+// of reference BLAS) and publishes them to LDS; after one barrier every later
+// wave subtracts the chunk's contribution from its rows. M's entries are LDS
+// broadcasts and the block needs one barrier per chunk. The diagonal's
+// reciprocals are formed once per block: x * RN(1/d) is within two ulps of
+// x / d, and zero, infinite and NaN diagonals give the quotient's special
+// values (only a diagonal below 2^-126 in magnitude, whose reciprocal
+// overflows, differs). alpha is applied as v is read. Rows past nb are
+// padding with a unit diagonal and zero right-hand side; they never feed real
+// rows. Loads are unconditional, from addresses clamped into the block, so
+// that all of them are in flight together (a guarded load is waited for
+// before the next one issues).
+template <int NB>
+__global__ __launch_bounds__(4 * NB) void trsm_leaf_kernel(int nb, int64_t nrhs,
+                                                          const float *__restrict__ Ablk, int64_t mi,
+                                                          int64_t mk, int rev, int unit,
+                                                          float *__restrict__ Bblk, int64_t vi,
+                                                          int64_t vr, float alpha) {
+  constexpr int kThreadsLeaf = 4 * NB;       // NB / 16 waves
+  constexpr int kSplit = NB / 16;            // waves = row chunks
+  constexpr int kRows = 16;                  // rows per wave
+  constexpr int kPer = NB * NB / kThreadsLeaf;
+  constexpr int kGroups = kThreadsLeaf / NB;  // left-side staging: column groups (4)
+  constexpr int kCols = 64 / kGroups;         // right-hand sides per column group (16)
+  static_assert(kCols == kRows, "one staging register set serves both sides");
+  __shared__ __attribute__((aligned(16))) float Ms[NB * NB];  // Ms[k*NB + i] = M(i, k)
+  __shared__ float Xs[NB][65];                                // Xs[i][rhs]
+  __shared__ float Rd[NB];                                    // 1 / M(k, k)
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int row0 = wave * kRows;
+  const int64_t rhs0 = (int64_t)blockIdx.x * 64;
+  const int64_t r = rhs0 + lane;  // this lane's right-hand side
+  const bool left = vi == 1;      // the frame index is B's contiguous one
+  const int si = t % NB, sg = t / NB;  // left-side staging: frame index, column group
+
+  // ---- every global load first
   float mv[kPer];
-#pragma unroll
-  for (int q = 0; q < kPer; ++q) {  // all loads in flight before the LDS stores
-    const int e = t + q * kThreadsLeaf;
-    const int i = e & (kLeaf - 1), k = e / kLeaf;
-    float v = 0.f;
-    if (i < nb && k <= i) {
-      const int ii = rev ? nb - 1 - i : i, kk = rev ? nb - 1 - k : k;
-      v = (i == k && unit) ? 1.f : Ablk[ii * mi + kk * mk];
-    } else if (i == k) {
-      v = 1.f;
-    }
-    mv[q] = v;
-  }
 #pragma unroll
   for (int q = 0; q < kPer; ++q) {
     const int e = t + q * kThreadsLeaf;
-    Ms[e & (kLeaf - 1)][e / kLeaf] = mv[q];
+    const int i = e % NB, k = e / NB;
+    const bool in = i < nb && k <= i;
+    const int ii = in ? (rev ? nb - 1 - i : i) : 0, kk = in ? (rev ? nb - 1 - k : k) : 0;
+    mv[q] = Ablk[ii * mi + kk * mk];
   }
-  const int64_t r = (int64_t)blockIdx.x * kLeafWaves + wave;  // this wave's right-hand side
-  const bool live = r < nrhs && lane < nb;
-  const int64_t at = (int64_t)(rev ? nb - 1 - lane : lane) * vi + r * vr;
-  float b = live ? alpha * Bblk[at] : 0.f;
-  __syncthreads();
-  float row[kLeaf];
+  // left: thread (si, sg) loads frame index si of right-hand sides sg,
+  // sg + kGroups, ...; right: lane = right-hand side, wave w its 16 rows
+  float bv[kRows];
 #pragma unroll
-  for (int k = 0; k < kLeaf; ++k) row[k] = Ms[lane][k];
-#pragma unroll
-  for (int k = 0; k < kLeaf; ++k) {
-    const float bk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(b), k));
-    const float dk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(row[k]), k));
-    const float xk = bk / dk;
-    b = lane > k ? fmaf(-row[k], xk, b) : (lane == k ? xk : b);
+  for (int q = 0; q < kRows; ++q) {
+    int64_t at;
+    if (left) {
+      const int64_t rc = rhs0 + sg + q * kGroups;
+      at = (si < nb ? (rev ? nb - 1 - si : si) : 0) + (rc < nrhs ? rc : 0) * vr;
+    } else {
+      const int i = row0 + q;
+      at = (int64_t)(i < nb ? (rev ? nb - 1 - i : i) : 0) * vi + (r < nrhs ? r : 0);
+    }
+    bv[q] = Bblk[at];
   }
-  if (live) Bblk[at] = b;
+
+  // ---- M (zero above the diagonal, unit diagonal for padding rows) and
+  // the reciprocals of its diagonal into LDS
+#pragma unroll
+  for (int q = 0; q < kPer; ++q) {
+    const int e = t + q * kThreadsLeaf;
+    const int i = e % NB, k = e / NB;
+    const bool in = i < nb && k <= i;
+    const float v = i == k ? ((unit || !in) ? 1.f : mv[q]) : (in ? mv[q] : 0.f);
+    Ms[e] = v;
+    if (i == k) Rd[k] = 1.f / v;
+  }
+  float x[kRows];
+  if (left) {
+#pragma unroll
+    for (int q = 0; q < kRows; ++q) {
+      const int c = sg + q * kGroups;
+      Xs[si][c] = (si < nb && rhs0 + c < nrhs) ? bv[q] : 0.f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kRows; ++j) x[j] = alpha * Xs[row0 + j][lane];
+  } else {
+#pragma unroll
+    for (int j = 0; j < kRows; ++j) x[j] = (r < nrhs && row0 + j < nb) ? alpha * bv[j] : 0.f;
+  }
+  __syncthreads();  // Ms and Rd complete; every read of the staged block done
+
+  // ---- chunked substitution
+  for (int c = 0; c < kSplit; ++c) {  // block-uniform chunk loop
+    if (wave == c) {
+#pragma unroll
+      for (int j = 0; j < kRows; ++j) {
+        const int k = row0 + j;
+        x[j] = x[j] * Rd[k];
+#pragma unroll
+        for (int jj = j + 1; jj < kRows; ++jj) x[jj] = fmaf(-Ms[k * NB + row0 + jj], x[j], x[jj]);
+        Xs[k][lane] = x[j];
+      }
+    }
+    __syncthreads();
+    if (wave > c) {
+#pragma unroll 4
+      for (int kk = 0; kk < kRows; ++kk) {
+        const int k = c * kRows + kk;
+        const float xk = Xs[k][lane];
+#pragma unroll
+        for (int j = 0; j < kRows; ++j) x[j] = fmaf(-Ms[k * NB + row0 + j], xk, x[j]);
+      }
+    }
+  }
+
+  // ---- write back (Xs holds every solved row: the last chunk was
+  // published before the loop's final barrier)
+  if (left) {
+    const bool ok = si < nb;
+    const int64_t at = rev ? nb - 1 - si : si;
+#pragma unroll
+    for (int q = 0; q < kRows; ++q) {
+      const int c = sg + q * kGroups;
+      const int64_t rc = rhs0 + c;
+      if (ok && rc < nrhs) Bblk[at + rc * vr] = Xs[si][c];
+    }
+  } else if (r < nrhs) {
+#pragma unroll
+    for (int j = 0; j < kRows; ++j) {
+      const int i = row0 + j;
+      if (i < nb) Bblk[(int64_t)(rev ? nb - 1 - i : i) * vi + r] = x[j];
+    }
+  }
 }
 
 // strsm in the solve frame: frame index = B's row (left side) or column
@@ -182,13 +267,13 @@ int trsm_leaf(const Trsm &p, int64_t lo, int64_t nb, float alpha) {
   const float *Ablk = p.A + lo + lo * p.lda;
   const int64_t mi = m_is_a ? 1 : p.lda, mk = m_is_a ? p.lda : 1;
   const int64_t nrhs = p.left ? p.n : p.m;
-  const int64_t grid = (nrhs + kLeafWaves - 1) / kLeafWaves;
+  const int64_t grid = (nrhs + 63) / 64;
   const int rev = p.forward ? 0 : 1;
   // left: frame index = row of B (stride 1), right-hand side = column;
   // right: frame index = column of B, right-hand side = row
   float *Bblk = p.left ? p.B + lo : p.B + lo * p.ldb;
   const int64_t vi = p.left ? 1 : p.ldb, vr = p.left ? p.ldb : 1;
-  trsm_leaf_kernel<<<(unsigned)grid, 64 * kLeafWaves, 0, p.ctx->stream>>>(
+  trsm_leaf_kernel<kLeaf><<<(unsigned)grid, 4 * kLeaf, 0, p.ctx->stream>>>(
       (int)nb, nrhs, Ablk, mi, mk, rev, p.unit, Bblk, vi, vr, alpha);
   WGB_CHECK_LAUNCH("trsm_leaf_kernel");
   return WGB_OK;

@@ -211,6 +211,20 @@ int wgb_strsm(wgb_ctx *ctx, int side, int uplo, int transA, int diag,
               int64_t m, int64_t n, float alpha, const float *A, int64_t lda,
               float *B, int64_t ldb);
 
+/* ---- level 2 -------------------------------------------------------------- */
+
+/* y <- alpha*op(A)*x + beta*y, A m-by-n column-major: op(A) = A (trans ==
+ * WGB_NO_TRANS: x of length n, y of length m) or A^T (x of length m, y of
+ * length n). Reference BLAS rules: m == 0, n == 0, or alpha == 0 with
+ * beta == 1 leave y untouched; alpha == 0 reads neither A nor x; beta == 0
+ * never reads y; the WGB_NO_TRANS form skips a column whose x entry is zero
+ * (its Inf / NaN entries never reach y), the transposed form takes every
+ * term. Replaces sgemv (src/sgemv/sgemv.mjs:19-254, src/shaders/sgemv_n.wgsl,
+ * sgemv_t.wgsl, reduce_partials.wgsl). */
+int wgb_sgemv(wgb_ctx *ctx, int trans, int64_t m, int64_t n, float alpha,
+              const float *A, int64_t lda, const float *x, int64_t incx,
+              float beta, float *y, int64_t incy);
+
 /* ---- level 1 reductions --------------------------------------------------- */
 /* n <= 0 returns 0 (index -1) without touching the device. incx, incy must be
  * positive. The host-result forms block until the value is on the host; the

@@ -651,3 +651,38 @@ void orc_strsm_ld(int side, int uplo, int trans, int unit, int64_t m, int64_t n,
     }
   }
 }
+
+/* ---- level 2: sgemv (src/sgemv/sgemv.mjs:19-254) -------------------------
+ * y <- alpha op(A) x + beta y, A m x n column-major, in long double, with
+ * reference BLAS's rules, which the reference's tests hold it to through
+ * stdlib (tests/sgemv/src/test.sgemv.js:157-202, 299-388): m == 0, n == 0,
+ * or alpha == 0 with beta == 1 leave y untouched; alpha == 0 reads neither A
+ * nor x; beta == 0 never reads y; the no-transpose form (column by column)
+ * skips a column whose x entry is zero, the transposed (dot-product) form
+ * takes every term. absdot (may be NULL, length of y, stride 1) gets
+ * sum |a x| over the terms taken. */
+void orc_sgemv_ld(int trans, int64_t m, int64_t n, double alpha, const double *A, int64_t lda,
+                  const double *x, int64_t incx, double beta, double *y, int64_t incy,
+                  double *absdot) {
+  int64_t len = trans ? n : m;
+  if (absdot)
+    for (int64_t i = 0; i < len; ++i) absdot[i] = 0.0;
+  if (m == 0 || n == 0 || (alpha == 0.0 && beta == 1.0)) return;
+  for (int64_t i = 0; i < len; ++i) {
+    long double s = 0, a = 0;
+    if (alpha != 0.0) {
+      int64_t terms = trans ? m : n;
+      for (int64_t p = 0; p < terms; ++p) {
+        long double xv = x[p * incx];
+        if (!trans && xv == 0.0L) continue;  /* the skipped column */
+        long double av = trans ? A[p + i * lda] : A[i + p * lda];
+        s += av * xv;
+        a += fabsl(av * xv);
+      }
+    }
+    long double v = (long double)alpha * s;
+    if (beta != 0.0) v += (long double)beta * y[i * incy];
+    y[i * incy] = (double)v;
+    if (absdot) absdot[i] = (double)a;
+  }
+}

@@ -45,6 +45,8 @@ _SIG = {
                             _i64, _f64p, _i64, _f64p, _f64p]),
     "orc_strsm_ld": (None, [C.c_int, C.c_int, C.c_int, C.c_int, _i64, _i64, C.c_double, _f64p,
                             _i64, _f64p, _i64]),
+    "orc_sgemv_ld": (None, [C.c_int, _i64, _i64, C.c_double, _f64p, _i64, _f64p, _i64, C.c_double,
+                            _f64p, _i64, _f64p]),
 }
 
 _lib = None
@@ -243,3 +245,16 @@ def strsm_ld(side, uplo, trans, unit, m, n, alpha, A, lda, B, ldb):
     lib().orc_strsm_ld(side, uplo, trans, unit, m, n, alpha, Ap, lda,
                        out.ctypes.data_as(_f64p), ldb)
     return out
+
+
+def sgemv_ld(trans, m, n, alpha, A, lda, x, incx, beta, y, incy):
+    """Returns (y_out, absdot): y_out the whole updated y buffer (long double
+    accumulation, reference BLAS's rules), absdot per output element."""
+    A, Ap = _f64(A if A is not None and len(A) else np.zeros(1))
+    x, xp = _f64(x if x is not None and len(x) else np.zeros(1))
+    out = np.array(y, dtype=np.float64, copy=True)
+    ln = max(n if trans else m, 1)
+    ad = np.zeros(ln)
+    lib().orc_sgemv_ld(trans, m, n, alpha, Ap, lda, xp, incx, beta, out.ctypes.data_as(_f64p), incy,
+                       ad.ctypes.data_as(_f64p))
+    return out, ad

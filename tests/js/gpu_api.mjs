@@ -472,6 +472,75 @@ test("level 3: multi-tile, mixed GpuMatrix layouts, alpha = 0, strsm many blocks
   assert(trsmResidual(await residentLevel3("strsm", s), s) <= 1, "strsm 600 resident residual");
 });
 
+// sgemv (tests/sgemv/): the fixtures exactly (as the reference's
+// assert.deepEqual against stdlib), host arrays and GpuMatrix / GpuVector
+function refGemv(c) {
+  const layout = c.layout || "row-major";
+  const at = (r, k) => (layout === "column-major" ? c.A[k * c.lda + r] : c.A[r * c.lda + k]);
+  const noT = c.trans === "no-transpose";
+  const yLen = noT ? c.m : c.n;
+  const out = Float64Array.from(c.y);
+  for (let i = 0; i < yLen; i++) {
+    let s = 0;
+    for (let p = 0; p < (noT ? c.n : c.m); p++) s += (noT ? at(i, p) : at(p, i)) * c.x[p * c.incx];
+    out[i * c.incy] = (c.alpha === 0 ? 0 : c.alpha * s) + (c.beta === 0 ? 0 : c.beta * c.y[i * c.incy]);
+  }
+  return out;
+}
+for (const file of ["sgemv.edge-cases", "sgemv.edge-cases-column-major"]) {
+  for (const c of fixture(file)) {
+    test(`sgemv ${file.includes("column") ? "cm" : "rm"}: ${c.label}`, async () => {
+      const layout = c.layout || "row-major";
+      const A = new Float32Array(c.A);
+      const x = new Float32Array(c.x);
+      const y = new Float32Array(c.y);
+      const want = refGemv(Object.assign({}, c, { layout }));
+      const got = await wg.sgemv(device, c.trans, c.m, c.n, c.alpha, A, c.lda, x, c.incx, c.beta, y, c.incy, layout);
+      exactEqual(got.y, want, c.label);
+      const outer = layout === "column-major" ? c.n : c.m;
+      const padded = new Float32Array(Math.max(outer * c.lda, A.length));
+      padded.set(A);
+      const gA = wg.GpuMatrix.from(device, padded, c.m, c.n, c.lda, layout);
+      const gx = wg.GpuVector.from(device, x);
+      const gy = wg.GpuVector.from(device, y);
+      try {
+        const r = await wg.sgemv(device, c.trans, c.m, c.n, c.alpha, gA, c.lda, gx, c.incx, c.beta, gy, c.incy, layout);
+        assertEqual(Object.keys(r).length, 0, "resident call returns {}");
+        exactEqual(await gy.read(), want, `${c.label} (GpuVector)`);
+      } finally {
+        gA.destroy();
+        gx.destroy();
+        gy.destroy();
+      }
+    });
+  }
+}
+
+test("sgemv: 600 x 300 split paths, zero dimension", async () => {
+  for (const layout of ["row-major", "column-major"])
+    for (const trans of ["no-transpose", "transpose"]) {
+      const [m, n] = layout === "row-major" ? [600, 300] : [300, 600];
+      const noT = trans === "no-transpose";
+      const c = { layout, trans, m, n, alpha: 1.5, beta: 0.75, incx: 3, incy: 2,
+        A: wg.randomFloat32Array(m * n, -1, 1, 21), lda: layout === "row-major" ? n : m };
+      c.x = wg.randomFloat32Array(((noT ? n : m) - 1) * 3 + 1, -1, 1, 22);
+      c.y = wg.randomFloat32Array(((noT ? m : n) - 1) * 2 + 1, -1, 1, 23);
+      const got = (await wg.sgemv(device, trans, m, n, c.alpha, c.A, c.lda, c.x, c.incx, c.beta, c.y, c.incy, layout)).y;
+      const want = refGemv(c);
+      const terms = noT ? n : m;
+      for (let i = 0; i < want.length; i++) {
+        if (i % 2) {
+          assert(Object.is(got[i], c.y[i]), "incy gap untouched");
+          continue;
+        }
+        assert(Math.abs(got[i] - want[i]) <= 2 ** -23 * (terms + 1) * 1.5 * terms + 1e-6, `${layout} ${trans} y[${i}]`);
+      }
+    }
+  const y = wg.randomFloat32Array(4, -1, 1, 9001);
+  const r = await wg.sgemv(device, "no-transpose", 4, 0, 1.5, new Float32Array(0), 1, new Float32Array(0), 1, 0.5, y, 1);
+  exactEqual(r.y, y, "n = 0 leaves y");
+});
+
 // fp64 level 1 (tests/{ddot,dasum,dnrm2,idamax}/): the reference's bounds
 // around float64 sums (ddot n 2^-48 sum|xy|, dasum 64 ULP by a relative
 // 64 * 2^-52, dnrm2 10 * 2^-48 relative), idamax exact

@@ -31,16 +31,18 @@ export async function assertRejects(fn, substring, msg) {
 }
 
 export async function run() {
-  let failed = 0;
+  const failures = [];
   for (const c of cases) {
     try {
       await c.fn();
       console.log(`ok   ${c.name}`);
     } catch (e) {
-      failed++;
+      failures.push(`${c.name}: ${(e && e.message) || e}`);
       console.log(`FAIL ${c.name}\n     ${(e && e.stack) || e}`);
     }
   }
-  console.log(`${cases.length - failed} passed, ${failed} failed`);
-  process.exitCode = failed ? 1 : 0;
+  // failures again at the end, where a truncated log still shows them
+  for (const f of failures) console.log(`FAILED ${f}`);
+  console.log(`${cases.length - failures.length} passed, ${failures.length} failed`);
+  process.exitCode = failures.length ? 1 : 0;
 }

@@ -204,3 +204,39 @@ def scipy_trsm(side, uplo, trans, unit, m, n, alpha, A, lda, B, ldb):
         X = solve_triangular(full, Bd.T, trans=1 - trans, lower=uplo == 1,
                              unit_diagonal=bool(unit)).T
     return put(np.array(B, np.float64, copy=True), X, ldb)
+
+
+def gemv_call(case, dtype=np.float32):
+    """Column-major (trans, m, n, alpha, A, lda, x, incx, beta, y, incy) for
+    sgemv. wgblas's frame is row-major (src/sgemv/sgemv.mjs:97-101): a
+    column-major case is first turned into it (m and n swap, trans flips),
+    and the row-major mr x nr matrix read column-major is its nr x mr
+    transpose (trans flips back)."""
+    layout = case.get("layout", "row-major")
+    m, n, t = case["m"], case["n"], TRANS[case["trans"]]
+    if layout == "column-major":
+        m, n, t = n, m, 1 - t
+    A, x, y = (np.array(case[k], dtype) for k in ("A", "x", "y"))
+    return (1 - t, n, m, case["alpha"], A, case["lda"], x, case["incx"], case["beta"], y, case["incy"])
+
+
+def numpy_gemv(trans, m, n, alpha, A, lda, x, incx, beta, y, incy):
+    """Column-major sgemv by numpy (float64), with reference BLAS's quick
+    returns and the no-transpose form's skipping of zero x entries."""
+    out = np.array(y, np.float64, copy=True)
+    if m == 0 or n == 0 or (alpha == 0 and beta == 1):
+        return out
+    Ad = dense_op(A, m, n, lda, 0)
+    xl = n if trans == 0 else m
+    xv = np.asarray(x, np.float64)[np.arange(xl) * incx]
+    if alpha == 0:
+        prod = np.zeros(m if trans == 0 else n)
+    elif trans == 0:
+        keep = xv != 0
+        prod = Ad[:, keep] @ xv[keep]
+    else:
+        prod = Ad.T @ xv
+    idx = np.arange(len(prod)) * incy
+    yin = out[idx]
+    out[idx] = alpha * prod + (beta * yin if beta != 0 else 0.0)
+    return out

@@ -54,6 +54,11 @@ void timing_end(wgb_ctx *ctx);
 constexpr int kMaxReduceBlocks = 2048;
 constexpr size_t kScratchBytes = (size_t)kMaxReduceBlocks * 32 + 256;  // 32-byte partial slots + result
 
+// Grows the context's operand workspace (ctx->op_ws) to at least `bytes`;
+// the stream is drained first, since an earlier launch may still read it.
+// Shared by the level-2 and level-3 routines (one stream orders them).
+int ensure_op_workspace(wgb_ctx *ctx, size_t bytes);
+
 // GEMM k-band: which operand is triangular (zero outside its triangle).
 enum { kBandNone = 0, kBandALower = 1, kBandAUpper = 2, kBandBLower = 3, kBandBUpper = 4 };
 

@@ -1,0 +1,257 @@
+// sgemv (wgblas src/sgemv/sgemv.mjs:19-254, shaders sgemv_n.wgsl,
+// sgemv_t.wgsl, reduce_partials.wgsl), column-major as in BLAS:
+//   trans = N: y (m) <- alpha A x + beta y, x of length n;
+//   trans = T: y (n) <- alpha A^T x + beta y, x of length m.
+//
+// Both forms read A once and are HBM-bound.
+//   N: a lane owns 4 consecutive rows (one 16-byte load per column); the
+//      columns are walked in order and a column whose x entry is zero is
+//      skipped, as reference BLAS does for this form (so 0 * Inf or 0 * NaN
+//      in that column never reaches y).
+//   T: a wave owns 8 columns and walks the rows 256 at a time (4 per lane,
+//      16-byte loads), keeping each x chunk in registers for all 8 columns;
+//      the dot products are folded with wave shuffles. No zero skipping: the
+//      dot-product form of reference BLAS takes every term.
+// When the output alone gives too few blocks to stream HBM, the contraction
+// dimension is split: each split writes partial sums, and a fold kernel adds
+// the splits in order (deterministic) and applies alpha and beta.
+#include "common.h"
+
+#include <hip/hip_runtime.h>
+
+#include "wgblas_hip.h"
+
+namespace {
+
+using wgb::fail;
+
+constexpr int kThreads = 256;
+constexpr int kColsPerWave = 8;    // T form
+constexpr int kTargetBlocks = 2048;  // blocks that keep HBM streaming
+
+int64_t imax(int64_t a, int64_t b) { return a > b ? a : b; }
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+// Writes one output element: alpha * acc + beta * y (beta == 0 never reads y).
+__device__ __forceinline__ void store_y(float *y, int64_t idx, float acc, float alpha,
+                                        float beta) {
+  float v = alpha * acc;
+  if (beta != 0.f) v = fmaf(beta, y[idx], v);
+  y[idx] = v;
+}
+
+// N form. Block b, split s: rows [4 (b*256 + t), +4), columns
+// [s*cps, min(n, (s+1)*cps)). VEC: lda % 4 == 0 and A 16-byte aligned.
+template <bool VEC>
+__global__ __launch_bounds__(kThreads) void gemv_n_kernel(int64_t m, int64_t n,
+                                                          const float *__restrict__ A, int64_t lda,
+                                                          const float *__restrict__ x, int64_t incx,
+                                                          int64_t cps, float *__restrict__ part,
+                                                          float alpha, float beta,
+                                                          float *__restrict__ y, int64_t incy) {
+  const int64_t i0 = ((int64_t)blockIdx.x * kThreads + threadIdx.x) * 4;
+  const int64_t j0 = (int64_t)blockIdx.y * cps;
+  const int64_t j1 = j0 + cps < n ? j0 + cps : n;
+  if (i0 >= m) return;
+  const bool full = i0 + 4 <= m;
+  // rows past m read row m-1 (in bounds) and are never stored
+  const int64_t ir[4] = {i0, i0 + 1 < m ? i0 + 1 : m - 1, i0 + 2 < m ? i0 + 2 : m - 1,
+                         i0 + 3 < m ? i0 + 3 : m - 1};
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  int64_t j = j0;
+  // four columns per step, loads issued before the arithmetic
+  for (; j + 4 <= j1; j += 4) {
+    float xv[4];
+    f4 av[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) xv[c] = x[(j + c) * incx];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const float *col = A + (j + c) * lda;
+      if (VEC && full) {
+        av[c] = *reinterpret_cast<const f4 *>(col + i0);
+      } else {
+        av[c] = f4{col[ir[0]], col[ir[1]], col[ir[2]], col[ir[3]]};
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      if (xv[c] != 0.f) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc[q] = fmaf(av[c][q], xv[c], acc[q]);
+      }
+    }
+  }
+  for (; j < j1; ++j) {
+    const float xj = x[j * incx];
+    const float *col = A + j * lda;
+    f4 a;
+    if (VEC && full)
+      a = *reinterpret_cast<const f4 *>(col + i0);
+    else
+      a = f4{col[ir[0]], col[ir[1]], col[ir[2]], col[ir[3]]};
+    if (xj != 0.f) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc[q] = fmaf(a[q], xj, acc[q]);
+    }
+  }
+  const int rows = full ? 4 : (int)(m - i0);
+  for (int q = 0; q < rows; ++q) {
+    if (part)
+      part[(int64_t)blockIdx.y * m + i0 + q] = acc[q];
+    else
+      store_y(y, (i0 + q) * incy, acc[q], alpha, beta);
+  }
+}
+
+// T form. Wave w (4 per block) owns columns [8w, 8w + 8) of split s, rows
+// [s*rps, min(m, (s+1)*rps)). VEC: lda % 4 == 0, A 16-byte aligned, incx == 1
+// and x 16-byte aligned (rps is a multiple of 4, so every 4-row group of a
+// split starts 16-byte aligned).
+template <bool VEC>
+__global__ __launch_bounds__(kThreads) void gemv_t_kernel(int64_t m, int64_t n,
+                                                          const float *__restrict__ A, int64_t lda,
+                                                          const float *__restrict__ x, int64_t incx,
+                                                          int64_t rps, float *__restrict__ part,
+                                                          float alpha, float beta,
+                                                          float *__restrict__ y, int64_t incy) {
+  const int lane = threadIdx.x & 63;
+  const int64_t col0 = ((int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6)) * kColsPerWave;
+  if (col0 >= n) return;  // wave-uniform
+  const int64_t r0 = (int64_t)blockIdx.y * rps;
+  const int64_t r1 = r0 + rps < m ? r0 + rps : m;
+  // columns past n repeat column n-1 (in bounds) and are never stored
+  const float *col[kColsPerWave];
+#pragma unroll
+  for (int c = 0; c < kColsPerWave; ++c) col[c] = A + (col0 + c < n ? col0 + c : n - 1) * lda;
+  float acc[kColsPerWave];
+#pragma unroll
+  for (int c = 0; c < kColsPerWave; ++c) acc[c] = 0.f;
+  for (int64_t i = r0 + 4 * lane; i < r1; i += 256) {
+    if (VEC && i + 4 <= r1) {
+      const f4 xv = *reinterpret_cast<const f4 *>(x + i);
+      f4 av[kColsPerWave];
+#pragma unroll
+      for (int c = 0; c < kColsPerWave; ++c) av[c] = *reinterpret_cast<const f4 *>(col[c] + i);
+#pragma unroll
+      for (int c = 0; c < kColsPerWave; ++c)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc[c] = fmaf(av[c][q], xv[q], acc[c]);
+    } else {
+      const int cnt = r1 - i < 4 ? (int)(r1 - i) : 4;
+      for (int q = 0; q < cnt; ++q) {
+        const float xv = x[(i + q) * incx];
+#pragma unroll
+        for (int c = 0; c < kColsPerWave; ++c) acc[c] = fmaf(col[c][i + q], xv, acc[c]);
+      }
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < kColsPerWave; ++c) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) acc[c] += __shfl_xor(acc[c], off, 64);
+  }
+  if (lane < kColsPerWave && col0 + lane < n) {
+    float v = acc[0];
+#pragma unroll
+    for (int c = 1; c < kColsPerWave; ++c) v = lane == c ? acc[c] : v;
+    if (part)
+      part[(int64_t)blockIdx.y * n + col0 + lane] = v;
+    else
+      store_y(y, (col0 + lane) * incy, v, alpha, beta);
+  }
+}
+
+// y[i*incy] <- alpha * sum_s part[s*len + i] + beta * y[i*incy], splits
+// added in order.
+__global__ __launch_bounds__(kThreads) void gemv_fold_kernel(int64_t len, int64_t splits,
+                                                             const float *__restrict__ part,
+                                                             float alpha, float beta,
+                                                             float *__restrict__ y, int64_t incy) {
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= len) return;
+  float s = part[i];
+  for (int64_t k = 1; k < splits; ++k) s += part[k * len + i];
+  store_y(y, i * incy, s, alpha, beta);
+}
+
+// y <- beta * y over len elements (0 when beta == 0): alpha == 0.
+__global__ __launch_bounds__(kThreads) void scale_y_kernel(int64_t len, float beta, float *y,
+                                                           int64_t incy) {
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i < len) y[i * incy] = beta == 0.f ? 0.f : beta * y[i * incy];
+}
+
+bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+}  // namespace
+
+extern "C" int wgb_sgemv(wgb_ctx *ctx, int trans, int64_t m, int64_t n, float alpha,
+                         const float *A, int64_t lda, const float *x, int64_t incx, float beta,
+                         float *y, int64_t incy) {
+  int st = wgb::enter(ctx);
+  if (st) return st;
+  if (trans != WGB_NO_TRANS && trans != WGB_TRANS)
+    return fail(WGB_ERR_INVALID_VALUE, "trans must be WGB_NO_TRANS or WGB_TRANS");
+  if (m < 0 || n < 0) return fail(WGB_ERR_INVALID_VALUE, "m and n must be non-negative");
+  if (lda < imax(1, m)) return fail(WGB_ERR_INVALID_VALUE, "lda must be >= max(1, m)");
+  if (incx <= 0 || incy <= 0) return fail(WGB_ERR_INVALID_VALUE, "incx and incy must be positive");
+  // reference BLAS quick return: nothing to do, y untouched
+  if (m == 0 || n == 0 || (alpha == 0.f && beta == 1.f)) return WGB_OK;
+  if (!y || (alpha != 0.f && (!A || !x))) return fail(WGB_ERR_INVALID_VALUE, "A, x or y is null");
+  const bool nt = trans == WGB_NO_TRANS;
+  const int64_t len = nt ? m : n;  // length of y
+  wgb::timing_begin(ctx);
+  if (alpha == 0.f) {
+    scale_y_kernel<<<(unsigned)cdiv(len, kThreads), kThreads, 0, ctx->stream>>>(len, beta, y, incy);
+    WGB_CHECK_LAUNCH("scale_y_kernel");
+    wgb::timing_end(ctx);
+    return WGB_OK;
+  }
+  const bool vecA = lda % 4 == 0 && aligned16(A);
+  // blocks along the output; split the contraction dimension until about
+  // kTargetBlocks blocks stream A (N: >= 64 columns per split; T: >= 256
+  // rows, a multiple of 256 so every split starts 16-byte aligned)
+  const int64_t bx = nt ? cdiv(cdiv(m, 4), kThreads) : cdiv(cdiv(n, kColsPerWave), kThreads / 64);
+  int64_t want = bx >= kTargetBlocks ? 1 : cdiv(kTargetBlocks, bx);
+  const int64_t most = nt ? cdiv(n, 64) : cdiv(m, 256);
+  if (want > most) want = most;
+  if (want > 65535) want = 65535;  // grid y limit
+  if (want < 1) want = 1;
+  const int64_t per = nt ? cdiv(n, want) : cdiv(cdiv(m, want), 256) * 256;
+  const int64_t splits = nt ? cdiv(n, per) : cdiv(m, per);
+  float *part = nullptr;
+  if (splits > 1) {
+    if ((st = wgb::ensure_op_workspace(ctx, (size_t)(splits * len) * sizeof(float)))) return st;
+    part = static_cast<float *>(ctx->op_ws);
+  }
+  dim3 grid((unsigned)bx, (unsigned)splits);
+  if (nt) {
+    if (vecA)
+      gemv_n_kernel<true><<<grid, kThreads, 0, ctx->stream>>>(m, n, A, lda, x, incx, per, part,
+                                                               alpha, beta, y, incy);
+    else
+      gemv_n_kernel<false><<<grid, kThreads, 0, ctx->stream>>>(m, n, A, lda, x, incx, per, part,
+                                                                alpha, beta, y, incy);
+    WGB_CHECK_LAUNCH("gemv_n_kernel");
+  } else {
+    const bool vec = vecA && incx == 1 && aligned16(x);
+    if (vec)
+      gemv_t_kernel<true><<<grid, kThreads, 0, ctx->stream>>>(m, n, A, lda, x, incx, per, part,
+                                                               alpha, beta, y, incy);
+    else
+      gemv_t_kernel<false><<<grid, kThreads, 0, ctx->stream>>>(m, n, A, lda, x, incx, per, part,
+                                                                alpha, beta, y, incy);
+    WGB_CHECK_LAUNCH("gemv_t_kernel");
+  }
+  if (part) {
+    gemv_fold_kernel<<<(unsigned)cdiv(len, kThreads), kThreads, 0, ctx->stream>>>(len, splits, part,
+                                                                                  alpha, beta, y,
+                                                                                  incy);
+    WGB_CHECK_LAUNCH("gemv_fold_kernel");
+  }
+  wgb::timing_end(ctx);
+  return WGB_OK;
+}

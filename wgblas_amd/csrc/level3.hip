@@ -28,25 +28,6 @@ constexpr int kLeaf = 128;  // order of strsm's substitution blocks
 int64_t imax(int64_t a, int64_t b) { return a > b ? a : b; }
 int64_t round4(int64_t v) { return (v + 3) / 4 * 4; }
 
-// Grows the context's operand workspace to at least `bytes`. The stream is
-// drained first: an earlier launch may still read the old buffer.
-int ensure_op_workspace(wgb_ctx *ctx, size_t bytes) {
-  if (ctx->op_ws_bytes >= bytes) return WGB_OK;
-  const size_t round = (size_t)16 << 20;
-  bytes = (bytes + round - 1) / round * round;
-  WGB_CHECK_HIP(hipStreamSynchronize(ctx->stream));
-  if (ctx->op_ws) WGB_CHECK_HIP(hipFree(ctx->op_ws));
-  ctx->op_ws = nullptr;
-  ctx->op_ws_bytes = 0;
-  if (hipMalloc(&ctx->op_ws, bytes) != hipSuccess) {
-    (void)hipGetLastError();
-    ctx->op_ws = nullptr;
-    return fail(WGB_ERR_ALLOC, "hipMalloc of the level-3 operand workspace failed");
-  }
-  ctx->op_ws_bytes = bytes;
-  return WGB_OK;
-}
-
 // W (order x order, column-major, ld ldw) <- the symmetric matrix whose uplo
 // triangle A holds (src/shaders/symmetrize.wgsl). Block (bi, bj) writes W's
 // 64 x 64 tile (bi, bj): a tile inside the stored triangle copies A's tile,
@@ -65,9 +46,18 @@ __global__ __launch_bounds__(256) void symmetrize_kernel(int64_t order, const fl
   const int si = (stored || diag) ? bi : bj, sj = (stored || diag) ? bj : bi;
   const int r = threadIdx.x & 63, ph = threadIdx.x >> 6;
   const int64_t srow = (int64_t)si * kTile + r;
-  for (int c = ph; c < kTile; c += 4) {
-    const int64_t scol = (int64_t)sj * kTile + c;
-    s[c][r] = (srow < order && scol < order) ? A[srow + scol * lda] : 0.f;
+  // unconditional loads from clamped addresses, all in flight together
+  float v[kTile / 4];
+#pragma unroll
+  for (int q = 0; q < kTile / 4; ++q) {
+    const int64_t scol = (int64_t)sj * kTile + ph + 4 * q;
+    const bool ok = srow < order && scol < order;
+    v[q] = A[(ok ? srow : 0) + (ok ? scol : 0) * lda];
+  }
+#pragma unroll
+  for (int q = 0; q < kTile / 4; ++q) {
+    const int64_t scol = (int64_t)sj * kTile + ph + 4 * q;
+    s[ph + 4 * q][r] = (srow < order && scol < order) ? v[q] : 0.f;
   }
   __syncthreads();
   const int64_t row = (int64_t)bi * kTile + r;
@@ -385,7 +375,7 @@ extern "C" int wgb_ssymm(wgb_ctx *ctx, int side, int uplo, int64_t m, int64_t n,
                        beta, C, ldc, wgb::kBandNone);
   } else {
     const int64_t ldw = round4(order);
-    if ((st = ensure_op_workspace(ctx, (size_t)ldw * order * sizeof(float)))) return st;
+    if ((st = wgb::ensure_op_workspace(ctx, (size_t)ldw * order * sizeof(float)))) return st;
     float *W = static_cast<float *>(ctx->op_ws);
     const int64_t tiles = (order + kTile - 1) / kTile;
     symmetrize_kernel<<<dim3((unsigned)tiles, (unsigned)tiles), 256, 0, ctx->stream>>>(order, A, lda,
@@ -416,7 +406,7 @@ extern "C" int wgb_strmm(wgb_ctx *ctx, int side, int uplo, int transA, int diag,
     const bool left = side == WGB_LEFT;
     const int64_t order = left ? m : n;
     const int64_t ldw = round4(order), ldbc = round4(m);
-    if ((st = ensure_op_workspace(ctx, (size_t)(ldw * order + ldbc * n) * sizeof(float)))) return st;
+    if ((st = wgb::ensure_op_workspace(ctx, (size_t)(ldw * order + ldbc * n) * sizeof(float)))) return st;
     float *W = static_cast<float *>(ctx->op_ws);
     float *Bc = W + ldw * order;  // 16-byte aligned: ldw is a multiple of 4
     const int64_t gy = order < 65535 ? order : 65535;

@@ -395,6 +395,28 @@ napi_value Tri(napi_env env, napi_callback_info info) {
   return nullptr;
 }
 
+// ---- level 2 ---------------------------------------------------------------
+
+// sgemv(ctx, trans, m, n, alpha, A, lda, x, incx, beta, y, incy)
+napi_value Sgemv(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 12)) return nullptr;
+  wgb_ctx *ctx = ctx_of(env, a.v[0]);
+  if (!ctx) return nullptr;
+  int trans;
+  int64_t m, n, lda, incx, incy;
+  double alpha, beta;
+  void *A, *x, *y;
+  if (!get_i32(env, a.v[1], &trans) || !get_i64(env, a.v[2], &m) || !get_i64(env, a.v[3], &n) ||
+      !get_f64(env, a.v[4], &alpha) || !get_ptr(env, a.v[5], &A) || !get_i64(env, a.v[6], &lda) ||
+      !get_ptr(env, a.v[7], &x) || !get_i64(env, a.v[8], &incx) || !get_f64(env, a.v[9], &beta) ||
+      !get_ptr(env, a.v[10], &y) || !get_i64(env, a.v[11], &incy))
+    return nullptr;
+  WGB_OK_OR_THROW(wgb_sgemv(ctx, trans, m, n, (float)alpha, (const float *)A, lda, (const float *)x,
+                            incx, (float)beta, (float *)y, incy), "wgb_sgemv");
+  return nullptr;
+}
+
 // ---- level 1 ---------------------------------------------------------------
 
 // reduce(kind, ctx, n, x, incx[, y, incy]) -> number; kind: 0 sdot, 1 sasum,
@@ -444,7 +466,7 @@ napi_value ModuleInit(napi_env env, napi_value exports) {
       {"synchronize", Synchronize}, {"malloc", Malloc}, {"free", Free},
       {"upload", Upload}, {"download", Download}, {"gemm", Gemm},
       {"ssyrk", Ssyrk}, {"ssyr2k", Ssyr2k}, {"ssymm", Ssymm},
-      {"tri", Tri}, {"reduce", Reduce},
+      {"tri", Tri}, {"sgemv", Sgemv}, {"reduce", Reduce},
   };
   for (const Fn &f : fns) {
     napi_value v;

@@ -42,6 +42,23 @@ void timing_end(wgb_ctx *ctx) {
   }
 }
 
+int ensure_op_workspace(wgb_ctx *ctx, size_t bytes) {
+  if (ctx->op_ws_bytes >= bytes) return WGB_OK;
+  const size_t round = (size_t)16 << 20;
+  bytes = (bytes + round - 1) / round * round;
+  WGB_CHECK_HIP(hipStreamSynchronize(ctx->stream));
+  if (ctx->op_ws) WGB_CHECK_HIP(hipFree(ctx->op_ws));
+  ctx->op_ws = nullptr;
+  ctx->op_ws_bytes = 0;
+  if (hipMalloc(&ctx->op_ws, bytes) != hipSuccess) {
+    (void)hipGetLastError();
+    ctx->op_ws = nullptr;
+    return fail(WGB_ERR_ALLOC, "hipMalloc of the level-2/3 operand workspace failed");
+  }
+  ctx->op_ws_bytes = bytes;
+  return WGB_OK;
+}
+
 }  // namespace wgb
 
 using wgb::fail;

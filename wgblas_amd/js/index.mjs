@@ -16,6 +16,7 @@ export { ssyr2k } from "./src/ssyr2k.mjs";
 export { ssymm } from "./src/ssymm.mjs";
 export { strmm } from "./src/strmm.mjs";
 export { strsm } from "./src/strsm.mjs";
+export { sgemv } from "./src/sgemv.mjs";
 export { sdot } from "./src/sdot.mjs";
 export { sasum } from "./src/sasum.mjs";
 export { snrm2 } from "./src/snrm2.mjs";

@@ -12,6 +12,7 @@
 // C^T = op(B)^T op(A)^T: A and B (with their flipped flags and leading
 // dimensions) swap places, m and n swap, and uplo names the other triangle.
 import { GpuMatrix } from "./classes/GpuMatrix.mjs";
+import { GpuVector } from "./classes/GpuVector.mjs";
 import { requireGpuDevice, requireSameDevice } from "./device.mjs";
 import { lastGpuTimeMs } from "./init.mjs";
 import { native } from "./native.mjs";
@@ -119,8 +120,9 @@ export function toColumnMajor(a, eff, uplo) {
 /**
  * Runs one device call. Host-array operands are copied to temporary device
  * buffers (freed before returning) and the output C is read back into a new
- * typed array (the input is not modified), returned under `key` ("C", or
- * "B" for strmm / strsm); GpuMatrix operands are used in place.
+ * typed array (the input is not modified), returned under `key` ("C", "B"
+ * for strmm / strsm, "y" for sgemv); GpuMatrix / GpuVector operands are used
+ * in place.
  * `launch(ctx, ptrs, ptrC)` issues the call.
  */
 export function execute(device, operands, C, CIsGpu, arrayType, launch, key = "C") {
@@ -136,14 +138,15 @@ export function execute(device, operands, C, CIsGpu, arrayType, launch, key = "C
   };
   // Read-only inputs passed as the same array share one upload; C always
   // gets its own buffer, so an input aliasing C is read unmodified.
+  const resident = (X) => X instanceof GpuMatrix || X instanceof GpuVector;
   const ptrOf = (X) => {
-    if (X instanceof GpuMatrix) return X._buf;
+    if (resident(X)) return X._buf;
     if (!cache.has(X)) cache.set(X, upload(X));
     return cache.get(X);
   };
   try {
     const ptrs = operands.map(ptrOf);
-    const pC = C instanceof GpuMatrix ? C._buf : upload(C);
+    const pC = resident(C) ? C._buf : upload(C);
     launch(ctx, ptrs, pC);
     const t = lastGpuTimeMs(device);
     if (CIsGpu) return t === undefined ? {} : { gpuTimeMs: t };

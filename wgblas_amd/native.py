@@ -61,6 +61,8 @@ _SIGNATURES = {
                   _ptr, _i64],
     "wgb_strsm": [_ptr, C.c_int, C.c_int, C.c_int, C.c_int, _i64, _i64, C.c_float, _ptr, _i64,
                   _ptr, _i64],
+    "wgb_sgemv": [_ptr, C.c_int, _i64, _i64, C.c_float, _ptr, _i64, _ptr, _i64, C.c_float, _ptr,
+                  _i64],
     "wgb_sdot": [_ptr, _i64, _ptr, _i64, _ptr, _i64, C.POINTER(C.c_float)],
     "wgb_sdot_dev": [_ptr, _i64, _ptr, _i64, _ptr, _i64, _ptr],
     "wgb_sasum": [_ptr, _i64, _ptr, _i64, C.POINTER(C.c_float)],
@@ -282,6 +284,11 @@ class Context:
     def strsm(self, side, uplo, transA, diag, m, n, alpha, A, lda, B, ldb):
         _check(self.lib.wgb_strsm(self.handle, side, uplo, transA, diag, m, n, alpha, _p(A), lda,
                                   _p(B), ldb), "wgb_strsm")
+
+    # ---- level 2 ----
+    def sgemv(self, trans, m, n, alpha, A, lda, x, incx, beta, y, incy):
+        _check(self.lib.wgb_sgemv(self.handle, trans, m, n, alpha, _p(A), lda, _p(x), incx, beta,
+                                  _p(y), incy), "wgb_sgemv")
 
     # ---- level 1 ----
     def sdot(self, n, x, incx, y, incy):

@@ -4,12 +4,13 @@
 //   trans = T: y (n) <- alpha A^T x + beta y, x of length m.
 //
 // Both forms read A once and are HBM-bound.
-//   N: a lane owns 4 consecutive rows (one 16-byte load per column); the
+//   N: a lane owns 4 consecutive rows in each of two 1024-row groups (a
+//      16-byte load per group and column, 8 columns loaded per step); the
 //      columns are walked in order and a column whose x entry is zero is
 //      skipped, as reference BLAS does for this form (so 0 * Inf or 0 * NaN
 //      in that column never reaches y).
-//   T: a wave owns 8 columns and walks the rows 256 at a time (4 per lane,
-//      16-byte loads), keeping each x chunk in registers for all 8 columns;
+//   T: a wave owns 8 columns and walks the rows 512 at a time (2 x 4 per
+//      lane, 16-byte loads), keeping each x chunk in registers for all 8 columns;
 //      the dot products are folded with wave shuffles. No zero skipping: the
 //      dot-product form of reference BLAS takes every term.
 // When the output alone gives too few blocks to stream HBM, the contraction
@@ -27,12 +28,20 @@ using wgb::fail;
 
 constexpr int kThreads = 256;
 constexpr int kColsPerWave = 8;    // T form
+constexpr int kStepN = 8;          // N form: columns loaded per step
+constexpr int kGroupsN = 2;        // N form: 1024-row groups per block
 constexpr int kTargetBlocks = 2048;  // blocks that keep HBM streaming
 
 int64_t imax(int64_t a, int64_t b) { return a > b ? a : b; }
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 typedef float f4 __attribute__((ext_vector_type(4)));
+
+// A is streamed once: non-temporal 16-byte loads keep it from displacing x
+// and the partial sums in the caches.
+__device__ __forceinline__ f4 ld_nt(const float *p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const f4 *>(p));
+}
 
 // Writes one output element: alpha * acc + beta * y (beta == 0 never reads y).
 __device__ __forceinline__ void store_y(float *y, int64_t idx, float acc, float alpha,
@@ -42,8 +51,10 @@ __device__ __forceinline__ void store_y(float *y, int64_t idx, float acc, float 
   y[idx] = v;
 }
 
-// N form. Block b, split s: rows [4 (b*256 + t), +4), columns
-// [s*cps, min(n, (s+1)*cps)). VEC: lda % 4 == 0 and A 16-byte aligned.
+// N form. Block b, split s: columns [s*cps, min(n, (s+1)*cps)); rows in
+// kGroupsN groups of 1024, lane t of group g owning rows
+// [b*1024*kGroupsN + g*1024 + 4t, +4) (every load instruction of a wave
+// reads 1 KB of one column). VEC: lda % 4 == 0 and A 16-byte aligned.
 template <bool VEC>
 __global__ __launch_bounds__(kThreads) void gemv_n_kernel(int64_t m, int64_t n,
                                                           const float *__restrict__ A, int64_t lda,
@@ -51,58 +62,73 @@ __global__ __launch_bounds__(kThreads) void gemv_n_kernel(int64_t m, int64_t n,
                                                           int64_t cps, float *__restrict__ part,
                                                           float alpha, float beta,
                                                           float *__restrict__ y, int64_t incy) {
-  const int64_t i0 = ((int64_t)blockIdx.x * kThreads + threadIdx.x) * 4;
+  constexpr int G = kGroupsN;
+  const int64_t rb = (int64_t)blockIdx.x * (4 * kThreads * G) + 4 * threadIdx.x;
   const int64_t j0 = (int64_t)blockIdx.y * cps;
   const int64_t j1 = j0 + cps < n ? j0 + cps : n;
-  if (i0 >= m) return;
-  const bool full = i0 + 4 <= m;
+  if (rb >= m) return;
   // rows past m read row m-1 (in bounds) and are never stored
-  const int64_t ir[4] = {i0, i0 + 1 < m ? i0 + 1 : m - 1, i0 + 2 < m ? i0 + 2 : m - 1,
-                         i0 + 3 < m ? i0 + 3 : m - 1};
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  int64_t ir[G][4];
+  bool full[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const int64_t i0 = rb + (int64_t)g * 4 * kThreads;
+    full[g] = i0 + 4 <= m;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) ir[g][q] = i0 + q < m ? i0 + q : m - 1;
+  }
+  float acc[G][4];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) acc[g][q] = 0.f;
+  auto load = [&](const float *col, int g) -> f4 {
+    if (VEC && full[g]) return ld_nt(col + ir[g][0]);
+    return f4{col[ir[g][0]], col[ir[g][1]], col[ir[g][2]], col[ir[g][3]]};
+  };
   int64_t j = j0;
-  // four columns per step, loads issued before the arithmetic
-  for (; j + 4 <= j1; j += 4) {
-    float xv[4];
-    f4 av[4];
+  // kStepN columns per step, every load issued before the arithmetic
+  for (; j + kStepN <= j1; j += kStepN) {
+    float xv[kStepN];
+    f4 av[kStepN][G];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) xv[c] = x[(j + c) * incx];
+    for (int c = 0; c < kStepN; ++c) xv[c] = x[(j + c) * incx];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const float *col = A + (j + c) * lda;
-      if (VEC && full) {
-        av[c] = *reinterpret_cast<const f4 *>(col + i0);
-      } else {
-        av[c] = f4{col[ir[0]], col[ir[1]], col[ir[2]], col[ir[3]]};
-      }
-    }
+    for (int c = 0; c < kStepN; ++c)
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
+      for (int g = 0; g < G; ++g) av[c][g] = load(A + (j + c) * lda, g);
+#pragma unroll
+    for (int c = 0; c < kStepN; ++c) {
       if (xv[c] != 0.f) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) acc[q] = fmaf(av[c][q], xv[c], acc[q]);
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) acc[g][q] = fmaf(av[c][g][q], xv[c], acc[g][q]);
       }
     }
   }
   for (; j < j1; ++j) {
     const float xj = x[j * incx];
-    const float *col = A + j * lda;
-    f4 a;
-    if (VEC && full)
-      a = *reinterpret_cast<const f4 *>(col + i0);
-    else
-      a = f4{col[ir[0]], col[ir[1]], col[ir[2]], col[ir[3]]};
+    f4 a[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) a[g] = load(A + j * lda, g);
     if (xj != 0.f) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) acc[q] = fmaf(a[q], xj, acc[q]);
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc[g][q] = fmaf(a[g][q], xj, acc[g][q]);
     }
   }
-  const int rows = full ? 4 : (int)(m - i0);
-  for (int q = 0; q < rows; ++q) {
-    if (part)
-      part[(int64_t)blockIdx.y * m + i0 + q] = acc[q];
-    else
-      store_y(y, (i0 + q) * incy, acc[q], alpha, beta);
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const int64_t i0 = rb + (int64_t)g * 4 * kThreads;
+    const int rows = i0 >= m ? 0 : (full[g] ? 4 : (int)(m - i0));
+    for (int q = 0; q < rows; ++q) {
+      if (part)
+        part[(int64_t)blockIdx.y * m + i0 + q] = acc[g][q];
+      else
+        store_y(y, (i0 + q) * incy, acc[g][q], alpha, beta);
+    }
   }
 }
 
@@ -129,12 +155,34 @@ __global__ __launch_bounds__(kThreads) void gemv_t_kernel(int64_t m, int64_t n,
   float acc[kColsPerWave];
 #pragma unroll
   for (int c = 0; c < kColsPerWave; ++c) acc[c] = 0.f;
-  for (int64_t i = r0 + 4 * lane; i < r1; i += 256) {
+  int64_t i = r0 + 4 * lane;
+  if (VEC) {
+    // two 256-row groups per step: 16 loads of A in flight per lane
+    for (; i + 256 + 4 <= r1; i += 512) {
+      const f4 xv0 = *reinterpret_cast<const f4 *>(x + i);
+      const f4 xv1 = *reinterpret_cast<const f4 *>(x + i + 256);
+      f4 av0[kColsPerWave], av1[kColsPerWave];
+#pragma unroll
+      for (int c = 0; c < kColsPerWave; ++c) {
+        av0[c] = ld_nt(col[c] + i);
+        av1[c] = ld_nt(col[c] + i + 256);
+      }
+#pragma unroll
+      for (int c = 0; c < kColsPerWave; ++c)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc[c] = fmaf(av0[c][q], xv0[q], acc[c]);
+#pragma unroll
+      for (int c = 0; c < kColsPerWave; ++c)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc[c] = fmaf(av1[c][q], xv1[q], acc[c]);
+    }
+  }
+  for (; i < r1; i += 256) {
     if (VEC && i + 4 <= r1) {
       const f4 xv = *reinterpret_cast<const f4 *>(x + i);
       f4 av[kColsPerWave];
 #pragma unroll
-      for (int c = 0; c < kColsPerWave; ++c) av[c] = *reinterpret_cast<const f4 *>(col[c] + i);
+      for (int c = 0; c < kColsPerWave; ++c) av[c] = ld_nt(col[c] + i);
 #pragma unroll
       for (int c = 0; c < kColsPerWave; ++c)
 #pragma unroll
@@ -164,17 +212,32 @@ __global__ __launch_bounds__(kThreads) void gemv_t_kernel(int64_t m, int64_t n,
   }
 }
 
-// y[i*incy] <- alpha * sum_s part[s*len + i] + beta * y[i*incy], splits
-// added in order.
+// One fold pass over groups of kFold splits: block (b, g) adds splits
+// [g*kFold, min(splits, (g+1)*kFold)) of outputs [256 b, 256 b + 256) in
+// split order, with all of a group's loads in flight (clamped addresses, so
+// none is guarded). The last pass (one group) writes alpha * sum + beta * y;
+// earlier ones write the group sums to out[g*len + i] for the next pass.
+constexpr int kFold = 32;
 __global__ __launch_bounds__(kThreads) void gemv_fold_kernel(int64_t len, int64_t splits,
                                                              const float *__restrict__ part,
-                                                             float alpha, float beta,
-                                                             float *__restrict__ y, int64_t incy) {
+                                                             float *__restrict__ out, float alpha,
+                                                             float beta, float *__restrict__ y,
+                                                             int64_t incy) {
   const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
   if (i >= len) return;
-  float s = part[i];
-  for (int64_t k = 1; k < splits; ++k) s += part[k * len + i];
-  store_y(y, i * incy, s, alpha, beta);
+  const int64_t s0 = (int64_t)blockIdx.y * kFold;
+  const int64_t last = (s0 + kFold < splits ? s0 + kFold : splits) - 1;
+  float v[kFold];
+#pragma unroll
+  for (int q = 0; q < kFold; ++q) v[q] = part[(s0 + q < last ? s0 + q : last) * len + i];
+  float sum = v[0];
+#pragma unroll
+  for (int q = 1; q < kFold; ++q)
+    if (s0 + q <= last) sum += v[q];
+  if (gridDim.y == 1 && out == nullptr)
+    store_y(y, i * incy, sum, alpha, beta);
+  else
+    out[(int64_t)blockIdx.y * len + i] = sum;
 }
 
 // y <- beta * y over len elements (0 when beta == 0): alpha == 0.
@@ -214,7 +277,7 @@ extern "C" int wgb_sgemv(wgb_ctx *ctx, int trans, int64_t m, int64_t n, float al
   // blocks along the output; split the contraction dimension until about
   // kTargetBlocks blocks stream A (N: >= 64 columns per split; T: >= 256
   // rows, a multiple of 256 so every split starts 16-byte aligned)
-  const int64_t bx = nt ? cdiv(cdiv(m, 4), kThreads) : cdiv(cdiv(n, kColsPerWave), kThreads / 64);
+  const int64_t bx = nt ? cdiv(m, 4 * kThreads * kGroupsN) : cdiv(cdiv(n, kColsPerWave), kThreads / 64);
   int64_t want = bx >= kTargetBlocks ? 1 : cdiv(kTargetBlocks, bx);
   const int64_t most = nt ? cdiv(n, 64) : cdiv(m, 256);
   if (want > most) want = most;
@@ -224,7 +287,10 @@ extern "C" int wgb_sgemv(wgb_ctx *ctx, int trans, int64_t m, int64_t n, float al
   const int64_t splits = nt ? cdiv(n, per) : cdiv(m, per);
   float *part = nullptr;
   if (splits > 1) {
-    if ((st = wgb::ensure_op_workspace(ctx, (size_t)(splits * len) * sizeof(float)))) return st;
+    // partials, then the fold passes' group sums after them
+    const int64_t groups = cdiv(splits, kFold);
+    if ((st = wgb::ensure_op_workspace(ctx, (size_t)((splits + groups) * len) * sizeof(float))))
+      return st;
     part = static_cast<float *>(ctx->op_ws);
   }
   dim3 grid((unsigned)bx, (unsigned)splits);
@@ -247,9 +313,22 @@ extern "C" int wgb_sgemv(wgb_ctx *ctx, int trans, int64_t m, int64_t n, float al
     WGB_CHECK_LAUNCH("gemv_t_kernel");
   }
   if (part) {
-    gemv_fold_kernel<<<(unsigned)cdiv(len, kThreads), kThreads, 0, ctx->stream>>>(len, splits, part,
-                                                                                  alpha, beta, y,
-                                                                                  incy);
+    // fold passes until one group of at most kFold remains; each pass
+    // alternates between the two halves of the workspace
+    float *src = part, *dst = part + splits * len;
+    int64_t k = splits;
+    while (k > kFold) {
+      const int64_t groups = cdiv(k, kFold);
+      gemv_fold_kernel<<<dim3((unsigned)cdiv(len, kThreads), (unsigned)groups), kThreads, 0,
+                         ctx->stream>>>(len, k, src, dst, alpha, beta, y, incy);
+      WGB_CHECK_LAUNCH("gemv_fold_kernel");
+      float *t = src;
+      src = dst;
+      dst = t;
+      k = groups;
+    }
+    gemv_fold_kernel<<<dim3((unsigned)cdiv(len, kThreads), 1), kThreads, 0, ctx->stream>>>(
+        len, k, src, nullptr, alpha, beta, y, incy);
     WGB_CHECK_LAUNCH("gemv_fold_kernel");
   }
   wgb::timing_end(ctx);

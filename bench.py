@@ -426,6 +426,32 @@ def run_only(ctx, name, reps):
     return {"algorithmic_bytes": (8 if name == "sdot" else 4) * n}
 
 
+def vendor_twin():
+    """rocBLAS on the same workloads and inputs (wgblas_amd/lib/vendor_twin,
+    run as a child process): {workload: {shape, ms, TFLOP/s | GB/s}}, or a
+    note when the twin is not built. Context next to the components, not a
+    parity check."""
+    import subprocess
+
+    exe = os.path.join(ROOT, "wgblas_amd", "lib", "vendor_twin")
+    if not os.path.exists(exe):
+        return {"note": "vendor_twin not built (python -m wgblas_amd.build)"}
+    res = subprocess.run([exe], stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True, timeout=600)
+    out = {}
+    for ln in res.stdout.splitlines():
+        try:
+            rec = json.loads(ln)
+        except ValueError:
+            continue
+        name = rec.pop("workload")
+        rec.pop("library", None)
+        out[name] = rec
+    out["version"] = res.stderr.strip().splitlines()[-1] if res.stderr.strip() else "rocBLAS"
+    if res.returncode != 0:
+        out["error"] = f"exit {res.returncode}"
+    return out
+
+
 def cpu_baseline(budget_s=12.0):
     """The oracle's fp32 restatement of the reference's per-element order
     (oracle/oracle.c orc_sgemm_wgsl), one host thread, on a bounded sample of
@@ -464,6 +490,8 @@ def main():
                          "ssyr2k_8192, ssymm_8192, strmm_8192, strsm_8192, sdot, sasum, snrm2, "
                          "isamax) for counter and kernel-trace collection")
     ap.add_argument("--reps", type=int, default=3)
+    ap.add_argument("--no-vendor", action="store_true",
+                    help="skip the rocBLAS twin (wgblas_amd/lib/vendor_twin) of the components")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
@@ -486,6 +514,7 @@ def main():
     achieved = flops / (mean_launch * 1e-3) / 1e12
     comps = {} if args.no_components else bench_components(ctx, ev, args.quick)
     ctx.close()
+    vendor = None if (args.no_vendor or args.no_components) else vendor_twin()
     line = {
         "metric": METRIC,
         "value": value,
@@ -507,6 +536,8 @@ def main():
         "sgemm_launch_ms": launch_ms,
         "components": comps,
     }
+    if vendor is not None:
+        line["vendor_rocblas"] = vendor
     if rank == 0 and not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline()
     if rank == 0:

@@ -100,6 +100,25 @@ def build_addon(verbose=False):
     return out_path
 
 
+def build_twin(verbose=False):
+    """The rocBLAS twin of bench.py's workloads (vendor context numbers):
+    host code only, linked to rocBLAS and to libwgblas_hip for its seeded
+    fills."""
+    src = os.path.join(CSRC, "vendor_twin.cpp")
+    out_path = os.path.join(LIBDIR, "vendor_twin")
+    tmp = out_path + ".tmp"
+    cmd = [
+        _hipcc(), f"--offload-arch={ARCH}", "-O2", "-std=c++17",
+        "-I", INCLUDE, src, "-o", tmp,
+        "-L", LIBDIR, "-lwgblas_hip", "-lrocblas", "-Wl,-rpath,$ORIGIN",
+    ]
+    out = _run(cmd)
+    if verbose and out.strip():
+        print(out)
+    os.replace(tmp, out_path)
+    return out_path
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--lib", action="store_true", help="build only the HIP library")
@@ -110,6 +129,8 @@ def main(argv=None):
     if not args.lib:
         addon = build_addon(args.verbose)
         print(f"built {addon}")
+        twin = build_twin(args.verbose)
+        print(f"built {twin}")
 
 
 if __name__ == "__main__":

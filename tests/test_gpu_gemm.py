@@ -233,6 +233,17 @@ def test_odd_leading_dimensions(ctx, ta, tb):
                ldc=ld(m))
 
 
+@pytest.mark.parametrize("ta", [0, 1])
+@pytest.mark.parametrize("lda", [(1 << 22) - 4, (1 << 22) + 4])
+def test_huge_leading_dimension(ctx, ta, lda):
+    # Aligned fp32 operands are copied into LDS with 32-bit lane offsets from
+    # the tile origin while 128 * ld * 4 bytes stays below 2^31; a larger ld
+    # (here 2^22 + 4 floats) runs the register-staged loads instead. Both
+    # sides of that limit, for k-contiguous (ta = 1) and m-contiguous A.
+    m, n, k = 130, 72, 48
+    check_case(ctx, 0, ta, 0, m, n, k, 1.25, 0.5, lda=lda, ldb=k, ldc=m)
+
+
 @pytest.mark.parametrize("uplo", [1, 2])
 @pytest.mark.parametrize("shape", [(2048, 2048, 40), (2100, 1900, 33)])
 def test_sgemmtr_large_tier(ctx, uplo, shape):

@@ -229,6 +229,7 @@ struct Stager {
   // k-tile 0 and this lane's byte offsets from it, one per load step.
   const T *origin;
   uint32_t voff[LOADS];
+  int copy_shift;  // elements from this thread's register-path vector to its copy source
 
   __device__ void init(const T *P, int64_t ld, int64_t row0, int t, int64_t rows_total_,
                        int64_t K_) {
@@ -236,16 +237,17 @@ struct Stager {
     K = K_;
     origin = KC ? P + row0 * ld : P + row0;
     if (KC) {
-      // Thread t fills LDS chunk t % 8 of row t / 8, so it reads the global
-      // chunk that the swizzle puts there (kc_swz(row + 32 r) == kc_swz(row)).
-      int row = t / 8, kv = (t % 8) ^ kc_swz(row);
+      int row = t / 8, kv = t % 8;
       row_first = row0 + row;
       k_first = kv * VW;
       base = P + (row0 + row) * ld + kv * VW;
       r_step = 32 * ld;
       k_step = BK;
-      lds_off = row * LDK + (t % 8) * VW;
+      lds_off = row * LDK + (kv ^ kc_swz(row)) * VW;  // kc_swz(row + 32 r) == kc_swz(row)
       lds_r_step = 32 * LDK;
+      // An LDS copy puts lane t at chunk t % 8 of the row, so that lane
+      // reads the chunk the swizzle places there instead.
+      copy_shift = ((kv ^ kc_swz(row)) - kv) * VW;
     } else {
       int mv = t % VPK, kk = t / VPK;
       row_first = row0 + mv * VW;
@@ -255,6 +257,7 @@ struct Stager {
       k_step = (int64_t)BK * ld;
       lds_off = kk * LDM + mv * VW;
       lds_r_step = KROWS * LDM;
+      copy_shift = 0;
     }
   }
 
@@ -330,15 +333,17 @@ struct Stager {
       const T *q = base + r * r_step;
       if (EDGE && KC) q = r < nvr ? q : fb;
       if (EDGE && !KC) q = vok ? q : fb + r * r_step;
-      voff[r] = (uint32_t)((const char *)q - (const char *)origin);
+      voff[r] = (uint32_t)((const char *)(q + copy_shift) - (const char *)origin);
     }
   }
 
   // Whole k-tile kt copied straight from global memory into `stage` with
   // global_load_lds_dwordx4 (no registers): lane l of wave w lands at
-  // 16 l bytes past a wave-uniform address, and in both layouts thread t's
-  // vector r sits at element lds_off + r lds_r_step = VW t + r lds_r_step, so
-  // the copy fills the stage exactly as store() would. Completion is tracked
+  // 16 l bytes past a wave-uniform address, i.e. thread t's vector r at
+  // element VW t + r lds_r_step. In the [k][row] layout that is where store()
+  // puts it; in the [row][k] layout it is chunk t % 8 of row t / 8, so the
+  // lane reads the global chunk the swizzle maps there (copy_shift), and the
+  // stage ends up exactly as store() would leave it. Completion is tracked
   // by vmcnt; readers wait for it and then a barrier.
   // SCALAR_BASE: the address is the scalar tile origin plus a 32-bit lane
   // offset (the instruction's saddr + voffset form); the empty asm
@@ -368,7 +373,7 @@ struct Stager {
         const T *q = p + r * r_step;
         if (EDGE && KC) q = r < nvr ? q : fb + (int64_t)kt * k_step;
         if (EDGE && !KC) q = vok ? q : fb + (int64_t)kt * k_step + r * r_step;
-        copy16_to_lds(q, dst + r * lds_r_step);
+        copy16_to_lds(q + copy_shift, dst + r * lds_r_step);
       }
     }
   }

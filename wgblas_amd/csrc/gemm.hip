@@ -756,6 +756,75 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs<T> &p, int tm, int tn, 
   #pragma unroll
             for (int j = 0; j < MB; ++j) acc[i][j] = Ty<T>::mfma(y[s][i], yb[s][j], acc[i][j]);
       }
+    } else if constexpr (VEC) {
+      // fp64 with 16-byte aligned operands: the same LDS copies, one 16-k
+      // chunk per k-tile, operands fetched one MFMA step (4 k) at a time and
+      // double buffered across steps. Tile kt, step s: fetch step s+1 (for
+      // s = 3: wait for this wave's copies, barrier, copies of tile kt+2
+      // into buffer kt&1, fetch step 0 of tile kt+1), then the MFMAs of step
+      // s. A copy has a whole k-tile to land; after each barrier the MFMAs of
+      // the last step cover the first LDS reads of the next tile.
+      static_assert(BK == 16, "the fp64 copy loop assumes one 16-k chunk per k-tile");
+      constexpr bool kScalarBase = AKC || BKC;
+      const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+      sa.template init_copy<EDGE>();
+      sb.template init_copy<EDGE>();
+      auto fill = [&](int kt) {
+        T *st = smem + (kt & 1) * STAGE;
+        if (kt < nkt_whole) {
+          sa.template load_lds<EDGE, kScalarBase>(st, kt, wave);
+          sb.template load_lds<EDGE, kScalarBase>(st + SA::ELEMS, kt, wave);
+        } else {
+          V ra[SA::LOADS], rb[SB::LOADS];
+          sa.template load<true>(ra, kt);
+          sb.template load<true>(rb, kt);
+          sa.store(st, ra);
+          sb.store(st + SA::ELEMS, rb);
+        }
+      };
+      fill(0);
+      if (1 < nkt) fill(1);
+      copies_landed_sync();
+      T a[2][MB], b[2][MB];
+      fetch_step<T, BT, AKC, MB>(smem, wm, 0, 0, lane, a[0]);
+      fetch_step<T, BT, BKC, MB>(smem + SA::ELEMS, wn, 0, 0, lane, b[0]);
+      // One k-tile; TAIL: tile kt+2 may be missing or partial (the last two
+      // k-tiles), otherwise it is whole and the loop body is branch-free.
+      auto tile = [&](int kt, auto tail_tag) {
+        constexpr bool TAIL = decltype(tail_tag)::value;
+        T *cur = smem + (kt & 1) * STAGE;
+        const T *nxt = smem + ((kt + 1) & 1) * STAGE;
+  #pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const int u = s & 1, w = u ^ 1;
+          if (s < 3) {
+            fetch_step<T, BT, AKC, MB>(cur, wm, 0, s + 1, lane, a[w]);
+            fetch_step<T, BT, BKC, MB>(cur + SA::ELEMS, wn, 0, s + 1, lane, b[w]);
+          } else {
+            __builtin_amdgcn_sched_barrier(0);
+            copies_landed_sync();
+            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (TAIL) {
+              if (kt + 2 < nkt) fill(kt + 2);
+            } else {
+              sa.template load_lds<EDGE, kScalarBase>(cur, kt + 2, wave);
+              sb.template load_lds<EDGE, kScalarBase>(cur + SA::ELEMS, kt + 2, wave);
+            }
+            if (!TAIL || kt + 1 < nkt) {
+              fetch_step<T, BT, AKC, MB>(nxt, wm, 0, 0, lane, a[w]);
+              fetch_step<T, BT, BKC, MB>(nxt + SA::ELEMS, wn, 0, 0, lane, b[w]);
+            }
+          }
+  #pragma unroll
+          for (int i = 0; i < MB; ++i)
+  #pragma unroll
+            for (int j = 0; j < MB; ++j) acc[i][j] = Ty<T>::mfma(a[u][i], b[u][j], acc[i][j]);
+        }
+      };
+      int kt = 0;
+      const int nsteady = (nkt < nkt_whole ? nkt : nkt_whole) - 2;
+      for (; kt < nsteady; ++kt) tile(kt, std::false_type{});
+      for (; kt < nkt; ++kt) tile(kt, std::true_type{});
     } else {
       V ra[SA::LOADS], rb[SB::LOADS];
       if (0 < nkt_whole) {
@@ -1262,13 +1331,12 @@ int gemm_launch(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64
   a.c_vec = (ldc % VW == 0) && aligned16(C);
   const bool akc = transA == WGB_TRANS;
   const bool bkc = transB == WGB_NO_TRANS;
-  // VEC: 16-byte aligned operand vectors. For fp32 that path copies k-tiles
-  // straight into LDS with 32-bit lane offsets from the tile origin, which
-  // stay below BT * ld * sizeof(T); larger leading dimensions take the
-  // element-aligned register path (same results, same loads).
+  // VEC: 16-byte aligned operand vectors. That path copies k-tiles straight
+  // into LDS with 32-bit lane offsets from the tile origin, which stay below
+  // BT * ld * sizeof(T); larger leading dimensions take the element-aligned
+  // register path (same results, same loads).
   const int64_t off_cap = (int64_t)1 << 31;
-  const bool offs32 = sizeof(T) != 4 || (128 * lda * (int64_t)sizeof(T) < off_cap &&
-                                         128 * ldb * (int64_t)sizeof(T) < off_cap);
+  const bool offs32 = 128 * lda * (int64_t)sizeof(T) < off_cap && 128 * ldb * (int64_t)sizeof(T) < off_cap;
   const bool vec = (lda % VW == 0) && (ldb % VW == 0) && aligned16(A) && aligned16(B) && offs32;
   // Large tier once the 128-tiles alone fill the chip; small tier otherwise.
   auto count = [&](int64_t bt, int64_t &tmn, int64_t &tnn) {

@@ -234,6 +234,19 @@ def test_odd_leading_dimensions(ctx, ta, tb):
 
 
 @pytest.mark.parametrize("ta", [0, 1])
+@pytest.mark.parametrize("tb", [0, 1])
+@pytest.mark.parametrize("shape", [(512, 512, 512), (700, 300, 1024), (33, 65, 17), (704, 704, 1000),
+                                   (31, 1, 5)])
+def test_small_kernel_shapes(ctx, ta, tb, shape):
+    # one-launch path (32x32 tiles, k split across the block's waves): taken
+    # while 64-tiles would fill under half the chip and k <= 1024; ragged
+    # m / n / k and padded leading dimensions
+    m, n, k = shape
+    check_case(ctx, 0, ta, tb, m, n, k, 1.5, 0.5, lda=(k if ta else m) + 3, ldb=(n if tb else k) + 1,
+               ldc=m + 2)
+
+
+@pytest.mark.parametrize("ta", [0, 1])
 @pytest.mark.parametrize("lda", [(1 << 22) - 4, (1 << 22) + 4])
 def test_huge_leading_dimension(ctx, ta, lda):
     # Aligned fp32 operands are copied into LDS with 32-bit lane offsets from

@@ -1128,6 +1128,139 @@ __global__ __launch_bounds__(kThreads, (sizeof(T) == 8 || AKC != BKC) ? 2 : 1) v
   }
 }
 
+// Small GEMMs (a few hundred 32x32 tiles of C, k <= kSmallMaxK): one block
+// of 16 waves per 32x32 tile, the waves splitting k (wave w takes the 16-k
+// chunks w, w+16, ..., CPW of them), each wave loading all its operands
+// straight from global memory into MFMA operand registers up front (no LDS
+// staging, one memory latency), the 16 partial tiles then added in wave
+// order through LDS. One launch and no split-k workspace, where the tiled
+// kernels would need a split-k launch plus its fixup to fill the chip.
+constexpr int kSmallTile = 32;
+constexpr int kSmallWaves = 16;
+constexpr int64_t kSmallMaxK = 1024;  // 16 waves x 4 chunks x 16 k
+
+// MFMA operands of one 16-k chunk (k0 .. k0+15) for the two 16-row blocks
+// of rows r0 .. r0+31 of op(X), in the k order and row placement of
+// fetch_operands (step s of lane group g takes k = k0 + 4g + s; an
+// mn-contiguous operand puts rows r0 + 2 i16 + c in block c). Rows past
+// `rows` read row rows-1 (their results are never stored); k past K reads 0.
+// WHOLE: every k of the chunk is in range and so are all 32 rows.
+template <bool KC, bool WHOLE>
+__device__ __forceinline__ void small_operands(const float *P, int64_t ld, int64_t rows, int64_t r0,
+                                               int64_t K, int64_t k0, int lane, float (&out)[4][2]) {
+  typedef float F4 __attribute__((ext_vector_type(4), aligned(4)));
+  typedef float F2 __attribute__((ext_vector_type(2), aligned(4)));
+  const int g = lane >> 4, i16 = lane & 15;
+  if constexpr (KC) {
+    const int64_t kk = k0 + 4 * g;
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      int64_t row = r0 + 16 * b + i16;
+      if (!WHOLE) row = row < rows ? row : rows - 1;
+      F4 v;
+      if (WHOLE) {
+        v = *reinterpret_cast<const F4 *>(P + row * ld + kk);
+      } else {
+        // k = kk + c for c < nv is in range; every other lane element reads
+        // k = min(kk, K - 1) (inside the row) and is replaced by 0: clamped
+        // addresses and selects, no branches
+        const int64_t nv = K - kk;
+        const float *q = P + row * ld + (kk < K ? kk : K - 1);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const float x = q[c < nv ? c : 0];
+          v[c] = (c < nv) ? x : 0.f;
+        }
+      }
+#pragma unroll
+      for (int s = 0; s < 4; ++s) out[s][b] = v[s];
+    }
+  } else {
+    int64_t row = r0 + 2 * i16;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int64_t kk = k0 + 4 * g + s;
+      F2 v;
+      if (WHOLE) {
+        v = *reinterpret_cast<const F2 *>(P + row + kk * ld);
+      } else {
+        const int64_t kc = kk < K ? kk : K - 1;
+        const int64_t ra = row < rows ? row : rows - 1, rb = row + 1 < rows ? row + 1 : rows - 1;
+        const float x0 = P[ra + kc * ld], x1 = P[rb + kc * ld];
+        v[0] = kk < K ? x0 : 0.f;
+        v[1] = kk < K ? x1 : 0.f;
+      }
+      out[s][0] = v[0];
+      out[s][1] = v[1];
+    }
+  }
+}
+
+template <bool AKC, bool BKC, int CPW>
+__global__ __launch_bounds__(64 * kSmallWaves) void gemm_small_kernel(GemmArgs<float> p) {
+  constexpr int MB = 2;
+  typedef Ty<float>::acc Acc;
+  __shared__ float red[kSmallWaves][kSmallTile][kSmallTile + 1];  // [wave][col][row]
+  const int t = (int)threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int tm = (int)blockIdx.x % p.tiles_m, tn = (int)blockIdx.x / p.tiles_m;
+  const int64_t m0 = (int64_t)tm * kSmallTile, n0 = (int64_t)tn * kSmallTile;
+  const bool inside = m0 + kSmallTile <= p.m && n0 + kSmallTile <= p.n;  // block-uniform
+  const int64_t nwhole = p.k / 16;
+  float a[CPW][4][2], b[CPW][4][2];
+#pragma unroll
+  for (int i = 0; i < CPW; ++i) {
+    // chunks past the end of k load zeros (the guarded form)
+    const int64_t c = wave + (int64_t)kSmallWaves * i;
+    if (inside && c < nwhole) {
+      small_operands<AKC, true>(p.A, p.lda, p.m, m0, p.k, 16 * c, lane, a[i]);
+      small_operands<BKC, true>(p.B, p.ldb, p.n, n0, p.k, 16 * c, lane, b[i]);
+    } else {
+      small_operands<AKC, false>(p.A, p.lda, p.m, m0, p.k, 16 * c, lane, a[i]);
+      small_operands<BKC, false>(p.B, p.ldb, p.n, n0, p.k, 16 * c, lane, b[i]);
+    }
+  }
+  Acc acc[MB][MB];
+#pragma unroll
+  for (int i = 0; i < MB; ++i)
+#pragma unroll
+    for (int j = 0; j < MB; ++j) acc[i][j] = Acc(0.f);
+#pragma unroll
+  for (int c = 0; c < CPW; ++c)
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int i = 0; i < MB; ++i)
+#pragma unroll
+        for (int j = 0; j < MB; ++j) acc[i][j] = Ty<float>::mfma(a[c][s][i], b[c][s][j], acc[i][j]);
+#pragma unroll
+  for (int i = 0; i < MB; ++i)
+#pragma unroll
+    for (int j = 0; j < MB; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        red[wave][out_col<BKC, MB, 4>(j, lane)][out_row<float, AKC, MB>(i, q, lane)] = acc[i][j][q];
+  __syncthreads();
+  // one C element per thread: 1024 threads, 32x32 tile
+  const int r = t % kSmallTile, cl = t / kSmallTile;
+  const int64_t row = m0 + r, col = n0 + cl;
+  if (row >= p.m || col >= p.n) return;
+  float sum = red[0][cl][r];
+#pragma unroll
+  for (int w = 1; w < kSmallWaves; ++w) sum += red[w][cl][r];
+  float *cp = p.C + row + col * p.ldc;
+  float v = p.alpha * sum;
+  if (p.beta != 0.f) v = fmaf(p.beta, *cp, v);
+  *cp = v;
+}
+
+template <bool AKC, bool BKC>
+const void *small_kernel_for(int64_t k) {
+  const int64_t nch = (k + 15) / 16;
+  if (nch <= kSmallWaves) return reinterpret_cast<const void *>(gemm_small_kernel<AKC, BKC, 1>);
+  if (nch <= 2 * kSmallWaves) return reinterpret_cast<const void *>(gemm_small_kernel<AKC, BKC, 2>);
+  return reinterpret_cast<const void *>(gemm_small_kernel<AKC, BKC, 4>);
+}
+
 // C <- beta*C (or 0 when beta == 0) on the uplo part of the m x n C: the
 // alpha == 0 / k == 0 path, which reads neither A nor B.
 template <typename T>
@@ -1331,6 +1464,27 @@ int gemm_launch(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64
   a.c_vec = (ldc % VW == 0) && aligned16(C);
   const bool akc = transA == WGB_TRANS;
   const bool bkc = transB == WGB_NO_TRANS;
+  const int64_t fill = ctx->num_cus > 0 ? ctx->num_cus : 256;
+  if constexpr (sizeof(T) == 4) {
+    // Small problems: below half a launch of 64-tiles the tiled kernels need
+    // split-k and a fixup launch; one 32x32 tile per block with k split
+    // across its waves does it in one launch.
+    const int64_t t32m = (m + kSmallTile - 1) / kSmallTile, t32n = (n + kSmallTile - 1) / kSmallTile;
+    const int64_t t64 = ((m + 63) / 64) * ((n + 63) / 64);
+    if (uplo == 0 && band == wgb::kBandNone && k <= kSmallMaxK && 2 * t64 < fill &&
+        t32m * t32n <= 4 * fill) {
+      a.tiles_m = (int)t32m;
+      a.tiles_n = (int)t32n;
+      a.ntiles = (int)(t32m * t32n);
+      void *args[] = {&a};
+      const void *fn = akc ? (bkc ? small_kernel_for<true, true>(k) : small_kernel_for<true, false>(k))
+                           : (bkc ? small_kernel_for<false, true>(k) : small_kernel_for<false, false>(k));
+      WGB_CHECK_HIP(hipLaunchKernel(fn, dim3((unsigned)a.ntiles), dim3(64 * kSmallWaves), args, 0,
+                                    ctx->stream));
+      WGB_CHECK_LAUNCH("gemm_small_kernel");
+      return WGB_OK;
+    }
+  }
   // VEC: 16-byte aligned operand vectors. That path copies k-tiles straight
   // into LDS with 32-bit lane offsets from the tile origin, which stay below
   // BT * ld * sizeof(T); larger leading dimensions take the element-aligned
@@ -1348,7 +1502,6 @@ int gemm_launch(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64
   };
   int64_t tm128, tn128;
   int64_t tiles128 = count(128, tm128, tn128);
-  const int64_t fill = ctx->num_cus > 0 ? ctx->num_cus : 256;
   const int bt = tiles128 >= fill ? 128 : 64;
   int64_t tmn, tnn;
   int64_t ntiles = count(bt, tmn, tnn);

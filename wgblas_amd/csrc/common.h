@@ -45,6 +45,9 @@ int fail_hip(hipError_t err, const char *what);
 // Makes ctx's device current; every entry point calls it first.
 int enter(wgb_ctx *ctx);
 
+// A pointer's 16-byte alignment (vector loads and stores).
+inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
 // Brackets a routine's kernels with the context's timing events.
 void timing_begin(wgb_ctx *ctx);
 void timing_end(wgb_ctx *ctx);

@@ -1402,7 +1402,7 @@ int launch_tier(wgb_ctx *ctx, GemmArgs<T> &a, bool akc, bool bkc, bool vec) {
   return WGB_OK;
 }
 
-bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+using wgb::aligned16;
 
 int64_t imax(int64_t a, int64_t b) { return a > b ? a : b; }
 

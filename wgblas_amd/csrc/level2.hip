@@ -250,7 +250,7 @@ __global__ __launch_bounds__(kThreads) void scale_y_kernel(int64_t len, float be
   if (i < len) y[i * incy] = beta == 0.f ? 0.f : beta * y[i * incy];
 }
 
-bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+using wgb::aligned16;
 
 }  // namespace
 

@@ -79,20 +79,47 @@ __global__ __launch_bounds__(256) void symmetrize_kernel(int64_t order, const fl
 // W <- A's uplo triangle, zero elsewhere, ones on the diagonal for a unit
 // triangle (src/shaders/triangularize.wgsl builds op(A); W keeps A's own
 // orientation and the GEMM applies transA).
+// A thread writes 4 consecutive rows of W (one 16-byte store; W's ld is a
+// multiple of 4) in columns blockIdx.y, blockIdx.y + gridDim.y, ...; a row
+// group wholly outside the triangle writes zeros without reading A. VEC: lda
+// a multiple of 4 and A 16-byte aligned (16-byte loads).
+template <bool VEC>
 __global__ __launch_bounds__(256) void triangle_copy_kernel(int64_t order,
                                                             const float *__restrict__ A,
                                                             int64_t lda, int uplo, int unit,
                                                             float *__restrict__ W, int64_t ldw) {
-  const int64_t row = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  typedef float F4 __attribute__((ext_vector_type(4)));
+  const int64_t row = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
   if (row >= order) return;
   const bool lower = uplo == WGB_LOWER;
+  const int nr = order - row < 4 ? (int)(order - row) : 4;
   for (int64_t col = blockIdx.y; col < order; col += gridDim.y) {
-    float v;
-    if (row == col)
-      v = unit ? 1.f : A[row + col * lda];
-    else
-      v = (lower ? row > col : row < col) ? A[row + col * lda] : 0.f;
-    W[row + col * ldw] = v;
+    // does any of rows row .. row+nr-1 lie in the triangle (diagonal included)?
+    const bool any = lower ? row + nr - 1 >= col : row <= col;
+    F4 v = F4(0.f);
+    if (any) {
+      const float *a = A + row + col * lda;
+      if (VEC && nr == 4) {
+        v = *reinterpret_cast<const F4 *>(a);
+      } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) v[c] = a[c < nr ? c : 0];
+      }
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int64_t r = row + c;
+        if (r == col)
+          v[c] = unit ? 1.f : v[c];
+        else if (!(lower ? r > col : r < col))
+          v[c] = 0.f;  // the other triangle: never used, whatever it holds
+      }
+    }
+    float *w = W + row + col * ldw;
+    if (nr == 4) {
+      *reinterpret_cast<F4 *>(w) = v;
+    } else {
+      for (int c = 0; c < nr; ++c) w[c] = v[c];
+    }
   }
 }
 
@@ -409,9 +436,12 @@ extern "C" int wgb_strmm(wgb_ctx *ctx, int side, int uplo, int transA, int diag,
     if ((st = wgb::ensure_op_workspace(ctx, (size_t)(ldw * order + ldbc * n) * sizeof(float)))) return st;
     float *W = static_cast<float *>(ctx->op_ws);
     float *Bc = W + ldw * order;  // 16-byte aligned: ldw is a multiple of 4
-    const int64_t gy = order < 65535 ? order : 65535;
-    triangle_copy_kernel<<<dim3((unsigned)((order + 255) / 256), (unsigned)gy), 256, 0,
-                           ctx->stream>>>(order, A, lda, uplo, diag == WGB_UNIT, W, ldw);
+    const int64_t gy = order < 4096 ? order : 4096;
+    const dim3 grid((unsigned)((order + 1023) / 1024), (unsigned)gy);
+    if (lda % 4 == 0 && wgb::aligned16(A))
+      triangle_copy_kernel<true><<<grid, 256, 0, ctx->stream>>>(order, A, lda, uplo, diag == WGB_UNIT, W, ldw);
+    else
+      triangle_copy_kernel<false><<<grid, 256, 0, ctx->stream>>>(order, A, lda, uplo, diag == WGB_UNIT, W, ldw);
     WGB_CHECK_LAUNCH("triangle_copy_kernel");
     WGB_CHECK_HIP(hipMemcpy2DAsync(Bc, (size_t)ldbc * sizeof(float), B, (size_t)ldb * sizeof(float),
                                    (size_t)m * sizeof(float), (size_t)n, hipMemcpyDeviceToDevice,

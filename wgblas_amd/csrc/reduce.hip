@@ -81,7 +81,7 @@ int reduce_blocks(int64_t n) {
   return (int)g;
 }
 
-bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+using wgb::aligned16;
 
 // ---- the four reductions as accumulate / merge policies -------------------
 //

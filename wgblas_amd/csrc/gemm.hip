@@ -606,8 +606,6 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs<T> &p, int tm, int tn, 
   typedef Stager<T, BT, AKC, VEC> SA;
   typedef Stager<T, BT, BKC, VEC> SB;
   constexpr int STAGE = SA::ELEMS + SB::ELEMS;
-  const int nkt_all = (int)((p.k + BK - 1) / BK);
-  (void)nkt_all;
   const int64_t m0 = (int64_t)tm * BT, n0 = (int64_t)tn * BT;
   const int lane = t & 63, wave = t >> 6;
   const int wm = (wave & 1) * WT, wn = (wave >> 1) * WT;
@@ -1277,24 +1275,44 @@ __global__ void scale_kernel(int64_t m, int64_t n, T beta, T *C, int64_t ldc, in
 }
 
 // Split-k fixup: C = alpha * (sum over splits, in split order) + beta * C on
-// the in-range, in-triangle elements of the tail tiles. One block per tile
-// column, one thread per tile row.
+// the in-range, in-triangle elements of the tail tiles. A block covers 8
+// columns of one tile; a thread takes 4 consecutive rows of one column and
+// issues the loads of every split (at most 16) before adding them in split
+// order, so the sums are those of a split-by-split loop.
+constexpr int kFixupCols = 8;
 template <typename T, int BT>
-__global__ __launch_bounds__(BT) void split_fixup(GemmArgs<T> p) {
-  const int tile = (int)blockIdx.x / BT, cl = (int)blockIdx.x % BT, rl = (int)threadIdx.x;
+__global__ __launch_bounds__(kFixupCols * BT / 4) void split_fixup(GemmArgs<T> p) {
+  typedef T V4 __attribute__((ext_vector_type(4)));
+  constexpr int kMaxSplits = 16;
+  constexpr int RG = BT / 4;  // row groups per column
+  const int per_tile = BT / kFixupCols;
+  const int tile = (int)blockIdx.x / per_tile;
+  const int cl = ((int)blockIdx.x % per_tile) * kFixupCols + (int)threadIdx.x / RG;
+  const int rl = 4 * ((int)threadIdx.x % RG);
   int tm, tn;
   logical_tile(p.nregular + tile, p.tiles_m, p.tiles_n, p.uplo, tm, tn);
-  const int64_t row = (int64_t)tm * BT + rl, col = (int64_t)tn * BT + cl;
-  if (row >= p.m || col >= p.n) return;
-  if (p.uplo == WGB_LOWER && row < col) return;
-  if (p.uplo == WGB_UPPER && row > col) return;
+  const int64_t row0 = (int64_t)tm * BT + rl, col = (int64_t)tn * BT + cl;
+  if (row0 >= p.m || col >= p.n) return;
   const T *src = p.ws + (int64_t)tile * p.splits * BT * BT + (int64_t)cl * BT + rl;
-  T sum = src[0];
-  for (int s = 1; s < p.splits; ++s) sum += src[(int64_t)s * BT * BT];
-  T *cp = p.C + row + col * p.ldc;
-  T v = p.alpha * sum;
-  if (p.beta != (T)0) v = fma(p.beta, *cp, v);
-  *cp = v;
+  V4 part[kMaxSplits];
+#pragma unroll
+  for (int s = 0; s < kMaxSplits; ++s)
+    if (s < p.splits) part[s] = *reinterpret_cast<const V4 *>(src + (int64_t)s * BT * BT);
+  V4 sum = part[0];
+#pragma unroll
+  for (int s = 1; s < kMaxSplits; ++s)
+    if (s < p.splits) sum += part[s];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int64_t row = row0 + q;
+    if (row >= p.m) break;
+    if (p.uplo == WGB_LOWER && row < col) continue;
+    if (p.uplo == WGB_UPPER && row > col) continue;
+    T *cp = p.C + row + col * p.ldc;
+    T v = p.alpha * sum[q];
+    if (p.beta != (T)0) v = fma(p.beta, *cp, v);
+    *cp = v;
+  }
 }
 
 template <typename T>
@@ -1396,7 +1414,8 @@ int launch_tier(wgb_ctx *ctx, GemmArgs<T> &a, bool akc, bool bkc, bool vec) {
   WGB_CHECK_HIP(hipLaunchKernel(reinterpret_cast<const void *>(fn), dim3((unsigned)grid),
                                 dim3(kThreads), args, 0, ctx->stream));
   if (a.splits > 1) {
-    split_fixup<T, BT><<<(unsigned)((a.ntiles - a.nregular) * BT), BT, 0, ctx->stream>>>(a);
+    split_fixup<T, BT><<<(unsigned)((a.ntiles - a.nregular) * (BT / kFixupCols)), kFixupCols * BT / 4, 0,
+                         ctx->stream>>>(a);
     WGB_CHECK_LAUNCH("split_fixup");
   }
   return WGB_OK;

@@ -452,6 +452,28 @@ def vendor_twin():
     return out
 
 
+def roof_probe():
+    """The roofs re-measured on this box (wgblas_amd/lib/roof_probe, run as a
+    child process): HBM read and copy bandwidth, fp32 / fp64 MFMA issue
+    rate. Context beside the published peaks that `roofline` uses."""
+    import subprocess
+
+    exe = os.path.join(ROOT, "wgblas_amd", "lib", "roof_probe")
+    if not os.path.exists(exe):
+        return {"note": "roof_probe not built (python -m wgblas_amd.build)"}
+    res = subprocess.run([exe], stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True, timeout=300)
+    out = {}
+    for ln in res.stdout.splitlines():
+        try:
+            rec = json.loads(ln)
+        except ValueError:
+            continue
+        out[rec.pop("probe")] = rec
+    if res.returncode != 0:
+        out["error"] = f"exit {res.returncode}: {res.stderr.strip()[-200:]}"
+    return out
+
+
 def cpu_baseline(budget_s=12.0):
     """The oracle's fp32 restatement of the reference's per-element order
     (oracle/oracle.c orc_sgemm_wgsl), one host thread, on a bounded sample of
@@ -491,7 +513,8 @@ def main():
                          "isamax) for counter and kernel-trace collection")
     ap.add_argument("--reps", type=int, default=3)
     ap.add_argument("--no-vendor", action="store_true",
-                    help="skip the rocBLAS twin (wgblas_amd/lib/vendor_twin) of the components")
+                    help="skip the rocBLAS twin (wgblas_amd/lib/vendor_twin) of the components "
+                         "and the roof probe (wgblas_amd/lib/roof_probe)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
@@ -515,6 +538,7 @@ def main():
     comps = {} if args.no_components else bench_components(ctx, ev, args.quick)
     ctx.close()
     vendor = None if (args.no_vendor or args.no_components) else vendor_twin()
+    roofs = None if (args.no_vendor or args.no_components) else roof_probe()
     line = {
         "metric": METRIC,
         "value": value,
@@ -538,6 +562,8 @@ def main():
     }
     if vendor is not None:
         line["vendor_rocblas"] = vendor
+    if roofs is not None:
+        line["roof_probe"] = roofs
     if rank == 0 and not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline()
     if rank == 0:

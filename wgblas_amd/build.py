@@ -119,6 +119,20 @@ def build_twin(verbose=False):
     return out_path
 
 
+def build_probe(verbose=False):
+    """The roof probe (HBM read / copy bandwidth, fp32 / fp64 MFMA issue
+    rate measured on the box; bench.py reports it beside the published
+    peaks)."""
+    src = os.path.join(CSRC, "roof_probe.hip")
+    out_path = os.path.join(LIBDIR, "roof_probe")
+    tmp = out_path + ".tmp"
+    out = _run([_hipcc(), *HIPCC_FLAGS, src, "-o", tmp])
+    if verbose and out.strip():
+        print(out)
+    os.replace(tmp, out_path)
+    return out_path
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--lib", action="store_true", help="build only the HIP library")
@@ -131,6 +145,8 @@ def main(argv=None):
         print(f"built {addon}")
         twin = build_twin(args.verbose)
         print(f"built {twin}")
+        probe = build_probe(args.verbose)
+        print(f"built {probe}")
 
 
 if __name__ == "__main__":

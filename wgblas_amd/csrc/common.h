@@ -54,7 +54,7 @@ void timing_end(wgb_ctx *ctx);
 
 // Largest number of first-pass blocks a reduction may use; the scratch
 // buffer is sized for this many 32-byte partials plus the result slot.
-constexpr int kMaxReduceBlocks = 2048;
+constexpr int kMaxReduceBlocks = 4096;
 constexpr size_t kScratchBytes = (size_t)kMaxReduceBlocks * 32 + 256;  // 32-byte partial slots + result
 
 // Grows the context's operand workspace (ctx->op_ws) to at least `bytes`;

@@ -247,11 +247,24 @@ def test_small_kernel_shapes(ctx, ta, tb, shape):
 
 
 @pytest.mark.parametrize("ta", [0, 1])
-@pytest.mark.parametrize("lda", [(1 << 22) - 4, (1 << 22) + 4])
+@pytest.mark.parametrize("case", [((4096, 4096, 64), "aligned"), ((4000, 4036, 70), "aligned"),
+                                  ((4000, 4036, 70), "ldc_odd"), ((4000, 4036, 70), "beta0")])
+def test_wide_tier(ctx, ta, case):
+    # 256 x 128 tiles with 512 threads (op(B) k-contiguous, aligned operands,
+    # at least two full rounds): interior and ragged tiles in m, n and k,
+    # the element-wise epilogue (ldc odd) and beta = 0
+    (m, n, k), variant = case
+    ldc = m + 1 if variant == "ldc_odd" else m
+    beta = 0.0 if variant == "beta0" else 0.5
+    check_case(ctx, 0, ta, 0, m, n, k, 1.25, beta, lda=(k if ta else m), ldb=k, ldc=ldc)
+
+
+@pytest.mark.parametrize("ta", [0, 1])
+@pytest.mark.parametrize("lda", [(1 << 21) - 4, (1 << 21) + 4])
 def test_huge_leading_dimension(ctx, ta, lda):
-    # Aligned fp32 operands are copied into LDS with 32-bit lane offsets from
-    # the tile origin while 128 * ld * 4 bytes stays below 2^31; a larger ld
-    # (here 2^22 + 4 floats) runs the register-staged loads instead. Both
+    # Aligned operands are copied into LDS with 32-bit lane offsets from the
+    # tile origin while 256 * ld * sizeof(T) stays below 2^31; a larger ld
+    # (here 2^21 + 4 floats) runs the register-staged loads instead. Both
     # sides of that limit, for k-contiguous (ta = 1) and m-contiguous A.
     m, n, k = 130, 72, 48
     check_case(ctx, 0, ta, 0, m, n, k, 1.25, 0.5, lda=lda, ldb=k, ldc=m)

@@ -193,14 +193,15 @@ __device__ __forceinline__ int kc_swz(int row) { return row & 7; }
 // KC: k-contiguous in memory, staged [row][k] (row stride BK, chunks
 //     swizzled by kc_swz).
 // !KC: row-contiguous in memory, staged [k][row] (row stride BT).
-template <typename T, int BT, bool KC, bool VEC>
+template <typename T, int BT, bool KC, bool VEC, int NT = kThreads>
 struct Stager {
   typedef typename Ty<T>::v16 V;
   static constexpr int VW = Ty<T>::VW;
   static constexpr int BK = 128 / (int)sizeof(T);
-  static constexpr int LOADS = BT / 32;      // 16-byte vectors per thread
+  static constexpr int LOADS = BT * 8 / NT;  // 16-byte vectors per thread (NT threads)
   static constexpr int VPK = BT / VW;        // vectors per k-row (!KC)
-  static constexpr int KROWS = kThreads / VPK;  // k-rows per load step (!KC)
+  static constexpr int KROWS = NT / VPK;     // k-rows per load step (!KC)
+  static constexpr int RPS = NT / 8;         // rows per load step (KC: 8 chunks per row)
   static constexpr int LDK = BK;
   static constexpr int LDM = BT;
   static constexpr int ELEMS = KC ? BT * LDK : BK * LDM;
@@ -241,10 +242,10 @@ struct Stager {
       row_first = row0 + row;
       k_first = kv * VW;
       base = P + (row0 + row) * ld + kv * VW;
-      r_step = 32 * ld;
+      r_step = RPS * ld;
       k_step = BK;
-      lds_off = row * LDK + (kv ^ kc_swz(row)) * VW;  // kc_swz(row + 32 r) == kc_swz(row)
-      lds_r_step = 32 * LDK;
+      lds_off = row * LDK + (kv ^ kc_swz(row)) * VW;  // kc_swz(row + RPS r) == kc_swz(row)
+      lds_r_step = RPS * LDK;
       // An LDS copy puts lane t at chunk t % 8 of the row, so that lane
       // reads the chunk the swizzle places there instead.
       copy_shift = ((kv ^ kc_swz(row)) - kv) * VW;
@@ -272,9 +273,9 @@ struct Stager {
   __device__ void init_edge() {
     const int64_t valid = rows_total - row_first;  // rows of this thread in range (may be <= 0)
     if (KC) {
-      const int64_t n = valid <= 0 ? 0 : (valid + 31) / 32;
+      const int64_t n = valid <= 0 ? 0 : (valid + RPS - 1) / RPS;
       nvr = (int)(n < LOADS ? n : LOADS);
-      fb = base + (rows_total - 1 - row_first) * (r_step / 32);
+      fb = base + (rows_total - 1 - row_first) * (r_step / RPS);
     } else {
       vok = valid > 0;
       fb = base + (rows_total - 1 - row_first);
@@ -592,23 +593,27 @@ __device__ __forceinline__ void copies_landed_sync() {
   __syncthreads();
 }
 
-// One BT x BT tile (tm, tn) of C over k-tiles [kt0, kt0 + nkt): the main
+// One BTM x BTN tile (tm, tn) of C over k-tiles [kt0, kt0 + nkt): the main
 // loop and the epilogue (unit >= 0: a split-k unit's raw partial to ws).
-template <typename T, int BT, bool AKC, bool BKC, bool VEC>
+// NT threads: 256 (2 x 2 waves) or 512 (4 x 2 waves); every wave owns a
+// square WT x WT part of the tile.
+template <typename T, int BTM, int BTN, int NT, bool AKC, bool BKC, bool VEC>
 __device__ __forceinline__ void gemm_tile(const GemmArgs<T> &p, int tm, int tn, int unit, int kt0,
                                           int nkt, T *smem, const int t) {
   typedef typename Ty<T>::acc Acc;
   typedef typename Ty<T>::v16 V;
   constexpr int VW = Ty<T>::VW;
   constexpr int BK = 128 / (int)sizeof(T);
-  constexpr int WT = BT / 2;
+  constexpr int WGM = NT == 512 ? 4 : 2;  // waves along m
+  constexpr int WT = BTM / WGM;
+  static_assert(WT == BTN / (NT / 64 / WGM), "square wave tiles");
   constexpr int MB = WT / 16;
-  typedef Stager<T, BT, AKC, VEC> SA;
-  typedef Stager<T, BT, BKC, VEC> SB;
+  typedef Stager<T, BTM, AKC, VEC, NT> SA;
+  typedef Stager<T, BTN, BKC, VEC, NT> SB;
   constexpr int STAGE = SA::ELEMS + SB::ELEMS;
-  const int64_t m0 = (int64_t)tm * BT, n0 = (int64_t)tn * BT;
+  const int64_t m0 = (int64_t)tm * BTM, n0 = (int64_t)tn * BTN;
   const int lane = t & 63, wave = t >> 6;
-  const int wm = (wave & 1) * WT, wn = (wave >> 1) * WT;
+  const int wm = (wave % WGM) * WT, wn = (wave / WGM) * WT;
 
   // k-tiles are counted from kt0 below: the stagers start at k = kt0 BK and
   // see K - kt0 BK columns.
@@ -618,7 +623,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs<T> &p, int tm, int tn, 
   sb.init(p.B, p.ldb, n0, t, p.n, p.k);
   sa.advance(kt0);
   sb.advance(kt0);
-  const bool interior = (m0 + BT <= p.m) && (n0 + BT <= p.n);
+  const bool interior = (m0 + BTM <= p.m) && (n0 + BTN <= p.n);
   const int nkt_full = (int)(p.k / BK) - kt0;  // whole k-tiles from kt0
 
   Acc acc[MB][MB];
@@ -679,8 +684,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs<T> &p, int tm, int tn, 
       if (1 < nkt) fill(1);
       copies_landed_sync();
       T x[4][MB], y[4][MB], xb[4][MB], yb[4][MB];
-      fetch_operands<T, BT, AKC, MB>(smem, wm, 0, lane, x);
-      fetch_operands<T, BT, BKC, MB>(smem + SA::ELEMS, wn, 0, lane, xb);
+      fetch_operands<T, BTM, AKC, MB>(smem, wm, 0, lane, x);
+      fetch_operands<T, BTN, BKC, MB>(smem + SA::ELEMS, wn, 0, lane, xb);
       // Steady state (tile kt+2 exists and is whole): branch-free, with the
       // LDS reads and copies spread among the MFMAs (sched_group_barrier) so
       // that neither wave on a SIMD sits in a long non-MFMA stretch.
@@ -689,8 +694,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs<T> &p, int tm, int tn, 
       for (; kt < nsteady; ++kt) {
         T *cur = smem + (kt & 1) * STAGE;
         const T *nxt = smem + ((kt + 1) & 1) * STAGE;
-        fetch_operands<T, BT, AKC, MB>(cur, wm, 16, lane, y);
-        fetch_operands<T, BT, BKC, MB>(cur + SA::ELEMS, wn, 16, lane, yb);
+        fetch_operands<T, BTM, AKC, MB>(cur, wm, 16, lane, y);
+        fetch_operands<T, BTN, BKC, MB>(cur + SA::ELEMS, wn, 16, lane, yb);
   #pragma unroll
         for (int s = 0; s < 4; ++s)
   #pragma unroll
@@ -710,8 +715,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs<T> &p, int tm, int tn, 
         __builtin_amdgcn_sched_barrier(0);
         sa.template load_lds<EDGE, kScalarBase>(cur, kt + 2, wave);
         sb.template load_lds<EDGE, kScalarBase>(cur + SA::ELEMS, kt + 2, wave);
-        fetch_operands<T, BT, AKC, MB>(nxt, wm, 0, lane, x);
-        fetch_operands<T, BT, BKC, MB>(nxt + SA::ELEMS, wn, 0, lane, xb);
+        fetch_operands<T, BTM, AKC, MB>(nxt, wm, 0, lane, x);
+        fetch_operands<T, BTN, BKC, MB>(nxt + SA::ELEMS, wn, 0, lane, xb);
   #pragma unroll
         for (int s = 0; s < 4; ++s)
   #pragma unroll
@@ -733,8 +738,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs<T> &p, int tm, int tn, 
       for (; kt < nkt; ++kt) {
         T *cur = smem + (kt & 1) * STAGE;
         const T *nxt = smem + ((kt + 1) & 1) * STAGE;
-        fetch_operands<T, BT, AKC, MB>(cur, wm, 16, lane, y);
-        fetch_operands<T, BT, BKC, MB>(cur + SA::ELEMS, wn, 16, lane, yb);
+        fetch_operands<T, BTM, AKC, MB>(cur, wm, 16, lane, y);
+        fetch_operands<T, BTN, BKC, MB>(cur + SA::ELEMS, wn, 16, lane, yb);
   #pragma unroll
         for (int s = 0; s < 4; ++s)
   #pragma unroll
@@ -744,8 +749,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs<T> &p, int tm, int tn, 
         copies_landed_sync();
         if (kt + 2 < nkt) fill(kt + 2);
         if (kt + 1 < nkt) {
-          fetch_operands<T, BT, AKC, MB>(nxt, wm, 0, lane, x);
-          fetch_operands<T, BT, BKC, MB>(nxt + SA::ELEMS, wn, 0, lane, xb);
+          fetch_operands<T, BTM, AKC, MB>(nxt, wm, 0, lane, x);
+          fetch_operands<T, BTN, BKC, MB>(nxt + SA::ELEMS, wn, 0, lane, xb);
         }
   #pragma unroll
         for (int s = 0; s < 4; ++s)
@@ -784,8 +789,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs<T> &p, int tm, int tn, 
       if (1 < nkt) fill(1);
       copies_landed_sync();
       T a[2][MB], b[2][MB];
-      fetch_step<T, BT, AKC, MB>(smem, wm, 0, 0, lane, a[0]);
-      fetch_step<T, BT, BKC, MB>(smem + SA::ELEMS, wn, 0, 0, lane, b[0]);
+      fetch_step<T, BTM, AKC, MB>(smem, wm, 0, 0, lane, a[0]);
+      fetch_step<T, BTN, BKC, MB>(smem + SA::ELEMS, wn, 0, 0, lane, b[0]);
       // One k-tile; TAIL: tile kt+2 may be missing or partial (the last two
       // k-tiles), otherwise it is whole and the loop body is branch-free.
       auto tile = [&](int kt, auto tail_tag) {
@@ -796,8 +801,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs<T> &p, int tm, int tn, 
         for (int s = 0; s < 4; ++s) {
           const int u = s & 1, w = u ^ 1;
           if (s < 3) {
-            fetch_step<T, BT, AKC, MB>(cur, wm, 0, s + 1, lane, a[w]);
-            fetch_step<T, BT, BKC, MB>(cur + SA::ELEMS, wn, 0, s + 1, lane, b[w]);
+            fetch_step<T, BTM, AKC, MB>(cur, wm, 0, s + 1, lane, a[w]);
+            fetch_step<T, BTN, BKC, MB>(cur + SA::ELEMS, wn, 0, s + 1, lane, b[w]);
           } else {
             __builtin_amdgcn_sched_barrier(0);
             copies_landed_sync();
@@ -809,8 +814,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs<T> &p, int tm, int tn, 
               sb.template load_lds<EDGE, kScalarBase>(cur + SA::ELEMS, kt + 2, wave);
             }
             if (!TAIL || kt + 1 < nkt) {
-              fetch_step<T, BT, AKC, MB>(nxt, wm, 0, 0, lane, a[w]);
-              fetch_step<T, BT, BKC, MB>(nxt + SA::ELEMS, wn, 0, 0, lane, b[w]);
+              fetch_step<T, BTM, AKC, MB>(nxt, wm, 0, 0, lane, a[w]);
+              fetch_step<T, BTN, BKC, MB>(nxt + SA::ELEMS, wn, 0, 0, lane, b[w]);
             }
           }
   #pragma unroll
@@ -855,8 +860,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs<T> &p, int tm, int tn, 
     #pragma unroll
             for (int s = 0; s < 4; ++s) {
               T a[MB], b[MB];
-              fetch_step<T, BT, AKC, MB>(As, wm, kc, s, lane, a);
-              fetch_step<T, BT, BKC, MB>(Bs, wn, kc, s, lane, b);
+              fetch_step<T, BTM, AKC, MB>(As, wm, kc, s, lane, a);
+              fetch_step<T, BTN, BKC, MB>(Bs, wn, kc, s, lane, b);
     #pragma unroll
               for (int i = 0; i < MB; ++i)
     #pragma unroll
@@ -895,8 +900,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs<T> &p, int tm, int tn, 
         }
         __syncthreads();
         T x[4][MB], y[4][MB], xb[4][MB], yb[4][MB];
-        fetch_operands<T, BT, AKC, MB>(smem, wm, 0, lane, x);
-        fetch_operands<T, BT, BKC, MB>(smem + SA::ELEMS, wn, 0, lane, xb);
+        fetch_operands<T, BTM, AKC, MB>(smem, wm, 0, lane, x);
+        fetch_operands<T, BTN, BKC, MB>(smem + SA::ELEMS, wn, 0, lane, xb);
         // Steady state (both next tiles exist and are whole): the same steps
         // without branches, with the chunk-1 reads, the LDS stores and the
         // global loads spread among the chunk-0 MFMAs (sched_group_barrier:
@@ -908,8 +913,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs<T> &p, int tm, int tn, 
         for (; kt < nsteady; ++kt) {
           const T *As = smem + (kt & 1) * STAGE;
           T *next = smem + ((kt + 1) & 1) * STAGE;
-          fetch_operands<T, BT, AKC, MB>(As, wm, 16, lane, y);
-          fetch_operands<T, BT, BKC, MB>(As + SA::ELEMS, wn, 16, lane, yb);
+          fetch_operands<T, BTM, AKC, MB>(As, wm, 16, lane, y);
+          fetch_operands<T, BTN, BKC, MB>(As + SA::ELEMS, wn, 16, lane, yb);
     #pragma unroll
           for (int s = 0; s < 4; ++s)
     #pragma unroll
@@ -946,8 +951,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs<T> &p, int tm, int tn, 
             __builtin_amdgcn_sched_group_barrier(kSchedVmemRead, 1, 0);
           }
           __syncthreads();
-          fetch_operands<T, BT, AKC, MB>(next, wm, 0, lane, x);
-          fetch_operands<T, BT, BKC, MB>(next + SA::ELEMS, wn, 0, lane, xb);
+          fetch_operands<T, BTM, AKC, MB>(next, wm, 0, lane, x);
+          fetch_operands<T, BTN, BKC, MB>(next + SA::ELEMS, wn, 0, lane, xb);
     #pragma unroll
           for (int s = 0; s < 4; ++s)
     #pragma unroll
@@ -959,8 +964,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs<T> &p, int tm, int tn, 
         for (; kt < nkt; ++kt) {
           const bool more = kt + 1 < nkt;
           const T *As = smem + (kt & 1) * STAGE;
-          fetch_operands<T, BT, AKC, MB>(As, wm, 16, lane, y);
-          fetch_operands<T, BT, BKC, MB>(As + SA::ELEMS, wn, 16, lane, yb);
+          fetch_operands<T, BTM, AKC, MB>(As, wm, 16, lane, y);
+          fetch_operands<T, BTN, BKC, MB>(As + SA::ELEMS, wn, 16, lane, yb);
     #pragma unroll
           for (int s = 0; s < 4; ++s)
     #pragma unroll
@@ -983,8 +988,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs<T> &p, int tm, int tn, 
           }
           __syncthreads();
           if (more) {
-            fetch_operands<T, BT, AKC, MB>(next, wm, 0, lane, x);
-            fetch_operands<T, BT, BKC, MB>(next + SA::ELEMS, wn, 0, lane, xb);
+            fetch_operands<T, BTM, AKC, MB>(next, wm, 0, lane, x);
+            fetch_operands<T, BTN, BKC, MB>(next + SA::ELEMS, wn, 0, lane, xb);
           }
     #pragma unroll
           for (int s = 0; s < 4; ++s)
@@ -1004,13 +1009,13 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs<T> &p, int tm, int tn, 
   // Epilogue: C = alpha*acc + beta*C on the tile's in-range (and, for
   // sgemmtr/ssyrk, in-triangle) elements.
   if (unit >= 0) {
-    // Split-k unit: raw partial sums of the whole BT x BT tile (rows and
+    // Split-k unit: raw partial sums of the whole BTM x BTN tile (rows and
     // columns past m, n hold zeros from the zero-filled operand loads).
-    T *slice = p.ws + (int64_t)unit * BT * BT;
+    T *slice = p.ws + (int64_t)unit * BTM * BTN;
     if constexpr (!AKC || sizeof(T) == 4) {
       GemmArgs<T> q = p;
       q.C = slice;
-      q.ldc = BT;
+      q.ldc = BTM;
       q.alpha = (T)1;
       q.beta = (T)0;
       epilogue_vec<T, AKC, BKC, MB>(q, acc, wm, wn, lane);
@@ -1022,7 +1027,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs<T> &p, int tm, int tn, 
 #pragma unroll
           for (int q = 0; q < 4; ++q)
             slice[(wm + out_row<T, AKC, MB>(i, q, lane)) +
-                  (int64_t)(wn + out_col<BKC, MB, VW>(j, lane)) * BT] = acc[i][j][q];
+                  (int64_t)(wn + out_col<BKC, MB, VW>(j, lane)) * BTM] = acc[i][j][q];
     }
     return;
   }
@@ -1090,7 +1095,7 @@ __global__ __launch_bounds__(kThreads, (sizeof(T) == 8 || AKC != BKC) ? 2 : 1) v
     // (nkt >= 1: k > 0 here, and the host never plans an empty split; an
     // explicit nkt check costs the fp32 loop ~60 VGPRs of scheduling freedom.)
     if (tm < 0 || tn < 0 || tm >= p.tiles_m || tn >= p.tiles_n) return;  // block-uniform
-    gemm_tile<T, BT, AKC, BKC, VEC>(p, tm, tn, unit, kt0, nkt, smem, (int)threadIdx.x);
+    gemm_tile<T, BT, BT, kThreads, AKC, BKC, VEC>(p, tm, tn, unit, kt0, nkt, smem, (int)threadIdx.x);
   } else {
     const int nkt_all = (int)((p.k + BK - 1) / BK);
     const bool on_rows = p.band == wgb::kBandALower || p.band == wgb::kBandAUpper;
@@ -1121,7 +1126,7 @@ __global__ __launch_bounds__(kThreads, (sizeof(T) == 8 || AKC != BKC) ? 2 : 1) v
       // out of this loop and held in registers across both tiles.
       int t = (int)threadIdx.x;
       asm volatile("" : "+v"(t));
-      gemm_tile<T, BT, AKC, BKC, VEC>(p, tm, tn, -1, lo, hi - lo, smem, t);
+      gemm_tile<T, BT, BT, kThreads, AKC, BKC, VEC>(p, tm, tn, -1, lo, hi - lo, smem, t);
     }
   }
 }
@@ -1257,6 +1262,28 @@ const void *small_kernel_for(int64_t k) {
   if (nch <= kSmallWaves) return reinterpret_cast<const void *>(gemm_small_kernel<AKC, BKC, 1>);
   if (nch <= 2 * kSmallWaves) return reinterpret_cast<const void *>(gemm_small_kernel<AKC, BKC, 2>);
   return reinterpret_cast<const void *>(gemm_small_kernel<AKC, BKC, 4>);
+}
+
+// fp32 with op(B) k-contiguous (NN, TN) and 16-byte aligned operands on
+// large problems: 256 x 128 tiles, 512 threads (4 x 2 waves, each the same
+// 64 x 64 wave tile and loop as the 128 tier), one block per CU (96 KB of
+// LDS). A quarter fewer operand bytes per flop than two 128 x 128 blocks;
+// measured at 8192^3 (A/B on one box): NN 146.0 -> 147.0, TN 142.9 -> 147.8
+// TFLOP/s, while NT and TT ran 1% slower and keep the 128 tier. Full C
+// only, no split-k (the host sends shapes whose last round is over half
+// full; the rest take the 128 tier).
+constexpr int kWideThreads = 512;
+constexpr int kWideM = 256, kWideN = 128;
+template <bool AKC>
+__global__ __launch_bounds__(kWideThreads, 1) void gemm_wide_kernel(GemmArgs<float> p) {
+  typedef Stager<float, kWideM, AKC, true, kWideThreads> SA;
+  typedef Stager<float, kWideN, true, true, kWideThreads> SB;
+  __shared__ __attribute__((aligned(16))) float smem[2 * (SA::ELEMS + SB::ELEMS)];
+  int tm, tn;
+  logical_tile(xcd_remap(blockIdx.x, p.ntiles), p.tiles_m, p.tiles_n, 0, tm, tn);
+  const int nkt = (int)((p.k + 31) / 32);
+  gemm_tile<float, kWideM, kWideN, kWideThreads, AKC, true, true>(p, tm, tn, -1, 0, nkt, smem,
+                                                                 (int)threadIdx.x);
 }
 
 // C <- beta*C (or 0 when beta == 0) on the uplo part of the m x n C: the
@@ -1506,11 +1533,33 @@ int gemm_launch(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64
   }
   // VEC: 16-byte aligned operand vectors. That path copies k-tiles straight
   // into LDS with 32-bit lane offsets from the tile origin, which stay below
-  // BT * ld * sizeof(T); larger leading dimensions take the element-aligned
-  // register path (same results, same loads).
+  // 256 * ld * sizeof(T) (the widest tile); larger leading dimensions take
+  // the element-aligned register path (same results, same loads).
   const int64_t off_cap = (int64_t)1 << 31;
-  const bool offs32 = 128 * lda * (int64_t)sizeof(T) < off_cap && 128 * ldb * (int64_t)sizeof(T) < off_cap;
+  const bool offs32 = 256 * lda * (int64_t)sizeof(T) < off_cap && 256 * ldb * (int64_t)sizeof(T) < off_cap;
   const bool vec = (lda % VW == 0) && (ldb % VW == 0) && aligned16(A) && aligned16(B) && offs32;
+  if constexpr (sizeof(T) == 4) {
+    // The 256 x 128 tier: at least two full rounds of one block per CU and a
+    // last round over half full.
+    const int64_t twm = (m + kWideM - 1) / kWideM, twn = (n + kWideN - 1) / kWideN;
+    const int64_t tw = twm * twn;
+    if (vec && bkc && uplo == 0 && band == wgb::kBandNone && tw >= 2 * fill &&
+        (tw % fill == 0 || 2 * (tw % fill) > fill) && tw <= INT32_MAX) {
+      a.tiles_m = (int)twm;
+      a.tiles_n = (int)twn;
+      a.ntiles = (int)tw;
+      a.nregular = a.ntiles;
+      a.splits = 1;
+      a.kt_split = (int)((k + 31) / 32);
+      a.ws = nullptr;
+      void *args[] = {&a};
+      const void *fn = akc ? reinterpret_cast<const void *>(gemm_wide_kernel<true>)
+                           : reinterpret_cast<const void *>(gemm_wide_kernel<false>);
+      WGB_CHECK_HIP(hipLaunchKernel(fn, dim3((unsigned)tw), dim3(kWideThreads), args, 0, ctx->stream));
+      WGB_CHECK_LAUNCH("gemm_wide_kernel");
+      return WGB_OK;
+    }
+  }
   // Large tier once the 128-tiles alone fill the chip; small tier otherwise.
   auto count = [&](int64_t bt, int64_t &tmn, int64_t &tnn) {
     tmn = (m + bt - 1) / bt;

@@ -9,11 +9,14 @@
 // v_mfma_f64_16x16x4f64 for fp64, one template for both.
 //
 // Block: 256 threads = 4 waves in a 2x2 grid, block tile BT x BT of C
-// (BT = 128 large tier, 64 small tier), k-tile BK = 128 bytes of k
-// (32 floats / 16 doubles). Each operand tile is staged in LDS, double
-// buffered, in the orientation it has in memory so the global->LDS path is
-// plain 16-byte copies (for fp32 with 16-byte aligned operands, copies made
-// by global_load_lds_dwordx4 without passing through registers):
+// (BT = 128 large tier, 64 small tier; fp32 NN / TN layouts on large
+// problems: 256 x 128 tiles with 512 threads in a 4x2 grid), k-tile BK =
+// 128 bytes of k (32 floats / 16 doubles); tiny fp32 problems take a
+// one-launch kernel of 32x32 tiles (gemm_small_kernel). Each operand tile is
+// staged in LDS, double buffered, in the orientation it has in memory so the
+// global->LDS path is plain 16-byte copies (for 16-byte aligned operands,
+// copies made by global_load_lds_dwordx4 without passing through
+// registers):
 //   * k-contiguous operands (op(A) with A transposed, op(B) with B not
 //     transposed) are stored [row][k], 128-byte rows whose eight 16-byte
 //     chunks are XOR-swizzled by row (kc_swz) so that both the stores and

@@ -329,3 +329,29 @@ def test_dgemm_ieee_specials(ctx):
         fin = np.isfinite(ref)
         assert np.array_equal(got[~fin & ~np.isnan(ref)], ref[~fin & ~np.isnan(ref)])
         assert np.allclose(got[fin], ref[fin], rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("shape,ta,tb", [((512, 512, 512), 0, 0), ((1024, 1100, 300), 1, 0),
+                                         ((1024, 1100, 300), 0, 1), ((4096, 4096, 64), 1, 0)])
+def test_sgemm_ieee_specials_every_tier(ctx, shape, ta, tb):
+    # NaN / Inf planted in A and B reach C as in real arithmetic on every
+    # path (one-launch small kernel, the 128 tier's LDS copies, the wide
+    # tier): the NaN / Inf pattern of C equals the long-double oracle's
+    m, n, k = shape
+    lda, ldb = (k if ta else m), (n if tb else k)
+    A = orc.random_f32(lda * (m if ta else k), -1, 1, 21)
+    B = orc.random_f32(ldb * (k if tb else n), -1, 1, 22)
+    C = orc.random_f32(m * n, -1, 1, 23)
+    at_a = lambda i, kk: (kk + i * lda) if ta else (i + kk * lda)   # op(A)(i, kk)
+    at_b = lambda kk, j: (j + kk * ldb) if tb else (kk + j * ldb)   # op(B)(kk, j)
+    A[at_a(m // 3, k // 2)] = np.nan
+    A[at_a(m - 1, 1)] = -np.inf
+    B[at_b(k - 1, n // 5)] = np.inf
+    got = run_gemm(ctx, 0, ta, tb, m, n, k, 1.5, A, lda, B, ldb, 0.5, C, m)
+    ref, _ = orc.gemm_ld(0, ta, tb, m, n, k, 1.5, A.astype(np.float64), lda, B.astype(np.float64),
+                         ldb, 0.5, C.astype(np.float64), m)
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    assert np.array_equal(np.isinf(got), np.isinf(ref))
+    inf = np.isinf(ref)
+    assert np.array_equal(np.sign(got[inf]), np.sign(ref[inf]))
+    assert np.isnan(got).any() and inf.any()

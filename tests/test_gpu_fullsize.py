@@ -1,4 +1,7 @@
-"""Parity at the BASELINE configurations' full sizes.
+"""Parity at the full sizes of the benchmark configurations (wgblas's
+benchmarks/*/wgblas/*.js: sgemm 512^3, sgemm 8192^3 in all four layouts,
+the ragged 8191 x 8193 x 4097 case, dgemm 4096^3, ten chained ssyrk calls at
+8192 x 4096; the reductions' full sizes are in test_gpu_level1.py).
 
 The inputs are the seeded device-generated ones bench.py times (their
 generator is pinned bit-for-bit to the oracle in test_gpu_level1.py). At

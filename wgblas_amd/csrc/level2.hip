@@ -5,7 +5,8 @@
 //
 // Both forms read A once and are HBM-bound.
 //   N: a lane owns 4 consecutive rows in each of kGroupsN 1024-row groups
-//      (a 16-byte load per group and column, kStepN columns per step); the
+//      (a 16-byte load per group and column, kStepN columns per step), and a
+//      block walks a long run of columns (few, deep blocks); the
 //      columns are walked in order and a column whose x entry is zero is
 //      skipped, as reference BLAS does for this form (so 0 * Inf or 0 * NaN
 //      in that column never reaches y).
@@ -28,12 +29,19 @@ using wgb::fail;
 
 constexpr int kThreads = 256;
 constexpr int kColsPerWave = 8;    // T form
-// N form: columns loaded per step and 1024-row groups per block. Measured
-// at 16384^2 on MI355X: 4 x 4 streams 3% faster than 8 x 2 (more waves
-// resident), 2 or 16 columns per step and 1 group slower.
-constexpr int kStepN = 4;
-constexpr int kGroupsN = 4;
-constexpr int kTargetBlocks = 2048;  // blocks that keep HBM streaming
+// N form: columns loaded per step, 1024-row groups per block, the blocks
+// aimed for and the fewest columns per split. Measured on MI355X over
+// 2048 x 65536, 8192^2, 16384^2, 32768^2 and 65536 x 2048 (sweep of 1 or 2
+// groups, 256 / 512 / 1024 target blocks, 256 or 512 columns): one group,
+// 8 columns per step, about 256 blocks of at least 256 columns each gave
+// the best geometric mean, 5.92 TB/s against 5.06 for 4 groups x 4 columns
+// with 2048 blocks of 64 columns (16384^2: 6.24 against 5.77 TB/s); fewer
+// splits also mean fewer partial sums to write and fold.
+constexpr int kStepN = 8;
+constexpr int kGroupsN = 1;
+constexpr int kTargetBlocksN = 256;
+constexpr int kMinColsN = 256;
+constexpr int kTargetBlocks = 2048;  // T form: blocks that keep HBM streaming
 
 int64_t imax(int64_t a, int64_t b) { return a > b ? a : b; }
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
@@ -278,11 +286,12 @@ extern "C" int wgb_sgemv(wgb_ctx *ctx, int trans, int64_t m, int64_t n, float al
   }
   const bool vecA = lda % 4 == 0 && aligned16(A);
   // blocks along the output; split the contraction dimension until about
-  // kTargetBlocks blocks stream A (N: >= 64 columns per split; T: >= 256
+  // the target block count streams A (N: >= kMinColsN columns per split; T: >= 256
   // rows, a multiple of 256 so every split starts 16-byte aligned)
   const int64_t bx = nt ? cdiv(m, 4 * kThreads * kGroupsN) : cdiv(cdiv(n, kColsPerWave), kThreads / 64);
-  int64_t want = bx >= kTargetBlocks ? 1 : cdiv(kTargetBlocks, bx);
-  const int64_t most = nt ? cdiv(n, 64) : cdiv(m, 256);
+  const int64_t target = nt ? kTargetBlocksN : kTargetBlocks;
+  int64_t want = bx >= target ? 1 : cdiv(target, bx);
+  const int64_t most = nt ? cdiv(n, kMinColsN) : cdiv(m, 256);
   if (want > most) want = most;
   if (want > 65535) want = 65535;  // grid y limit
   if (want < 1) want = 1;

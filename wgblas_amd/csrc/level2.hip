@@ -10,8 +10,9 @@
 //      columns are walked in order and a column whose x entry is zero is
 //      skipped, as reference BLAS does for this form (so 0 * Inf or 0 * NaN
 //      in that column never reaches y).
-//   T: a wave owns 8 columns and walks the rows 512 at a time (2 x 4 per
-//      lane, 16-byte loads), keeping each x chunk in registers for all 8 columns;
+//   T: a wave owns 8 columns (4 for short columns) and walks the rows 512
+//      at a time (2 x 4 per lane, 16-byte loads), keeping each x chunk in
+//      registers for all of its columns;
 //      the dot products are folded with wave shuffles. No zero skipping: the
 //      dot-product form of reference BLAS takes every term.
 // When the output alone gives too few blocks to stream HBM, the contraction
@@ -28,7 +29,13 @@ namespace {
 using wgb::fail;
 
 constexpr int kThreads = 256;
-constexpr int kColsPerWave = 8;    // T form
+// T form: columns per wave. 8 (x reused from registers for 8 columns);
+// columns of at most kShortColsRows rows take 4, which gives twice the
+// waves: measured on MI355X at 2048 x 65536, 4.8 -> 6.4 TB/s, while 4 was
+// slower at 8192^2 (5.3 -> 4.8) and even at 16384^2 and 32768^2.
+constexpr int kColsPerWave = 8;
+constexpr int kColsPerWaveShort = 4;
+constexpr int64_t kShortColsRows = 4096;
 // N form: columns loaded per step, 1024-row groups per block, the blocks
 // aimed for and the fewest columns per split. Measured on MI355X over
 // 2048 x 65536, 8192^2, 16384^2, 32768^2 and 65536 x 2048 (sweep of 1 or 2
@@ -143,11 +150,11 @@ __global__ __launch_bounds__(kThreads) void gemv_n_kernel(int64_t m, int64_t n,
   }
 }
 
-// T form. Wave w (4 per block) owns columns [8w, 8w + 8) of split s, rows
+// T form. Wave w (4 per block) owns columns [CPW w, CPW w + CPW) of split s, rows
 // [s*rps, min(m, (s+1)*rps)). VEC: lda % 4 == 0, A 16-byte aligned, incx == 1
 // and x 16-byte aligned (rps is a multiple of 4, so every 4-row group of a
 // split starts 16-byte aligned).
-template <bool VEC>
+template <bool VEC, int CPW>
 __global__ __launch_bounds__(kThreads) void gemv_t_kernel(int64_t m, int64_t n,
                                                           const float *__restrict__ A, int64_t lda,
                                                           const float *__restrict__ x, int64_t incx,
@@ -155,35 +162,35 @@ __global__ __launch_bounds__(kThreads) void gemv_t_kernel(int64_t m, int64_t n,
                                                           float alpha, float beta,
                                                           float *__restrict__ y, int64_t incy) {
   const int lane = threadIdx.x & 63;
-  const int64_t col0 = ((int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6)) * kColsPerWave;
+  const int64_t col0 = ((int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6)) * CPW;
   if (col0 >= n) return;  // wave-uniform
   const int64_t r0 = (int64_t)blockIdx.y * rps;
   const int64_t r1 = r0 + rps < m ? r0 + rps : m;
   // columns past n repeat column n-1 (in bounds) and are never stored
-  const float *col[kColsPerWave];
+  const float *col[CPW];
 #pragma unroll
-  for (int c = 0; c < kColsPerWave; ++c) col[c] = A + (col0 + c < n ? col0 + c : n - 1) * lda;
-  float acc[kColsPerWave];
+  for (int c = 0; c < CPW; ++c) col[c] = A + (col0 + c < n ? col0 + c : n - 1) * lda;
+  float acc[CPW];
 #pragma unroll
-  for (int c = 0; c < kColsPerWave; ++c) acc[c] = 0.f;
+  for (int c = 0; c < CPW; ++c) acc[c] = 0.f;
   int64_t i = r0 + 4 * lane;
   if (VEC) {
     // two 256-row groups per step: 16 loads of A in flight per lane
     for (; i + 256 + 4 <= r1; i += 512) {
       const f4 xv0 = *reinterpret_cast<const f4 *>(x + i);
       const f4 xv1 = *reinterpret_cast<const f4 *>(x + i + 256);
-      f4 av0[kColsPerWave], av1[kColsPerWave];
+      f4 av0[CPW], av1[CPW];
 #pragma unroll
-      for (int c = 0; c < kColsPerWave; ++c) {
+      for (int c = 0; c < CPW; ++c) {
         av0[c] = ld_nt(col[c] + i);
         av1[c] = ld_nt(col[c] + i + 256);
       }
 #pragma unroll
-      for (int c = 0; c < kColsPerWave; ++c)
+      for (int c = 0; c < CPW; ++c)
 #pragma unroll
         for (int q = 0; q < 4; ++q) acc[c] = fmaf(av0[c][q], xv0[q], acc[c]);
 #pragma unroll
-      for (int c = 0; c < kColsPerWave; ++c)
+      for (int c = 0; c < CPW; ++c)
 #pragma unroll
         for (int q = 0; q < 4; ++q) acc[c] = fmaf(av1[c][q], xv1[q], acc[c]);
     }
@@ -191,11 +198,11 @@ __global__ __launch_bounds__(kThreads) void gemv_t_kernel(int64_t m, int64_t n,
   for (; i < r1; i += 256) {
     if (VEC && i + 4 <= r1) {
       const f4 xv = *reinterpret_cast<const f4 *>(x + i);
-      f4 av[kColsPerWave];
+      f4 av[CPW];
 #pragma unroll
-      for (int c = 0; c < kColsPerWave; ++c) av[c] = ld_nt(col[c] + i);
+      for (int c = 0; c < CPW; ++c) av[c] = ld_nt(col[c] + i);
 #pragma unroll
-      for (int c = 0; c < kColsPerWave; ++c)
+      for (int c = 0; c < CPW; ++c)
 #pragma unroll
         for (int q = 0; q < 4; ++q) acc[c] = fmaf(av[c][q], xv[q], acc[c]);
     } else {
@@ -203,19 +210,19 @@ __global__ __launch_bounds__(kThreads) void gemv_t_kernel(int64_t m, int64_t n,
       for (int q = 0; q < cnt; ++q) {
         const float xv = x[(i + q) * incx];
 #pragma unroll
-        for (int c = 0; c < kColsPerWave; ++c) acc[c] = fmaf(col[c][i + q], xv, acc[c]);
+        for (int c = 0; c < CPW; ++c) acc[c] = fmaf(col[c][i + q], xv, acc[c]);
       }
     }
   }
 #pragma unroll
-  for (int c = 0; c < kColsPerWave; ++c) {
+  for (int c = 0; c < CPW; ++c) {
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) acc[c] += __shfl_xor(acc[c], off, 64);
   }
-  if (lane < kColsPerWave && col0 + lane < n) {
+  if (lane < CPW && col0 + lane < n) {
     float v = acc[0];
 #pragma unroll
-    for (int c = 1; c < kColsPerWave; ++c) v = lane == c ? acc[c] : v;
+    for (int c = 1; c < CPW; ++c) v = lane == c ? acc[c] : v;
     if (part)
       part[(int64_t)blockIdx.y * n + col0 + lane] = v;
     else
@@ -288,7 +295,8 @@ extern "C" int wgb_sgemv(wgb_ctx *ctx, int trans, int64_t m, int64_t n, float al
   // blocks along the output; split the contraction dimension until about
   // the target block count streams A (N: >= kMinColsN columns per split; T: >= 256
   // rows, a multiple of 256 so every split starts 16-byte aligned)
-  const int64_t bx = nt ? cdiv(m, 4 * kThreads * kGroupsN) : cdiv(cdiv(n, kColsPerWave), kThreads / 64);
+  const int cpw = m <= kShortColsRows ? kColsPerWaveShort : kColsPerWave;  // T form
+  const int64_t bx = nt ? cdiv(m, 4 * kThreads * kGroupsN) : cdiv(cdiv(n, cpw), kThreads / 64);
   const int64_t target = nt ? kTargetBlocksN : kTargetBlocks;
   int64_t want = bx >= target ? 1 : cdiv(target, bx);
   const int64_t most = nt ? cdiv(n, kMinColsN) : cdiv(m, 256);
@@ -316,12 +324,13 @@ extern "C" int wgb_sgemv(wgb_ctx *ctx, int trans, int64_t m, int64_t n, float al
     WGB_CHECK_LAUNCH("gemv_n_kernel");
   } else {
     const bool vec = vecA && incx == 1 && aligned16(x);
-    if (vec)
-      gemv_t_kernel<true><<<grid, kThreads, 0, ctx->stream>>>(m, n, A, lda, x, incx, per, part,
-                                                               alpha, beta, y, incy);
+    auto launch = [&](auto kern) {
+      kern<<<grid, kThreads, 0, ctx->stream>>>(m, n, A, lda, x, incx, per, part, alpha, beta, y, incy);
+    };
+    if (cpw == kColsPerWaveShort)
+      launch(vec ? gemv_t_kernel<true, kColsPerWaveShort> : gemv_t_kernel<false, kColsPerWaveShort>);
     else
-      gemv_t_kernel<false><<<grid, kThreads, 0, ctx->stream>>>(m, n, A, lda, x, incx, per, part,
-                                                                alpha, beta, y, incy);
+      launch(vec ? gemv_t_kernel<true, kColsPerWave> : gemv_t_kernel<false, kColsPerWave>);
     WGB_CHECK_LAUNCH("gemv_t_kernel");
   }
   if (part) {

@@ -66,8 +66,10 @@ def test_dgemm_repeats_bit_identical(ctx):
 
 
 @pytest.mark.parametrize("trans", [0, 1])
-def test_sgemv_split_fold_repeats_bit_identical(ctx, trans):
-    m, n = 4096, 6000
+@pytest.mark.parametrize("m,n", [(4096, 6000), (8192, 3000)])
+def test_sgemv_split_fold_repeats_bit_identical(ctx, trans, m, n):
+    # 4096 rows: the transpose form's short-column kernel (4 columns per
+    # wave); 8192 rows: its 8-column kernel; both split and fold
     A = orc.random_f32(m * n, -1, 1, 9)
     x = orc.random_f32(m if trans else n, -1, 1, 10)
     y = orc.random_f32(n if trans else m, -1, 1, 11)

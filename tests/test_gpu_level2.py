@@ -120,10 +120,12 @@ def test_zero_x_entries_skip_their_column(ctx, layout, trans, n):
 
 @pytest.mark.parametrize("trans", [0, 1])
 @pytest.mark.parametrize("shape", [(4096, 4096, 4096), (65536, 48, 65536), (48, 65536, 49),
-                                   (3001, 2999, 3003)])
+                                   (3001, 2999, 3003), (4097, 1000, 4099), (4096, 1000, 4096)])
 def test_large_and_skinny(ctx, trans, shape):
     # one block column / one block row of output (contraction split many
-    # ways), odd sizes with an odd lda (element loads), and misaligned x
+    # ways), odd sizes with an odd lda (element loads), and misaligned x;
+    # 4096 / 4097 rows sit either side of the transpose form's switch from
+    # 4 to 8 columns per wave
     m, n, lda = shape
     A = orc.random_f32(lda * n, -1, 1, 31)
     xl, yl = (n, m) if trans == 0 else (m, n)

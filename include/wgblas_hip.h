@@ -132,6 +132,23 @@ int wgb_sgemm(wgb_ctx *ctx, int transA, int transB, int64_t m, int64_t n,
               int64_t k, float alpha, const float *A, int64_t lda,
               const float *B, int64_t ldb, float beta, float *C, int64_t ldc);
 
+/* Allocation-free sgemm: wgb_sgemm's operation, launches and results (the
+ * same bits on the same inputs), with its split-k workspace taken from a
+ * fixed 32 MiB device array of the library instead of a buffer grown with
+ * hipMalloc; the call makes no hipMalloc, hipFree or other allocation.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * allocation). Each GPU holds one copy of the array until the process ends,
+ * shared by every call on that GPU and keeping the last call's contents:
+ * calls that overlap on one GPU (two contexts' streams, or two host threads)
+ * race on it. A problem whose split-k tail would need more than 32 MiB is
+ * rejected with WGB_ERR_INVALID_VALUE (on MI355X's 256 CUs no problem does:
+ * the tail holds at most one round of 128 x 128 tiles, 32 MiB). */
+int wgb_sgemm_noalloc(wgb_ctx *ctx, int transA, int transB, int64_t m,
+                      int64_t n, int64_t k, float alpha, const float *A,
+                      int64_t lda, const float *B, int64_t ldb, float beta,
+                      float *C, int64_t ldc);
+
 /* Same as wgb_sgemm on the uplo triangle of the m-by-n C only
  * (WGB_LOWER: i >= j, WGB_UPPER: i <= j); the other triangle is never read
  * nor written. Replaces sgemmtr (src/sgemmtr/sgemmtr.mjs:25-278). */

@@ -53,6 +53,8 @@ def test_status_strings_and_null_context():
     st = lib.wgb_sgemm(None, 0, 0, 2, 2, 2, 1.0, None, 2, None, 2, 0.0, None, 2)
     assert st == -5
     assert b"wgb_init" in lib.wgb_last_error()
+    st = lib.wgb_sgemm_noalloc(None, 0, 0, 2, 2, 2, 1.0, None, 2, None, 2, 0.0, None, 2)
+    assert st == -5
     r = C.c_float(1.0)
     assert lib.wgb_sdot(None, 4, None, 1, None, 1, C.byref(r)) == -5
 

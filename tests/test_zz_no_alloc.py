@@ -1,0 +1,126 @@
+"""GPU parity of wgb_sgemm_noalloc, the allocation-free sgemm entry point.
+
+It runs wgb_sgemm's launches with the split-k partials in the library's fixed
+per-GPU array instead of the context's hipMalloc'd workspace, so on the same
+inputs it must return wgb_sgemm's bits exactly. The shapes put the launch on
+the split-k path on an MI355X (256 CUs, two resident 128-tiles per CU):
+  * 2048 x 2048 x 1024: 256 tiles of 128 on 512 slots, every tile in 2
+    k-slices, 512 slices = the whole 32 MiB array;
+  * 2944 x 2944 x 2048: 529 tiles, the last 17 in 16 k-slices each (17 MiB);
+  * 1024 x 1024 x 2048: 64-tiles (256 of them), split on the small tier;
+  * 1999 x 2001 x 777, ldc padded: edge tiles and a partial k-tile in a slice.
+Each case is two calls in a row on the one array, the second with a smaller
+input, so the second call runs over whatever the first left in the array.
+Every result is also checked on sampled columns against a float64 product
+under the reference's forward-error bound (tests/sgemm/helpers.js:1-57), and
+C's ld padding is bit-checked.
+"""
+import numpy as np
+import pytest
+
+from tests.helpers import EPS32
+
+pytestmark = pytest.mark.gpu
+
+
+def _stored_rows(trans, rows, cols):
+    """(rows, cols) of the column-major array holding op(X) = rows x cols."""
+    return (cols, rows) if trans else (rows, cols)
+
+
+def _make(ctx, ta, tb, m, n, k, ldc, seed):
+    ar, ac = _stored_rows(ta, m, k)
+    br, bc = _stored_rows(tb, k, n)
+    A = ctx.empty(ac * ar, np.float32)
+    B = ctx.empty(bc * br, np.float32)
+    C0 = ctx.empty(n * ldc, np.float32)
+    ctx.fill_uniform(A, -1, 1, seed)
+    ctx.fill_uniform(B, -1, 1, seed + 1)
+    ctx.fill_uniform(C0, -1, 1, seed + 2)
+    return A, ar, B, br, C0
+
+
+def _op(host, trans, rows, cols, ld):
+    """op(X) as a dense float64 rows x cols array from column-major storage."""
+    if trans:
+        # stored cols x rows: stored column j is row j of op(X)
+        return host.reshape(rows, ld)[:, :cols].astype(np.float64)
+    return host.reshape(cols, ld)[:, :rows].T.astype(np.float64)
+
+
+def _run_pair(ctx, ta, tb, m, n, k, alpha, beta, ldc, seed):
+    A, lda, B, ldb, C0 = _make(ctx, ta, tb, m, n, k, ldc, seed)
+    c_ref = ctx.empty(n * ldc, np.float32)
+    c_new = ctx.empty(n * ldc, np.float32)
+    try:
+        ctx.synchronize()
+        cin = C0.to_host()
+        ctx.h2d(c_ref.ptr, cin)
+        ctx.h2d(c_new.ptr, cin)
+        ctx.sgemm(ta, tb, m, n, k, alpha, A, lda, B, ldb, beta, c_ref, ldc)
+        ctx.sgemm_noalloc(ta, tb, m, n, k, alpha, A, lda, B, ldb, beta, c_new, ldc)
+        ctx.synchronize()
+        got_ref, got_new = c_ref.to_host(), c_new.to_host()
+        # the same launches on the same inputs: the same bits
+        assert np.array_equal(got_ref.view(np.uint32), got_new.view(np.uint32)), \
+            f"noalloc differs from wgb_sgemm at {m}x{n}x{k} ta={ta} tb={tb}"
+        # ld padding of C untouched
+        pad = np.ones((n, ldc), bool)
+        pad[:, :m] = False
+        assert np.array_equal(got_new.reshape(n, ldc)[pad].view(np.uint32),
+                              cin.reshape(n, ldc)[pad].view(np.uint32))
+        # sampled columns against float64 under the reference's bound
+        ah = A.to_host()
+        bh = B.to_host()
+        opA = _op(ah, ta, m, k, lda)
+        opB = _op(bh, tb, k, n, ldb)
+        rng = np.random.default_rng(seed)
+        cols = np.unique(np.concatenate([[0, n - 1], rng.integers(0, n, 24)]))
+        ref = alpha * (opA @ opB[:, cols]) + beta * cin.reshape(n, ldc)[cols, :m].T.astype(np.float64)
+        absdot = np.abs(opA) @ np.abs(opB[:, cols])
+        bound = EPS32 * ((k + 1) * abs(alpha) * absdot
+                         + abs(beta) * np.abs(cin.reshape(n, ldc)[cols, :m].T))
+        got = got_new.reshape(n, ldc)[cols, :m].T.astype(np.float64)
+        assert np.all(np.abs(got - ref) <= bound)
+    finally:
+        for x in (A, B, C0, c_ref, c_new):
+            x.free()
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_noalloc_matches_sgemm_two_calls(ctx, ta, tb):
+    # first call: the whole array (512 slices of 64 KiB); second, smaller:
+    # 64-tiles split on the small tier
+    for (m, n, k, ldc, seed) in [(2048, 2048, 1024, 2048, 31), (1024, 1024, 2048, 1024, 32)]:
+        print(f"noalloc case ta={ta} tb={tb} {m}x{n}x{k}", flush=True)
+        _run_pair(ctx, ta, tb, m, n, k, 1.5, 0.5, ldc, seed)
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 1), (1, 0)])
+def test_noalloc_tail_split_then_ragged(ctx, ta, tb):
+    # 529 tiles (17 tail tiles in 16 slices), then a smaller ragged problem
+    # with a padded ldc, beta = 1 and a partial k-tile
+    print(f"noalloc case ta={ta} tb={tb} 2944^2x2048 then 1999x2001x777", flush=True)
+    _run_pair(ctx, ta, tb, 2944, 2944, 2048, 1.0, 0.25, 2944, 33)
+    _run_pair(ctx, ta, tb, 1999, 2001, 777, -0.75, 1.0, 2000, 34)
+
+
+def test_noalloc_paths_without_split(ctx):
+    # the one-launch small kernel, and alpha = 0 (the scale kernel): no
+    # workspace, still wgb_sgemm's results
+    print("noalloc case small kernel 300x200x100 and alpha = 0", flush=True)
+    _run_pair(ctx, 0, 0, 300, 200, 100, 1.25, -0.5, 301, 35)
+    _run_pair(ctx, 1, 1, 256, 128, 64, 0.0, 2.0, 256, 36)
+
+
+def test_noalloc_rejects_bad_arguments(ctx):
+    from wgblas_amd.native import WgblasError
+
+    A = ctx.empty(16, np.float32)
+    try:
+        with pytest.raises(WgblasError, match="lda"):
+            ctx.sgemm_noalloc(0, 0, 4, 4, 4, 1.0, A, 3, A, 4, 0.0, A, 4)
+        with pytest.raises(WgblasError, match="C is null"):
+            ctx.sgemm_noalloc(0, 0, 4, 4, 4, 1.0, A, 4, A, 4, 0.0, None, 4)
+    finally:
+        A.free()

@@ -52,6 +52,8 @@
 #include "common.h"
 
 #include <cmath>
+#include <mutex>
+#include <string>
 #include <type_traits>
 
 namespace {
@@ -1401,12 +1403,22 @@ int ensure_workspace(wgb_ctx *ctx, size_t bytes) {
   return WGB_OK;
 }
 
+// Where a launch's split-k partials go: ptr == nullptr grows the context's
+// workspace (ctx->gemm_ws) with hipMalloc as needed; otherwise a fixed
+// buffer of `bytes` that a launch needing more rejects.
+struct WsSource {
+  void *ptr = nullptr;
+  size_t bytes = 0;
+};
+
 // Launches one GEMM on a BT tier. Tiles fill `slots` = CUs x resident blocks
 // per round; when the last round is at most half full, its tiles are split
 // along k into up to 16 units (at least 4 k-tiles each) so the last round is
 // as full as the rest, and split_fixup combines the partials in split order.
+// The partials of rem tail tiles in S splits take rem * S <= slots tiles of
+// workspace.
 template <typename T, int BT>
-int launch_tier(wgb_ctx *ctx, GemmArgs<T> &a, bool akc, bool bkc, bool vec) {
+int launch_tier(wgb_ctx *ctx, GemmArgs<T> &a, bool akc, bool bkc, bool vec, WsSource wsrc) {
   constexpr int BK = 128 / (int)sizeof(T);
   const bool pair = sizeof(T) == 4 && a.band != wgb::kBandNone;
   KernelFn<T> fn = pick_kernel<T, BT>(akc, bkc, vec, pair);
@@ -1431,12 +1443,21 @@ int launch_tier(wgb_ctx *ctx, GemmArgs<T> &a, bool akc, bool bkc, bool vec) {
     if (S >= 2) {
       const int64_t kts = (nkt + S - 1) / S;
       S = (nkt + kts - 1) / kts;  // every split non-empty
-      int st = ensure_workspace(ctx, (size_t)(rem * S) * BT * BT * sizeof(T));
-      if (st) return st;
+      const size_t need = (size_t)(rem * S) * BT * BT * sizeof(T);
+      if (wsrc.ptr) {
+        if (need > wsrc.bytes)
+          return wgb::fail(WGB_ERR_INVALID_VALUE,
+                           "the split-k tail of this problem needs " + std::to_string(need) +
+                               " bytes of workspace; the allocation-free entry point holds " +
+                               std::to_string(wsrc.bytes));
+      } else {
+        int st = ensure_workspace(ctx, need);
+        if (st) return st;
+      }
       a.nregular = (int)(a.ntiles - rem);
       a.splits = (int)S;
       a.kt_split = (int)kts;
-      a.ws = static_cast<T *>(ctx->gemm_ws);
+      a.ws = static_cast<T *>(wsrc.ptr ? wsrc.ptr : ctx->gemm_ws);
     }
   }
   const int64_t grid = pair ? a.nregular : a.nregular + (int64_t)(a.ntiles - a.nregular) * a.splits;
@@ -1485,7 +1506,7 @@ int check_gemm_args(int uplo, bool want_uplo, int transA, int transB, int64_t m,
 template <typename T>
 int gemm_launch(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64_t n, int64_t k,
                 T alpha, const T *A, int64_t lda, const T *B, int64_t ldb, T beta, T *C,
-                int64_t ldc, int band) {
+                int64_t ldc, int band, WsSource wsrc = WsSource()) {
   if (m == 0 || n == 0) return WGB_OK;
   if (alpha == (T)0 || k == 0) {
     dim3 block(256);
@@ -1580,8 +1601,8 @@ int gemm_launch(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64
   a.tiles_m = (int)tmn;
   a.tiles_n = (int)tnn;
   a.ntiles = (int)ntiles;
-  int st = bt == 128 ? launch_tier<T, 128>(ctx, a, akc, bkc, vec)
-                     : launch_tier<T, 64>(ctx, a, akc, bkc, vec);
+  int st = bt == 128 ? launch_tier<T, 128>(ctx, a, akc, bkc, vec, wsrc)
+                     : launch_tier<T, 64>(ctx, a, akc, bkc, vec, wsrc);
   if (st) return st;
   WGB_CHECK_LAUNCH("gemm_kernel");
   return WGB_OK;
@@ -1590,17 +1611,59 @@ int gemm_launch(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64
 template <typename T>
 int gemm_run(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64_t n, int64_t k,
              T alpha, const T *A, int64_t lda, const T *B, int64_t ldb, T beta, T *C,
-             int64_t ldc) {
+             int64_t ldc, WsSource wsrc = WsSource()) {
   if (m == 0 || n == 0) return WGB_OK;
   wgb::timing_begin(ctx);
   int st = gemm_launch<T>(ctx, uplo, transA, transB, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc,
-                          wgb::kBandNone);
+                          wgb::kBandNone, wsrc);
   if (st) return st;
   wgb::timing_end(ctx);
   return WGB_OK;
 }
 
+// ---- allocation-free sgemm ------------------------------------------------
+//
+// wgb_sgemm_noalloc keeps its split-k partials in `scratch`, a fixed device
+// array of this library (every GPU holds its own copy until the process
+// ends), instead of the context's workspace that wgb_sgemm grows with
+// hipMalloc. A split tail holds at most one round of tiles (rem * S <= slots,
+// launch_tier), so with 128 x 128 fp32 tiles at two blocks per CU on 256 CUs
+// it needs at most 512 * 64 KiB = 32 MiB: that is the array's size. In host
+// code `scratch` names a host-side stand-in, never the device address: the
+// address is looked up once per device (hipGetSymbolAddress, with that device
+// current) when a context is created, and only that pointer is passed on.
+constexpr size_t kNoallocWsBytes = (size_t)32 << 20;
+static __device__ __align__(256) float scratch[kNoallocWsBytes / sizeof(float)];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices] = {nullptr};
+
 }  // namespace
+
+namespace wgb {
+
+// Looks up `scratch`'s device address on ctx's device (current on entry)
+// once per device and stores it in ctx->noalloc_ws; called by wgb_init.
+int noalloc_setup(wgb_ctx *ctx) {
+  if (ctx->device < 0 || ctx->device >= kMaxDevices)
+    return fail(WGB_ERR_INVALID_VALUE, "device index beyond the allocation-free workspace table");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[ctx->device]) {
+    void *ptr = nullptr;
+    hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+      (void)hipGetLastError();
+      return fail_hip(e == hipSuccess ? hipErrorInvalidSymbol : e,
+                      "hipGetSymbolAddress of the allocation-free GEMM workspace");
+    }
+    g_scratch_ptr[ctx->device] = ptr;
+  }
+  ctx->noalloc_ws = g_scratch_ptr[ctx->device];
+  return WGB_OK;
+}
+
+}  // namespace wgb
 
 namespace wgb {
 
@@ -1626,6 +1689,24 @@ extern "C" int wgb_sgemm(wgb_ctx *ctx, int transA, int transB, int64_t m, int64_
   if (st) return st;
   if ((st = check_gemm_args(0, false, transA, transB, m, n, k, A, lda, B, ldb, C, ldc))) return st;
   return gemm_run<float>(ctx, 0, transA, transB, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc);
+}
+
+// wgb_sgemm's launches with the split-k partials in `scratch` (through the
+// per-device address looked up at wgb_init): no hipMalloc, hipFree or other
+// allocation on this path. Calls that overlap on one GPU share the array.
+extern "C" int wgb_sgemm_noalloc(wgb_ctx *ctx, int transA, int transB, int64_t m, int64_t n,
+                                 int64_t k, float alpha, const float *A, int64_t lda,
+                                 const float *B, int64_t ldb, float beta, float *C, int64_t ldc) {
+  int st = wgb::enter(ctx);
+  if (st) return st;
+  if (!ctx->noalloc_ws)
+    return wgb::fail(WGB_ERR_NOT_INITIALIZED,
+                     "the allocation-free GEMM workspace was not set up on this device");
+  if ((st = check_gemm_args(0, false, transA, transB, m, n, k, A, lda, B, ldb, C, ldc))) return st;
+  WsSource ws;
+  ws.ptr = ctx->noalloc_ws;
+  ws.bytes = kNoallocWsBytes;
+  return gemm_run<float>(ctx, 0, transA, transB, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc, ws);
 }
 
 extern "C" int wgb_sgemmtr(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64_t n,

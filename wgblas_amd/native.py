@@ -43,6 +43,8 @@ _SIGNATURES = {
     "wgb_fill_normal_f32": [_ptr, _ptr, _i64, C.c_uint32],
     "wgb_sgemm": [_ptr, C.c_int, C.c_int, _i64, _i64, _i64, C.c_float, _ptr, _i64, _ptr, _i64,
                   C.c_float, _ptr, _i64],
+    "wgb_sgemm_noalloc": [_ptr, C.c_int, C.c_int, _i64, _i64, _i64, C.c_float, _ptr, _i64, _ptr,
+                          _i64, C.c_float, _ptr, _i64],
     "wgb_sgemmtr": [_ptr, C.c_int, C.c_int, C.c_int, _i64, _i64, _i64, C.c_float, _ptr, _i64,
                     _ptr, _i64, C.c_float, _ptr, _i64],
     "wgb_ssyrk": [_ptr, C.c_int, C.c_int, _i64, _i64, C.c_float, _ptr, _i64, C.c_float, _ptr,
@@ -248,6 +250,10 @@ class Context:
     def sgemm(self, transA, transB, m, n, k, alpha, A, lda, B, ldb, beta, C_, ldc):
         _check(self.lib.wgb_sgemm(self.handle, transA, transB, m, n, k, alpha, _p(A), lda,
                                   _p(B), ldb, beta, _p(C_), ldc), "wgb_sgemm")
+
+    def sgemm_noalloc(self, transA, transB, m, n, k, alpha, A, lda, B, ldb, beta, C_, ldc):
+        _check(self.lib.wgb_sgemm_noalloc(self.handle, transA, transB, m, n, k, alpha, _p(A), lda,
+                                          _p(B), ldb, beta, _p(C_), ldc), "wgb_sgemm_noalloc")
 
     def sgemmtr(self, uplo, transA, transB, m, n, k, alpha, A, lda, B, ldb, beta, C_, ldc):
         _check(self.lib.wgb_sgemmtr(self.handle, uplo, transA, transB, m, n, k, alpha, _p(A),

@@ -41,8 +41,9 @@
 // run of tiles; inside that run tiles are grouped 8 tile-rows at a time so
 // concurrent tiles share A and B panels. sgemmtr/ssyrk launch only the
 // tiles that meet the requested triangle (wgblas launches all of them and
-// returns early, src/shaders/sgemm_large.wgsl:78-83) and mask stores inside
-// the diagonal tiles.
+// returns early, src/shaders/sgemm_large.wgsl:78-83), in bands of 8 tile rows
+// walked column by column for the same sharing, and mask stores inside the
+// diagonal tiles (tile_order.h holds these orders).
 //
 // Result rules kept from wgblas (src/shaders/sgemm_large.wgsl:288-308,
 // src/shaders/dgemm_small.wgsl:230-273): beta == 0 never reads C;
@@ -50,6 +51,7 @@
 // columns outside m x n, and the other triangle for sgemmtr/ssyrk, are
 // never written.
 #include "common.h"
+#include "tile_order.h"
 
 #include <cmath>
 #include <mutex>
@@ -128,62 +130,9 @@ constexpr int kSchedMfma = 0x008;
 constexpr int kSchedVmemRead = 0x020;
 constexpr int kSchedDsRead = 0x100;
 constexpr int kSchedDsWrite = 0x200;
-constexpr int kGroupM = 8;
-constexpr int kXcds = 8;
-
-// Number of tiles of a tiles_m x tiles_n grid (square tiles) that meet the
-// lower (tile row >= tile col) triangle; upper swaps the roles.
-int64_t triangle_tiles(int64_t rows, int64_t cols) {
-  int64_t t = 0;
-  int64_t full = rows < cols ? rows : cols;
-  t = full * (full + 1) / 2;  // rows 0..full-1 hold tm+1 tiles each
-  if (rows > cols) t += (rows - cols) * cols;
-  return t;
-}
-
-// Decodes the L-th tile (row-major over the triangle) of a grid whose row r
-// holds min(r+1, cols) tiles.
-__device__ inline void triangle_decode(int L, int cols, int &r, int &c) {
-  int64_t t0 = (int64_t)cols * (cols + 1) / 2;
-  if ((int64_t)L < t0) {
-    int rr = (int)((sqrt(8.0 * (double)L + 1.0) - 1.0) * 0.5);
-    while ((int64_t)(rr + 1) * (rr + 2) / 2 <= L) ++rr;
-    while ((int64_t)rr * (rr + 1) / 2 > L) --rr;
-    r = rr;
-    c = L - (int)((int64_t)rr * (rr + 1) / 2);
-  } else {
-    int64_t rem = (int64_t)L - t0;
-    r = cols + (int)(rem / cols);
-    c = (int)(rem % cols);
-  }
-}
-
-// XCD-aware remap of workgroup w of a grid of n: the hardware deals
-// workgroups round-robin over the 8 XCDs (w % 8); give each XCD a contiguous
-// run of logical tiles so its L2 sees shared A and B panels.
-__device__ inline int xcd_remap(int w, int n) {
-  int x = w % kXcds, j = w / kXcds;
-  int q = n / kXcds, r = n % kXcds;
-  return x * q + (x < r ? x : r) + j;
-}
-
-// Logical tile L -> (tile row, tile col): row-major over the triangle for
-// sgemmtr/ssyrk, otherwise groups of kGroupM tile-rows walked column-wise.
-__device__ inline void logical_tile(int L, int tiles_m, int tiles_n, int uplo, int &tm, int &tn) {
-  if (uplo == WGB_LOWER) {
-    triangle_decode(L, tiles_n, tm, tn);
-  } else if (uplo == WGB_UPPER) {
-    triangle_decode(L, tiles_m, tn, tm);
-  } else {
-    int group_size = kGroupM * tiles_n;
-    int gid = L / group_size;
-    int first_m = gid * kGroupM;
-    int gm = tiles_m - first_m < kGroupM ? tiles_m - first_m : kGroupM;
-    int in_group = L % group_size;
-    tm = first_m + in_group % gm;
-    tn = in_group / gm;
-  }
-}
+using wgb_tiles::logical_tile;
+using wgb_tiles::triangle_tiles;
+using wgb_tiles::xcd_remap;
 
 // Chunk position of 16-byte chunk c of staged row r in the [row][k] layout
 // is c ^ kc_swz(r). A ds_write_b128 phase (8 lanes) fills one 128-byte row;
@@ -1014,8 +963,9 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs<T> &p, int tm, int tn, 
   // Epilogue: C = alpha*acc + beta*C on the tile's in-range (and, for
   // sgemmtr/ssyrk, in-triangle) elements.
   if (unit >= 0) {
-    // Split-k unit: raw partial sums of the whole BTM x BTN tile (rows and
-    // columns past m, n hold zeros from the zero-filled operand loads).
+    // Split-k unit: raw partial sums of the whole BTM x BTN tile; rows and
+    // columns past m, n hold sums over clamped operand rows, which
+    // split_fixup never stores.
     T *slice = p.ws + (int64_t)unit * BTM * BTN;
     if constexpr (!AKC || sizeof(T) == 4) {
       GemmArgs<T> q = p;

@@ -192,22 +192,27 @@ int wgb_dsyrk(wgb_ctx *ctx, int uplo, int trans, int64_t n, int64_t k,
               double *C, int64_t ldc);
 
 /* C <- alpha*op(A)*op(B)^T + alpha*op(B)*op(A)^T + beta*C on the uplo
- * triangle of the n-by-n C; op(X) is n-by-k (trans == WGB_NO_TRANS) or X^T
- * for a k-by-n X, the same trans for A and B. Two triangle GEMM launches, the
- * second with beta = 1, as wgblas runs it; alpha == 0 or k == 0 is
- * C <- beta*C on the triangle without reading A or B.
+ * triangle of the n-by-n C; op(X) is n-by-k (trans flag WGB_NO_TRANS) or X^T
+ * for a k-by-n X. wgblas has one trans for both operands; a flag per operand
+ * takes its GpuMatrix operands of different storage orders in one call.
+ * Two triangle GEMM launches, the second with beta = 1, as wgblas runs it,
+ * timed as one span; alpha == 0 or k == 0 is C <- beta*C on the triangle
+ * without reading A or B.
  * Replaces ssyr2k (src/ssyr2k/ssyr2k.mjs:27-301). */
-int wgb_ssyr2k(wgb_ctx *ctx, int uplo, int trans, int64_t n, int64_t k,
-               float alpha, const float *A, int64_t lda, const float *B,
-               int64_t ldb, float beta, float *C, int64_t ldc);
+int wgb_ssyr2k(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t n,
+               int64_t k, float alpha, const float *A, int64_t lda,
+               const float *B, int64_t ldb, float beta, float *C, int64_t ldc);
 
-/* C <- alpha*A*B + beta*C (side WGB_LEFT, A m-by-m) or alpha*B*A + beta*C
- * (WGB_RIGHT, A n-by-n); A symmetric, only its uplo triangle is read.
- * C and B are m-by-n. alpha == 0 reads neither A nor B.
- * Replaces ssymm (src/ssymm/ssymm.mjs:30-318: symmetrize.wgsl, then sgemm). */
-int wgb_ssymm(wgb_ctx *ctx, int side, int uplo, int64_t m, int64_t n,
-              float alpha, const float *A, int64_t lda, const float *B,
-              int64_t ldb, float beta, float *C, int64_t ldc);
+/* C <- alpha*A*op(B) + beta*C (side WGB_LEFT, A m-by-m) or
+ * alpha*op(B)*A + beta*C (WGB_RIGHT, A n-by-n); A symmetric, only its uplo
+ * triangle is read. C and op(B) are m-by-n: B is stored m-by-n (transB ==
+ * WGB_NO_TRANS) or n-by-m (WGB_TRANS, wgblas's B and C of different storage
+ * orders, src/ssymm/ssymm.mjs:85-87, 149-163). alpha == 0 reads neither A
+ * nor B. Replaces ssymm (src/ssymm/ssymm.mjs:30-318: symmetrize.wgsl, then
+ * sgemm). */
+int wgb_ssymm(wgb_ctx *ctx, int side, int uplo, int transB, int64_t m,
+              int64_t n, float alpha, const float *A, int64_t lda,
+              const float *B, int64_t ldb, float beta, float *C, int64_t ldc);
 
 /* B <- alpha*op(A)*B (WGB_LEFT, A m-by-m) or alpha*B*op(A) (WGB_RIGHT,
  * A n-by-n); A triangular (uplo triangle read; diag WGB_UNIT takes its

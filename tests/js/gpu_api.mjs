@@ -9,7 +9,7 @@
 import { readFileSync } from "fs";
 import { fileURLToPath } from "url";
 import { dirname, join } from "path";
-import { test, run, assert, assertEqual } from "./harness.mjs";
+import { test, run, assert, assertEqual, assertRejects } from "./harness.mjs";
 import * as wg from "../../wgblas_amd/js/index.mjs";
 
 const here = dirname(fileURLToPath(import.meta.url));
@@ -249,9 +249,13 @@ function triEl(A, lda, layout, uplo, transA, diag, r, c) {
   return transA === "transpose" ? el(A, lda, layout, c, r) : el(A, lda, layout, r, c);
 }
 
+// Storage order of operand `nm` of call `a`: its own (a.layoutA, ...), for
+// GpuMatrix operands of different layouts, else the call's `layout`.
+const layoutOf = (a, nm) => a["layout" + nm] || a.layout || "row-major";
+
 // Expected output buffer and per-element bound of a level-3 call `a`.
 function refLevel3(routine, a) {
-  const layout = a.layout || "row-major";
+  const [la, lb, lc] = [layoutOf(a, "A"), layoutOf(a, "B"), layoutOf(a, routine === "strmm" ? "B" : "C")];
   const out = Float64Array.from(routine === "strmm" ? a.B : a.C);
   const bound = new Float64Array(out.length);
   const eps = 2 ** -23;
@@ -266,11 +270,11 @@ function refLevel3(routine, a) {
         if (!inTri(a.uplo, i, j)) continue;
         const t = a.trans;
         for (let p = 0; p < a.k; p++) {
-          const v = opElem(a.A, a.lda, layout, t, i, p) * opElem(a.B, a.ldb, layout, t, j, p) +
-            opElem(a.B, a.ldb, layout, t, i, p) * opElem(a.A, a.lda, layout, t, j, p);
+          const v = opElem(a.A, a.lda, la, t, i, p) * opElem(a.B, a.ldb, lb, t, j, p) +
+            opElem(a.B, a.ldb, lb, t, i, p) * opElem(a.A, a.lda, la, t, j, p);
           s += v;
-          d += Math.abs(opElem(a.A, a.lda, layout, t, i, p) * opElem(a.B, a.ldb, layout, t, j, p)) +
-            Math.abs(opElem(a.B, a.ldb, layout, t, i, p) * opElem(a.A, a.lda, layout, t, j, p));
+          d += Math.abs(opElem(a.A, a.lda, la, t, i, p) * opElem(a.B, a.ldb, lb, t, j, p)) +
+            Math.abs(opElem(a.B, a.ldb, lb, t, i, p) * opElem(a.A, a.lda, la, t, j, p));
         }
         coef = a.k + 3;
       } else {
@@ -278,18 +282,18 @@ function refLevel3(routine, a) {
         for (let p = 0; p < order; p++) {
           let v;
           if (routine === "ssymm")
-            v = a.side === "left" ? symEl(a.A, a.lda, layout, a.uplo, i, p) * el(a.B, a.ldb, layout, p, j)
-              : el(a.B, a.ldb, layout, i, p) * symEl(a.A, a.lda, layout, a.uplo, p, j);
+            v = a.side === "left" ? symEl(a.A, a.lda, la, a.uplo, i, p) * el(a.B, a.ldb, lb, p, j)
+              : el(a.B, a.ldb, lb, i, p) * symEl(a.A, a.lda, la, a.uplo, p, j);
           else
-            v = a.side === "left" ? triEl(a.A, a.lda, layout, a.uplo, a.transA, a.diag, i, p) * el(a.B, a.ldb, layout, p, j)
-              : el(a.B, a.ldb, layout, i, p) * triEl(a.A, a.lda, layout, a.uplo, a.transA, a.diag, p, j);
+            v = a.side === "left" ? triEl(a.A, a.lda, la, a.uplo, a.transA, a.diag, i, p) * el(a.B, a.ldb, lb, p, j)
+              : el(a.B, a.ldb, lb, i, p) * triEl(a.A, a.lda, la, a.uplo, a.transA, a.diag, p, j);
           s += v;
           d += Math.abs(v);
         }
         coef = order + 1;
       }
       const ld = routine === "strmm" ? a.ldb : a.ldc;
-      const idx = cIndex(ld, layout, i, j);
+      const idx = cIndex(ld, lc, i, j);
       const cin = routine === "strmm" ? 0 : a.C[idx];
       out[idx] = (a.alpha === 0 ? 0 : a.alpha * s) + (routine === "strmm" || a.beta === 0 ? 0 : a.beta * cin);
       bound[idx] = eps * (coef * Math.abs(a.alpha) * d + (routine === "strmm" ? 0 : 3 * Math.abs(a.beta) * Math.abs(cin)));
@@ -341,7 +345,6 @@ const level3Call = {
 // GpuMatrix forms of a level-3 call's operands (shapes as wgblas's
 // gpustorage tests build them) and the output read back with its ld.
 async function residentLevel3(routine, a) {
-  const layout = a.layout || "row-major";
   const mats = {};
   const shape = (name) => {
     if (routine === "ssyr2k") {
@@ -360,17 +363,17 @@ async function residentLevel3(routine, a) {
   try {
     for (const nm of names) {
       const [r, c, ld] = shape(nm);
-      const outer = layout === "column-major" ? c : r;
+      const outer = layoutOf(a, nm) === "column-major" ? c : r;
       const padded = new Float32Array(Math.max(outer * ld, a[nm].length));
       padded.set(a[nm]);
-      mats[nm] = wg.GpuMatrix.from(device, padded, r, c, ld, layout);
+      mats[nm] = wg.GpuMatrix.from(device, padded, r, c, ld, layoutOf(a, nm));
     }
     const res = await level3Call[routine](Object.assign({}, a, mats));
     assertEqual(Object.keys(res).length, 0, "resident call returns {}");
     const [r, c, ld] = shape(outName);
     const dense = await mats[outName].read();
-    const inner = layout === "column-major" ? r : c;
-    const outer = layout === "column-major" ? c : r;
+    const inner = layoutOf(a, outName) === "column-major" ? r : c;
+    const outer = layoutOf(a, outName) === "column-major" ? c : r;
     const raw = Float32Array.from(a[outName]);
     for (let o = 0; o < outer; o++) raw.set(dense.subarray(o * inner, o * inner + inner), o * ld);
     return raw;
@@ -755,6 +758,108 @@ test("dgemmtr / dsyrk: random within the double-double bound, resident and host"
           gA.destroy();
           gC.destroy();
         }
+      }
+    }
+});
+
+// ssymm with B and C of different storage orders, and ssyr2k with A and B of
+// different storage orders (GpuMatrix operands carry their own layout;
+// wgblas accepts both: src/ssymm/ssymm.mjs:85-87, 149-163,
+// src/ssyr2k/ssyr2k.mjs:149-205).
+for (const [lB, lC] of [["row-major", "column-major"], ["column-major", "row-major"]])
+  for (const side of ["left", "right"])
+    test(`ssymm GpuMatrix B ${lB}, C ${lC}, side ${side}`, async () => {
+      const [m, n] = side === "left" ? [70, 45] : [45, 70];
+      const order = side === "left" ? m : n;
+      const ldb = (lB === "column-major" ? m : n) + 2;
+      const ldc = (lC === "column-major" ? m : n) + 1;
+      const a = { side, uplo: "lower", m, n, alpha: 1.25, beta: 0.5, layoutA: "column-major", layoutB: lB, layoutC: lC,
+        A: wg.randomFloat32Array(order * order, -1, 1, 71), lda: order,
+        B: wg.randomFloat32Array((lB === "column-major" ? n : m) * ldb, -1, 1, 72), ldb,
+        C: wg.randomFloat32Array((lC === "column-major" ? n : m) * ldc, -1, 1, 73), ldc };
+      checkLevel3("ssymm", await residentLevel3("ssymm", a), a);
+    });
+
+for (const [lA, lB] of [["row-major", "column-major"], ["column-major", "row-major"]])
+  for (const trans of ["no-transpose", "transpose"])
+    test(`ssyr2k GpuMatrix A ${lA}, B ${lB}, ${trans}, benchmark mode times both passes`, async () => {
+      const n = 90;
+      const k = 33;
+      const [r, c] = trans === "no-transpose" ? [n, k] : [k, n];
+      const lda = (lA === "column-major" ? r : c) + 1;
+      const ldb = (lB === "column-major" ? r : c) + 3;
+      const a = { uplo: "upper", trans, n, k, alpha: 0.75, beta: -0.5, layoutA: lA, layoutB: lB, layoutC: "row-major",
+        A: wg.randomFloat32Array((lA === "column-major" ? c : r) * lda, -1, 1, 74), lda,
+        B: wg.randomFloat32Array((lB === "column-major" ? c : r) * ldb, -1, 1, 75), ldb,
+        C: wg.randomFloat32Array(n * n, -1, 1, 76), ldc: n };
+      checkLevel3("ssyr2k", await residentLevel3("ssyr2k", a), a);
+      const bench = await wg.init({ benchmark: true });
+      const gA = wg.GpuMatrix.from(bench, a.A, r, c, lda, lA);
+      const gB = wg.GpuMatrix.from(bench, a.B, r, c, ldb, lB);
+      const gC = wg.GpuMatrix.from(bench, a.C, n, n, n, "row-major");
+      try {
+        const res = await wg.ssyr2k(bench, "upper", trans, n, k, 0.75, gA, lda, gB, ldb, -0.5, gC, n);
+        assert(typeof res.gpuTimeMs === "number" && res.gpuTimeMs > 0, "one gpuTimeMs span for the call");
+      } finally {
+        gA.destroy();
+        gB.destroy();
+        gC.destroy();
+        wg.cleanup(bench);
+      }
+    });
+
+test("sgemv alpha = 0, beta = 1 in benchmark mode reports this call's gpuTimeMs", async () => {
+  const bench = await wg.init({ benchmark: true });
+  const A = wg.GpuMatrix.from(bench, wg.randomFloat32Array(64 * 32, -1, 1, 77), 64, 32, 32);
+  const x = wg.GpuVector.from(bench, wg.randomFloat32Array(32, -1, 1, 78));
+  const y0 = wg.randomFloat32Array(64, -1, 1, 79);
+  const y = wg.GpuVector.from(bench, y0);
+  try {
+    // a fresh benchmark device: no earlier timed call to fall back on
+    const r = await wg.sgemv(bench, "no-transpose", 64, 32, 0, A, 32, x, 1, 1, y, 1);
+    assert(typeof r.gpuTimeMs === "number" && r.gpuTimeMs >= 0, "gpuTimeMs present");
+    exactEqual(await y.read(), y0, "y untouched");
+  } finally {
+    A.destroy();
+    x.destroy();
+    y.destroy();
+    wg.cleanup(bench);
+  }
+});
+
+// A GpuMatrix / GpuVector holds native elements of its dtype: the fp32
+// routines reject Float64Array-backed resident operands (they cannot read
+// doubles as floats).
+test("fp32 routines reject Float64Array-backed resident operands", async () => {
+  const M = (dt) => wg.GpuMatrix.from(device, new dt(64).fill(1), 8, 8, 8, "column-major");
+  const V = (dt) => wg.GpuVector.from(device, new dt(8).fill(1));
+  const N = "no-transpose";
+  const cases = [
+    ["sgemm", ["A", "B", "C"], (o) => wg.sgemm(device, N, N, 8, 8, 8, 1, o.A, 8, o.B, 8, 0, o.C, 8)],
+    ["sgemmtr", ["A", "B", "C"], (o) => wg.sgemmtr(device, "lower", N, N, 8, 8, 8, 1, o.A, 8, o.B, 8, 0, o.C, 8)],
+    ["ssyrk", ["A", "C"], (o) => wg.ssyrk(device, "lower", N, 8, 8, 1, o.A, 8, 0, o.C, 8)],
+    ["ssyr2k", ["A", "B", "C"], (o) => wg.ssyr2k(device, "lower", N, 8, 8, 1, o.A, 8, o.B, 8, 0, o.C, 8)],
+    ["ssymm", ["A", "B", "C"], (o) => wg.ssymm(device, "left", "lower", 8, 8, 1, o.A, 8, o.B, 8, 0, o.C, 8)],
+    ["strmm", ["A", "B"], (o) => wg.strmm(device, "left", "lower", N, "non-unit", 8, 8, 1, o.A, 8, o.B, 8)],
+    ["strsm", ["A", "B"], (o) => wg.strsm(device, "left", "lower", N, "non-unit", 8, 8, 1, o.A, 8, o.B, 8)],
+    ["sgemv", ["A", "x", "y"], (o) => wg.sgemv(device, N, 8, 8, 1, o.A, 8, o.x, 1, 0, o.y, 1)],
+    ["sdot", ["x", "y"], (o) => wg.sdot(device, 8, o.x, 1, o.y, 1)],
+    ["sasum", ["x"], (o) => wg.sasum(device, 8, o.x, 1)],
+    ["snrm2", ["x"], (o) => wg.snrm2(device, 8, o.x, 1)],
+    ["isamax", ["x"], (o) => wg.isamax(device, 8, o.x, 1)],
+  ];
+  for (const [routine, names, fn] of cases)
+    for (const bad of names) {
+      const o = {};
+      for (const nm of names) {
+        const dt = nm === bad ? Float64Array : Float32Array;
+        o[nm] = nm === "x" || nm === "y" ? V(dt) : M(dt);
+      }
+      try {
+        const kind = bad === "x" || bad === "y" ? "GpuVector" : "GpuMatrix";
+        await assertRejects(() => fn(o), `${bad} must be a Float32Array-backed ${kind}`, `${routine} ${bad}`);
+      } finally {
+        for (const nm of names) o[nm].destroy();
       }
     }
 });

@@ -403,3 +403,61 @@ def test_strsm_large_round_trip(ctx, side, uplo, trans):
     back = rc.dense_op(dB.to_host(), m, n, ldb, 0)
     want = 1.5 * rc.dense_op(B, m, n, ldb, 0)
     assert np.max(np.abs(back - want)) <= 1e-4 * np.max(np.abs(want))
+
+
+# ------------------------------------------- operands of different storage orders
+def _cm_transpose(X, rows, cols, ld):
+    """Column-major rows x cols (leading dimension ld) -> its transpose as a
+    dense column-major cols x rows array (leading dimension cols)."""
+    M = np.asarray(X, F32)[: ld * cols].reshape(cols, ld)[:, :rows]  # M[j, i] = X(i, j)
+    return np.ascontiguousarray(M.T).reshape(-1)  # X^T(j, i) = X(i, j) at j + i*cols
+
+
+@pytest.mark.parametrize("side", [1, 2])
+@pytest.mark.parametrize("uplo", [1, 2])
+def test_ssymm_b_other_storage_order(ctx, side, uplo):
+    # wgblas accepts a B whose storage order differs from C's
+    # (src/ssymm/ssymm.mjs:85-87, 149-163): in C's column-major frame that B
+    # is op(B) = B^T of its memory, stored n x m
+    m, n = (300, 170) if side == 1 else (170, 300)
+    order = m if side == 1 else n
+    lda, ldb_t, ldc = order + 2, n + 3, m + 1
+    A = orc.random_f32(lda * order, -1, 1, 61)
+    Bt = orc.random_f32(ldb_t * m, -1, 1, 62)  # n x m stored, op(B) = its transpose
+    C = orc.random_f32(ldc * n, -1, 1, 63)
+    dC = up(ctx, C)
+    ctx.ssymm(side, uplo, m, n, 1.25, up(ctx, A), lda, up(ctx, Bt), ldb_t, 0.5, dC, ldc, transB=1)
+    got = dC.to_host()
+    B = _cm_transpose(Bt, n, m, ldb_t)  # m x n, ld m
+    ref, ad = orc.ssymm_ld(side, uplo, m, n, 1.25, A, lda, B, m, 0.5, C, ldc)
+    idx = region(m, n, ldc)
+    bound = EPS32 * ((order + 1) * 1.25 * ad + c_term(0.5, C))
+    assert factor(got, ref, bound, idx) <= 1
+    keep = outside(len(C), idx)
+    assert bits_equal(got[keep], np.asarray(C, F32)[keep])
+
+
+@pytest.mark.parametrize("uplo", [1, 2])
+@pytest.mark.parametrize("ta,tb", [(0, 1), (1, 0)])
+def test_ssyr2k_operands_of_different_storage_orders(ctx, uplo, ta, tb):
+    # GpuMatrix A and B of different layouts reach one wgb_ssyr2k call with a
+    # flag per operand; the oracle sees B converted to A's orientation
+    n, k = 333, 150
+    lda = (k if ta else n) + 2
+    ldb = (k if tb else n) + 1
+    ldc = n + 4
+    A = orc.random_f32(lda * (n if ta else k), -1, 1, 64)
+    B = orc.random_f32(ldb * (n if tb else k), -1, 1, 65)
+    C = orc.random_f32(ldc * n, -1, 1, 66)
+    dC = up(ctx, C)
+    ctx.ssyr2k(uplo, ta, n, k, 0.75, up(ctx, A), lda, up(ctx, B), ldb, -0.5, dC, ldc, transB=tb)
+    got = dC.to_host()
+    rows_b, cols_b = (k, n) if tb else (n, k)
+    Bc = _cm_transpose(B, rows_b, cols_b, ldb)  # the other orientation, ld = cols_b
+    call = (uplo, ta, n, k, 0.75, A, lda, Bc, cols_b, -0.5, C, ldc)
+    ref, d1, d2 = orc.ssyr2k_ld(*call)
+    idx = region(n, n, ldc, uplo)
+    bound = EPS32 * ((k + 3) * 0.75 * d1 + (k + 2) * 0.75 * d2 + 3 * c_term(-0.5, C))
+    assert factor(got, ref, bound, idx) <= 1
+    keep = outside(len(C), idx)
+    assert bits_equal(got[keep], np.asarray(C, F32)[keep])

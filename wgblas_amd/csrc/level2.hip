@@ -280,7 +280,15 @@ extern "C" int wgb_sgemv(wgb_ctx *ctx, int trans, int64_t m, int64_t n, float al
   if (lda < imax(1, m)) return fail(WGB_ERR_INVALID_VALUE, "lda must be >= max(1, m)");
   if (incx <= 0 || incy <= 0) return fail(WGB_ERR_INVALID_VALUE, "incx and incy must be positive");
   // reference BLAS quick return: nothing to do, y untouched
-  if (m == 0 || n == 0 || (alpha == 0.f && beta == 1.f)) return WGB_OK;
+  if (m == 0 || n == 0) return WGB_OK;
+  if (alpha == 0.f && beta == 1.f) {
+    // y untouched as well, but wgblas runs (and times) a kernel here
+    // (src/sgemv/sgemv.mjs:85 returns early only for m or n == 0): record
+    // this call's empty span so per-call timing reports it, not an older call
+    wgb::timing_begin(ctx);
+    wgb::timing_end(ctx);
+    return WGB_OK;
+  }
   if (!y || (alpha != 0.f && (!A || !x))) return fail(WGB_ERR_INVALID_VALUE, "A, x or y is null");
   const bool nt = trans == WGB_NO_TRANS;
   const int64_t len = nt ? m : n;  // length of y

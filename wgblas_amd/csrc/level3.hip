@@ -354,44 +354,52 @@ int check_tri(int side, int uplo, int transA, int diag, int64_t m, int64_t n, co
 
 }  // namespace
 
-extern "C" int wgb_ssyr2k(wgb_ctx *ctx, int uplo, int trans, int64_t n, int64_t k, float alpha,
-                          const float *A, int64_t lda, const float *B, int64_t ldb, float beta,
-                          float *C, int64_t ldc) {
+extern "C" int wgb_ssyr2k(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t n, int64_t k,
+                          float alpha, const float *A, int64_t lda, const float *B, int64_t ldb,
+                          float beta, float *C, int64_t ldc) {
   int st = wgb::enter(ctx);
   if (st) return st;
-  if (trans != WGB_NO_TRANS && trans != WGB_TRANS)
-    return fail(WGB_ERR_INVALID_VALUE, "trans must be WGB_NO_TRANS or WGB_TRANS");
-  const int tB = trans == WGB_NO_TRANS ? WGB_TRANS : WGB_NO_TRANS;
-  if ((st = wgb::check_gemm(uplo, true, trans, tB, n, n, k, A, lda, B, ldb, C, ldc))) return st;
+  if (transA != WGB_NO_TRANS && transA != WGB_TRANS)
+    return fail(WGB_ERR_INVALID_VALUE, "transA must be WGB_NO_TRANS or WGB_TRANS");
+  if (transB != WGB_NO_TRANS && transB != WGB_TRANS)
+    return fail(WGB_ERR_INVALID_VALUE, "transB must be WGB_NO_TRANS or WGB_TRANS");
+  // op(X)^T as the second GEMM operand: the opposite flag
+  const int tAt = transA == WGB_NO_TRANS ? WGB_TRANS : WGB_NO_TRANS;
+  const int tBt = transB == WGB_NO_TRANS ? WGB_TRANS : WGB_NO_TRANS;
+  if ((st = wgb::check_gemm(uplo, true, transA, tBt, n, n, k, A, lda, B, ldb, C, ldc))) return st;
   if (n == 0) return WGB_OK;
   wgb::timing_begin(ctx);
   // pass 1: alpha op(A) op(B)^T + beta C; pass 2: alpha op(B) op(A)^T + C
-  // (src/ssyr2k/ssyr2k.mjs:206-262)
-  if ((st = wgb::gemm_f32(ctx, uplo, trans, tB, n, n, k, alpha, A, lda, B, ldb, beta, C, ldc,
+  // (src/ssyr2k/ssyr2k.mjs:206-262), one timed span
+  if ((st = wgb::gemm_f32(ctx, uplo, transA, tBt, n, n, k, alpha, A, lda, B, ldb, beta, C, ldc,
                           wgb::kBandNone)))
     return st;
   if (alpha != 0.f && k != 0 &&
-      (st = wgb::gemm_f32(ctx, uplo, trans, tB, n, n, k, alpha, B, ldb, A, lda, 1.f, C, ldc,
+      (st = wgb::gemm_f32(ctx, uplo, transB, tAt, n, n, k, alpha, B, ldb, A, lda, 1.f, C, ldc,
                           wgb::kBandNone)))
     return st;
   wgb::timing_end(ctx);
   return WGB_OK;
 }
 
-extern "C" int wgb_ssymm(wgb_ctx *ctx, int side, int uplo, int64_t m, int64_t n, float alpha,
-                         const float *A, int64_t lda, const float *B, int64_t ldb, float beta,
-                         float *C, int64_t ldc) {
+extern "C" int wgb_ssymm(wgb_ctx *ctx, int side, int uplo, int transB, int64_t m, int64_t n,
+                         float alpha, const float *A, int64_t lda, const float *B, int64_t ldb,
+                         float beta, float *C, int64_t ldc) {
   int st = wgb::enter(ctx);
   if (st) return st;
   if (side != WGB_LEFT && side != WGB_RIGHT)
     return fail(WGB_ERR_INVALID_VALUE, "side must be WGB_LEFT or WGB_RIGHT");
   if (uplo != WGB_LOWER && uplo != WGB_UPPER)
     return fail(WGB_ERR_INVALID_VALUE, "uplo must be WGB_LOWER or WGB_UPPER");
+  if (transB != WGB_NO_TRANS && transB != WGB_TRANS)
+    return fail(WGB_ERR_INVALID_VALUE, "transB must be WGB_NO_TRANS or WGB_TRANS");
   if (m < 0 || n < 0) return fail(WGB_ERR_INVALID_VALUE, "m and n must be non-negative");
   if (m > INT32_MAX || n > INT32_MAX) return fail(WGB_ERR_INVALID_VALUE, "m and n must be below 2^31");
   const int64_t order = side == WGB_LEFT ? m : n;
   if (lda < imax(1, order)) return fail(WGB_ERR_INVALID_VALUE, "lda must be >= max(1, order of A)");
-  if (ldb < imax(1, m)) return fail(WGB_ERR_INVALID_VALUE, "ldb must be >= max(1, m)");
+  // op(B) is m x n: B is stored m x n, or n x m when transB
+  if (ldb < imax(1, transB == WGB_NO_TRANS ? m : n))
+    return fail(WGB_ERR_INVALID_VALUE, "ldb must be >= max(1, rows of B)");
   if (ldc < imax(1, m)) return fail(WGB_ERR_INVALID_VALUE, "ldc must be >= max(1, m)");
   if (m == 0 || n == 0) return WGB_OK;
   if (!C || (alpha != 0.f && (!A || !B))) return fail(WGB_ERR_INVALID_VALUE, "A, B or C is null");
@@ -409,10 +417,10 @@ extern "C" int wgb_ssymm(wgb_ctx *ctx, int side, int uplo, int64_t m, int64_t n,
                                                                                       uplo, W, ldw);
     WGB_CHECK_LAUNCH("symmetrize_kernel");
     st = side == WGB_LEFT
-             ? wgb::gemm_f32(ctx, 0, WGB_NO_TRANS, WGB_NO_TRANS, m, n, m, alpha, W, ldw, B, ldb,
-                             beta, C, ldc, wgb::kBandNone)
-             : wgb::gemm_f32(ctx, 0, WGB_NO_TRANS, WGB_NO_TRANS, m, n, n, alpha, B, ldb, W, ldw,
-                             beta, C, ldc, wgb::kBandNone);
+             ? wgb::gemm_f32(ctx, 0, WGB_NO_TRANS, transB, m, n, m, alpha, W, ldw, B, ldb, beta, C,
+                             ldc, wgb::kBandNone)
+             : wgb::gemm_f32(ctx, 0, transB, WGB_NO_TRANS, m, n, n, alpha, B, ldb, W, ldw, beta, C,
+                             ldc, wgb::kBandNone);
   }
   if (st) return st;
   wgb::timing_end(ctx);

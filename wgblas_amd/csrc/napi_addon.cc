@@ -328,42 +328,44 @@ napi_value Ssyrk(napi_env env, napi_callback_info info) {
   return nullptr;
 }
 
-// ssyr2k(ctx, uplo, trans, n, k, alpha, A, lda, B, ldb, beta, C, ldc)
+// ssyr2k(ctx, uplo, transA, transB, n, k, alpha, A, lda, B, ldb, beta, C, ldc)
 napi_value Ssyr2k(napi_env env, napi_callback_info info) {
   Args a;
-  if (!get_args(env, info, a, 13)) return nullptr;
+  if (!get_args(env, info, a, 14)) return nullptr;
   wgb_ctx *ctx = ctx_of(env, a.v[0]);
   if (!ctx) return nullptr;
-  int uplo, trans;
+  int uplo, ta, tb;
   int64_t n, k, lda, ldb, ldc;
   double alpha, beta;
   void *A, *B, *C;
-  if (!get_i32(env, a.v[1], &uplo) || !get_i32(env, a.v[2], &trans) || !get_i64(env, a.v[3], &n) ||
-      !get_i64(env, a.v[4], &k) || !get_f64(env, a.v[5], &alpha) || !get_ptr(env, a.v[6], &A) ||
-      !get_i64(env, a.v[7], &lda) || !get_ptr(env, a.v[8], &B) || !get_i64(env, a.v[9], &ldb) ||
-      !get_f64(env, a.v[10], &beta) || !get_ptr(env, a.v[11], &C) || !get_i64(env, a.v[12], &ldc))
+  if (!get_i32(env, a.v[1], &uplo) || !get_i32(env, a.v[2], &ta) || !get_i32(env, a.v[3], &tb) ||
+      !get_i64(env, a.v[4], &n) || !get_i64(env, a.v[5], &k) || !get_f64(env, a.v[6], &alpha) ||
+      !get_ptr(env, a.v[7], &A) || !get_i64(env, a.v[8], &lda) || !get_ptr(env, a.v[9], &B) ||
+      !get_i64(env, a.v[10], &ldb) || !get_f64(env, a.v[11], &beta) || !get_ptr(env, a.v[12], &C) ||
+      !get_i64(env, a.v[13], &ldc))
     return nullptr;
-  WGB_OK_OR_THROW(wgb_ssyr2k(ctx, uplo, trans, n, k, (float)alpha, (const float *)A, lda,
+  WGB_OK_OR_THROW(wgb_ssyr2k(ctx, uplo, ta, tb, n, k, (float)alpha, (const float *)A, lda,
                              (const float *)B, ldb, (float)beta, (float *)C, ldc), "wgb_ssyr2k");
   return nullptr;
 }
 
-// ssymm(ctx, side, uplo, m, n, alpha, A, lda, B, ldb, beta, C, ldc)
+// ssymm(ctx, side, uplo, transB, m, n, alpha, A, lda, B, ldb, beta, C, ldc)
 napi_value Ssymm(napi_env env, napi_callback_info info) {
   Args a;
-  if (!get_args(env, info, a, 13)) return nullptr;
+  if (!get_args(env, info, a, 14)) return nullptr;
   wgb_ctx *ctx = ctx_of(env, a.v[0]);
   if (!ctx) return nullptr;
-  int side, uplo;
+  int side, uplo, tb;
   int64_t m, n, lda, ldb, ldc;
   double alpha, beta;
   void *A, *B, *C;
-  if (!get_i32(env, a.v[1], &side) || !get_i32(env, a.v[2], &uplo) || !get_i64(env, a.v[3], &m) ||
-      !get_i64(env, a.v[4], &n) || !get_f64(env, a.v[5], &alpha) || !get_ptr(env, a.v[6], &A) ||
-      !get_i64(env, a.v[7], &lda) || !get_ptr(env, a.v[8], &B) || !get_i64(env, a.v[9], &ldb) ||
-      !get_f64(env, a.v[10], &beta) || !get_ptr(env, a.v[11], &C) || !get_i64(env, a.v[12], &ldc))
+  if (!get_i32(env, a.v[1], &side) || !get_i32(env, a.v[2], &uplo) || !get_i32(env, a.v[3], &tb) ||
+      !get_i64(env, a.v[4], &m) || !get_i64(env, a.v[5], &n) || !get_f64(env, a.v[6], &alpha) ||
+      !get_ptr(env, a.v[7], &A) || !get_i64(env, a.v[8], &lda) || !get_ptr(env, a.v[9], &B) ||
+      !get_i64(env, a.v[10], &ldb) || !get_f64(env, a.v[11], &beta) || !get_ptr(env, a.v[12], &C) ||
+      !get_i64(env, a.v[13], &ldc))
     return nullptr;
-  WGB_OK_OR_THROW(wgb_ssymm(ctx, side, uplo, m, n, (float)alpha, (const float *)A, lda,
+  WGB_OK_OR_THROW(wgb_ssymm(ctx, side, uplo, tb, m, n, (float)alpha, (const float *)A, lda,
                             (const float *)B, ldb, (float)beta, (float *)C, ldc), "wgb_ssymm");
   return nullptr;
 }

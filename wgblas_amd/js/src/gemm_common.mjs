@@ -37,6 +37,11 @@ export function checkScalar(name, v) {
   if (!Number.isFinite(v)) throw new Error(`${name} must be finite.`);
 }
 
+/** A resident operand must hold elements of the routine's type. */
+export function checkResidentDtype(name, X, isGpu, arr, kind = "GpuMatrix") {
+  if (isGpu && X.dtype !== arr) throw new Error(`${name} must be a ${arr.name}-backed ${kind}.`);
+}
+
 export function checkUplo(uplo) {
   if (uplo !== "lower" && uplo !== "upper") throw new Error("uplo must be 'lower' or 'upper'.");
 }
@@ -88,9 +93,10 @@ export function checkGemm(device, a, opts) {
   for (const [name, X, isGpu] of [["A", a.A, AIsGpu], ["B", a.B, BIsGpu], ["C", a.C, CIsGpu]]) {
     if (!isGpu && !(X instanceof arr)) throw new Error(`${name} must be a ${arrName} or GpuMatrix.`);
   }
-  if (opts.f64)
-    for (const [name, X, isGpu] of [["A", a.A, AIsGpu], ["B", a.B, BIsGpu], ["C", a.C, CIsGpu]])
-      if (isGpu && X.dtype !== Float64Array) throw new Error(`${name} must be a Float64Array-backed GpuMatrix.`);
+  // A GpuMatrix holds native elements of its dtype: an fp32 routine cannot
+  // read a Float64Array-backed one, nor an fp64 routine a Float32Array one.
+  for (const [name, X, isGpu] of [["A", a.A, AIsGpu], ["B", a.B, BIsGpu], ["C", a.C, CIsGpu]])
+    if (isGpu && X.dtype !== arr) throw new Error(`${name} must be a ${arrName}-backed GpuMatrix.`);
   if ((AIsGpu || BIsGpu) && !CIsGpu) throw new Error("C must be a GpuMatrix when A or B is a GpuMatrix.");
   if (CIsGpu && (!AIsGpu || !BIsGpu)) throw new Error("A and B must be GpuMatrix when C is a GpuMatrix.");
   if (a.m < 0 || a.n < 0 || a.k < 0) throw new Error("m, n, and k must be non-negative.");

@@ -24,7 +24,8 @@ export function reduceOne(routine, device, n, x, incx, emptyValue) {
   if (incx <= 0) throw new Error("incx must be positive.");
   if (!xIsGpu && !(x instanceof (f64 ? Float64Array : Float32Array)))
     throw new Error(`x must be a ${arrName} or GpuVector.`);
-  if (f64 && xIsGpu && x.dtype !== Float64Array) throw new Error("x must be a Float64Array-backed GpuVector.");
+  if (xIsGpu && x.dtype !== (f64 ? Float64Array : Float32Array))
+    throw new Error(`x must be a ${arrName}-backed GpuVector.`);
   if (n <= 0) return { value: emptyValue };
   if (x.length < (n - 1) * incx + 1)
     throw new Error("x does not have enough elements for the given n and incx.");
@@ -45,8 +46,8 @@ export function reduceDot(device, n, x, incx, y, incy, routine = "sdot") {
   if (incx <= 0 || incy <= 0) throw new Error("incx and incy must be positive.");
   if (!xIsGpu && !(x instanceof Arr)) throw new Error(`x must be a ${arrName} or GpuVector.`);
   if (!yIsGpu && !(y instanceof Arr)) throw new Error(`y must be a ${arrName} or GpuVector.`);
-  if (f64 && xIsGpu && x.dtype !== Float64Array) throw new Error("x must be a Float64Array-backed GpuVector.");
-  if (f64 && yIsGpu && y.dtype !== Float64Array) throw new Error("y must be a Float64Array-backed GpuVector.");
+  if (xIsGpu && x.dtype !== Arr) throw new Error(`x must be a ${arrName}-backed GpuVector.`);
+  if (yIsGpu && y.dtype !== Arr) throw new Error(`y must be a ${arrName}-backed GpuVector.`);
   if (xIsGpu !== yIsGpu)
     throw new Error(`x and y must be the same type (both ${arrName} or both GpuVector).`);
   if (n <= 0) return { value: 0 };

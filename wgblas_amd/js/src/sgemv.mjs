@@ -6,7 +6,7 @@
 import { GpuMatrix } from "./classes/GpuMatrix.mjs";
 import { GpuVector } from "./classes/GpuVector.mjs";
 import { requireGpuDevice, requireSameDevice } from "./device.mjs";
-import { checkLayout, checkScalar, checkTrans, execute } from "./gemm_common.mjs";
+import { checkLayout, checkResidentDtype, checkScalar, checkTrans, execute } from "./gemm_common.mjs";
 import { native } from "./native.mjs";
 
 export async function sgemv(device, trans, m, n, alpha, A, lda, x, incx, beta, y, incy,
@@ -26,6 +26,9 @@ export async function sgemv(device, trans, m, n, alpha, A, lda, x, incx, beta, y
   if (!AIsGpu && !(A instanceof Float32Array)) throw new Error("A must be a Float32Array or GpuMatrix.");
   if (!xIsGpu && !(x instanceof Float32Array)) throw new Error("x must be a Float32Array or GpuVector.");
   if (!yIsGpu && !(y instanceof Float32Array)) throw new Error("y must be a Float32Array or GpuVector.");
+  checkResidentDtype("A", A, AIsGpu, Float32Array);
+  checkResidentDtype("x", x, xIsGpu, Float32Array, "GpuVector");
+  checkResidentDtype("y", y, yIsGpu, Float32Array, "GpuVector");
   if (xIsGpu !== yIsGpu)
     throw new Error("x and y must be the same type (both Float32Array or both GpuVector).");
   if (xIsGpu && !AIsGpu) throw new Error("A must be a GpuMatrix when x and y are GpuVectors.");

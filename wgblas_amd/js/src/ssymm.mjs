@@ -4,7 +4,9 @@
 // order and messages (ssymm.mjs:48-134).
 import { GpuMatrix } from "./classes/GpuMatrix.mjs";
 import { requireGpuDevice, requireSameDevice } from "./device.mjs";
-import { checkLayout, checkOperand, checkScalar, checkUplo, execute, UPLO } from "./gemm_common.mjs";
+import {
+  checkLayout, checkOperand, checkResidentDtype, checkScalar, checkUplo, execute, NO_TRANS, TRANS, UPLO,
+} from "./gemm_common.mjs";
 import { checkSide, SIDE } from "./tri_common.mjs";
 import { native } from "./native.mjs";
 
@@ -25,6 +27,9 @@ export async function ssymm(device, side, uplo, m, n, alpha, A, lda, B, ldb, bet
   if (!AIsGpu && !(A instanceof Float32Array)) throw new Error("A must be a Float32Array or GpuMatrix.");
   if (!BIsGpu && !(B instanceof Float32Array)) throw new Error("B must be a Float32Array or GpuMatrix.");
   if (!CIsGpu && !(C instanceof Float32Array)) throw new Error("C must be a Float32Array or GpuMatrix.");
+  checkResidentDtype("A", A, AIsGpu, Float32Array);
+  checkResidentDtype("B", B, BIsGpu, Float32Array);
+  checkResidentDtype("C", C, CIsGpu, Float32Array);
   if ((AIsGpu || BIsGpu) && !CIsGpu) throw new Error("C must be a GpuMatrix when A or B is a GpuMatrix.");
   if (CIsGpu && (!AIsGpu || !BIsGpu)) throw new Error("A and B must be GpuMatrix when C is a GpuMatrix.");
   if (m < 0 || n < 0) throw new Error("m and n must be non-negative.");
@@ -42,16 +47,17 @@ export async function ssymm(device, side, uplo, m, n, alpha, A, lda, B, ldb, bet
   }
   checkOperand(B, BIsGpu, layoutB, "no-transpose", m, n, ldb, { X: "B", ld: "ldb", dims: "m and n" });
   checkOperand(C, CIsGpu, layoutC, "no-transpose", m, n, ldc, { X: "C", ld: "ldc", dims: "m and n" });
-  // The C ABI has no trans flag for B: B and C must share a storage order.
-  if (layoutB !== layoutC) throw new Error("B and C must have the same layout.");
   // Column-major frame: a row-major A stores the other triangle of the same
   // symmetric matrix; a row-major C = S B is the column-major C^T = B^T S.
+  // B read in C's frame is op(B): itself when B and C share a storage order,
+  // its transpose otherwise (wgblas's effLayoutB, ssymm.mjs:85-87, 149-163).
   let u = UPLO[uplo];
   if (layoutA !== "column-major") u = u === 1 ? 2 : 1;
   let s = SIDE[side];
   let [mm, nn] = [m, n];
   if (layoutC !== "column-major") [s, mm, nn] = [3 - s, n, m];
+  const tB = layoutB === layoutC ? NO_TRANS : TRANS;
   return execute(device, [A, B], C, CIsGpu, Float32Array, (ctx, p, pC) =>
-    native().ssymm(ctx, s, u, mm, nn, alpha, p[0], lda, p[1], ldb, beta, pC, ldc),
+    native().ssymm(ctx, s, u, tB, mm, nn, alpha, p[0], lda, p[1], ldb, beta, pC, ldc),
   );
 }

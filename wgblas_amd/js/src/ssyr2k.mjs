@@ -5,7 +5,8 @@
 import { GpuMatrix } from "./classes/GpuMatrix.mjs";
 import { requireGpuDevice, requireSameDevice } from "./device.mjs";
 import {
-  checkLayout, checkOperand, checkScalar, checkTrans, checkUplo, execute, TRANS, NO_TRANS, UPLO,
+  checkLayout, checkOperand, checkResidentDtype, checkScalar, checkTrans, checkUplo, execute, TRANS, NO_TRANS,
+  UPLO,
 } from "./gemm_common.mjs";
 import { native } from "./native.mjs";
 
@@ -26,6 +27,9 @@ export async function ssyr2k(device, uplo, trans, n, k, alpha, A, lda, B, ldb, b
   if (!AIsGpu && !(A instanceof Float32Array)) throw new Error("A must be a Float32Array or GpuMatrix.");
   if (!BIsGpu && !(B instanceof Float32Array)) throw new Error("B must be a Float32Array or GpuMatrix.");
   if (!CIsGpu && !(C instanceof Float32Array)) throw new Error("C must be a Float32Array or GpuMatrix.");
+  checkResidentDtype("A", A, AIsGpu, Float32Array);
+  checkResidentDtype("B", B, BIsGpu, Float32Array);
+  checkResidentDtype("C", C, CIsGpu, Float32Array);
   if ((AIsGpu || BIsGpu) && !CIsGpu) throw new Error("C must be a GpuMatrix when A or B is a GpuMatrix.");
   if (CIsGpu && (!AIsGpu || !BIsGpu)) throw new Error("A and B must be GpuMatrix when C is a GpuMatrix.");
   if (n < 0 || k < 0) throw new Error("n and k must be non-negative.");
@@ -49,16 +53,9 @@ export async function ssyr2k(device, uplo, trans, n, k, alpha, A, lda, B, ldb, b
   const tB = (trans === "transpose") !== (layoutB !== "column-major") ? TRANS : NO_TRANS;
   let u = UPLO[uplo];
   if (layoutC !== "column-major") u = u === 1 ? 2 : 1;
-  return execute(device, [A, B], C, CIsGpu, Float32Array, (ctx, p, pC) => {
-    const nat = native();
-    if (tA === tB) {
-      nat.ssyr2k(ctx, u, tA, n, k, alpha, p[0], lda, p[1], ldb, beta, pC, ldc);
-      return;
-    }
-    // A and B in different layouts (GpuMatrix operands): the same two
-    // triangle passes with a trans flag per operand.
-    nat.gemm(1, ctx, u, tA, 1 - tB, n, n, k, alpha, p[0], lda, p[1], ldb, beta, pC, ldc);
-    if (alpha !== 0 && k !== 0)
-      nat.gemm(1, ctx, u, tB, 1 - tA, n, n, k, alpha, p[1], ldb, p[0], lda, 1, pC, ldc);
-  });
+  // A and B of different storage orders (GpuMatrix operands) get different
+  // flags: one native call either way (one gpuTimeMs span).
+  return execute(device, [A, B], C, CIsGpu, Float32Array, (ctx, p, pC) =>
+    native().ssyr2k(ctx, u, tA, tB, n, k, alpha, p[0], lda, p[1], ldb, beta, pC, ldc),
+  );
 }

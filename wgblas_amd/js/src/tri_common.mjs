@@ -3,7 +3,9 @@
 // in the same order, with the same messages), and ssymm's side check.
 import { GpuMatrix } from "./classes/GpuMatrix.mjs";
 import { requireGpuDevice, requireSameDevice } from "./device.mjs";
-import { checkLayout, checkOperand, checkTrans, checkUplo, execute, UPLO } from "./gemm_common.mjs";
+import {
+  checkLayout, checkOperand, checkResidentDtype, checkTrans, checkUplo, execute, UPLO,
+} from "./gemm_common.mjs";
 import { native } from "./native.mjs";
 
 export const SIDE = { left: 1, right: 2 };
@@ -36,6 +38,8 @@ export function runTri(kind, routine, device, side, uplo, transA, diag, m, n, al
     if (!Number.isInteger(v)) throw new Error("m, n, lda, and ldb must be integers.");
   if (!AIsGpu && !(A instanceof Float32Array)) throw new Error("A must be a Float32Array or GpuMatrix.");
   if (!BIsGpu && !(B instanceof Float32Array)) throw new Error("B must be a Float32Array or GpuMatrix.");
+  checkResidentDtype("A", A, AIsGpu, Float32Array);
+  checkResidentDtype("B", B, BIsGpu, Float32Array);
   if (AIsGpu !== BIsGpu) throw new Error("A and B must both be GpuMatrix or both be Float32Array.");
   if (m < 0 || n < 0) throw new Error("m and n must be non-negative.");
   if (m === 0 || n === 0) return BIsGpu ? {} : { B };

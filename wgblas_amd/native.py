@@ -55,9 +55,9 @@ _SIGNATURES = {
                     _ptr, _i64, C.c_double, _ptr, _i64],
     "wgb_dsyrk": [_ptr, C.c_int, C.c_int, _i64, _i64, C.c_double, _ptr, _i64, C.c_double, _ptr,
                   _i64],
-    "wgb_ssyr2k": [_ptr, C.c_int, C.c_int, _i64, _i64, C.c_float, _ptr, _i64, _ptr, _i64,
+    "wgb_ssyr2k": [_ptr, C.c_int, C.c_int, C.c_int, _i64, _i64, C.c_float, _ptr, _i64, _ptr, _i64,
                    C.c_float, _ptr, _i64],
-    "wgb_ssymm": [_ptr, C.c_int, C.c_int, _i64, _i64, C.c_float, _ptr, _i64, _ptr, _i64,
+    "wgb_ssymm": [_ptr, C.c_int, C.c_int, C.c_int, _i64, _i64, C.c_float, _ptr, _i64, _ptr, _i64,
                   C.c_float, _ptr, _i64],
     "wgb_strmm": [_ptr, C.c_int, C.c_int, C.c_int, C.c_int, _i64, _i64, C.c_float, _ptr, _i64,
                   _ptr, _i64],
@@ -275,13 +275,15 @@ class Context:
         _check(self.lib.wgb_dsyrk(self.handle, uplo, trans, n, k, alpha, _p(A), lda, beta,
                                   _p(C_), ldc), "wgb_dsyrk")
 
-    def ssyr2k(self, uplo, trans, n, k, alpha, A, lda, B, ldb, beta, C_, ldc):
-        _check(self.lib.wgb_ssyr2k(self.handle, uplo, trans, n, k, alpha, _p(A), lda, _p(B), ldb,
-                                   beta, _p(C_), ldc), "wgb_ssyr2k")
+    def ssyr2k(self, uplo, trans, n, k, alpha, A, lda, B, ldb, beta, C_, ldc, transB=None):
+        """`trans` applies to A, and to B unless `transB` is given."""
+        tb = trans if transB is None else transB
+        _check(self.lib.wgb_ssyr2k(self.handle, uplo, trans, tb, n, k, alpha, _p(A), lda, _p(B),
+                                   ldb, beta, _p(C_), ldc), "wgb_ssyr2k")
 
-    def ssymm(self, side, uplo, m, n, alpha, A, lda, B, ldb, beta, C_, ldc):
-        _check(self.lib.wgb_ssymm(self.handle, side, uplo, m, n, alpha, _p(A), lda, _p(B), ldb,
-                                  beta, _p(C_), ldc), "wgb_ssymm")
+    def ssymm(self, side, uplo, m, n, alpha, A, lda, B, ldb, beta, C_, ldc, transB=NO_TRANS):
+        _check(self.lib.wgb_ssymm(self.handle, side, uplo, transB, m, n, alpha, _p(A), lda, _p(B),
+                                  ldb, beta, _p(C_), ldc), "wgb_ssymm")
 
     def strmm(self, side, uplo, transA, diag, m, n, alpha, A, lda, B, ldb):
         _check(self.lib.wgb_strmm(self.handle, side, uplo, transA, diag, m, n, alpha, _p(A), lda,

@@ -97,22 +97,41 @@ def rf(bound, achieved, peak, unit, traffic=None):
             "frac": achieved / peak, "traffic": traffic}
 
 
-def load_traffic(name):
-    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE +
-    WRITE_SIZE, scaled by a copy-kernel calibration), recorded as
-    `name = bytes` lines in profiles/traffic.txt; None when not measured."""
+def traffic_entry(name):
+    """(HBM bytes per launch, kernel) of workload `name`, measured with
+    rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, scaled by a copy-kernel
+    calibration) and recorded as `name = bytes  kernel` lines in
+    profiles/traffic.txt; (None, None) when not measured."""
     path = os.path.join(ROOT, "profiles", "traffic.txt")
     if not os.path.exists(path):
-        return None
+        return None, None
     for line in open(path):
-        if "=" in line and not line.lstrip().startswith("#"):
-            k, v = line.split("=", 1)
-            if k.strip() == name:
-                try:
-                    return float(v.split()[0])
-                except ValueError:
-                    return None
-    return None
+        if "=" not in line or line.lstrip().startswith("#"):
+            continue
+        key, rest = line.split("=", 1)
+        if key.strip() != name:
+            continue
+        parts = rest.split(None, 1)
+        try:
+            return float(parts[0]), (parts[1].strip() if len(parts) > 1 else None)
+        except (ValueError, IndexError):
+            return None, None
+    return None, None
+
+
+def load_traffic(name):
+    return traffic_entry(name)[0]
+
+
+def headline_traffic():
+    """Mean HBM bytes per launch over the four headline launches (the launches
+    `roofline.achieved` averages) and, per layout, the bytes and the kernel
+    that layout runs; (None, None) when any layout is unmeasured."""
+    per = {lay: traffic_entry(f"sgemm_8192_{lay}") for lay in ("NN", "NT", "TN", "TT")}
+    if any(v[0] is None for v in per.values()):
+        return None, None
+    mean = sum(v[0] for v in per.values()) / len(per)
+    return mean, {lay: {"bytes": v[0], "kernel": v[1]} for lay, v in per.items()}
 
 
 def bench_gemm_headline(ctx, ev, steps, warmup):
@@ -145,10 +164,12 @@ def bench_components(ctx, ev, quick):
     comps = {}
     reps = 3 if quick else 10
 
-    # config 1: sgemm 512^3 NN, alpha 1, beta 0
+    # config 1: sgemm 512^3 NN, alpha 1, beta 0; A then B from one seed-0
+    # stream, C zero-initialised (the inputs test_gpu_fullsize.py checks)
     n = 512
     buf = ctx.empty(3 * n * n, np.float32)
-    ctx.fill_uniform(buf, -1.0, 1.0, 0)
+    ctx.fill_uniform(buf, -1.0, 1.0, 0, n=2 * n * n)
+    ctx.h2d(buf.offset(2 * n * n), np.zeros(n * n, np.float32))
     A, B, Cm = buf.offset(0), buf.offset(n * n), buf.offset(2 * n * n)
     f = lambda: ctx.sgemm(NO_TRANS, NO_TRANS, n, n, n, 1.0, A, n, B, n, 0.0, Cm, n)
     ms = per_launch_ms(ctx, f, 20)
@@ -156,22 +177,28 @@ def bench_components(ctx, ev, quick):
                           "frac_fp32_peak": 2 * n ** 3 / ms / 1e-3 / PEAK_FP32}
     buf.free()
 
-    # config 3 ragged: 8191 x 8193 x 4097, ld = 1 (mod 64)
+    # config 3 ragged: 8191 x 8193 x 4097, ld = 1 (mod 64), all four layouts
     m, n, k = 8191, 8193, 4097
     ld = lambda r: ((r + 63) // 64) * 64 + 1
-    lda, ldb, ldc = ld(m), ld(k), ld(m)
-    sa, sb, sc = lda * k, ldb * n, ldc * n
-    buf = ctx.empty(sa + sb + sc, np.float32)
-    ctx.fill_uniform(buf, -1.0, 1.0, 2)
-    A, B, Cm = buf.offset(0), buf.offset(sa), buf.offset(sa + sb)
-    f = lambda: ctx.sgemm(NO_TRANS, NO_TRANS, m, n, k, 1.5, A, lda, B, ldb, 0.5, Cm, ldc)
-    f()
-    ms = per_launch_ms(ctx, f, reps)
     fl = 2.0 * m * n * k
-    comps["sgemm_ragged_8191x8193x4097"] = {"ms": ms, "tflops": fl / ms / 1e9,
-                                           "frac_fp32_peak": fl / ms / 1e-3 / PEAK_FP32,
-                                           "ld": [lda, ldb, ldc]}
-    buf.free()
+    per = {}
+    for ta, tb in ((NO_TRANS, NO_TRANS), (NO_TRANS, TRANS), (TRANS, NO_TRANS), (TRANS, TRANS)):
+        a_rows, a_cols = (k, m) if ta else (m, k)
+        b_rows, b_cols = (n, k) if tb else (k, n)
+        lda, ldb, ldc = ld(a_rows), ld(b_rows), ld(m)
+        sa, sb, sc = lda * a_cols, ldb * b_cols, ldc * n
+        buf = ctx.empty(sa + sb + sc, np.float32)
+        ctx.fill_uniform(buf, -1.0, 1.0, 2)
+        A, B, Cm = buf.offset(0), buf.offset(sa), buf.offset(sa + sb)
+        f = lambda: ctx.sgemm(ta, tb, m, n, k, 1.5, A, lda, B, ldb, 0.5, Cm, ldc)
+        f()
+        ms = per_launch_ms(ctx, f, reps)
+        per["NT"[ta] + "NT"[tb]] = {"ms": ms, "tflops": fl / ms / 1e9, "ld": [lda, ldb, ldc]}
+        buf.free()
+    mean_ms = sum(v["ms"] for v in per.values()) / len(per)
+    comps["sgemm_ragged_8191x8193x4097"] = {"ms": mean_ms, "tflops": fl / mean_ms / 1e9,
+                                           "frac_fp32_peak": fl / mean_ms / 1e-3 / PEAK_FP32,
+                                           "per_layout": per}
 
     # config 4: dgemm 4096^3, A N, B T, alpha = beta = 1, seed 3
     n = 4096
@@ -364,12 +391,15 @@ def run_only(ctx, name, reps):
             ctx.lib.wgb_memcpy_d2d(ctx.handle, b.ptr, a.ptr, 4 * n)
         ctx.synchronize()
         return {"bytes_read": 4 * n, "bytes_written": 4 * n}
-    if name == "sgemm_8192":
+    if name.startswith("sgemm_8192"):
+        # sgemm_8192_NN / _NT / _TN / _TT: one headline launch (bare name: NN)
+        lay = name[len("sgemm_8192_"):] or "NN"
+        ta, tb = (TRANS if lay[0] == "T" else NO_TRANS), (TRANS if lay[1] == "T" else NO_TRANS)
         n = 8192
         buf = ctx.empty(3 * n * n, np.float32)
         ctx.fill_uniform(buf, -1.0, 1.0, 2)
         for _ in range(reps):
-            ctx.sgemm(NO_TRANS, NO_TRANS, n, n, n, 1.5, buf.offset(0), n, buf.offset(n * n), n, 0.5,
+            ctx.sgemm(ta, tb, n, n, n, 1.5, buf.offset(0), n, buf.offset(n * n), n, 0.5,
                       buf.offset(2 * n * n), n)
         ctx.synchronize()
         return {"algorithmic_bytes": 4 * 4 * n * n}
@@ -474,41 +504,93 @@ def roof_probe():
     return out
 
 
-def cpu_baseline(budget_s=12.0):
+def reference_cpu_adapter_probe():
+    """What this host offers for running the reference itself on a CPU
+    WebGPU adapter (Dawn on Mesa lavapipe, the recipe of wgblas's
+    .github/actions/lavapipe/action.yml): Node >= 22 (wgblas's package.json
+    engines), the `webgpu` npm package (prebuilt Dawn) and a Vulkan ICD."""
+    import shutil
+    import subprocess
+
+    info = {"node": None, "webgpu_package": False, "vulkan_icds": []}
+    node = shutil.which("node")
+    if node:
+        r = subprocess.run([node, "--version"], capture_output=True, text=True, timeout=30)
+        info["node"] = r.stdout.strip() or None
+        r = subprocess.run([node, "-e", "require.resolve('webgpu')"], capture_output=True, text=True,
+                           timeout=30)
+        info["webgpu_package"] = r.returncode == 0
+    for d in ("/usr/share/vulkan/icd.d", "/etc/vulkan/icd.d", "/usr/local/share/vulkan/icd.d"):
+        if os.path.isdir(d):
+            info["vulkan_icds"] += sorted(os.path.join(d, f) for f in os.listdir(d))
+    major = None
+    if info["node"] and info["node"].startswith("v"):
+        try:
+            major = int(info["node"][1:].split(".")[0])
+        except ValueError:
+            major = None
+    missing = []
+    if major is None or major < 22:
+        missing.append(f"Node >= 22 (found {info['node']})")
+    if not info["webgpu_package"]:
+        missing.append("the webgpu npm package")
+    if not info["vulkan_icds"]:
+        missing.append("a Vulkan ICD (lavapipe)")
+    info["runnable"] = not missing
+    if missing:
+        info["reason"] = "missing " + ", ".join(missing) + "; nothing can be installed (no network)"
+    return info
+
+
+def cpu_baseline(budget_s=4.0):
     """The oracle's fp32 restatement of the reference's per-element order
-    (oracle/oracle.c orc_sgemm_wgsl), one host thread, on a bounded sample of
-    the headline workload: the first columns of C for the (T, N) combination
-    of the 8192^3 problem, until `budget_s` seconds of CPU work."""
+    (oracle/oracle.c orc_sgemm_wgsl) on the headline workload's inputs (A, B,
+    C from one mulberry32(2) stream), transA = T, transB = N, alpha 1.5,
+    beta 0.5: every host core the process may use runs its own 8-column
+    chunks of C (ctypes releases the GIL), for `budget_s` seconds. A bounded
+    sample, reported beside the reference's own CPU-adapter status."""
+    from concurrent.futures import ThreadPoolExecutor
+
     from oracle import orc
 
-    n = 8192
-    A = orc.random_f32(n * n, -1.0, 1.0, 2)
-    B = orc.random_f32(n * n, -1.0, 1.0, 3)
-    cols, flops, t_total = 0, 0.0, 0.0
-    chunk = 8
-    while t_total < budget_s and cols < n:
-        Cc = np.zeros(n * chunk, np.float32)
-        Bc = B[cols * n:(cols + chunk) * n]
+    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    n, chunk = 8192, 8
+    stream = orc.random_f32(3 * n * n, -1.0, 1.0, 2)
+    A, B, C0 = stream[:n * n], stream[n * n:2 * n * n], stream[2 * n * n:]
+
+    def worker(t):
+        cols, c = 0, t * chunk
         t0 = time.perf_counter()
-        orc.sgemm_wgsl(0, 1, 0, n, chunk, n, 1.5, A, n, Bc, n, 0.5, Cc, n)
-        t_total += time.perf_counter() - t0
-        cols += chunk
-        flops += 2.0 * n * chunk * n
-    return {"value": flops / t_total / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
+        while time.perf_counter() - t0 < budget_s and c < n:
+            orc.sgemm_wgsl(0, 1, 0, n, chunk, n, 1.5, A, n, B[c * n:(c + chunk) * n], n, 0.5,
+                           C0[c * n:(c + chunk) * n], n)
+            cols += chunk
+            c += threads * chunk
+        return cols
+
+    t0 = time.perf_counter()
+    with ThreadPoolExecutor(threads) as ex:
+        cols = sum(ex.map(worker, range(threads)))
+    wall = time.perf_counter() - t0
+    flops = 2.0 * n * n * cols
+    return {"value": flops / wall / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "host_cpus": os.cpu_count(), "host_cpus_usable": len(os.sched_getaffinity(0)),
             "sample": f"oracle orc_sgemm_wgsl (reference per-element fp32 order), transA=T transB=N, "
-                      f"m=k=8192, first {cols} columns of C ({flops:.3g} flop in {t_total:.1f} s)"}
+                      f"m=k=8192, {cols} columns of C over {threads} threads ({flops:.3g} flop in "
+                      f"{wall:.1f} s wall)",
+            "reference_cpu_adapter": reference_cpu_adapter_probe()}
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=40)
+    ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="fewer repetitions for the components")
     ap.add_argument("--no-components", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default=None,
-                    help="run one workload alone (copy, sgemm_8192, dgemm_4096, ssyrk_8192, "
+                    help="run one workload alone (copy, sgemm_8192_{NN,NT,TN,TT}, dgemm_4096, ssyrk_8192, "
                          "ssyr2k_8192, ssymm_8192, strmm_8192, strsm_8192, sdot, sasum, snrm2, "
                          "isamax) for counter and kernel-trace collection")
     ap.add_argument("--reps", type=int, default=3)
@@ -532,6 +614,7 @@ def main():
         return 0
     ev = HipEvents(ctx.stream)
     name, arch = ctx.name()
+    traffic, traffic_detail = headline_traffic()
     ms, flops, launch_ms, mean_launch = bench_gemm_headline(ctx, ev, args.steps, args.warmup)
     value = 4 * flops / (ms * 1e-3) / 1e12
     achieved = flops / (mean_launch * 1e-3) / 1e12
@@ -555,8 +638,8 @@ def main():
         "config": {"workload": "sgemm fp32 column-major m=n=k=8192, transA/transB in {N,T}^2 "
                                "(4 GEMMs per step), alpha=1.5, beta=0.5, seed 2",
                    "m": 8192, "n": 8192, "k": 8192, "device": name, "arch": arch},
-        "roofline": rf("mfma", achieved, PEAK_FP32 / 1e12, "TFLOP/s",
-                       load_traffic("sgemm_8192")),
+        "roofline": rf("mfma", achieved, PEAK_FP32 / 1e12, "TFLOP/s", traffic),
+        "traffic_per_layout": traffic_detail,
         "sgemm_launch_ms": launch_ms,
         "components": comps,
     }

@@ -40,7 +40,7 @@ def test_config3_sgemm_8192(ctx, ta, tb):
                      n, rows=(127, 128, 4095, 4096), cols=(127, 128, 4095, 4096), seed=ta * 2 + tb)
 
 
-@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 1)])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 def test_config3_sgemm_ragged_ld(ctx, ta, tb):
     m, n, k = 8191, 8193, 4097
     ld = lambda r: ((r + 63) // 64) * 64 + 1
@@ -116,9 +116,10 @@ def test_config5_ssyrk_chained(ctx):
 
 
 def test_config1_sgemm_512_full_oracle(ctx):
+    # A then B from one seed-0 stream, C zero: the inputs bench.py times
     n = 512
-    A = orc.random_f32(n * n, -1, 1, 0)
-    B = orc.random_f32(n * n, -1, 1, 1)
+    AB = orc.random_f32(2 * n * n, -1, 1, 0)
+    A, B = AB[:n * n], AB[n * n:]
     C0 = np.zeros(n * n, np.float32)
     dA, dB, dC = ctx.upload(A), ctx.upload(B), ctx.upload(C0)
     ctx.sgemm(0, 0, n, n, n, 1.0, dA, n, dB, n, 0.0, dC, n)

@@ -90,10 +90,10 @@ const char *wgb_status_string(int status);
 
 /* Device allocation of `bytes` (256-byte aligned). Replaces the GPUBuffer
  * that GpuVector.from / GpuMatrix.from create through uploadBuffer
- * (src/classes/GpuVector.mjs:41-74, src/classes/GpuMatrix.mjs:149-246,
+ * (src/classes/GpuVector.mjs:41-74, src/classes/GpuMatrix.mjs:43-140,
  * src/util/buffer.mjs:58-77). */
 int wgb_malloc(wgb_ctx *ctx, size_t bytes, void **dptr);
-/* Replaces GpuVector/GpuMatrix.destroy() (GpuVector.mjs:102, GpuMatrix.mjs:310). */
+/* Replaces GpuVector/GpuMatrix.destroy() (GpuVector.mjs:102, GpuMatrix.mjs:204). */
 int wgb_free(wgb_ctx *ctx, void *dptr);
 /* Host -> device copy, ordered on the context's stream and complete on return.
  * Replaces queue.writeBuffer (src/util/buffer.mjs:73-74). */

@@ -13,7 +13,7 @@
  *                           dispatch src/sdot/sdot.mjs:89-92 (2*WGS workgroups of WGS=64)
  *       orc_sasum_wgsl      src/shaders/sasum.wgsl:17-51 + reduction/sum.wgsl
  *       orc_snrm2_wgsl      src/shaders/snrm2.wgsl:33-95 + reduction/scaledSum.wgsl:32-101
- *       orc_isamax_wgsl     src/shaders/isamax.wgsl:19-82 + reduction/argmax.wgsl:96-125
+ *       orc_isamax_wgsl     src/shaders/isamax.wgsl:19-82 + reduction/argmax.wgsl:14-43
  *       orc_sgemm_wgsl      src/shaders/sgemm_large.wgsl:112-308 per-element order
  *                           (sequential k, then alpha*acc, then + beta*C, masks)
  *
@@ -176,7 +176,7 @@ static nrm3 nrm_add(nrm3 a, nrm3 b) {
   return r;
 }
 
-/* scaledSum.wgsl:117-136 */
+/* scaledSum.wgsl:20-24 (NaN test on the bit pattern) */
 static int is_nan_bits(float v) {
   uint32_t b;
   memcpy(&b, &v, 4);
@@ -199,7 +199,7 @@ static float ldexp_bits(float v, int e) {
   return r;
 }
 
-/* scaledSum.wgsl:159-196: the LAPACK 3.10 combine. */
+/* scaledSum.wgsl:64-101: the LAPACK 3.10 combine. */
 float orc_nrm_combine(float abig, float amed, float asml) {
   if (is_nan_bits(amed)) return amed;
   int med_live = amed > 0.0f;
@@ -655,7 +655,7 @@ void orc_strsm_ld(int side, int uplo, int trans, int unit, int64_t m, int64_t n,
 /* ---- level 2: sgemv (src/sgemv/sgemv.mjs:19-254) -------------------------
  * y <- alpha op(A) x + beta y, A m x n column-major, in long double, with
  * reference BLAS's rules, which the reference's tests hold it to through
- * stdlib (tests/sgemv/src/test.sgemv.js:157-202, 299-388): m == 0, n == 0,
+ * stdlib (tests/sgemv/src/test.sgemv.js:157-202, 299-387): m == 0, n == 0,
  * or alpha == 0 with beta == 1 leave y untouched; alpha == 0 reads neither A
  * nor x; beta == 0 never reads y; the no-transpose form (column by column)
  * skips a column whose x entry is zero, the transposed (dot-product) form

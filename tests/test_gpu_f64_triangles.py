@@ -96,7 +96,7 @@ def test_dgemmtr_beta0_ignores_nan_inf_in_c(ctx, uplo, n):
 @pytest.mark.parametrize("uplo", [1, 2])
 @pytest.mark.parametrize("beta", [0.0, 0.5])
 def test_dgemmtr_alpha0_reads_neither_a_nor_b(ctx, uplo, beta):
-    # test.dgemmtr.js:671-720
+    # test.dgemmtr.js:671-719
     n = 150
     A = orc.random_f64(n * n, -1, 1, 1)
     B = orc.random_f64(n * n, -1, 1, 2)

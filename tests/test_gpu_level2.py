@@ -101,7 +101,7 @@ def test_alpha_zero_reads_neither_a_nor_x(ctx, trans, n, beta):
 @pytest.mark.parametrize("trans", ["no-transpose", "transpose"])
 @pytest.mark.parametrize("n", [7, 300])
 def test_zero_x_entries_skip_their_column(ctx, layout, trans, n):
-    # test.sgemv.js:344-388: NaN / Inf land where reference BLAS puts them
+    # test.sgemv.js:344-387: NaN / Inf land where reference BLAS puts them
     at = lambda r, cc: r * n + cc
     A = orc.random_f32(n * n, -1, 1, 1)
     A[at(1, 2)], A[at(2, 1)], A[at(4, 0)], A[at(0, 4)] = np.inf, -np.inf, np.nan, np.inf

@@ -2,7 +2,7 @@
 reference's edge cases (tests/sgemv/edge-cases*.json, both layouts) against
 numpy and hand values, random strided cases, reference BLAS's quick returns,
 alpha = 0 and the no-transpose form's skipping of zero x entries
-(tests/sgemv/src/test.sgemv.js:157-202, 299-388), and a planted mistake."""
+(tests/sgemv/src/test.sgemv.js:157-202, 299-387), and a planted mistake."""
 import numpy as np
 import pytest
 

@@ -564,7 +564,7 @@ __device__ __forceinline__ bool is_nan_bits(float v) {
   return (__float_as_uint(v) & 0x7fffffffu) > 0x7f800000u;
 }
 
-// LAPACK 3.10 combine of the three sums (scaledSum.wgsl:159-196).
+// LAPACK 3.10 combine of the three sums (scaledSum.wgsl:64-101).
 __device__ float nrm_combine(float abig, float amed, float asml) {
   if (is_nan_bits(amed)) return amed;
   bool med_live = amed > 0.0f;

@@ -54,7 +54,6 @@
 #include "tile_order.h"
 
 #include <cmath>
-#include <mutex>
 #include <string>
 #include <type_traits>
 
@@ -614,10 +613,11 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs<T> &p, int tm, int tn, 
       // A copy has a whole k-tile of MFMAs (steps 6, 1, 2) to land, and no
       // registers or LDS store instructions are spent on staging.
       static_assert(BK == 32, "the pipelined fp32 loop assumes two 16-k chunks per k-tile");
-      // Scalar-base copies measured faster (2-3%) at 8192^3 for every
-      // layout with a k-contiguous operand and slower (3%) when both are
-      // mn-contiguous.
-      constexpr bool kScalarBase = AKC || BKC;
+      // Scalar-base copies (scalar tile origin + 32-bit lane offsets):
+      // measured against per-lane 64-bit pointers at 8192^3 on one box, NT
+      // 144.6 -> 147.1 TFLOP/s and ssyrk 8192/4096 138.9 -> 141.1, the other
+      // layouts (which already used them) unchanged.
+      constexpr bool kScalarBase = true;
       const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
       sa.template init_copy<EDGE>();
       sb.template init_copy<EDGE>();
@@ -1016,17 +1016,18 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs<T> &p, int tm, int tn, 
 }
 
 
-// fp64 and the fp32 kernels with one k-contiguous and one mn-contiguous
-// operand are held to 256 registers (two waves per SIMD) explicitly; the
-// other fp32 kernels fit on their own with accumulators in AGPRs, which
-// measured faster for them.
+// Every instantiation is held to 256 registers (two waves per SIMD)
+// explicitly. The fp32 kernels whose operands are both k-contiguous or both
+// mn-contiguous would fit without the bound too, with accumulators in AGPRs;
+// with scalar-base copies the bound measured faster for them (NT 8192^3
+// 146.8 -> 148.2 TFLOP/s, ssyrk 8192/4096 140.9 -> 141.9; A/B on one box).
 //
 // PAIR (launches with a k band, p.band != kBandNone): a tile row's (or
 // column's) k range grows with its index, so block b takes the tile pair
 // (r, c) and (tiles-1-r, c) (columns for a band on op(B)) and every block
 // does the same work, whatever order the dispatcher fills the CUs in.
 template <typename T, int BT, bool AKC, bool BKC, bool VEC, bool PAIR>
-__global__ __launch_bounds__(kThreads, (sizeof(T) == 8 || AKC != BKC) ? 2 : 1) void gemm_kernel(GemmArgs<T> p) {
+__global__ __launch_bounds__(kThreads, 2) void gemm_kernel(GemmArgs<T> p) {
   constexpr int BK = 128 / (int)sizeof(T);
   typedef Stager<T, BT, AKC, VEC> SA;
   typedef Stager<T, BT, BKC, VEC> SB;
@@ -1219,14 +1220,15 @@ const void *small_kernel_for(int64_t k) {
   return reinterpret_cast<const void *>(gemm_small_kernel<AKC, BKC, 4>);
 }
 
-// fp32 with op(B) k-contiguous (NN, TN) and 16-byte aligned operands on
-// large problems: 256 x 128 tiles, 512 threads (4 x 2 waves, each the same
-// 64 x 64 wave tile and loop as the 128 tier), one block per CU (96 KB of
-// LDS). A quarter fewer operand bytes per flop than two 128 x 128 blocks;
-// measured at 8192^3 (A/B on one box): NN 146.0 -> 147.0, TN 142.9 -> 147.8
-// TFLOP/s, while NT and TT ran 1% slower and keep the 128 tier. Full C
-// only, no split-k (the host sends shapes whose last round is over half
-// full; the rest take the 128 tier).
+// fp32 with both operands k-contiguous (TN) and 16-byte aligned on large
+// problems: 256 x 128 tiles, 512 threads (4 x 2 waves, each the same 64 x 64
+// wave tile and loop as the 128 tier), one block per CU (96 KB of LDS). A
+// quarter fewer operand bytes per flop than two 128 x 128 blocks; measured
+// at 8192^3 (A/B on one box): TN 142.9 -> 147.8 TFLOP/s. With scalar-base
+// copies NN runs faster on the 128 tier (148.0 against 145.8), and NT / TT
+// were slower here (143.4 / 145.6 against 144.6 / 149.0). Full C only, no
+// split-k (the host sends shapes whose last round is over half full; the
+// rest take the 128 tier).
 constexpr int kWideThreads = 512;
 constexpr int kWideM = 256, kWideN = 128;
 template <bool AKC>
@@ -1517,7 +1519,7 @@ int gemm_launch(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64
     // last round over half full.
     const int64_t twm = (m + kWideM - 1) / kWideM, twn = (n + kWideN - 1) / kWideN;
     const int64_t tw = twm * twn;
-    if (vec && bkc && uplo == 0 && band == wgb::kBandNone && tw >= 2 * fill &&
+    if (vec && akc && bkc && uplo == 0 && band == wgb::kBandNone && tw >= 2 * fill &&
         (tw % fill == 0 || 2 * (tw % fill) > fill) && tw <= INT32_MAX) {
       a.tiles_m = (int)twm;
       a.tiles_n = (int)twn;
@@ -1527,8 +1529,7 @@ int gemm_launch(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64
       a.kt_split = (int)((k + 31) / 32);
       a.ws = nullptr;
       void *args[] = {&a};
-      const void *fn = akc ? reinterpret_cast<const void *>(gemm_wide_kernel<true>)
-                           : reinterpret_cast<const void *>(gemm_wide_kernel<false>);
+      const void *fn = reinterpret_cast<const void *>(gemm_wide_kernel<true>);
       WGB_CHECK_HIP(hipLaunchKernel(fn, dim3((unsigned)tw), dim3(kWideThreads), args, 0, ctx->stream));
       WGB_CHECK_LAUNCH("gemm_wide_kernel");
       return WGB_OK;
@@ -1571,49 +1572,7 @@ int gemm_run(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64_t 
   return WGB_OK;
 }
 
-// ---- allocation-free sgemm ------------------------------------------------
-//
-// wgb_sgemm_noalloc keeps its split-k partials in `scratch`, a fixed device
-// array of this library (every GPU holds its own copy until the process
-// ends), instead of the context's workspace that wgb_sgemm grows with
-// hipMalloc. A split tail holds at most one round of tiles (rem * S <= slots,
-// launch_tier), so with 128 x 128 fp32 tiles at two blocks per CU on 256 CUs
-// it needs at most 512 * 64 KiB = 32 MiB: that is the array's size. In host
-// code `scratch` names a host-side stand-in, never the device address: the
-// address is looked up once per device (hipGetSymbolAddress, with that device
-// current) when a context is created, and only that pointer is passed on.
-constexpr size_t kNoallocWsBytes = (size_t)32 << 20;
-static __device__ __align__(256) float scratch[kNoallocWsBytes / sizeof(float)];
-
-constexpr int kMaxDevices = 64;
-std::mutex g_scratch_mu;
-void *g_scratch_ptr[kMaxDevices] = {nullptr};
-
 }  // namespace
-
-namespace wgb {
-
-// Looks up `scratch`'s device address on ctx's device (current on entry)
-// once per device and stores it in ctx->noalloc_ws; called by wgb_init.
-int noalloc_setup(wgb_ctx *ctx) {
-  if (ctx->device < 0 || ctx->device >= kMaxDevices)
-    return fail(WGB_ERR_INVALID_VALUE, "device index beyond the allocation-free workspace table");
-  std::lock_guard<std::mutex> lock(g_scratch_mu);
-  if (!g_scratch_ptr[ctx->device]) {
-    void *ptr = nullptr;
-    hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
-    if (e != hipSuccess || !ptr) {
-      (void)hipGetLastError();
-      return fail_hip(e == hipSuccess ? hipErrorInvalidSymbol : e,
-                      "hipGetSymbolAddress of the allocation-free GEMM workspace");
-    }
-    g_scratch_ptr[ctx->device] = ptr;
-  }
-  ctx->noalloc_ws = g_scratch_ptr[ctx->device];
-  return WGB_OK;
-}
-
-}  // namespace wgb
 
 namespace wgb {
 
@@ -1641,21 +1600,18 @@ extern "C" int wgb_sgemm(wgb_ctx *ctx, int transA, int transB, int64_t m, int64_
   return gemm_run<float>(ctx, 0, transA, transB, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc);
 }
 
-// wgb_sgemm's launches with the split-k partials in `scratch` (through the
-// per-device address looked up at wgb_init): no hipMalloc, hipFree or other
-// allocation on this path. Calls that overlap on one GPU share the array.
+// wgb_sgemm's launches with the split-k partials in the library's fixed
+// per-GPU array (noalloc.hip): no hipMalloc, hipFree or other allocation on
+// this path. Calls that overlap on one GPU share the array.
 extern "C" int wgb_sgemm_noalloc(wgb_ctx *ctx, int transA, int transB, int64_t m, int64_t n,
                                  int64_t k, float alpha, const float *A, int64_t lda,
                                  const float *B, int64_t ldb, float beta, float *C, int64_t ldc) {
   int st = wgb::enter(ctx);
   if (st) return st;
-  if (!ctx->noalloc_ws)
-    return wgb::fail(WGB_ERR_NOT_INITIALIZED,
-                     "the allocation-free GEMM workspace was not set up on this device");
   if ((st = check_gemm_args(0, false, transA, transB, m, n, k, A, lda, B, ldb, C, ldc))) return st;
   WsSource ws;
-  ws.ptr = ctx->noalloc_ws;
-  ws.bytes = kNoallocWsBytes;
+  if ((st = wgb::noalloc_workspace(ctx, &ws.ptr))) return st;
+  ws.bytes = wgb::kNoallocWsBytes;
   return gemm_run<float>(ctx, 0, transA, transB, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc, ws);
 }
 

@@ -20,7 +20,7 @@ CSRC = os.path.join(HERE, "csrc")
 LIBDIR = os.path.join(HERE, "lib")
 INCLUDE = os.path.join(ROOT, "include")
 
-HIP_SOURCES = ["runtime.hip", "reduce.hip", "gemm.hip", "level3.hip", "level2.hip"]
+HIP_SOURCES = ["runtime.hip", "reduce.hip", "gemm.hip", "level3.hip", "level2.hip", "noalloc.hip"]
 LIB_NAME = "libwgblas_hip.so"
 ADDON_NAME = "wgblas_hip.node"
 ARCH = os.environ.get("WGBLAS_OFFLOAD_ARCH", "gfx950")

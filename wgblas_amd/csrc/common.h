@@ -30,9 +30,6 @@ struct wgb_ctx {
   // its copy of B (grown on demand, reused in stream order).
   void *op_ws = nullptr;
   size_t op_ws_bytes = 0;
-  // Device address of the library's fixed split-k array on this context's
-  // device (wgb_sgemm_noalloc); null if its lookup failed at wgb_init.
-  void *noalloc_ws = nullptr;
   // Pinned host slot the host-result reductions copy their scalar into.
   void *host_result = nullptr;
   char name[256] = {0};
@@ -73,9 +70,11 @@ enum { kBandNone = 0, kBandALower = 1, kBandAUpper = 2, kBandBLower = 3, kBandBU
 int gemm_f32(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64_t n, int64_t k,
              float alpha, const float *A, int64_t lda, const float *B, int64_t ldb, float beta,
              float *C, int64_t ldc, int band);
-// Looks up the allocation-free GEMM workspace's address on ctx's device
-// (current on entry) and stores it in ctx->noalloc_ws (gemm.hip).
-int noalloc_setup(wgb_ctx *ctx);
+// wgb_sgemm_noalloc's fixed per-GPU split-k workspace (noalloc.hip): its
+// size, and its device address on ctx's device (current on entry), looked
+// up on the first call for that device.
+constexpr size_t kNoallocWsBytes = (size_t)32 << 20;
+int noalloc_workspace(wgb_ctx *ctx, void **ptr);
 // The GEMM entry points' argument checks.
 int check_gemm(int uplo, bool want_uplo, int transA, int transB, int64_t m, int64_t n, int64_t k,
                const void *A, int64_t lda, const void *B, int64_t ldb, const void *C,

@@ -123,9 +123,6 @@ extern "C" int wgb_init(int device, wgb_ctx **out) {
     wgb_destroy(ctx);
     return st;
   }
-  // wgb_sgemm_noalloc's workspace address on this device; a failed lookup
-  // leaves it null, which only that entry point reports.
-  if (wgb::noalloc_setup(ctx) != WGB_OK) ctx->noalloc_ws = nullptr;
   *out = ctx;
   return WGB_OK;
 }

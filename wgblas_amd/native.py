@@ -11,7 +11,8 @@ import os
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "lib", "libwgblas_hip.so")
+# WGBLAS_HIP_LIB points the binding at another build of the library.
+LIB_PATH = os.environ.get("WGBLAS_HIP_LIB") or os.path.join(_HERE, "lib", "libwgblas_hip.so")
 
 NO_TRANS, TRANS = 0, 1
 LOWER, UPPER = 1, 2

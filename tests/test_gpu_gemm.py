@@ -249,11 +249,10 @@ def test_small_kernel_shapes(ctx, ta, tb, shape):
 @pytest.mark.parametrize("ta", [0, 1])
 @pytest.mark.parametrize("case", [((4096, 4096, 64), "aligned"), ((4000, 4036, 70), "aligned"),
                                   ((4000, 4036, 70), "ldc_odd"), ((4000, 4036, 70), "beta0")])
-def test_wide_tier(ctx, ta, case):
-    # 256 x 128 tiles with 512 threads (both operands k-contiguous: ta = 1;
-    # aligned operands, at least two full rounds): interior and ragged tiles
-    # in m, n and k, the element-wise epilogue (ldc odd) and beta = 0; ta = 0
-    # runs the same shapes on the 128 tier
+def test_large_aligned_tier(ctx, ta, case):
+    # large aligned problems on the 128 tier (several full rounds, the LDS
+    # copy loop): interior and ragged tiles in m, n and k, the element-wise
+    # epilogue (ldc odd) and beta = 0
     (m, n, k), variant = case
     ldc = m + 1 if variant == "ldc_odd" else m
     beta = 0.0 if variant == "beta0" else 0.5

@@ -9,9 +9,8 @@
 // v_mfma_f64_16x16x4f64 for fp64, one template for both.
 //
 // Block: 256 threads = 4 waves in a 2x2 grid, block tile BT x BT of C
-// (BT = 128 large tier, 64 small tier; fp32 NN / TN layouts on large
-// problems: 256 x 128 tiles with 512 threads in a 4x2 grid), k-tile BK =
-// 128 bytes of k (32 floats / 16 doubles); tiny fp32 problems take a
+// (BT = 128 large tier, 64 small tier), k-tile BK = 128 bytes of k (32
+// floats / 16 doubles); tiny fp32 problems take a
 // one-launch kernel of 32x32 tiles (gemm_small_kernel). Each operand tile is
 // staged in LDS, double buffered, in the orientation it has in memory so the
 // global->LDS path is plain 16-byte copies (for 16-byte aligned operands,
@@ -548,8 +547,8 @@ __device__ __forceinline__ void copies_landed_sync() {
 
 // One BTM x BTN tile (tm, tn) of C over k-tiles [kt0, kt0 + nkt): the main
 // loop and the epilogue (unit >= 0: a split-k unit's raw partial to ws).
-// NT threads: 256 (2 x 2 waves) or 512 (4 x 2 waves); every wave owns a
-// square WT x WT part of the tile.
+// NT = 256 threads (2 x 2 waves); every wave owns a square WT x WT part of
+// the tile.
 template <typename T, int BTM, int BTN, int NT, bool AKC, bool BKC, bool VEC>
 __device__ __forceinline__ void gemm_tile(const GemmArgs<T> &p, int tm, int tn, int unit, int kt0,
                                           int nkt, T *smem, const int t) {
@@ -557,7 +556,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs<T> &p, int tm, int tn, 
   typedef typename Ty<T>::v16 V;
   constexpr int VW = Ty<T>::VW;
   constexpr int BK = 128 / (int)sizeof(T);
-  constexpr int WGM = NT == 512 ? 4 : 2;  // waves along m
+  static_assert(NT == 256, "2 x 2 waves per block");
+  constexpr int WGM = 2;  // waves along m
   constexpr int WT = BTM / WGM;
   static_assert(WT == BTN / (NT / 64 / WGM), "square wave tiles");
   constexpr int MB = WT / 16;
@@ -677,9 +677,16 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs<T> &p, int tm, int tn, 
           for (int i = 0; i < MB; ++i)
   #pragma unroll
             for (int j = 0; j < MB; ++j) acc[i][j] = Ty<T>::mfma(y[s][i], yb[s][j], acc[i][j]);
+        // The copies go out spread over the MFMAs: a burst of them right
+        // after the barrier backs up the L1 and stalls the wave on a copy
+        // (a timing-only copy without the steady-state copies ran 2.8%
+        // faster). 6 MFMAs per copy (8192^3, A/B on one box: NN 147.9 ->
+        // 149.0, NT 147.9 -> 149.0, TT 148.2 -> 149.0; 3 or 4 per copy the
+        // same within noise).
+        constexpr int kMfmaPerCopy = 6;
   #pragma unroll
         for (int g = 0; g < SA::LOADS + SB::LOADS; ++g) {
-          __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(kSchedMfma, kMfmaPerCopy, 0);
           __builtin_amdgcn_sched_group_barrier(kSchedVmemRead, 1, 0);
         }
   #pragma unroll
@@ -1223,29 +1230,6 @@ const void *small_kernel_for(int64_t k) {
   return reinterpret_cast<const void *>(gemm_small_kernel<AKC, BKC, 4>);
 }
 
-// fp32 with both operands k-contiguous (TN) and 16-byte aligned on large
-// problems: 256 x 128 tiles, 512 threads (4 x 2 waves, each the same 64 x 64
-// wave tile and loop as the 128 tier), one block per CU (96 KB of LDS). A
-// quarter fewer operand bytes per flop than two 128 x 128 blocks; measured
-// at 8192^3 (A/B on one box): TN 142.9 -> 147.8 TFLOP/s. With scalar-base
-// copies NN runs faster on the 128 tier (148.0 against 145.8), and NT / TT
-// were slower here (143.4 / 145.6 against 144.6 / 149.0). Full C only, no
-// split-k (the host sends shapes whose last round is over half full; the
-// rest take the 128 tier).
-constexpr int kWideThreads = 512;
-constexpr int kWideM = 256, kWideN = 128;
-template <bool AKC>
-__global__ __launch_bounds__(kWideThreads, 1) void gemm_wide_kernel(GemmArgs<float> p) {
-  typedef Stager<float, kWideM, AKC, true, kWideThreads> SA;
-  typedef Stager<float, kWideN, true, true, kWideThreads> SB;
-  __shared__ __attribute__((aligned(16))) float smem[2 * (SA::ELEMS + SB::ELEMS)];
-  int tm, tn;
-  logical_tile(xcd_remap(blockIdx.x, p.ntiles), p.tiles_m, p.tiles_n, 0, tm, tn);
-  const int nkt = (int)((p.k + 31) / 32);
-  gemm_tile<float, kWideM, kWideN, kWideThreads, AKC, true, true>(p, tm, tn, -1, 0, nkt, smem,
-                                                                 (int)threadIdx.x);
-}
-
 // C <- beta*C (or 0 when beta == 0) on the uplo part of the m x n C: the
 // alpha == 0 / k == 0 path, which reads neither A nor B.
 template <typename T>
@@ -1512,32 +1496,12 @@ int gemm_launch(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64
   }
   // VEC: 16-byte aligned operand vectors. That path copies k-tiles straight
   // into LDS with 32-bit lane offsets from the tile origin, which stay below
-  // 256 * ld * sizeof(T) (the widest tile); larger leading dimensions take
-  // the element-aligned register path (same results, same loads).
+  // 256 * ld * sizeof(T) (a tile spans at most 128 rows or k-rows of ld
+  // elements); larger leading dimensions take the element-aligned register
+  // path (same results, same loads).
   const int64_t off_cap = (int64_t)1 << 31;
   const bool offs32 = 256 * lda * (int64_t)sizeof(T) < off_cap && 256 * ldb * (int64_t)sizeof(T) < off_cap;
   const bool vec = (lda % VW == 0) && (ldb % VW == 0) && aligned16(A) && aligned16(B) && offs32;
-  if constexpr (sizeof(T) == 4) {
-    // The 256 x 128 tier: at least two full rounds of one block per CU and a
-    // last round over half full.
-    const int64_t twm = (m + kWideM - 1) / kWideM, twn = (n + kWideN - 1) / kWideN;
-    const int64_t tw = twm * twn;
-    if (vec && akc && bkc && uplo == 0 && band == wgb::kBandNone && tw >= 2 * fill &&
-        (tw % fill == 0 || 2 * (tw % fill) > fill) && tw <= INT32_MAX) {
-      a.tiles_m = (int)twm;
-      a.tiles_n = (int)twn;
-      a.ntiles = (int)tw;
-      a.nregular = a.ntiles;
-      a.splits = 1;
-      a.kt_split = (int)((k + 31) / 32);
-      a.ws = nullptr;
-      void *args[] = {&a};
-      const void *fn = reinterpret_cast<const void *>(gemm_wide_kernel<true>);
-      WGB_CHECK_HIP(hipLaunchKernel(fn, dim3((unsigned)tw), dim3(kWideThreads), args, 0, ctx->stream));
-      WGB_CHECK_LAUNCH("gemm_wide_kernel");
-      return WGB_OK;
-    }
-  }
   // Large tier once the 128-tiles alone fill the chip; small tier otherwise.
   auto count = [&](int64_t bt, int64_t &tmn, int64_t &tnn) {
     tmn = (m + bt - 1) / bt;

@@ -205,12 +205,17 @@ def bench_components(ctx, ev, quick):
     buf = ctx.empty(3 * n * n, np.float64)
     ctx.fill_uniform(buf, -1.0, 1.0, 3)
     A, B, Cm = buf.offset(0), buf.offset(n * n), buf.offset(2 * n * n)
-    f = lambda: ctx.dgemm(NO_TRANS, TRANS, n, n, n, 1.0, A, n, B, n, 1.0, Cm, n)
-    f()
-    ms = per_launch_ms(ctx, f, reps)
     fl = 2.0 * n ** 3
+    per = {}
+    # the configured NT first, then the other layouts on the same buffers
+    for ta, tb in ((NO_TRANS, TRANS), (NO_TRANS, NO_TRANS), (TRANS, NO_TRANS), (TRANS, TRANS)):
+        f = lambda: ctx.dgemm(ta, tb, n, n, n, 1.0, A, n, B, n, 1.0, Cm, n)
+        f()
+        ms = per_launch_ms(ctx, f, reps)
+        per["NT"[ta] + "NT"[tb]] = {"ms": ms, "tflops": fl / ms / 1e9}
+    ms = per["NT"]["ms"]
     comps["dgemm_4096"] = {"ms": ms, "tflops": fl / ms / 1e9, "frac_fp64_peak": fl / ms / 1e-3 / PEAK_FP64,
-                           "traffic_bytes": load_traffic("dgemm_4096")}
+                           "traffic_bytes": load_traffic("dgemm_4096"), "per_layout": per}
     buf.free()
 
     # config 5: ssyrk lower, n = 8192, k = 4096, alpha 1, beta 0.25, 10 chained

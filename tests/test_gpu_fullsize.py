@@ -1,6 +1,6 @@
 """Parity at the full sizes of the benchmark configurations (wgblas's
 benchmarks/*/wgblas/*.js: sgemm 512^3, sgemm 8192^3 in all four layouts,
-the ragged 8191 x 8193 x 4097 case, dgemm 4096^3, ten chained ssyrk calls at
+the ragged 8191 x 8193 x 4097 case, dgemm 4096^3 in all four layouts, ten chained ssyrk calls at
 8192 x 4096; the reductions' full sizes are in test_gpu_level1.py).
 
 The inputs are the seeded device-generated ones bench.py times (their
@@ -66,18 +66,20 @@ def test_config3_sgemm_ragged_ld(ctx, ta, tb):
                      1.5, 0.5, k, rows=(127, 128, 8063, 8064, 8190), cols=(127, 128, 8192), seed=7)
 
 
-def test_config4_dgemm_4096(ctx):
+@pytest.mark.parametrize("ta,tb", [(0, 1), (0, 0), (1, 0), (1, 1)])
+def test_config4_dgemm_4096(ctx, ta, tb):
+    # (0, 1) is config 4 itself; the other layouts run their own kernels
     n = 4096
     buf = ctx.empty(3 * n * n, np.float64)
     ctx.fill_uniform(buf, -1.0, 1.0, 3)
     host = buf.to_host()
-    ctx.dgemm(0, 1, n, n, n, 1.0, buf.offset(0), n, buf.offset(n * n), n, 1.0, buf.offset(2 * n * n), n)
+    ctx.dgemm(ta, tb, n, n, n, 1.0, buf.offset(0), n, buf.offset(n * n), n, 1.0, buf.offset(2 * n * n), n)
     C = buf.to_host()[2 * n * n:]
     buf.free()
     A, B, C0 = host[:n * n], host[n * n:2 * n * n], host[2 * n * n:]
-    check_gemm_props(cm_view(C, n, n, n), cm_view(C0, n, n, n), cm_view(A, n, n, n),
-                     cm_view(B, n, n, n).T, 1.0, 1.0, n, eps=EPS_DD, kterm=2, cterm=3.0,
-                     rows=(127, 128, 2047, 2048), cols=(127, 128, 2047, 2048), seed=3)
+    check_gemm_props(cm_view(C, n, n, n), cm_view(C0, n, n, n), op(cm_view(A, n, n, n), ta),
+                     op(cm_view(B, n, n, n), tb), 1.0, 1.0, n, eps=EPS_DD, kterm=2, cterm=3.0,
+                     rows=(127, 128, 2047, 2048), cols=(127, 128, 2047, 2048), seed=3 + 4 * ta + 2 * tb)
 
 
 def test_config5_ssyrk_chained(ctx):

@@ -405,6 +405,29 @@ def test_strsm_large_round_trip(ctx, side, uplo, trans):
     assert np.max(np.abs(back - want)) <= 1e-4 * np.max(np.abs(want))
 
 
+@pytest.mark.parametrize("side,uplo,trans", list(itertools.product([1, 2], [1, 2], [0, 1])))
+def test_strsm_many_right_hand_sides(ctx, side, uplo, trans):
+    # 4100 right-hand sides: past 4096 each solve lane carries two of them.
+    # Order 300 (diagonal blocks of 128, 128 and 44, GEMM updates between):
+    # the residual bound. Order 100 (one padded diagonal block, no GEMM):
+    # every right-hand side's solution is bit-equal to solving it among only
+    # 100 (one per lane), since a right-hand side's operations do not depend
+    # on how many are solved together.
+    other = 4100
+    for order in (300, 100):
+        m, n = (order, other) if side == 1 else (other, order)
+        lda, ldb = order + 2, m + 1
+        A = orc.random_f32(lda * order, -1.0 / order, 1.0 / order, 15)
+        A[np.arange(order) * (lda + 1)] = 2.0
+        B = orc.random_f32(ldb * n, -1, 1, 16)
+        X = check_trsm(ctx, (side, uplo, trans, 0, m, n, 0.75, A, lda, B, ldb))
+    ms, ns = (order, 100) if side == 1 else (100, order)
+    Bs = np.asarray(rc.dense_op(B, m, n, ldb, 0)[:ms, :ns], F32).reshape(-1, order="F")
+    Xs = run_trsm(ctx, (side, uplo, trans, 0, ms, ns, 0.75, A, lda, Bs, ms))
+    Xd = np.asarray(rc.dense_op(X, m, n, ldb, 0)[:ms, :ns], F32).reshape(-1, order="F")
+    assert bits_equal(Xs, Xd)
+
+
 # ------------------------------------------- operands of different storage orders
 def _cm_transpose(X, rows, cols, ld):
     """Column-major rows x cols (leading dimension ld) -> its transpose as a

@@ -8,13 +8,17 @@
 //   cannot read and write B at once), then one GEMM whose tiles only run the
 //   k-tiles the triangle reaches (about half the flops of a dense product).
 // strsm: recursive halving of the triangular dimension. Diagonal blocks of
-//   order <= 128 are solved by substitution, one lane per right-hand side,
-//   eight waves splitting its unknowns; the off-diagonal updates are GEMMs that
+//   order <= 128 are solved by substitution, 16 lanes per right-hand side
+//   exchanging solved unknowns by DPP broadcasts; the off-diagonal updates are GEMMs that
 //   read the solved rows of B and write other rows of B in place (disjoint
-//   memory), so strsm needs no workspace and no explicit inverse.
+//   memory). The diagonal blocks are packed once per call into the operand
+//   workspace; no explicit inverse is formed.
 #include "common.h"
 
 #include <hip/hip_runtime.h>
+
+#include <type_traits>
+#include <utility>
 
 #include "wgblas_hip.h"
 
@@ -123,144 +127,195 @@ __global__ __launch_bounds__(256) void triangle_copy_kernel(int64_t order,
   }
 }
 
+// Compile-time loop: f(std::integral_constant<int, I>{}) for I = 0 .. N-1.
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F &&f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// Lane L of every 16-lane row of the wave, copied to the row's 16 lanes
+// (DPP row_newbcast).
+template <int L>
+__device__ __forceinline__ float row_bcast(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x150 + L, 0xf, 0xf, false));
+}
+
+// strsm's diagonal blocks in the layout trsm_leaf_kernel stages in LDS: the
+// solve frame splits into blocks of kLeaf rows (the last one nb < kLeaf
+// rows), and block l's image is kImg floats at P + l kImg: P[k kLeaf + i] =
+// M(i, k) for k < i < nb (zero elsewhere, the diagonal included), then
+// P[kLeaf^2 + k] = 1 / M(k, k) (1 for a unit diagonal and for padding rows).
+// Frame element (i, k) of block l's M is Ablk[ia(i) mi + ia(k) mk], Ablk at
+// A + kLeaf l (1 + lda), where ia(i) = nb-1-i for an upper system solved
+// backward (rev) and i otherwise. Block (l, c) packs columns 16c .. 16c+15 of
+// image l through an LDS tile: read with the stride-1 index fastest, written
+// with i fastest. The diagonal's reciprocals are formed once here: x * RN(1/d)
+// is within two ulps of x / d, and zero, infinite and NaN diagonals give the
+// quotient's special values (only a diagonal below 2^-126 in magnitude, whose
+// reciprocal overflows, differs).
+constexpr int kImg = kLeaf * kLeaf + kLeaf;
+
+__global__ __launch_bounds__(256) void trsm_pack_kernel(int64_t order, const float *__restrict__ A,
+                                                        int64_t lda, int64_t mi, int64_t mk, int rev,
+                                                        int unit, float *__restrict__ P) {
+  __shared__ float T[16][kLeaf + 1];
+  const int t = threadIdx.x, c = blockIdx.y;
+  const int64_t l = blockIdx.x, lo = l * kLeaf;
+  const int nb = (int)(order - lo < kLeaf ? order - lo : kLeaf);
+  const float *Ablk = A + lo + lo * lda;
+  const bool kfast = mk == 1;  // consecutive k are adjacent in memory
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const int e = t + 256 * q;
+    const int i = kfast ? e / 16 : e % kLeaf, kl = kfast ? e % 16 : e / kLeaf;
+    const int k = 16 * c + kl;
+    const bool in = i < nb && k <= i;
+    const int64_t ii = in ? (rev ? nb - 1 - i : i) : 0, kk = in ? (rev ? nb - 1 - k : k) : 0;
+    const float v = Ablk[ii * mi + kk * mk];
+    T[kl][i] = in ? v : 0.f;
+  }
+  __syncthreads();
+  float *img = P + l * kImg;
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const int e = t + 256 * q;
+    const int i = e % kLeaf, kl = e / kLeaf, k = 16 * c + kl;
+    img[k * kLeaf + i] = i > k ? T[kl][i] : 0.f;
+  }
+  if (t < 16) {
+    const int k = 16 * c + t;
+    img[kLeaf * kLeaf + k] = 1.f / ((unit || k >= nb) ? 1.f : T[t][k]);
+  }
+}
+
 // Substitution solve of one diagonal block, in the solve frame: for every
-// right-hand side v, M x = alpha v with M lower triangular of order nb <= NB.
-// Frame element (i, k) of M is Ablk[ia(i) mi + ia(k) mk] and element i of
+// right-hand side v, M x = alpha v with M lower triangular of order
+// nb <= kLeaf, given as its image `img` (trsm_pack_kernel). Element i of
 // right-hand side r is Bblk[ia(i) vi + r vr], where ia(i) = nb-1-i for an
 // upper system solved backward (rev) and i otherwise; the solution
 // overwrites v.
 //
-// A block takes 64 right-hand sides, one per lane, and its NB / 16 waves
-// each own 16 consecutive rows of them in registers. Chunk c: wave c
-// substitutes through its rows (x_k *= 1/M(k,k), then x_i -= M(i,k) x_k for
-// its later rows: the column-oriented order of wgblas's strsm_small.wgsl and
-// of reference BLAS) and publishes them to LDS; after one barrier every later
-// wave subtracts the chunk's contribution from its rows. M's entries are LDS
-// broadcasts and the block needs one barrier per chunk. The diagonal's
-// reciprocals are formed once per block: x * RN(1/d) is within two ulps of
-// x / d, and zero, infinite and NaN diagonals give the quotient's special
-// values (only a diagonal below 2^-126 in magnitude, whose reciprocal
-// overflows, differs). alpha is applied as v is read. Rows past nb are
-// padding with a unit diagonal and zero right-hand side; they never feed real
-// rows. Loads are unconditional, from addresses clamped into the block, so
-// that all of them are in flight together (a guarded load is waited for
-// before the next one issues).
-template <int NB>
-__global__ __launch_bounds__(4 * NB) void trsm_leaf_kernel(int nb, int64_t nrhs,
-                                                          const float *__restrict__ Ablk, int64_t mi,
-                                                          int64_t mk, int rev, int unit,
-                                                          float *__restrict__ Bblk, int64_t vi,
-                                                          int64_t vr, float alpha) {
-  constexpr int kThreadsLeaf = 4 * NB;       // NB / 16 waves
-  constexpr int kSplit = NB / 16;            // waves = row chunks
-  constexpr int kRows = 16;                  // rows per wave
-  constexpr int kPer = NB * NB / kThreadsLeaf;
-  constexpr int kGroups = kThreadsLeaf / NB;  // left-side staging: column groups (4)
-  constexpr int kCols = 64 / kGroups;         // right-hand sides per column group (16)
-  static_assert(kCols == kRows, "one staging register set serves both sides");
-  __shared__ __attribute__((aligned(16))) float Ms[NB * NB];  // Ms[k*NB + i] = M(i, k)
-  __shared__ float Xs[NB][65];                                // Xs[i][rhs]
-  __shared__ float Rd[NB];                                    // 1 / M(k, k)
+// Each 16-lane row of a wave owns R right-hand sides; lane j of the row
+// holds frame rows j, j+16, ..., j+112 of them in registers (x[h][g] is row
+// 16g + j of right-hand side h). Step k, in the column-oriented order of
+// wgblas's strsm_small.wgsl and of reference BLAS: x_k = x_k * (1 / M(k,k)),
+// computed by every lane on its register of row k's group and broadcast from
+// lane k % 16 across the row; then every lane subtracts M(i,k) x_k from each
+// of its rows i (one fused multiply-add each). A wave solves its right-hand
+// sides alone, with no barrier. The image sits in LDS (Ms[k*kLeaf + i] =
+// M(i,k), zero for i <= k); the rows i <= k that step k also touches are
+// already solved (their values were kept in s at their own step), so what
+// the update leaves there is never read. Per row the operations are those of
+// substitution: the products are subtracted in k order, then the row is
+// scaled by the diagonal's reciprocal. alpha is applied as v is read. Rows
+// past nb are padding with a unit diagonal and zero right-hand side; they
+// never feed real rows. Loads are unconditional, from addresses clamped into
+// the block, so that all of them are in flight together.
+template <int R>
+__global__ __launch_bounds__(256) void trsm_leaf_kernel(int nb, int64_t nrhs,
+                                                       const float *__restrict__ img, int rev,
+                                                       float *__restrict__ Bblk, int64_t vi,
+                                                       int64_t vr, float alpha) {
+  constexpr int NB = kLeaf, kG = NB / 16, kV = NB * NB / 4 / 256;
+  __shared__ float4 img_s[kImg / 4];
+  float *Ms = reinterpret_cast<float *>(img_s), *Rd = Ms + NB * NB;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int row0 = wave * kRows;
-  const int64_t rhs0 = (int64_t)blockIdx.x * 64;
-  const int64_t r = rhs0 + lane;  // this lane's right-hand side
-  const bool left = vi == 1;      // the frame index is B's contiguous one
-  const int si = t % NB, sg = t / NB;  // left-side staging: frame index, column group
+  const int j = lane & 15;
+  // right-hand sides r0 .. r0 + R - 1 of this lane's row
+  const int64_t r0 = ((int64_t)blockIdx.x * 16 + wave * 4 + (lane >> 4)) * R;
 
-  // ---- every global load first
-  float mv[kPer];
+  // ---- every global load first: the image, 16-byte aligned (kImg is a
+  // multiple of 4 and the workspace is 256-byte aligned), then B
+  const float4 *img4 = reinterpret_cast<const float4 *>(img);
+  float4 mv[kV];
 #pragma unroll
-  for (int q = 0; q < kPer; ++q) {
-    const int e = t + q * kThreadsLeaf;
-    const int i = e % NB, k = e / NB;
-    const bool in = i < nb && k <= i;
-    const int ii = in ? (rev ? nb - 1 - i : i) : 0, kk = in ? (rev ? nb - 1 - k : k) : 0;
-    mv[q] = Ablk[ii * mi + kk * mk];
-  }
-  // left: thread (si, sg) loads frame index si of right-hand sides sg,
-  // sg + kGroups, ...; right: lane = right-hand side, wave w its 16 rows
-  float bv[kRows];
+  for (int q = 0; q < kV; ++q) mv[q] = img4[t + 256 * q];
+  const float4 rv = img4[NB * NB / 4 + (t & (NB / 4 - 1))];
+  float x[R][kG];
 #pragma unroll
-  for (int q = 0; q < kRows; ++q) {
-    int64_t at;
-    if (left) {
-      const int64_t rc = rhs0 + sg + q * kGroups;
-      at = (si < nb ? (rev ? nb - 1 - si : si) : 0) + (rc < nrhs ? rc : 0) * vr;
-    } else {
-      const int i = row0 + q;
-      at = (int64_t)(i < nb ? (rev ? nb - 1 - i : i) : 0) * vi + (r < nrhs ? r : 0);
-    }
-    bv[q] = Bblk[at];
-  }
-
-  // ---- M (zero above the diagonal, unit diagonal for padding rows) and
-  // the reciprocals of its diagonal into LDS
+  for (int h = 0; h < R; ++h) {
+    const int64_t r = r0 + h < nrhs ? r0 + h : 0;
 #pragma unroll
-  for (int q = 0; q < kPer; ++q) {
-    const int e = t + q * kThreadsLeaf;
-    const int i = e % NB, k = e / NB;
-    const bool in = i < nb && k <= i;
-    const float v = i == k ? ((unit || !in) ? 1.f : mv[q]) : (in ? mv[q] : 0.f);
-    Ms[e] = v;
-    if (i == k) Rd[k] = 1.f / v;
-  }
-  float x[kRows];
-  if (left) {
-#pragma unroll
-    for (int q = 0; q < kRows; ++q) {
-      const int c = sg + q * kGroups;
-      Xs[si][c] = (si < nb && rhs0 + c < nrhs) ? bv[q] : 0.f;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < kRows; ++j) x[j] = alpha * Xs[row0 + j][lane];
-  } else {
-#pragma unroll
-    for (int j = 0; j < kRows; ++j) x[j] = (r < nrhs && row0 + j < nb) ? alpha * bv[j] : 0.f;
-  }
-  __syncthreads();  // Ms and Rd complete; every read of the staged block done
-
-  // ---- chunked substitution
-  for (int c = 0; c < kSplit; ++c) {  // block-uniform chunk loop
-    if (wave == c) {
-#pragma unroll
-      for (int j = 0; j < kRows; ++j) {
-        const int k = row0 + j;
-        x[j] = x[j] * Rd[k];
-#pragma unroll
-        for (int jj = j + 1; jj < kRows; ++jj) x[jj] = fmaf(-Ms[k * NB + row0 + jj], x[j], x[jj]);
-        Xs[k][lane] = x[j];
-      }
-    }
-    __syncthreads();
-    if (wave > c) {
-#pragma unroll 4
-      for (int kk = 0; kk < kRows; ++kk) {
-        const int k = c * kRows + kk;
-        const float xk = Xs[k][lane];
-#pragma unroll
-        for (int j = 0; j < kRows; ++j) x[j] = fmaf(-Ms[k * NB + row0 + j], xk, x[j]);
-      }
+    for (int g = 0; g < kG; ++g) {
+      const int i = 16 * g + j;
+      x[h][g] = Bblk[(int64_t)(i < nb ? (rev ? nb - 1 - i : i) : 0) * vi + r * vr];
     }
   }
 
-  // ---- write back (Xs holds every solved row: the last chunk was
-  // published before the loop's final barrier)
-  if (left) {
-    const bool ok = si < nb;
-    const int64_t at = rev ? nb - 1 - si : si;
 #pragma unroll
-    for (int q = 0; q < kRows; ++q) {
-      const int c = sg + q * kGroups;
-      const int64_t rc = rhs0 + c;
-      if (ok && rc < nrhs) Bblk[at + rc * vr] = Xs[si][c];
+  for (int q = 0; q < kV; ++q) img_s[t + 256 * q] = mv[q];
+  if (t < NB / 4) img_s[NB * NB / 4 + t] = rv;
+#pragma unroll
+  for (int h = 0; h < R; ++h)
+#pragma unroll
+    for (int g = 0; g < kG; ++g)
+      x[h][g] = (r0 + h < nrhs && 16 * g + j < nb) ? alpha * x[h][g] : 0.f;
+  __syncthreads();
+
+  // ---- substitution, one row-group of 16 steps at a time
+  float s[R][kG];
+#pragma unroll
+  for (int h = 0; h < R; ++h)
+#pragma unroll
+    for (int g = 0; g < kG; ++g) s[h][g] = 0.f;
+  // M's entries are read kD steps ahead of their use (each step pinned in
+  // place by a scheduling barrier, so the reads stay ahead), the group's
+  // reciprocals at its start.
+  constexpr int kD = 4;
+  static_for<kG>([&](auto gc) {
+    constexpr int g = decltype(gc)::value;
+    if (16 * g < nb) {  // block-uniform: groups past nb are padding
+      float rd[16], mb[kD][kG - g];
+#pragma unroll
+      for (int l = 0; l < 16; ++l) rd[l] = Rd[16 * g + l];
+#pragma unroll
+      for (int l = 0; l < kD; ++l)
+#pragma unroll
+        for (int gg = g; gg < kG; ++gg) mb[l][gg - g] = Ms[(16 * g + l) * NB + 16 * gg + j];
+      static_for<16>([&](auto lc) {
+        constexpr int l = decltype(lc)::value, k = 16 * g + l;
+        float mik[kG - g];
+#pragma unroll
+        for (int gg = 0; gg < kG - g; ++gg) mik[gg] = mb[l % kD][gg];
+        if constexpr (l + kD < 16) {
+#pragma unroll
+          for (int gg = g; gg < kG; ++gg) mb[l % kD][gg - g] = Ms[(k + kD) * NB + 16 * gg + j];
+        }
+        float xk[R];
+#pragma unroll
+        for (int h = 0; h < R; ++h) {
+          xk[h] = row_bcast<l>(x[h][g] * rd[l]);
+          s[h][g] = j == l ? xk[h] : s[h][g];
+        }
+#pragma unroll
+        for (int gg = g; gg < kG; ++gg)
+#pragma unroll
+          for (int h = 0; h < R; ++h) {
+            x[h][gg] = fmaf(-mik[gg - g], xk[h], x[h][gg]);
+            // keeps the update in this step: otherwise it is sunk to the
+            // start of group gg, where the updates form one dependent chain
+            asm volatile("" : "+v"(x[h][gg]));
+          }
+#pragma unroll
+        for (int h = 0; h < R; ++h) asm volatile("" : "+v"(s[h][g]));
+        __builtin_amdgcn_sched_barrier(0);
+      });
     }
-  } else if (r < nrhs) {
+  });
+
+  // ---- write back
 #pragma unroll
-    for (int j = 0; j < kRows; ++j) {
-      const int i = row0 + j;
-      if (i < nb) Bblk[(int64_t)(rev ? nb - 1 - i : i) * vi + r] = x[j];
+  for (int h = 0; h < R; ++h) {
+    if (r0 + h >= nrhs) continue;
+#pragma unroll
+    for (int g = 0; g < kG; ++g) {
+      const int i = 16 * g + j;
+      if (i < nb) Bblk[(int64_t)(rev ? nb - 1 - i : i) * vi + (r0 + h) * vr] = s[h][g];
     }
   }
 }
@@ -277,22 +332,42 @@ struct Trsm {
   int64_t lda;
   float *B;
   int64_t ldb;
+  float *img;  // packed diagonal blocks (trsm_pack)
 };
 
 int trsm_leaf(const Trsm &p, int64_t lo, int64_t nb, float alpha) {
-  const bool m_is_a = p.left != p.trans;  // M is A itself, else A^T
-  const float *Ablk = p.A + lo + lo * p.lda;
-  const int64_t mi = m_is_a ? 1 : p.lda, mk = m_is_a ? p.lda : 1;
+  const float *img = p.img + lo / kLeaf * kImg;
   const int64_t nrhs = p.left ? p.n : p.m;
-  const int64_t grid = (nrhs + 63) / 64;
   const int rev = p.forward ? 0 : 1;
   // left: frame index = row of B (stride 1), right-hand side = column;
   // right: frame index = column of B, right-hand side = row
   float *Bblk = p.left ? p.B + lo : p.B + lo * p.ldb;
   const int64_t vi = p.left ? 1 : p.ldb, vr = p.left ? p.ldb : 1;
-  trsm_leaf_kernel<kLeaf><<<(unsigned)grid, 4 * kLeaf, 0, p.ctx->stream>>>(
-      (int)nb, nrhs, Ablk, mi, mk, rev, p.unit, Bblk, vi, vr, alpha);
+  // Up to 4096 right-hand sides each 16-lane row takes one (1024 waves: one
+  // per SIMD), beyond that two (half as many LDS reads per solved value).
+  if (nrhs > 4096)
+    trsm_leaf_kernel<2><<<(unsigned)((nrhs + 31) / 32), 256, 0, p.ctx->stream>>>(
+        (int)nb, nrhs, img, rev, Bblk, vi, vr, alpha);
+  else
+    trsm_leaf_kernel<1><<<(unsigned)((nrhs + 15) / 16), 256, 0, p.ctx->stream>>>(
+        (int)nb, nrhs, img, rev, Bblk, vi, vr, alpha);
   WGB_CHECK_LAUNCH("trsm_leaf_kernel");
+  return WGB_OK;
+}
+
+// Packs every diagonal block of the solve frame into p.img (the context's
+// operand workspace).
+int trsm_pack(Trsm &p) {
+  const int64_t order = p.left ? p.m : p.n;
+  const int64_t nblk = (order + kLeaf - 1) / kLeaf;
+  int st = wgb::ensure_op_workspace(p.ctx, (size_t)nblk * kImg * sizeof(float));
+  if (st) return st;
+  p.img = static_cast<float *>(p.ctx->op_ws);
+  const bool m_is_a = p.left != p.trans;  // M is A itself, else A^T
+  const int64_t mi = m_is_a ? 1 : p.lda, mk = m_is_a ? p.lda : 1;
+  trsm_pack_kernel<<<dim3((unsigned)nblk, kLeaf / 16), 256, 0, p.ctx->stream>>>(
+      order, p.A, p.lda, mi, mk, p.forward ? 0 : 1, p.unit, p.img);
+  WGB_CHECK_LAUNCH("trsm_pack_kernel");
   return WGB_OK;
 }
 
@@ -491,7 +566,7 @@ extern "C" int wgb_strsm(wgb_ctx *ctx, int side, int uplo, int transA, int diag,
     p.lda = lda;
     p.B = B;
     p.ldb = ldb;
-    st = trsm_solve(p, 0, p.left ? m : n, false);
+    if (!(st = trsm_pack(p))) st = trsm_solve(p, 0, p.left ? m : n, false);
   }
   if (st) return st;
   wgb::timing_end(ctx);

@@ -3,12 +3,15 @@
 It runs wgb_sgemm's launches with the split-k partials in the library's fixed
 per-GPU array instead of the context's hipMalloc'd workspace, so on the same
 inputs it must return wgb_sgemm's bits exactly. The shapes put the launch on
-the split-k path on an MI355X (256 CUs, two resident 128-tiles per CU):
-  * 2048 x 2048 x 1024: 256 tiles of 128 on 512 slots, every tile in 2
-    k-slices, 512 slices = the whole 32 MiB array;
+the split-k path on an MI355X (256 CUs, two resident 128-tiles per CU, 512
+slots: a round of whole tiles, then a tail at most half a round):
+  * 3072 x 4096 x 1024: 768 tiles, the last 256 in 2 k-slices each, 512
+    slices = the whole 32 MiB array;
+  * 3071 x 3073 x 1777, ldc padded: 600 tiles, the last 88 in 5 slices, edge
+    tiles and a partial k-tile in a slice;
   * 2944 x 2944 x 2048: 529 tiles, the last 17 in 16 k-slices each (17 MiB);
-  * 1024 x 1024 x 2048: 64-tiles (256 of them), split on the small tier;
-  * 1999 x 2001 x 777, ldc padded: edge tiles and a partial k-tile in a slice.
+  * 2900 x 2950 x 1500, ldc padded, beta = 1: 552 tiles, the last 40 in 10
+    slices.
 Each case is two calls in a row on the one array, the second with a smaller
 input, so the second call runs over whatever the first left in the array.
 Every result is also checked on sampled columns against a float64 product
@@ -90,8 +93,8 @@ def _run_pair(ctx, ta, tb, m, n, k, alpha, beta, ldc, seed):
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 def test_noalloc_matches_sgemm_two_calls(ctx, ta, tb):
     # first call: the whole array (512 slices of 64 KiB); second, smaller:
-    # 64-tiles split on the small tier
-    for (m, n, k, ldc, seed) in [(2048, 2048, 1024, 2048, 31), (1024, 1024, 2048, 1024, 32)]:
+    # 440 slices with edge tiles and a partial k-tile
+    for (m, n, k, ldc, seed) in [(3072, 4096, 1024, 3072, 31), (3071, 3073, 1777, 3072, 32)]:
         print(f"noalloc case ta={ta} tb={tb} {m}x{n}x{k}", flush=True)
         _run_pair(ctx, ta, tb, m, n, k, 1.5, 0.5, ldc, seed)
 
@@ -99,10 +102,10 @@ def test_noalloc_matches_sgemm_two_calls(ctx, ta, tb):
 @pytest.mark.parametrize("ta,tb", [(0, 1), (1, 0)])
 def test_noalloc_tail_split_then_ragged(ctx, ta, tb):
     # 529 tiles (17 tail tiles in 16 slices), then a smaller ragged problem
-    # with a padded ldc, beta = 1 and a partial k-tile
-    print(f"noalloc case ta={ta} tb={tb} 2944^2x2048 then 1999x2001x777", flush=True)
+    # with a padded ldc, beta = 1 and a partial k-tile (40 tail tiles in 10)
+    print(f"noalloc case ta={ta} tb={tb} 2944^2x2048 then 2900x2950x1500", flush=True)
     _run_pair(ctx, ta, tb, 2944, 2944, 2048, 1.0, 0.25, 2944, 33)
-    _run_pair(ctx, ta, tb, 1999, 2001, 777, -0.75, 1.0, 2000, 34)
+    _run_pair(ctx, ta, tb, 2900, 2950, 1500, -0.75, 1.0, 2901, 34)
 
 
 def test_noalloc_paths_without_split(ctx):

@@ -1351,11 +1351,16 @@ struct WsSource {
 };
 
 // Launches one GEMM on a BT tier. Tiles fill `slots` = CUs x resident blocks
-// per round; when the last round is at most half full, its tiles are split
-// along k into up to 16 units (at least 4 k-tiles each) so the last round is
-// as full as the rest, and split_fixup combines the partials in split order.
-// The partials of rem tail tiles in S splits take rem * S <= slots tiles of
-// workspace.
+// per round; when at least one full round precedes a last round that is at
+// most half full, and the tiles have at least 32 k-tiles, the last round's
+// tiles are split along k into up to 16 units (at least 4 k-tiles each) so
+// that round is as full as the rest, and split_fixup combines the partials
+// in split order. A launch of one partial round, or a short k, runs
+// unsplit: the fixup rereads and rewrites every tail tile through HBM, which
+// cost more than the idle slots did (measured: 1024^3 77 against 61
+// TFLOP/s split, 1024 x 4096 x 1024 102 against 89, strsm 4096 69 against
+// 61). The partials of rem tail tiles in S splits take rem * S <= slots
+// tiles of workspace.
 template <typename T, int BT>
 int launch_tier(wgb_ctx *ctx, GemmArgs<T> &a, bool akc, bool bkc, bool vec, WsSource wsrc) {
   constexpr int BK = 128 / (int)sizeof(T);
@@ -1375,7 +1380,7 @@ int launch_tier(wgb_ctx *ctx, GemmArgs<T> &a, bool akc, bool bkc, bool vec, WsSo
   a.kt_split = (int)nkt;
   a.ws = nullptr;
   const int64_t rem = a.ntiles % slots;
-  if (a.band == wgb::kBandNone && rem > 0 && 2 * rem <= slots) {
+  if (a.band == wgb::kBandNone && a.ntiles > slots && rem > 0 && 2 * rem <= slots && nkt >= 32) {
     int64_t S = slots / rem;
     if (S > 16) S = 16;
     if (S > nkt / 4) S = nkt / 4;

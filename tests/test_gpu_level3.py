@@ -408,8 +408,8 @@ def test_strsm_large_round_trip(ctx, side, uplo, trans):
 @pytest.mark.parametrize("side,uplo,trans", list(itertools.product([1, 2], [1, 2], [0, 1])))
 def test_strsm_many_right_hand_sides(ctx, side, uplo, trans):
     # 4100 right-hand sides: past 4096 each solve lane carries two of them.
-    # Order 300 (diagonal blocks of 128, 128 and 44, GEMM updates between):
-    # the residual bound. Order 100 (one padded diagonal block, no GEMM):
+    # Order 300 (diagonal blocks of 256 and 44, a GEMM update between): the
+    # residual bound. Order 100 (one padded diagonal block, no GEMM):
     # every right-hand side's solution is bit-equal to solving it among only
     # 100 (one per lane), since a right-hand side's operations do not depend
     # on how many are solved together.

@@ -8,7 +8,7 @@
 //   cannot read and write B at once), then one GEMM whose tiles only run the
 //   k-tiles the triangle reaches (about half the flops of a dense product).
 // strsm: recursive halving of the triangular dimension. Diagonal blocks of
-//   order <= 128 are solved by substitution, 16 lanes per right-hand side
+//   order <= 256 are solved by substitution, 16 lanes per right-hand side
 //   exchanging solved unknowns by DPP broadcasts; the off-diagonal updates are GEMMs that
 //   read the solved rows of B and write other rows of B in place (disjoint
 //   memory). The diagonal blocks are packed once per call into the operand
@@ -27,7 +27,8 @@ namespace {
 using wgb::fail;
 
 constexpr int kTile = 64;  // symmetrize tile (64 x 64)
-constexpr int kLeaf = 128;  // order of strsm's substitution blocks
+constexpr int kLeaf = 256;  // order of strsm's substitution blocks
+typedef float Vec4 __attribute__((ext_vector_type(4)));  // a native 16-byte vector
 
 int64_t imax(int64_t a, int64_t b) { return a > b ? a : b; }
 int64_t round4(int64_t v) { return (v + 3) / 4 * 4; }
@@ -169,8 +170,9 @@ __global__ __launch_bounds__(256) void trsm_pack_kernel(int64_t order, const flo
   const int nb = (int)(order - lo < kLeaf ? order - lo : kLeaf);
   const float *Ablk = A + lo + lo * lda;
   const bool kfast = mk == 1;  // consecutive k are adjacent in memory
+  constexpr int kQ = 16 * kLeaf / 256;  // elements per thread
 #pragma unroll
-  for (int q = 0; q < 8; ++q) {
+  for (int q = 0; q < kQ; ++q) {
     const int e = t + 256 * q;
     const int i = kfast ? e / 16 : e % kLeaf, kl = kfast ? e % 16 : e / kLeaf;
     const int k = 16 * c + kl;
@@ -182,7 +184,7 @@ __global__ __launch_bounds__(256) void trsm_pack_kernel(int64_t order, const flo
   __syncthreads();
   float *img = P + l * kImg;
 #pragma unroll
-  for (int q = 0; q < 8; ++q) {
+  for (int q = 0; q < kQ; ++q) {
     const int e = t + 256 * q;
     const int i = e % kLeaf, kl = e / kLeaf, k = 16 * c + kl;
     img[k * kLeaf + i] = i > k ? T[kl][i] : 0.f;
@@ -201,41 +203,60 @@ __global__ __launch_bounds__(256) void trsm_pack_kernel(int64_t order, const flo
 // overwrites v.
 //
 // Each 16-lane row of a wave owns R right-hand sides; lane j of the row
-// holds frame rows j, j+16, ..., j+112 of them in registers (x[h][g] is row
+// holds frame rows j, j+16, ..., j+240 of them in registers (x[h][g] is row
 // 16g + j of right-hand side h). Step k, in the column-oriented order of
 // wgblas's strsm_small.wgsl and of reference BLAS: x_k = x_k * (1 / M(k,k)),
 // computed by every lane on its register of row k's group and broadcast from
 // lane k % 16 across the row; then every lane subtracts M(i,k) x_k from each
-// of its rows i (one fused multiply-add each). A wave solves its right-hand
-// sides alone, with no barrier. The image sits in LDS (Ms[k*kLeaf + i] =
-// M(i,k), zero for i <= k); the rows i <= k that step k also touches are
-// already solved (their values were kept in s at their own step), so what
-// the update leaves there is never read. Per row the operations are those of
-// substitution: the products are subtracted in k order, then the row is
-// scaled by the diagonal's reciprocal. alpha is applied as v is read. Rows
-// past nb are padding with a unit diagonal and zero right-hand side; they
-// never feed real rows. Loads are unconditional, from addresses clamped into
-// the block, so that all of them are in flight together.
+// of its rows i (one fused multiply-add each). The rows i <= k that step k
+// also touches are already solved (each lane keeps its row of the group as
+// it is broadcast and stores it when the group ends) and M(i,k) is zero
+// there, so what the update leaves in them is never read. Per row the operations are those of substitution: the
+// products are subtracted in k order, then the row is scaled by the
+// diagonal's reciprocal. alpha is applied as v is read. Rows past nb are
+// padding with a unit diagonal and zero right-hand side; they never feed
+// real rows.
+//
+// Scheduling. A wave solves its right-hand sides alone: x_k moves between
+// lanes by one DPP row_newbcast, so the substitution needs no barrier. One
+// wave issues in order, and each step's chain (scale, broadcast, update of
+// the next row of the group) is about 26 cycles of dependent latency, so
+// the step's other updates (rows of later groups) are deferred by one step:
+// they use the previous step's x_k and fill that wait. M streams through
+// LDS in 16-column panels (panel g = the image's columns 16g .. 16g+15, 16
+// KiB), three buffers deep: panel g+2 is loaded into registers while group
+// g runs and written to LDS after it, behind the group's one barrier. Each
+// lane reads its entries of M two steps ahead of their use. The panel in
+// flight is a native vector array (Vec4): HIP's float4 struct, copied
+// member-wise from memory, was kept in scratch.
 template <int R>
 __global__ __launch_bounds__(256) void trsm_leaf_kernel(int nb, int64_t nrhs,
                                                        const float *__restrict__ img, int rev,
                                                        float *__restrict__ Bblk, int64_t vi,
                                                        int64_t vr, float alpha) {
-  constexpr int NB = kLeaf, kG = NB / 16, kV = NB * NB / 4 / 256;
-  __shared__ float4 img_s[kImg / 4];
-  float *Ms = reinterpret_cast<float *>(img_s), *Rd = Ms + NB * NB;
+  constexpr int NB = kLeaf, kG = NB / 16;
+  constexpr int kPanel4 = 16 * NB / 4;   // Vec4 per panel
+  constexpr int kPV = kPanel4 / 256;     // Vec4 per thread per panel
+  constexpr int kBufs = 3;
+  __shared__ Vec4 pan_s[kBufs][kPanel4];
+  __shared__ float Rd[NB];
+  static_assert(NB == 256, "one reciprocal per thread");
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int j = lane & 15;
   // right-hand sides r0 .. r0 + R - 1 of this lane's row
   const int64_t r0 = ((int64_t)blockIdx.x * 16 + wave * 4 + (lane >> 4)) * R;
 
-  // ---- every global load first: the image, 16-byte aligned (kImg is a
-  // multiple of 4 and the workspace is 256-byte aligned), then B
-  const float4 *img4 = reinterpret_cast<const float4 *>(img);
-  float4 mv[kV];
+  // ---- every global load first: panels 0 and 1 and the reciprocals (the
+  // image is 16-byte aligned: kImg is a multiple of 4 and the workspace
+  // 256-byte aligned), then B
+  const Vec4 *img4 = reinterpret_cast<const Vec4 *>(img);
+  Vec4 p0[kPV], p1[kPV];
 #pragma unroll
-  for (int q = 0; q < kV; ++q) mv[q] = img4[t + 256 * q];
-  const float4 rv = img4[NB * NB / 4 + (t & (NB / 4 - 1))];
+  for (int q = 0; q < kPV; ++q) {
+    p0[q] = img4[t + 256 * q];
+    p1[q] = img4[kPanel4 + t + 256 * q];
+  }
+  const float rdv = img[NB * NB + t];
   float x[R][kG];
 #pragma unroll
   for (int h = 0; h < R; ++h) {
@@ -246,10 +267,12 @@ __global__ __launch_bounds__(256) void trsm_leaf_kernel(int nb, int64_t nrhs,
       x[h][g] = Bblk[(int64_t)(i < nb ? (rev ? nb - 1 - i : i) : 0) * vi + r * vr];
     }
   }
-
 #pragma unroll
-  for (int q = 0; q < kV; ++q) img_s[t + 256 * q] = mv[q];
-  if (t < NB / 4) img_s[NB * NB / 4 + t] = rv;
+  for (int q = 0; q < kPV; ++q) {
+    pan_s[0][t + 256 * q] = p0[q];
+    pan_s[1][t + 256 * q] = p1[q];
+  }
+  Rd[t] = rdv;
 #pragma unroll
   for (int h = 0; h < R; ++h)
 #pragma unroll
@@ -257,67 +280,107 @@ __global__ __launch_bounds__(256) void trsm_leaf_kernel(int nb, int64_t nrhs,
       x[h][g] = (r0 + h < nrhs && 16 * g + j < nb) ? alpha * x[h][g] : 0.f;
   __syncthreads();
 
-  // ---- substitution, one row-group of 16 steps at a time
-  float s[R][kG];
+  // ---- substitution
+  // M(16 gg + j, k) for the lane: column k % 16 of panel k / 16
+  auto m_at = [&](int k, int gg) {
+    return reinterpret_cast<const float *>(pan_s[(k / 16) % kBufs])[(k % 16) * NB + 16 * gg + j];
+  };
+  // Entries of M are read ahead into a ring of kD steps: step k's slot is
+  // k % kD, used by step k's own update of its group's rows and by step
+  // k + 1's deferred updates, then refilled for step k + kD (two steps
+  // ahead of its use).
+  constexpr int kD = 3;
+  float mb[kD][kG];
+  float xd[R];  // the previous step's x_k
 #pragma unroll
-  for (int h = 0; h < R; ++h)
+  for (int l = 0; l < kD; ++l)
 #pragma unroll
-    for (int g = 0; g < kG; ++g) s[h][g] = 0.f;
-  // M's entries are read kD steps ahead of their use (each step pinned in
-  // place by a scheduling barrier, so the reads stay ahead), the group's
-  // reciprocals at its start.
-  constexpr int kD = 4;
+    for (int gg = 0; gg < kG; ++gg) mb[l][gg] = m_at(l, gg);
   static_for<kG>([&](auto gc) {
     constexpr int g = decltype(gc)::value;
-    if (16 * g < nb) {  // block-uniform: groups past nb are padding
-      float rd[16], mb[kD][kG - g];
+    Vec4 pn[kPV];  // panel g + 2, in flight during this group
+    if constexpr (g + 2 < kG) {
 #pragma unroll
-      for (int l = 0; l < 16; ++l) rd[l] = Rd[16 * g + l];
-#pragma unroll
-      for (int l = 0; l < kD; ++l)
-#pragma unroll
-        for (int gg = g; gg < kG; ++gg) mb[l][gg - g] = Ms[(16 * g + l) * NB + 16 * gg + j];
-      static_for<16>([&](auto lc) {
-        constexpr int l = decltype(lc)::value, k = 16 * g + l;
-        float mik[kG - g];
-#pragma unroll
-        for (int gg = 0; gg < kG - g; ++gg) mik[gg] = mb[l % kD][gg];
-        if constexpr (l + kD < 16) {
-#pragma unroll
-          for (int gg = g; gg < kG; ++gg) mb[l % kD][gg - g] = Ms[(k + kD) * NB + 16 * gg + j];
-        }
-        float xk[R];
-#pragma unroll
-        for (int h = 0; h < R; ++h) {
-          xk[h] = row_bcast<l>(x[h][g] * rd[l]);
-          s[h][g] = j == l ? xk[h] : s[h][g];
-        }
-#pragma unroll
-        for (int gg = g; gg < kG; ++gg)
-#pragma unroll
-          for (int h = 0; h < R; ++h) {
-            x[h][gg] = fmaf(-mik[gg - g], xk[h], x[h][gg]);
-            // keeps the update in this step: otherwise it is sunk to the
-            // start of group gg, where the updates form one dependent chain
-            asm volatile("" : "+v"(x[h][gg]));
-          }
-#pragma unroll
-        for (int h = 0; h < R; ++h) asm volatile("" : "+v"(s[h][g]));
-        __builtin_amdgcn_sched_barrier(0);
-      });
+      for (int q = 0; q < kPV; ++q) pn[q] = img4[(g + 2) * kPanel4 + t + 256 * q];
     }
+    float rd[16], sg[R];  // sg: this lane's solved row 16 g + j
+#pragma unroll
+    for (int l = 0; l < 16; ++l) rd[l] = Rd[16 * g + l];
+#pragma unroll
+    for (int h = 0; h < R; ++h) sg[h] = 0.f;
+    static_for<16>([&](auto lc) {
+      constexpr int l = decltype(lc)::value, k = 16 * g + l;
+      // Issue order, held by empty asm statements on each result (each
+      // one a side effect the compiler keeps in source order): the scale
+      // that starts this step's chain, two deferred updates (the DPP read
+      // of the scaled value needs two wait states), the broadcast, up to
+      // four more deferred updates (the broadcast's latency), the update of
+      // the group's rows that ends the chain, then the remaining deferred
+      // updates. The deferred updates are the previous step's, of rows in
+      // later groups, with the previous step's x_k.
+      constexpr int kDef = l > 0 ? (kG - 1 - g) * R : 0;
+      auto deferred = [&](auto ic) {
+        constexpr int i = decltype(ic)::value, gg = g + 1 + i / R, h = i % R;
+        x[h][gg] = fmaf(-mb[(k - 1 + kD) % kD][gg], xd[h], x[h][gg]);
+        asm volatile("" : "+v"(x[h][gg]));
+      };
+      float xk[R];
+#pragma unroll
+      for (int h = 0; h < R; ++h) {
+        xk[h] = x[h][g] * rd[l];
+        asm volatile("" : "+v"(xk[h]));
+      }
+      constexpr int kA = kDef < 2 ? kDef : 2, kB = kDef - kA < 4 ? kDef - kA : 4;
+      static_for<kA>([&](auto ic) { deferred(ic); });
+#pragma unroll
+      for (int h = 0; h < R; ++h) {
+        xk[h] = row_bcast<l>(xk[h]);
+        asm volatile("" : "+v"(xk[h]));
+      }
+      static_for<kB>([&](auto ic) { deferred(std::integral_constant<int, kA + decltype(ic)::value>{}); });
+      // this step's update of the group's rows: it feeds the next step
+#pragma unroll
+      for (int h = 0; h < R; ++h) {
+        x[h][g] = fmaf(-mb[k % kD][g], xk[h], x[h][g]);
+        asm volatile("" : "+v"(x[h][g]));
+        sg[h] = j == l ? xk[h] : sg[h];
+      }
+      static_for<kDef - kA - kB>(
+          [&](auto ic) { deferred(std::integral_constant<int, kA + kB + decltype(ic)::value>{}); });
+      if constexpr (l > 0 && k - 1 + kD < NB) {
+        // the previous step's slot, refilled for step k - 1 + kD
+#pragma unroll
+        for (int gg = (k - 1 + kD) / 16; gg < kG; ++gg) mb[(k - 1) % kD][gg] = m_at(k - 1 + kD, gg);
+      }
+#pragma unroll
+      for (int h = 0; h < R; ++h) xd[h] = xk[h];
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    // the group's last deferred updates, then that step's slot refilled
+    constexpr int kl = 16 * g + 15;
+#pragma unroll
+    for (int gg = g + 1; gg < kG; ++gg)
+#pragma unroll
+      for (int h = 0; h < R; ++h) x[h][gg] = fmaf(-mb[kl % kD][gg], xd[h], x[h][gg]);
+    if constexpr (kl + kD < NB) {
+#pragma unroll
+      for (int gg = (kl + kD) / 16; gg < kG; ++gg) mb[kl % kD][gg] = m_at(kl + kD, gg);
+    }
+    // panel g + 2 into the buffer group g - 1 used; the barrier also makes it
+    // visible before group g + 2 (and panel g + 1's reads ahead are already
+    // covered by the previous group's barrier)
+    if constexpr (g + 2 < kG) {
+#pragma unroll
+      for (int q = 0; q < kPV; ++q) pan_s[(g + 2) % kBufs][t + 256 * q] = pn[q];
+    }
+    // the group's solved rows go out now
+    if (16 * g + j < nb) {
+#pragma unroll
+      for (int h = 0; h < R; ++h)
+        if (r0 + h < nrhs) Bblk[(int64_t)(rev ? nb - 1 - (16 * g + j) : 16 * g + j) * vi + (r0 + h) * vr] = sg[h];
+    }
+    if constexpr (g + 1 < kG) __syncthreads();
   });
-
-  // ---- write back
-#pragma unroll
-  for (int h = 0; h < R; ++h) {
-    if (r0 + h >= nrhs) continue;
-#pragma unroll
-    for (int g = 0; g < kG; ++g) {
-      const int i = 16 * g + j;
-      if (i < nb) Bblk[(int64_t)(rev ? nb - 1 - i : i) * vi + (r0 + h) * vr] = s[h][g];
-    }
-  }
 }
 
 // strsm in the solve frame: frame index = B's row (left side) or column

@@ -80,9 +80,27 @@ def timed(ctx, ev, fn, steps, warmup):
     return total / steps
 
 
-def per_launch_ms(ctx, fn, reps):
+def warm_up(ctx, fn, ms=30.0, max_calls=400):
+    """Untimed calls of fn until about `ms` of wall time has passed: after
+    the host-side set-up between workloads the clocks take some tens of
+    milliseconds of load to settle (the first ragged 8191 x 8193 x 4097 NN
+    calls ran 4.70, 4.45, 4.30, 4.17 ms, then 4.03 from the fifth on)."""
+    t0 = time.perf_counter()
+    for i in range(1, max_calls + 1):
+        fn()
+        if i % 4 == 0:
+            ctx.synchronize()
+            if (time.perf_counter() - t0) * 1e3 >= ms:
+                break
+    ctx.synchronize()
+
+
+def per_launch_ms(ctx, fn, reps, warm=False):
     """Mean duration of one library call measured by the library's events
-    (wgb_set_timing), i.e. around that call's kernels only."""
+    (wgb_set_timing), i.e. around that call's kernels only; with `warm`,
+    after warm_up."""
+    if warm:
+        warm_up(ctx, fn)
     ctx.set_timing(True)
     acc = 0.0
     for _ in range(reps):
@@ -172,7 +190,7 @@ def bench_components(ctx, ev, quick):
     ctx.h2d(buf.offset(2 * n * n), np.zeros(n * n, np.float32))
     A, B, Cm = buf.offset(0), buf.offset(n * n), buf.offset(2 * n * n)
     f = lambda: ctx.sgemm(NO_TRANS, NO_TRANS, n, n, n, 1.0, A, n, B, n, 0.0, Cm, n)
-    ms = per_launch_ms(ctx, f, 20)
+    ms = per_launch_ms(ctx, f, 20, warm=True)
     comps["sgemm_512"] = {"ms": ms, "tflops": 2 * n ** 3 / ms / 1e9,
                           "frac_fp32_peak": 2 * n ** 3 / ms / 1e-3 / PEAK_FP32}
     buf.free()
@@ -191,8 +209,7 @@ def bench_components(ctx, ev, quick):
         ctx.fill_uniform(buf, -1.0, 1.0, 2)
         A, B, Cm = buf.offset(0), buf.offset(sa), buf.offset(sa + sb)
         f = lambda: ctx.sgemm(ta, tb, m, n, k, 1.5, A, lda, B, ldb, 0.5, Cm, ldc)
-        f()
-        ms = per_launch_ms(ctx, f, reps)
+        ms = per_launch_ms(ctx, f, reps, warm=True)
         per["NT"[ta] + "NT"[tb]] = {"ms": ms, "tflops": fl / ms / 1e9, "ld": [lda, ldb, ldc]}
         buf.free()
     mean_ms = sum(v["ms"] for v in per.values()) / len(per)
@@ -210,8 +227,7 @@ def bench_components(ctx, ev, quick):
     # the configured NT first, then the other layouts on the same buffers
     for ta, tb in ((NO_TRANS, TRANS), (NO_TRANS, NO_TRANS), (TRANS, NO_TRANS), (TRANS, TRANS)):
         f = lambda: ctx.dgemm(ta, tb, n, n, n, 1.0, A, n, B, n, 1.0, Cm, n)
-        f()
-        ms = per_launch_ms(ctx, f, reps)
+        ms = per_launch_ms(ctx, f, reps, warm=True)
         per["NT"[ta] + "NT"[tb]] = {"ms": ms, "tflops": fl / ms / 1e9}
     ms = per["NT"]["ms"]
     comps["dgemm_4096"] = {"ms": ms, "tflops": fl / ms / 1e9, "frac_fp64_peak": fl / ms / 1e-3 / PEAK_FP64,
@@ -225,8 +241,7 @@ def bench_components(ctx, ev, quick):
     dC = ctx.empty(n * n, np.float32)
     ctx.fill_uniform(dC, -1.0, 1.0, 5)
     f = lambda: ctx.ssyrk(LOWER, NO_TRANS, n, k, 1.0, dA, n, 0.25, dC, n)
-    f()
-    ctx.synchronize()
+    warm_up(ctx, f)
     ev.start()
     for _ in range(10):
         f()
@@ -236,8 +251,7 @@ def bench_components(ctx, ev, quick):
                                     "frac_fp32_peak": fl / ms / 1e-3 / PEAK_FP32}
     # the same configuration through sgemmtr (lower, op(A) = A, op(B) = A^T)
     g = lambda: ctx.sgemmtr(LOWER, NO_TRANS, TRANS, n, n, k, 1.0, dA, n, dA, n, 0.25, dC, n)
-    g()
-    ctx.synchronize()
+    warm_up(ctx, g)
     ev.start()
     for _ in range(10):
         g()
@@ -249,8 +263,7 @@ def bench_components(ctx, ev, quick):
     dB = ctx.empty(n * k, np.float32)
     ctx.fill_normal(dB, 6)
     h = lambda: ctx.ssyr2k(LOWER, NO_TRANS, n, k, 1.0, dA, n, dB, n, 0.25, dC, n)
-    h()
-    ms = per_launch_ms(ctx, h, reps)
+    ms = per_launch_ms(ctx, h, reps, warm=True)
     fl = 2.0 * n * (n + 1) * k
     comps["ssyr2k_8192x4096"] = {"ms": ms, "tflops": fl / ms / 1e9,
                                  "frac_fp32_peak": fl / ms / 1e-3 / PEAK_FP32}
@@ -268,8 +281,7 @@ def bench_components(ctx, ev, quick):
     ctx.fill_uniform(dy, -1.0, 1.0, 14)
     for t, tname in ((NO_TRANS, "N"), (TRANS, "T")):
         f = lambda: ctx.sgemv(t, n, n, 1.0, dA, n, dx, 1, 0.5, dy, 1)
-        f()
-        ms = per_launch_ms(ctx, f, 5 * reps)
+        ms = per_launch_ms(ctx, f, 5 * reps, warm=True)
         gbs = 4.0 * (n * n + 3 * n) / ms / 1e6
         comps[f"sgemv_{tname}_16384"] = {"ms": ms, "GB/s": gbs, "frac_hbm_peak": gbs * 1e9 / PEAK_HBM}
     dA.free()
@@ -295,12 +307,12 @@ def bench_components(ctx, ev, quick):
     }
     for name, (fn, bpe) in red.items():
         fn(1, n)
-        ms = per_launch_ms(ctx, lambda: fn(1, n), lreps)
+        ms = per_launch_ms(ctx, lambda: fn(1, n), lreps, warm=True)
         gbs = bpe * n / ms / 1e6
         comps[f"{name}_2^28"] = {"ms": ms, "GB/s": gbs, "frac_hbm_peak": gbs * 1e9 / PEAK_HBM,
                                  "traffic_bytes": load_traffic(f"{name}_2^28")}
         ns = 1 << 26
-        ms = per_launch_ms(ctx, lambda: fn(3, ns), lreps)
+        ms = per_launch_ms(ctx, lambda: fn(3, ns), lreps, warm=True)
         useful = bpe * ns / ms / 1e6
         comps[f"{name}_2^26_incx3"] = {"ms": ms, "GB/s_useful": useful,
                                        "GB/s_span": 3 * useful,
@@ -322,7 +334,7 @@ def bench_components(ctx, ev, quick):
     }
     for name, (fn, bpe) in red.items():
         fn(n)
-        ms = per_launch_ms(ctx, lambda: fn(n), lreps)
+        ms = per_launch_ms(ctx, lambda: fn(n), lreps, warm=True)
         gbs = bpe * n / ms / 1e6
         comps[f"{name}_2^27"] = {"ms": ms, "GB/s": gbs, "frac_hbm_peak": gbs * 1e9 / PEAK_HBM}
     dx.free()
@@ -348,20 +360,18 @@ def bench_level3(ctx, reps):
     ctx.fill_uniform(dB, -1.0, 1.0, 8)
     ctx.fill_uniform(dC, -1.0, 1.0, 9)
     f = lambda: ctx.ssymm(LEFT, LOWER, n, n, 1.0, dA, n, dB, n, 0.5, dC, n)
-    f()
-    ms = per_launch_ms(ctx, f, reps)
+    ms = per_launch_ms(ctx, f, reps, warm=True)
     fl = 2.0 * n * n * n + 2.0 * n * n
     comps["ssymm_8192"] = {"ms": ms, "tflops": fl / ms / 1e9, "frac_fp32_peak": fl / ms / 1e-3 / PEAK_FP32}
     f = lambda: ctx.strmm(LEFT, LOWER, NO_TRANS, NON_UNIT, n, n, 1.0, dA, n, dB, n)
-    f()
-    ms = per_launch_ms(ctx, f, reps)
+    ms = per_launch_ms(ctx, f, reps, warm=True)
     fl_ref, fl = 2.0 * n * n * n + 1.0 * n * n, 1.0 * n * n * n
     comps["strmm_8192"] = {"ms": ms, "tflops": fl_ref / ms / 1e9, "tflops_triangle": fl / ms / 1e9,
                            "frac_fp32_peak": fl / ms / 1e-3 / PEAK_FP32}
     # strsm: a well-conditioned lower triangle (off-diagonals in [-1/n, 1/n),
     # diagonal 2, as wgblas's tests build it); B is re-filled before each
-    # solve, outside the timed launch; two untimed solves first, as every
-    # other workload here has its untimed call
+    # timed solve, outside the timed launch; untimed solves first (warm_up,
+    # then two more on re-filled B)
     for order in (4096, 8192):
         ctx.fill_uniform(dA, -1.0 / order, 1.0 / order, 10)
         diag = np.full(1, 2.0, np.float32)
@@ -370,6 +380,7 @@ def bench_level3(ctx, reps):
         fl = 1.0 * order * order * order
         solve = lambda: ctx.strsm(LEFT, LOWER, NO_TRANS, NON_UNIT, order, order, 1.0, dA, order,
                                   dB, order)
+        warm_up(ctx, solve)
         times = []
         for it in range(2 + max(2, reps)):
             ctx.fill_uniform(dB, -1.0, 1.0, 11)

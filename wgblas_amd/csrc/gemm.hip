@@ -783,6 +783,27 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs<T> &p, int tm, int tn, 
           for (int i = 0; i < MB; ++i)
   #pragma unroll
             for (int j = 0; j < MB; ++j) acc[i][j] = Ty<T>::mfma(a[u][i], b[u][j], acc[i][j]);
+          if constexpr (!TAIL) {
+            if (s == 3) {
+              // The step after the barrier: one copy after each of its
+              // first MFMAs, then the next tile's operand reads one per
+              // MFMA. Left to the scheduler the eight copies issued as one
+              // burst ahead of the MFMAs, and a copy the L1 could not yet
+              // take stalled them (4096^3, A/B on one box: NT 70.4 -> 73.1,
+              // NN 69.5 -> 72.2, TN 68.9 -> 72.0, TT 68.8 -> 71.5 TFLOP/s;
+              // two MFMAs per copy: 72.8 / 70.9 / 69.5 / 70.7).
+  #pragma unroll
+              for (int c = 0; c < SA::LOADS + SB::LOADS; ++c) {
+                __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(kSchedVmemRead, 1, 0);
+              }
+  #pragma unroll
+              for (int c = 0; c < MB * MB - (SA::LOADS + SB::LOADS); ++c) {
+                __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+              }
+            }
+          }
         }
       };
       int kt = 0;

@@ -1045,20 +1045,25 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs<T> &p, int tm, int tn, 
 
 
 // The instantiations are held to 256 registers (two waves per SIMD)
-// explicitly, except the register-staged NT kernel (element-aligned
-// operands, both mn-contiguous). The fp32 kernels whose operands are both
-// k-contiguous or both mn-contiguous would fit without the bound too, with
-// accumulators in AGPRs; with scalar-base LDS copies the bound measured
-// faster for them (NT 8192^3 146.8 -> 148.2 TFLOP/s, ssyrk 8192/4096
-// 140.9 -> 141.9), while the register-staged NT kernel ran faster without
-// it (ragged 8191 x 8193 x 4097 NT 130.7 against 136.5; A/B on one box).
+// explicitly, except the register-staged ones (element-aligned operands)
+// other than fp32 TN and, for the paired fp32 kernels and fp64, other than
+// those with a k-contiguous operand (their earlier bound, not re-measured). The fp32 kernels whose operands are both k-contiguous or
+// both mn-contiguous would fit without the bound too, with accumulators in
+// AGPRs; with scalar-base LDS copies the bound measured faster for them (NT
+// 8192^3 146.8 -> 148.2 TFLOP/s, ssyrk 8192/4096 140.9 -> 141.9). The
+// register-staged kernels ran faster without it except TN (ragged 8191 x
+// 8193 x 4097, A/B on one box: NT 130.7 -> 136.5, NN 136.1 -> 138.0, TT
+// 133.9 -> 135.5; TN 137.8 -> 135.2).
 //
 // PAIR (launches with a k band, p.band != kBandNone): a tile row's (or
 // column's) k range grows with its index, so block b takes the tile pair
 // (r, c) and (tiles-1-r, c) (columns for a band on op(B)) and every block
 // does the same work, whatever order the dispatcher fills the CUs in.
 template <typename T, int BT, bool AKC, bool BKC, bool VEC, bool PAIR>
-__global__ __launch_bounds__(kThreads, (VEC || AKC || BKC) ? 2 : 1) void gemm_kernel(GemmArgs<T> p) {
+__global__ __launch_bounds__(kThreads, (VEC || (AKC && BKC) ||
+                                       ((PAIR || sizeof(T) == 8) && (AKC || BKC)))
+                                          ? 2
+                                          : 1) void gemm_kernel(GemmArgs<T> p) {
   constexpr int BK = 128 / (int)sizeof(T);
   typedef Stager<T, BT, AKC, VEC> SA;
   typedef Stager<T, BT, BKC, VEC> SB;

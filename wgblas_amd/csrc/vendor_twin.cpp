@@ -14,6 +14,7 @@
 #include <rocblas/rocblas.h>
 
 #include <algorithm>
+#include <chrono>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -75,13 +76,21 @@ struct Twin {
     for (void *p : bufs) WGB_OK_(wgb_free(ctx, p));
     bufs.clear();
   }
-  // median of `iters` per-call durations after `warmup` calls; `before`
-  // (untimed) runs ahead of every call
+  // median of `iters` per-call durations after at least `warmup` untimed
+  // calls and ~30 ms of them (bench.py's warm_up: the clocks take some tens
+  // of milliseconds of load to settle after the set-up between workloads);
+  // `before` (untimed) runs ahead of every call
   double median_ms(const std::function<void()> &f, int warmup, int iters,
                    const std::function<void()> &before = nullptr) {
-    for (int i = 0; i < warmup; ++i) {
+    const auto t0 = std::chrono::steady_clock::now();
+    for (int i = 0; i < 400; ++i) {
       if (before) before();
       f();
+      if (i + 1 >= warmup && (i + 1) % 4 == 0) {
+        HIP_OK(hipStreamSynchronize(stream));
+        if (std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count() >= 30.0)
+          break;
+      }
     }
     std::vector<float> t;
     for (int i = 0; i < iters; ++i) {

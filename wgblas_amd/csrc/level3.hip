@@ -406,9 +406,11 @@ int trsm_leaf(const Trsm &p, int64_t lo, int64_t nb, float alpha) {
   // right: frame index = column of B, right-hand side = row
   float *Bblk = p.left ? p.B + lo : p.B + lo * p.ldb;
   const int64_t vi = p.left ? 1 : p.ldb, vr = p.left ? p.ldb : 1;
-  // Up to 4096 right-hand sides each 16-lane row takes one (1024 waves: one
-  // per SIMD), beyond that two (half as many LDS reads per solved value).
-  if (nrhs > 4096)
+  // Up to 8192 right-hand sides each 16-lane row takes one (up to 2048
+  // waves: two per SIMD), beyond that two (half as many LDS reads per solved
+  // value). At 8192 one per row measured 26.8 against 27.0 us per leaf
+  // (strsm 113.0 against 111.7 TFLOP/s).
+  if (nrhs > 8192)
     trsm_leaf_kernel<2><<<(unsigned)((nrhs + 31) / 32), 256, 0, p.ctx->stream>>>(
         (int)nb, nrhs, img, rev, Bblk, vi, vr, alpha);
   else

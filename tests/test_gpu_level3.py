@@ -407,12 +407,12 @@ def test_strsm_large_round_trip(ctx, side, uplo, trans):
 
 @pytest.mark.parametrize("side,uplo,trans", list(itertools.product([1, 2], [1, 2], [0, 1])))
 def test_strsm_many_right_hand_sides(ctx, side, uplo, trans):
-    # 8200 right-hand sides: past 8192 each solve lane carries two of them.
+    # 8200 right-hand sides: 513 groups of 16, the last one padded.
     # Order 300 (diagonal blocks of 256 and 44, a GEMM update between): the
     # residual bound. Order 100 (one padded diagonal block, no GEMM):
     # every right-hand side's solution is bit-equal to solving it among only
-    # 100 (one per lane), since a right-hand side's operations do not depend
-    # on how many are solved together.
+    # 100, since a right-hand side's operations do not depend on how many
+    # are solved together (each is one column of the MFMA products).
     other = 8200
     for order in (300, 100):
         m, n = (order, other) if side == 1 else (other, order)

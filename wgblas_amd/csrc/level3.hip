@@ -8,8 +8,9 @@
 //   cannot read and write B at once), then one GEMM whose tiles only run the
 //   k-tiles the triangle reaches (about half the flops of a dense product).
 // strsm: recursive halving of the triangular dimension. Diagonal blocks of
-//   order <= 256 are solved by substitution, 16 lanes per right-hand side
-//   exchanging solved unknowns by DPP broadcasts; the off-diagonal updates are GEMMs that
+//   order <= 256 are solved by substitution inside 16-row sub-blocks
+//   (solved unknowns broadcast by DPP), the updates between sub-blocks on
+//   MFMA; the off-diagonal updates between diagonal blocks are GEMMs that
 //   read the solved rows of B and write other rows of B in place (disjoint
 //   memory). The diagonal blocks are packed once per call into the operand
 //   workspace; no explicit inverse is formed.
@@ -138,34 +139,38 @@ __device__ __forceinline__ void static_for(F &&f) {
   static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
-// Lane L of every 16-lane row of the wave, copied to the row's 16 lanes
-// (DPP row_newbcast).
-template <int L>
-__device__ __forceinline__ float row_bcast(float v) {
-  return __builtin_bit_cast(
-      float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x150 + L, 0xf, 0xf, false));
-}
-
-// strsm's diagonal blocks in the layout trsm_leaf_kernel stages in LDS: the
-// solve frame splits into blocks of kLeaf rows (the last one nb < kLeaf
-// rows), and block l's image is kImg floats at P + l kImg: P[k kLeaf + i] =
-// M(i, k) for k < i < nb (zero elsewhere, the diagonal included), then
-// P[kLeaf^2 + k] = 1 / M(k, k) (1 for a unit diagonal and for padding rows).
+// strsm's diagonal blocks, packed for trsm_leaf_kernel. The solve frame
+// splits into blocks of kLeaf rows (the last one nb < kLeaf rows), each
+// into kSub sub-blocks of 16 rows. With N = -M (M the block in frame
+// indices, zero past nb), block l's image is kImg floats at P + l kImg:
+//   * pair (t, s), s < t: 256 floats at pair_at(t, s); float 4 e + c =
+//     N(16 t + e % 16, 16 s + 4 (e / 16) + c) for e = 0..63, i.e. lane e's
+//     B operands of the four MFMAs that update sub-block t with the
+//     solved sub-block s;
+//   * diagonal sub-block s: 256 floats at kDiagAt + 256 s; float 16 j + k =
+//     N(16 s + j, 16 s + k) for k < j, zero for k >= j;
+//   * kLeaf floats at kRdAt: 1 / M(i, i) (1 for a unit diagonal and for
+//     padding rows).
 // Frame element (i, k) of block l's M is Ablk[ia(i) mi + ia(k) mk], Ablk at
 // A + kLeaf l (1 + lda), where ia(i) = nb-1-i for an upper system solved
-// backward (rev) and i otherwise. Block (l, c) packs columns 16c .. 16c+15 of
-// image l through an LDS tile: read with the stride-1 index fastest, written
-// with i fastest. The diagonal's reciprocals are formed once here: x * RN(1/d)
-// is within two ulps of x / d, and zero, infinite and NaN diagonals give the
-// quotient's special values (only a diagonal below 2^-126 in magnitude, whose
+// backward (rev) and i otherwise. Block (l, s) packs columns 16s .. 16s+15
+// of block l through an LDS tile read with the stride-1 index fastest. The
+// diagonal's reciprocals are formed once here: x * RN(1/d) is within two
+// ulps of x / d, and zero, infinite and NaN diagonals give the quotient's
+// special values (only a diagonal below 2^-126 in magnitude, whose
 // reciprocal overflows, differs).
-constexpr int kImg = kLeaf * kLeaf + kLeaf;
+constexpr int kSub = kLeaf / 16, kPairs = kSub * (kSub - 1) / 2;
+constexpr int kDiagAt = 256 * kPairs, kRdAt = 256 * (kPairs + kSub);
+constexpr int kImg = kRdAt + (kLeaf + 63) / 64 * 64;
+constexpr int kNU = kSub / 4;   // sub-blocks per wave
+constexpr int kRing = 3;        // B operand slots: loaded kRing - 1 steps ahead
+__host__ __device__ constexpr int pair_at(int t, int s) { return 256 * (t * (t - 1) / 2 + s); }
 
 __global__ __launch_bounds__(256) void trsm_pack_kernel(int64_t order, const float *__restrict__ A,
                                                         int64_t lda, int64_t mi, int64_t mk, int rev,
                                                         int unit, float *__restrict__ P) {
   __shared__ float T[16][kLeaf + 1];
-  const int t = threadIdx.x, c = blockIdx.y;
+  const int tid = threadIdx.x, s = blockIdx.y;
   const int64_t l = blockIdx.x, lo = l * kLeaf;
   const int nb = (int)(order - lo < kLeaf ? order - lo : kLeaf);
   const float *Ablk = A + lo + lo * lda;
@@ -173,214 +178,261 @@ __global__ __launch_bounds__(256) void trsm_pack_kernel(int64_t order, const flo
   constexpr int kQ = 16 * kLeaf / 256;  // elements per thread
 #pragma unroll
   for (int q = 0; q < kQ; ++q) {
-    const int e = t + 256 * q;
+    const int e = tid + 256 * q;
     const int i = kfast ? e / 16 : e % kLeaf, kl = kfast ? e % 16 : e / kLeaf;
-    const int k = 16 * c + kl;
+    const int k = 16 * s + kl;
     const bool in = i < nb && k <= i;
     const int64_t ii = in ? (rev ? nb - 1 - i : i) : 0, kk = in ? (rev ? nb - 1 - k : k) : 0;
     const float v = Ablk[ii * mi + kk * mk];
-    T[kl][i] = in ? v : 0.f;
+    T[kl][i] = in ? v : 0.f;  // T[kl][i] = M(i, 16 s + kl)
   }
   __syncthreads();
   float *img = P + l * kImg;
-#pragma unroll
-  for (int q = 0; q < kQ; ++q) {
-    const int e = t + 256 * q;
-    const int i = e % kLeaf, kl = e / kLeaf, k = 16 * c + kl;
-    img[k * kLeaf + i] = i > k ? T[kl][i] : 0.f;
-  }
-  if (t < 16) {
-    const int k = 16 * c + t;
-    img[kLeaf * kLeaf + k] = 1.f / ((unit || k >= nb) ? 1.f : T[t][k]);
+  const int e = tid >> 2, c = tid & 3;
+  for (int t = s + 1; t < kSub; ++t) img[pair_at(t, s) + tid] = -T[4 * (e >> 4) + c][16 * t + (e & 15)];
+  const int jj = tid >> 4, kk = tid & 15;
+  img[kDiagAt + 256 * s + tid] = kk < jj ? -T[kk][16 * s + jj] : 0.f;
+  if (tid < 16) {
+    const int k = 16 * s + tid;
+    img[kRdAt + k] = 1.f / ((unit || k >= nb) ? 1.f : T[tid][k]);
   }
 }
 
-// Substitution solve of one diagonal block, in the solve frame: for every
-// right-hand side v, M x = alpha v with M lower triangular of order
+// The solved sub-block handed between waves, [row k][right-hand side], rows
+// 20 floats apart: both the 16-byte stores of the solving wave and the
+// column reads of the MFMA A operand are free of bank conflicts.
+constexpr int kXs = 20;
+
+// One substitution step for four right-hand sides: x = acc * rd in every
+// lane, then acc += md * (x of lane K of the 16-lane row): v_fmac_f32 with a
+// DPP row_newbcast source, the broadcast and the update in one instruction.
+// Each DPP source is written four instructions before it is read (the
+// hardware needs two wait states between a VALU write and a DPP read).
+template <int K>
+__device__ __forceinline__ void subst_step(Vec4 &acc, float rd, float md) {
+  float a0 = acc[0], a1 = acc[1], a2 = acc[2], a3 = acc[3], t0, t1, t2, t3;
+  asm volatile(
+      "v_mul_f32 %4, %8, %0\n\t"
+      "v_mul_f32 %5, %8, %1\n\t"
+      "v_mul_f32 %6, %8, %2\n\t"
+      "v_mul_f32 %7, %8, %3\n\t"
+      "v_fmac_f32_dpp %0, %4, %9 row_newbcast:%10 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %1, %5, %9 row_newbcast:%10 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %2, %6, %9 row_newbcast:%10 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %3, %7, %9 row_newbcast:%10 row_mask:0xf bank_mask:0xf"
+      : "+v"(a0), "+v"(a1), "+v"(a2), "+v"(a3), "=&v"(t0), "=&v"(t1), "=&v"(t2), "=&v"(t3)
+      : "s"(rd), "v"(md), "n"(K));
+  acc = Vec4{a0, a1, a2, a3};
+}
+
+// acc += sum over c of the 16x16x4 products (a[c], b[c]): one 16 x 16 x 16
+// update.
+__device__ __forceinline__ Vec4 mfma4(Vec4 acc, const float (&a)[4], Vec4 b) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[0], b[0], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[1], b[1], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[2], b[2], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[3], b[3], acc, 0, 0, 0);
+  return acc;
+}
+
+// Substitution solve of one diagonal block, in the solve frame: for 16
+// right-hand sides v, M x = alpha v with M lower triangular of order
 // nb <= kLeaf, given as its image `img` (trsm_pack_kernel). Element i of
 // right-hand side r is Bblk[ia(i) vi + r vr], where ia(i) = nb-1-i for an
 // upper system solved backward (rev) and i otherwise; the solution
 // overwrites v.
 //
-// Each 16-lane row of a wave owns R right-hand sides; lane j of the row
-// holds frame rows j, j+16, ..., j+240 of them in registers (x[h][g] is row
-// 16g + j of right-hand side h). Step k, in the column-oriented order of
-// wgblas's strsm_small.wgsl and of reference BLAS: x_k = x_k * (1 / M(k,k)),
-// computed by every lane on its register of row k's group and broadcast from
-// lane k % 16 across the row; then every lane subtracts M(i,k) x_k from each
-// of its rows i (one fused multiply-add each). The rows i <= k that step k
-// also touches are already solved (each lane keeps its row of the group as
-// it is broadcast and stores it when the group ends) and M(i,k) is zero
-// there, so what the update leaves in them is never read. Per row the operations are those of substitution: the
-// products are subtracted in k order, then the row is scaled by the
-// diagonal's reciprocal. alpha is applied as v is read. Rows past nb are
+// The block's kSub sub-blocks of 16 rows are dealt to its 4 waves: the wave
+// playing part w (W, trsm_leaf_kernel) owns sub-blocks t = 4u + w
+// (u = 0 .. kNU-1) and holds each as a 16x16x4
+// MFMA accumulator of (right-hand side) x (row): lane j + 16 q holds row
+// 16 t + j of right-hand sides 4q .. 4q+3. Step s (s = 0 .. kSub-1):
+//   * the owner of sub-block s solves it by substitution, in the
+//     column-oriented order of wgblas's strsm_small.wgsl and of reference
+//     BLAS: x_k = x_k * (1 / M(k,k)), broadcast from lane k by DPP
+//     row_newbcast, and every lane subtracts M(16s + j, 16s + k) x_k from
+//     its row (one v_fmac_f32 with the DPP source). Rows j <= k are
+//     multiplied by the image's zeros there and keep their value while
+//     every x_k is finite, so each lane's solution is its row times the
+//     reciprocal once more at the end. A wave that saw a non-finite value
+//     redoes the sub-block from its saved rows, keeping each row's x_k as it
+//     is broadcast: IEEE specials land where substitution puts them. The
+//     solved rows go to LDS (Xs) and out to B;
+//   * barrier; every wave updates its sub-blocks t > s with them: four MFMAs
+//     whose A operand is the solved rows (from Xs) and B operand the pair
+//     (t, s) of the image, read from global memory kRing - 1 steps ahead.
+//     The owner of sub-block s+1 updates that one first and defers its
+//     others into its substitution (up to two MFMAs per substitution step),
+//     so the next step's substitution starts right after the four MFMAs it
+//     needs.
+// The step loop is unrolled with s and the wave's part w known at compile
+// time (register arrays need constant indices), one copy per part. Making w
+// a uniform runtime branch instead (one copy of the code for all four) held
+// more registers and measured slower (18.1 against 16.2 us per leaf at 4096
+// right-hand sides).
+// The off-diagonal products are summed by the MFMA (four per instruction)
+// rather than one subtraction at a time; within a sub-block the order is
+// that of substitution. alpha is applied as v is read. Rows past nb are
 // padding with a unit diagonal and zero right-hand side; they never feed
 // real rows.
-//
-// Scheduling. A wave solves its right-hand sides alone: x_k moves between
-// lanes by one DPP row_newbcast, so the substitution needs no barrier. One
-// wave issues in order, and each step's chain (scale, broadcast, update of
-// the next row of the group) is about 26 cycles of dependent latency, so
-// the step's other updates (rows of later groups) are deferred by one step:
-// they use the previous step's x_k and fill that wait. M streams through
-// LDS in 16-column panels (panel g = the image's columns 16g .. 16g+15, 16
-// KiB), three buffers deep: panel g+2 is loaded into registers while group
-// g runs and written to LDS after it, behind the group's one barrier. Each
-// lane reads its entries of M two steps ahead of their use. The panel in
-// flight is a native vector array (Vec4): HIP's float4 struct, copied
-// member-wise from memory, was kept in scratch.
-template <int R>
+template <int W>
+__device__ __forceinline__ void trsm_leaf_wave(int nb, int64_t nrhs, const float *__restrict__ img,
+                                               int rev, float *__restrict__ Bblk, int64_t vi,
+                                               int64_t vr, float alpha, int64_t r0, int lane,
+                                               float (*__restrict__ Xs)[16][kXs]) {
+  const int j = lane & 15, q = lane >> 4;
+  const Vec4 *img4 = reinterpret_cast<const Vec4 *>(img);
+  const float *rdp = img + kRdAt;
+  auto frame = [&](int i) -> int64_t { return rev ? nb - 1 - i : i; };
+  auto rhs_ok = [&](int v) { return r0 + 4 * q + v < nrhs; };
+
+  // ---- global loads: this wave's rows of the right-hand sides, the B
+  // operands of the first steps, the first diagonal sub-block it solves
+  Vec4 acc[kNU];
+  static_for<kNU>([&](auto uc) {
+    constexpr int u = decltype(uc)::value;
+    const int i = 16 * (4 * u + W) + j;
+    const int64_t ii = i < nb ? frame(i) : 0;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) acc[u][v] = Bblk[ii * vi + (rhs_ok(v) ? r0 + 4 * q + v : 0) * vr];
+  });
+  // B operands of step s's update of sub-block 4u + w: slot s % kRing
+  Vec4 bop[kRing][kNU];
+  static_for<kRing - 1>([&](auto sc) {
+    constexpr int s = decltype(sc)::value;
+    static_for<kNU>([&](auto uc) {
+      constexpr int u = decltype(uc)::value;
+      if constexpr (4 * u + W > s) bop[s][u] = img4[pair_at(4 * u + W, s) / 4 + lane];
+    });
+  });
+  Vec4 md4[4];    // row j of the next diagonal sub-block this wave solves,
+  float rdj;      // that row's reciprocal
+  float rdn[16];  // and the sub-block's reciprocals (uniform)
+#pragma unroll
+  for (int m = 0; m < 4; ++m) md4[m] = img4[(kDiagAt + 256 * W + 16 * j) / 4 + m];
+  rdj = rdp[16 * W + j];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) rdn[k] = rdp[16 * W + k];
+  static_for<kNU>([&](auto uc) {
+    constexpr int u = decltype(uc)::value;
+    const bool row_ok = 16 * (4 * u + W) + j < nb;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) acc[u][v] = (row_ok && rhs_ok(v)) ? alpha * acc[u][v] : 0.f;
+  });
+
+  float apend[4];  // a deferred update: solved rows and B operands
+  Vec4 bpend[kNU];
+  static_for<kSub>([&](auto sc) {
+    constexpr int s = decltype(sc)::value, us = s / 4;
+    Vec4 x;  // this lane's solved row of sub-block s (owner)
+    if constexpr (s % 4 == W) {
+      // deferred MFMAs of the previous step: sub-blocks u > us
+      constexpr int kPend = s > 0 ? 4 * (kNU - 1 - us) : 0;
+      const Vec4 keep = acc[us];
+      float rds[16], md[16];
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        rds[k] = rdn[k];
+        md[k] = md4[k / 4][k % 4];
+      }
+      static_for<16>([&](auto kc) {
+        constexpr int k = decltype(kc)::value;
+        static_for<2>([&](auto hc) {
+          constexpr int i = k + 16 * decltype(hc)::value;
+          if constexpr (i < kPend) {
+            constexpr int u = us + 1 + i / 4, c = i % 4;
+            acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(apend[c], bpend[u][c], acc[u], 0, 0, 0);
+          }
+        });
+        subst_step<k>(acc[us], rds[k], md[k]);
+        __builtin_amdgcn_sched_barrier(0);
+      });
+      bool bad = false;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) bad |= !__builtin_isfinite(acc[us][v]);
+      if (__ballot(bad)) {
+        // a non-finite value: substitution again, each row kept as solved
+        acc[us] = keep;
+        x = Vec4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 1
+        for (int k = 0; k < 16; ++k) {
+          const Vec4 xk = acc[us] * rdp[16 * s + k];
+          const float mk = img[kDiagAt + 256 * s + 16 * j + k];
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            x[v] = j == k ? xk[v] : x[v];
+            acc[us][v] = fmaf(mk, __shfl(xk[v], (lane & 48) | k), acc[us][v]);
+          }
+        }
+      } else {
+        x = acc[us] * rdj;
+      }
+      *reinterpret_cast<Vec4 *>(&Xs[s & 1][j][4 * q]) = x;
+      if constexpr (s + 4 < kSub) {
+#pragma unroll
+        for (int m = 0; m < 4; ++m) md4[m] = img4[(kDiagAt + 256 * (s + 4) + 16 * j) / 4 + m];
+        rdj = rdp[16 * (s + 4) + j];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) rdn[k] = rdp[16 * (s + 4) + k];
+      }
+    }
+    __syncthreads();
+    if constexpr (s + 1 < kSub) {
+      float a[4];  // A operand: solved row 4q + c of right-hand side j
+#pragma unroll
+      for (int c = 0; c < 4; ++c) a[c] = Xs[s & 1][4 * q + c][j];
+      constexpr int sa = s + kRing - 1;  // the step whose operands load now
+      if constexpr (sa < kSub) {
+        static_for<kNU>([&](auto uc) {
+          constexpr int u = decltype(uc)::value;
+          if constexpr (4 * u + W > sa) bop[sa % kRing][u] = img4[pair_at(4 * u + W, sa) / 4 + lane];
+        });
+      }
+      Vec4(&bcur)[kNU] = bop[s % kRing];
+      if constexpr ((s + 1) % 4 == W) {
+        constexpr int un = (s + 1) / 4;
+        acc[un] = mfma4(acc[un], a, bcur[un]);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) apend[c] = a[c];
+        static_for<kNU>([&](auto uc) {
+          constexpr int u = decltype(uc)::value;
+          if constexpr (u > un) bpend[u] = bcur[u];
+        });
+      } else {
+        static_for<kNU>([&](auto uc) {
+          constexpr int u = decltype(uc)::value;
+          if constexpr (4 * u + W > s) acc[u] = mfma4(acc[u], a, bcur[u]);
+        });
+      }
+    }
+    if constexpr (s % 4 == W) {
+      const int i = 16 * s + j;
+      if (i < nb) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          if (rhs_ok(v)) Bblk[frame(i) * vi + (r0 + 4 * q + v) * vr] = x[v];
+      }
+    }
+  });
+}
+
+// One block per 16 right-hand sides; wave w plays part w. (Rotating the
+// parts by block parity, so that two blocks sharing a compute unit
+// substitute on different SIMDs, measured no different.)
 __global__ __launch_bounds__(256) void trsm_leaf_kernel(int nb, int64_t nrhs,
                                                        const float *__restrict__ img, int rev,
                                                        float *__restrict__ Bblk, int64_t vi,
                                                        int64_t vr, float alpha) {
-  constexpr int NB = kLeaf, kG = NB / 16;
-  constexpr int kPanel4 = 16 * NB / 4;   // Vec4 per panel
-  constexpr int kPV = kPanel4 / 256;     // Vec4 per thread per panel
-  constexpr int kBufs = 3;
-  __shared__ Vec4 pan_s[kBufs][kPanel4];
-  __shared__ float Rd[NB];
-  static_assert(NB == 256, "one reciprocal per thread");
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int j = lane & 15;
-  // right-hand sides r0 .. r0 + R - 1 of this lane's row
-  const int64_t r0 = ((int64_t)blockIdx.x * 16 + wave * 4 + (lane >> 4)) * R;
-
-  // ---- every global load first: panels 0 and 1 and the reciprocals (the
-  // image is 16-byte aligned: kImg is a multiple of 4 and the workspace
-  // 256-byte aligned), then B
-  const Vec4 *img4 = reinterpret_cast<const Vec4 *>(img);
-  Vec4 p0[kPV], p1[kPV];
-#pragma unroll
-  for (int q = 0; q < kPV; ++q) {
-    p0[q] = img4[t + 256 * q];
-    p1[q] = img4[kPanel4 + t + 256 * q];
+  __shared__ float Xs[2][16][kXs];
+  const int lane = threadIdx.x & 63;
+  const int part = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t r0 = (int64_t)blockIdx.x * 16;
+  switch (part) {
+    case 0: trsm_leaf_wave<0>(nb, nrhs, img, rev, Bblk, vi, vr, alpha, r0, lane, Xs); break;
+    case 1: trsm_leaf_wave<1>(nb, nrhs, img, rev, Bblk, vi, vr, alpha, r0, lane, Xs); break;
+    case 2: trsm_leaf_wave<2>(nb, nrhs, img, rev, Bblk, vi, vr, alpha, r0, lane, Xs); break;
+    default: trsm_leaf_wave<3>(nb, nrhs, img, rev, Bblk, vi, vr, alpha, r0, lane, Xs); break;
   }
-  const float rdv = img[NB * NB + t];
-  float x[R][kG];
-#pragma unroll
-  for (int h = 0; h < R; ++h) {
-    const int64_t r = r0 + h < nrhs ? r0 + h : 0;
-#pragma unroll
-    for (int g = 0; g < kG; ++g) {
-      const int i = 16 * g + j;
-      x[h][g] = Bblk[(int64_t)(i < nb ? (rev ? nb - 1 - i : i) : 0) * vi + r * vr];
-    }
-  }
-#pragma unroll
-  for (int q = 0; q < kPV; ++q) {
-    pan_s[0][t + 256 * q] = p0[q];
-    pan_s[1][t + 256 * q] = p1[q];
-  }
-  Rd[t] = rdv;
-#pragma unroll
-  for (int h = 0; h < R; ++h)
-#pragma unroll
-    for (int g = 0; g < kG; ++g)
-      x[h][g] = (r0 + h < nrhs && 16 * g + j < nb) ? alpha * x[h][g] : 0.f;
-  __syncthreads();
-
-  // ---- substitution
-  // M(16 gg + j, k) for the lane: column k % 16 of panel k / 16
-  auto m_at = [&](int k, int gg) {
-    return reinterpret_cast<const float *>(pan_s[(k / 16) % kBufs])[(k % 16) * NB + 16 * gg + j];
-  };
-  // Entries of M are read ahead into a ring of kD steps: step k's slot is
-  // k % kD, used by step k's own update of its group's rows and by step
-  // k + 1's deferred updates, then refilled for step k + kD (two steps
-  // ahead of its use).
-  constexpr int kD = 3;
-  float mb[kD][kG];
-  float xd[R];  // the previous step's x_k
-#pragma unroll
-  for (int l = 0; l < kD; ++l)
-#pragma unroll
-    for (int gg = 0; gg < kG; ++gg) mb[l][gg] = m_at(l, gg);
-  static_for<kG>([&](auto gc) {
-    constexpr int g = decltype(gc)::value;
-    Vec4 pn[kPV];  // panel g + 2, in flight during this group
-    if constexpr (g + 2 < kG) {
-#pragma unroll
-      for (int q = 0; q < kPV; ++q) pn[q] = img4[(g + 2) * kPanel4 + t + 256 * q];
-    }
-    float rd[16], sg[R];  // sg: this lane's solved row 16 g + j
-#pragma unroll
-    for (int l = 0; l < 16; ++l) rd[l] = Rd[16 * g + l];
-#pragma unroll
-    for (int h = 0; h < R; ++h) sg[h] = 0.f;
-    static_for<16>([&](auto lc) {
-      constexpr int l = decltype(lc)::value, k = 16 * g + l;
-      // Issue order, held by empty asm statements on each result (each
-      // one a side effect the compiler keeps in source order): the scale
-      // that starts this step's chain, two deferred updates (the DPP read
-      // of the scaled value needs two wait states), the broadcast, up to
-      // four more deferred updates (the broadcast's latency), the update of
-      // the group's rows that ends the chain, then the remaining deferred
-      // updates. The deferred updates are the previous step's, of rows in
-      // later groups, with the previous step's x_k.
-      constexpr int kDef = l > 0 ? (kG - 1 - g) * R : 0;
-      auto deferred = [&](auto ic) {
-        constexpr int i = decltype(ic)::value, gg = g + 1 + i / R, h = i % R;
-        x[h][gg] = fmaf(-mb[(k - 1 + kD) % kD][gg], xd[h], x[h][gg]);
-        asm volatile("" : "+v"(x[h][gg]));
-      };
-      float xk[R];
-#pragma unroll
-      for (int h = 0; h < R; ++h) {
-        xk[h] = x[h][g] * rd[l];
-        asm volatile("" : "+v"(xk[h]));
-      }
-      constexpr int kA = kDef < 2 ? kDef : 2, kB = kDef - kA < 4 ? kDef - kA : 4;
-      static_for<kA>([&](auto ic) { deferred(ic); });
-#pragma unroll
-      for (int h = 0; h < R; ++h) {
-        xk[h] = row_bcast<l>(xk[h]);
-        asm volatile("" : "+v"(xk[h]));
-      }
-      static_for<kB>([&](auto ic) { deferred(std::integral_constant<int, kA + decltype(ic)::value>{}); });
-      // this step's update of the group's rows: it feeds the next step
-#pragma unroll
-      for (int h = 0; h < R; ++h) {
-        x[h][g] = fmaf(-mb[k % kD][g], xk[h], x[h][g]);
-        asm volatile("" : "+v"(x[h][g]));
-        sg[h] = j == l ? xk[h] : sg[h];
-      }
-      static_for<kDef - kA - kB>(
-          [&](auto ic) { deferred(std::integral_constant<int, kA + kB + decltype(ic)::value>{}); });
-      if constexpr (l > 0 && k - 1 + kD < NB) {
-        // the previous step's slot, refilled for step k - 1 + kD
-#pragma unroll
-        for (int gg = (k - 1 + kD) / 16; gg < kG; ++gg) mb[(k - 1) % kD][gg] = m_at(k - 1 + kD, gg);
-      }
-#pragma unroll
-      for (int h = 0; h < R; ++h) xd[h] = xk[h];
-      __builtin_amdgcn_sched_barrier(0);
-    });
-    // the group's last deferred updates, then that step's slot refilled
-    constexpr int kl = 16 * g + 15;
-#pragma unroll
-    for (int gg = g + 1; gg < kG; ++gg)
-#pragma unroll
-      for (int h = 0; h < R; ++h) x[h][gg] = fmaf(-mb[kl % kD][gg], xd[h], x[h][gg]);
-    if constexpr (kl + kD < NB) {
-#pragma unroll
-      for (int gg = (kl + kD) / 16; gg < kG; ++gg) mb[kl % kD][gg] = m_at(kl + kD, gg);
-    }
-    // panel g + 2 into the buffer group g - 1 used; the barrier also makes it
-    // visible before group g + 2 (and panel g + 1's reads ahead are already
-    // covered by the previous group's barrier)
-    if constexpr (g + 2 < kG) {
-#pragma unroll
-      for (int q = 0; q < kPV; ++q) pan_s[(g + 2) % kBufs][t + 256 * q] = pn[q];
-    }
-    // the group's solved rows go out now
-    if (16 * g + j < nb) {
-#pragma unroll
-      for (int h = 0; h < R; ++h)
-        if (r0 + h < nrhs) Bblk[(int64_t)(rev ? nb - 1 - (16 * g + j) : 16 * g + j) * vi + (r0 + h) * vr] = sg[h];
-    }
-    if constexpr (g + 1 < kG) __syncthreads();
-  });
 }
 
 // strsm in the solve frame: frame index = B's row (left side) or column
@@ -406,16 +458,8 @@ int trsm_leaf(const Trsm &p, int64_t lo, int64_t nb, float alpha) {
   // right: frame index = column of B, right-hand side = row
   float *Bblk = p.left ? p.B + lo : p.B + lo * p.ldb;
   const int64_t vi = p.left ? 1 : p.ldb, vr = p.left ? p.ldb : 1;
-  // Up to 8192 right-hand sides each 16-lane row takes one (up to 2048
-  // waves: two per SIMD), beyond that two (half as many LDS reads per solved
-  // value). At 8192 one per row measured 26.8 against 27.0 us per leaf
-  // (strsm 113.0 against 111.7 TFLOP/s).
-  if (nrhs > 8192)
-    trsm_leaf_kernel<2><<<(unsigned)((nrhs + 31) / 32), 256, 0, p.ctx->stream>>>(
-        (int)nb, nrhs, img, rev, Bblk, vi, vr, alpha);
-  else
-    trsm_leaf_kernel<1><<<(unsigned)((nrhs + 15) / 16), 256, 0, p.ctx->stream>>>(
-        (int)nb, nrhs, img, rev, Bblk, vi, vr, alpha);
+  trsm_leaf_kernel<<<(unsigned)((nrhs + 15) / 16), 256, 0, p.ctx->stream>>>(
+      (int)nb, nrhs, img, rev, Bblk, vi, vr, alpha);
   WGB_CHECK_LAUNCH("trsm_leaf_kernel");
   return WGB_OK;
 }

@@ -428,6 +428,39 @@ def test_strsm_many_right_hand_sides(ctx, side, uplo, trans):
     assert bits_equal(Xs, Xd)
 
 
+@pytest.mark.parametrize("side,uplo,trans", [(1, 1, 0), (1, 2, 1), (2, 1, 1), (2, 2, 0)])
+def test_strsm_special_path_matches(ctx, side, uplo, trans):
+    # A right-hand side that holds Inf or NaN sends the 16 it is solved with
+    # through the substitution that keeps each row as it is solved (the
+    # IEEE-special path), from the sub-block where the value appears to the
+    # end of its diagonal block. The other right-hand sides of the group
+    # must come out bit-equal to a solve without the specials (the regular
+    # path), and the poisoned ones non-finite. Order 300: diagonal blocks of
+    # frame rows [0, 256) and [256, 300), the Inf at frame row 100, the NaN
+    # at 270 (one in each block, whichever way the solve runs); 40
+    # right-hand sides = groups of 16, 16 and 8.
+    order, other = 300, 40
+    m, n = (order, other) if side == 1 else (other, order)
+    lda, ldb = order + 3, m + 2
+    A = orc.random_f32(lda * order, -1.0 / order, 1.0 / order, 21)
+    A[np.arange(order) * (lda + 1)] = 2.0
+    B = orc.random_f32(ldb * n, -1, 1, 22)
+    # frame row f of right-hand side r sits at B(f, r) (left) or B(r, f) (right)
+    at = (lambda f, r: f + r * ldb) if side == 1 else (lambda f, r: r + f * ldb)
+    Bs = B.copy()
+    Bs[at(100, 5)] = np.inf
+    Bs[at(270, 37)] = np.nan
+    call = lambda Bx: (side, uplo, trans, 0, m, n, 0.75, A, lda, Bx, ldb)
+    X = run_trsm(ctx, call(B))
+    Xs = run_trsm(ctx, call(Bs))
+    rhs = lambda Xa, r: np.array([Xa[at(f, r)] for f in range(order)], F32)
+    for r in range(other):
+        if r in (5, 37):
+            assert not np.all(np.isfinite(rhs(Xs, r)))
+        else:
+            assert bits_equal(rhs(X, r), rhs(Xs, r)), r
+
+
 # ------------------------------------------- operands of different storage orders
 def _cm_transpose(X, rows, cols, ld):
     """Column-major rows x cols (leading dimension ld) -> its transpose as a

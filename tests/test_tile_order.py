@@ -59,6 +59,7 @@ def test_banded_triangle_shares_panels(checker):
     # tiles; ~64 tiles resident per XCD (32 CUs x 2 blocks)
     rows, out = checker([(64, 64, 1, 64), (64, 64, 2, 64), (64, 64, 0, 64)])
     lower, upper, full = (int(x[5]) for x in rows)
-    # kGroupM = 8 rows and ~8-9 columns, plus a spill into the next band
+    # triangle bands of kGroupTri = 4 rows and ~16 columns, full launches
+    # kGroupM = 8 rows and ~8 columns, plus a spill into the next band
     assert lower <= 32 and upper <= 32, out
     assert full <= 32, out

@@ -40,7 +40,7 @@
 // run of tiles; inside that run tiles are grouped 8 tile-rows at a time so
 // concurrent tiles share A and B panels. sgemmtr/ssyrk launch only the
 // tiles that meet the requested triangle (wgblas launches all of them and
-// returns early, src/shaders/sgemm_large.wgsl:78-83), in bands of 8 tile rows
+// returns early, src/shaders/sgemm_large.wgsl:78-83), in bands of 4 tile rows
 // walked column by column for the same sharing, and mask stores inside the
 // diagonal tiles (tile_order.h holds these orders).
 //

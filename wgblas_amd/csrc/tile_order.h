@@ -15,6 +15,13 @@ namespace wgb_tiles {
 constexpr int kGroupM = 8;
 // MI355X's XCD count: the hardware deals workgroups round-robin over them.
 constexpr int kXcds = 8;
+// Tile rows per band of a triangle launch. Measured on ssyrk n = 8192,
+// k = 4096 (HBM bytes per launch from FETCH_SIZE / WRITE_SIZE, against the
+// 402.7 MB algorithmic): bands of 4 rows 2.75 GB (6.8x), 8 rows 2.86 GB
+// (7.1x), 16 rows 3.49 GB (8.7x), at 142.0 / 142.0 / 141.1 TFLOP/s. A band's
+// row panels stay hot for all of its columns, and each column panel is
+// shared by the band's few consecutive tiles, which start close together.
+constexpr int kGroupTri = 4;
 
 // Number of tiles of a rows x cols tile grid that meet the lower (tile row
 // >= tile col) triangle: row r holds min(r + 1, cols) tiles. The upper
@@ -34,8 +41,8 @@ __host__ __device__ inline int xcd_remap(int w, int n) {
   return x * q + (x < r ? x : r) + j;
 }
 
-// Lower-triangle tile L of a rows x cols tile grid, in bands of kGroupM tile
-// rows: band b holds rows [kGroupM b, kGroupM b + kGroupM), walked column by
+// Lower-triangle tile L of a rows x cols tile grid, in bands of kGroupTri
+// tile rows: band b holds rows [kGroupTri b, kGroupTri b + kGroupTri), walked column by
 // column (column c of the band holds its rows r >= c). Every tile of the
 // triangle gets exactly one L in [0, triangle_tiles(rows, cols)).
 __host__ __device__ inline void triangle_decode_banded(int L, int rows, int cols, int &r, int &c) {
@@ -44,17 +51,17 @@ __host__ __device__ inline void triangle_decode_banded(int L, int rows, int cols
     if (x <= cols) return x * (x + 1) / 2;
     return (int64_t)cols * (cols + 1) / 2 + (x - cols) * cols;
   };
-  // largest band b with before(kGroupM b) <= L
-  int lo = 0, hi = (rows + kGroupM - 1) / kGroupM - 1;
+  // largest band b with before(kGroupTri b) <= L
+  int lo = 0, hi = (rows + kGroupTri - 1) / kGroupTri - 1;
   while (lo < hi) {
     const int mid = (lo + hi + 1) / 2;
-    if (before((int64_t)mid * kGroupM) <= (int64_t)L)
+    if (before((int64_t)mid * kGroupTri) <= (int64_t)L)
       lo = mid;
     else
       hi = mid - 1;
   }
-  const int b0 = lo * kGroupM;
-  const int gh = rows - b0 < kGroupM ? rows - b0 : kGroupM;
+  const int b0 = lo * kGroupTri;
+  const int gh = rows - b0 < kGroupTri ? rows - b0 : kGroupTri;
   int o = (int)((int64_t)L - before(b0));
   // columns 0 .. min(b0, cols - 1) hold all gh rows of the band
   const int nfull = b0 + 1 < cols ? b0 + 1 : cols;
@@ -78,8 +85,8 @@ __host__ __device__ inline void triangle_decode_banded(int L, int rows, int cols
 // Logical tile L -> (tile row tm, tile col tn) of a tiles_m x tiles_n grid.
 // uplo 0 (full C): groups of kGroupM tile rows walked column by column.
 // uplo 1 (lower, tm >= tn) / 2 (upper, tm <= tn): the banded triangle order
-// (upper as the lower triangle of the transposed grid, i.e. bands of kGroupM
-// tile columns walked row by row).
+// (upper as the lower triangle of the transposed grid, i.e. bands of
+// kGroupTri tile columns walked row by row).
 __host__ __device__ inline void logical_tile(int L, int tiles_m, int tiles_n, int uplo, int &tm,
                                              int &tn) {
   if (uplo == 1) {

@@ -260,11 +260,13 @@ __device__ __forceinline__ Vec4 mfma4(Vec4 acc, const float (&a)[4], Vec4 b) {
 //     solved rows go to LDS (Xs) and out to B;
 //   * barrier; every wave updates its sub-blocks t > s with them: four MFMAs
 //     whose A operand is the solved rows (from Xs) and B operand the pair
-//     (t, s) of the image, read from global memory kRing - 1 steps ahead.
-//     The owner of sub-block s+1 updates that one first and defers its
-//     others into its substitution (up to two MFMAs per substitution step),
-//     so the next step's substitution starts right after the four MFMAs it
-//     needs.
+//     (t, s) of the image, read from global memory (written kRing - 1
+//     steps ahead; the scheduler issues them at the end of the previous
+//     step, and holding them at the earlier point measured slower). The
+//     owner of sub-block s+1 updates that one first and defers its others
+//     into its substitution (one MFMA per substitution step at kLeaf 256,
+//     up to two for larger blocks), so the next step's substitution starts
+//     right after the four MFMAs it needs.
 // The step loop is unrolled with s and the wave's part w known at compile
 // time (register arrays need constant indices), one copy per part. Making w
 // a uniform runtime branch instead (one copy of the code for all four) held

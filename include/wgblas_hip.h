@@ -203,6 +203,16 @@ int wgb_ssyr2k(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t n,
                int64_t k, float alpha, const float *A, int64_t lda,
                const float *B, int64_t ldb, float beta, float *C, int64_t ldc);
 
+/* Native-FP64 dsyr2k: wgb_ssyr2k's operation in fp64, with reference BLAS's
+ * quick return (alpha == 0 or k == 0 with beta == 1 leaves C,
+ * src/dsyr2k/dsyr2k.mjs:172-174). Replaces dsyr2k
+ * (src/dsyr2k/dsyr2k.mjs:24-331, two dgemm_small passes with its triangle
+ * mask in double-double). */
+int wgb_dsyr2k(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t n,
+               int64_t k, double alpha, const double *A, int64_t lda,
+               const double *B, int64_t ldb, double beta, double *C,
+               int64_t ldc);
+
 /* C <- alpha*A*op(B) + beta*C (side WGB_LEFT, A m-by-m) or
  * alpha*op(B)*A + beta*C (WGB_RIGHT, A n-by-n); A symmetric, only its uplo
  * triangle is read. C and op(B) are m-by-n: B is stored m-by-n (transB ==
@@ -214,6 +224,15 @@ int wgb_ssymm(wgb_ctx *ctx, int side, int uplo, int transB, int64_t m,
               int64_t n, float alpha, const float *A, int64_t lda,
               const float *B, int64_t ldb, float beta, float *C, int64_t ldc);
 
+/* Native-FP64 dsymm: wgb_ssymm's operation in fp64, with reference BLAS's
+ * quick return (alpha == 0 with beta == 1 leaves C,
+ * src/dsymm/dsymm.mjs:143-145). Replaces dsymm (src/dsymm/dsymm.mjs:26-381:
+ * symmetrize.wgsl on both halves, then dgemm_small in double-double). */
+int wgb_dsymm(wgb_ctx *ctx, int side, int uplo, int transB, int64_t m,
+              int64_t n, double alpha, const double *A, int64_t lda,
+              const double *B, int64_t ldb, double beta, double *C,
+              int64_t ldc);
+
 /* B <- alpha*op(A)*B (WGB_LEFT, A m-by-m) or alpha*B*op(A) (WGB_RIGHT,
  * A n-by-n); A triangular (uplo triangle read; diag WGB_UNIT takes its
  * diagonal as 1 without reading it). B is m-by-n, overwritten in place;
@@ -224,10 +243,19 @@ int wgb_strmm(wgb_ctx *ctx, int side, int uplo, int transA, int diag,
               int64_t m, int64_t n, float alpha, const float *A, int64_t lda,
               float *B, int64_t ldb);
 
+/* Native-FP64 dtrmm: wgb_strmm's operation in fp64 (alpha == 0 sets B to
+ * zero). The GEMM multiplies the whole zero-filled triangle copy, as
+ * wgblas's dtrmm does. Replaces dtrmm (src/dtrmm/dtrmm.mjs:28-400:
+ * triangularize.wgsl on both halves, then dgemm_small). */
+int wgb_dtrmm(wgb_ctx *ctx, int side, int uplo, int transA, int diag,
+              int64_t m, int64_t n, double alpha, const double *A, int64_t lda,
+              double *B, int64_t ldb);
+
 /* Solves op(A)*X = alpha*B (WGB_LEFT, A m-by-m) or X*op(A) = alpha*B
  * (WGB_RIGHT, A n-by-n) for X, overwriting the m-by-n B; A triangular as in
- * wgb_strmm. Substitution on diagonal blocks of order <= 64, GEMM updates in
- * between; no explicit inverse. alpha == 0 sets B to zero without reading A
+ * wgb_strmm. Substitution on diagonal blocks of order <= 256 (inside 16-row
+ * sub-blocks, MFMA updates between them), GEMM updates in between the
+ * blocks; no explicit inverse. alpha == 0 sets B to zero without reading A
  * or B. Replaces strsm (src/strsm/strsm.mjs:148-583). */
 int wgb_strsm(wgb_ctx *ctx, int side, int uplo, int transA, int diag,
               int64_t m, int64_t n, float alpha, const float *A, int64_t lda,

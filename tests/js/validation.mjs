@@ -318,6 +318,65 @@ async function main() {
       ldb: loadParam("ld"),
     }, (a) => wg[r](a.device, a.side, a.uplo, a.transA, a.diag, a.m, a.n, a.alpha, a.A, a.lda, a.B, a.ldb,
       a.layout), device);
+  // fp64 level 3: wgblas's tests/{dsyr2k,dsymm,dtrmm}/src/test.*.js
+  // compositions (A64 / B64 / C64; dsyr2k's A with the level-3 cases in f64
+  // wording, as dsyrk's).
+  register("dsyr2k", {
+    device: loadParam("device"),
+    uplo: loadParam("uplo"),
+    trans: loadParam("trans"),
+    layout: loadParam("layout"),
+    n: nWithNegative("must be non-negative"),
+    k: loadParam("k"),
+    alpha: loadParam("alpha"),
+    beta: loadParam("beta"),
+    A: Object.assign({}, A64, {
+      edge: A["level-3"].edge,
+      invalid: A["level-3"].invalid
+        .map((e) => Object.assign({}, e, { error: e.error.replace("Float32Array", "Float64Array") }))
+        .concat(A64.invalid.filter((e) => e.scenario === "wrongDtypeGpuMatrix")),
+      dependsOn: ["n", "k", "lda", "trans"],
+    }),
+    lda: loadParam("ld"),
+    B: Object.assign({}, loadParam("B64"), { dependsOn: ["n", "k", "ldb", "trans"] }),
+    ldb: loadParam("ld"),
+    C: Object.assign({}, loadParam("C64"), { dependsOn: ["n", "ldc"] }),
+    ldc: loadParam("ld"),
+  }, (a) => wg.dsyr2k(a.device, a.uplo, a.trans, a.n, a.k, a.alpha, a.A, a.lda, a.B, a.ldb, a.beta, a.C, a.ldc,
+    a.layout), device);
+  register("dsymm", {
+    device: loadParam("device"),
+    side: loadParam("side"),
+    uplo: loadParam("uplo"),
+    layout: loadParam("layout"),
+    m: Object.assign({}, loadParam("m"), { baseline: 2 }),
+    n: nWithNegative("must be non-negative"),
+    alpha: loadParam("alpha"),
+    beta: loadParam("beta"),
+    A: Object.assign({}, A64, { dependsOn: ["m", "n", "lda", "side"] }),
+    lda: loadParam("ld"),
+    B: Object.assign({}, loadParam("B64"), { dependsOn: ["m", "n", "ldb"] }),
+    ldb: loadParam("ld"),
+    C: loadParam("C64"),
+    ldc: loadParam("ld"),
+  }, (a) => wg.dsymm(a.device, a.side, a.uplo, a.m, a.n, a.alpha, a.A, a.lda, a.B, a.ldb, a.beta, a.C, a.ldc,
+    a.layout), device);
+  register("dtrmm", {
+    device: loadParam("device"),
+    side: loadParam("side"),
+    uplo: loadParam("uplo"),
+    transA: loadParam("trans"),
+    diag: loadParam("diag"),
+    layout: loadParam("layout"),
+    m: Object.assign({}, loadParam("m"), { baseline: 2 }),
+    n: nWithNegative("must be non-negative"),
+    alpha: loadParam("alpha"),
+    A: Object.assign({}, A64, { dependsOn: ["m", "n", "lda", "side"] }),
+    lda: loadParam("ld"),
+    B: Object.assign({}, loadParam("B64"), { dependsOn: ["m", "n", "ldb"] }),
+    ldb: loadParam("ld"),
+  }, (a) => wg.dtrmm(a.device, a.side, a.uplo, a.transA, a.diag, a.m, a.n, a.alpha, a.A, a.lda, a.B, a.ldb,
+    a.layout), device);
   // sgemv: wgblas's tests/sgemv/src/test.sgemv.js composition
   const nS = loadParam("n");
   register("sgemv", {

@@ -1,5 +1,6 @@
 """Pins the oracle's ssyr2k / ssymm / strmm / strsm restatements
-(oracle/oracle.c, orc_*_ld) before the GPU tests trust them.
+(oracle/oracle.c, orc_*_ld; dsyr2k / dsymm / dtrmm use the first three on
+doubles) before the GPU tests trust them.
 
 Checks: every reference edge case (tests/<routine>/edge-cases*.json, both
 layouts) against an independent numpy product (or scipy's
@@ -24,25 +25,30 @@ def close(a, b, rel=1e-12):
 
 
 # ------------------------------------------------------------ edge cases
+# the fp64 routines (dsyr2k / dsymm / dtrmm) run the same restatements on
+# doubles: their own fixtures pin them too
+@pytest.mark.parametrize("routine", ["ssyr2k", "dsyr2k"])
 @pytest.mark.parametrize("cm", [False, True])
-def test_ssyr2k_edge_cases(cm):
-    for c in rc.load("ssyr2k", cm):
+def test_syr2k_edge_cases(routine, cm):
+    for c in rc.load(routine, cm):
         call = rc.syr2k_call(c, np.float64)
         out, _, _ = orc.ssyr2k_ld(*call)
         assert close(out, rc.numpy_syr2k(*call)), c["label"]
 
 
+@pytest.mark.parametrize("routine", ["ssymm", "dsymm"])
 @pytest.mark.parametrize("cm", [False, True])
-def test_ssymm_edge_cases(cm):
-    for c in rc.load("ssymm", cm):
+def test_symm_edge_cases(routine, cm):
+    for c in rc.load(routine, cm):
         call = rc.symm_call(c, np.float64)
         out, _ = orc.ssymm_ld(*call)
         assert close(out, rc.numpy_symm(*call)), c["label"]
 
 
+@pytest.mark.parametrize("routine", ["strmm", "dtrmm"])
 @pytest.mark.parametrize("cm", [False, True])
-def test_strmm_edge_cases(cm):
-    for c in rc.load("strmm", cm):
+def test_trmm_edge_cases(routine, cm):
+    for c in rc.load(routine, cm):
         call = rc.tri_call(c, np.float64)
         out, _ = orc.strmm_ld(*call)
         assert close(out, rc.numpy_trmm(*call)), c["label"]

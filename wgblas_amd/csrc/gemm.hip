@@ -1581,6 +1581,13 @@ int gemm_f32(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64_t 
                             band);
 }
 
+int gemm_f64(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64_t n, int64_t k,
+             double alpha, const double *A, int64_t lda, const double *B, int64_t ldb,
+             double beta, double *C, int64_t ldc) {
+  return gemm_launch<double>(ctx, uplo, transA, transB, m, n, k, alpha, A, lda, B, ldb, beta, C,
+                             ldc, wgb::kBandNone);
+}
+
 int check_gemm(int uplo, bool want_uplo, int transA, int transB, int64_t m, int64_t n, int64_t k,
                const void *A, int64_t lda, const void *B, int64_t ldb, const void *C,
                int64_t ldc) {

@@ -1,5 +1,6 @@
 // The level-3 routines that run on the GEMM kernel: ssyr2k, ssymm, strmm,
-// strsm (wgblas src/{ssyr2k,ssymm,strmm,strsm}/*.mjs).
+// strsm (wgblas src/{ssyr2k,ssymm,strmm,strsm}/*.mjs), and the native-fp64
+// dsyr2k, dsymm, dtrmm (src/{dsyr2k,dsymm,dtrmm}/*.mjs) on its fp64 form.
 //
 // ssyr2k: two triangle GEMM launches, the second with beta = 1.
 // ssymm: the symmetric operand is expanded into a dense workspace copy
@@ -41,10 +42,11 @@ int64_t round4(int64_t v) { return (v + 3) / 4 * 4; }
 // transposes it through LDS, a diagonal tile takes each element from
 // whichever of (i, j), (j, i) is stored. 256 threads = 64 rows x 4 column
 // phases, so every wave reads and writes 256 contiguous bytes of a column.
-__global__ __launch_bounds__(256) void symmetrize_kernel(int64_t order, const float *__restrict__ A,
+template <typename T>
+__global__ __launch_bounds__(256) void symmetrize_kernel(int64_t order, const T *__restrict__ A,
                                                          int64_t lda, int uplo,
-                                                         float *__restrict__ W, int64_t ldw) {
-  __shared__ float s[kTile][kTile + 1];  // s[col][row] of the source tile
+                                                         T *__restrict__ W, int64_t ldw) {
+  __shared__ T s[kTile][kTile + 1];  // s[col][row] of the source tile
   const int bi = blockIdx.x, bj = blockIdx.y;
   const bool lower = uplo == WGB_LOWER;
   const bool diag = bi == bj;
@@ -53,7 +55,7 @@ __global__ __launch_bounds__(256) void symmetrize_kernel(int64_t order, const fl
   const int r = threadIdx.x & 63, ph = threadIdx.x >> 6;
   const int64_t srow = (int64_t)si * kTile + r;
   // unconditional loads from clamped addresses, all in flight together
-  float v[kTile / 4];
+  T v[kTile / 4];
 #pragma unroll
   for (int q = 0; q < kTile / 4; ++q) {
     const int64_t scol = (int64_t)sj * kTile + ph + 4 * q;
@@ -63,7 +65,7 @@ __global__ __launch_bounds__(256) void symmetrize_kernel(int64_t order, const fl
 #pragma unroll
   for (int q = 0; q < kTile / 4; ++q) {
     const int64_t scol = (int64_t)sj * kTile + ph + 4 * q;
-    s[ph + 4 * q][r] = (srow < order && scol < order) ? v[q] : 0.f;
+    s[ph + 4 * q][r] = (srow < order && scol < order) ? v[q] : (T)0;
   }
   __syncthreads();
   const int64_t row = (int64_t)bi * kTile + r;
@@ -71,7 +73,7 @@ __global__ __launch_bounds__(256) void symmetrize_kernel(int64_t order, const fl
   for (int c = ph; c < kTile; c += 4) {
     const int64_t col = (int64_t)bj * kTile + c;
     if (col >= order) break;
-    float v;
+    T v;
     if (stored)
       v = s[c][r];
     else if (!diag)
@@ -85,16 +87,16 @@ __global__ __launch_bounds__(256) void symmetrize_kernel(int64_t order, const fl
 // W <- A's uplo triangle, zero elsewhere, ones on the diagonal for a unit
 // triangle (src/shaders/triangularize.wgsl builds op(A); W keeps A's own
 // orientation and the GEMM applies transA).
-// A thread writes 4 consecutive rows of W (one 16-byte store; W's ld is a
-// multiple of 4) in columns blockIdx.y, blockIdx.y + gridDim.y, ...; a row
+// A thread writes 4 consecutive rows of W (one 16-byte store in fp32, two
+// in fp64; W's ld is a multiple of 4) in columns blockIdx.y, blockIdx.y + gridDim.y, ...; a row
 // group wholly outside the triangle writes zeros without reading A. VEC: lda
-// a multiple of 4 and A 16-byte aligned (16-byte loads).
-template <bool VEC>
+// a multiple of 4 and A aligned to 4 elements (4-element loads).
+template <typename T, bool VEC>
 __global__ __launch_bounds__(256) void triangle_copy_kernel(int64_t order,
-                                                            const float *__restrict__ A,
+                                                            const T *__restrict__ A,
                                                             int64_t lda, int uplo, int unit,
-                                                            float *__restrict__ W, int64_t ldw) {
-  typedef float F4 __attribute__((ext_vector_type(4)));
+                                                            T *__restrict__ W, int64_t ldw) {
+  typedef T F4 __attribute__((ext_vector_type(4)));
   const int64_t row = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
   if (row >= order) return;
   const bool lower = uplo == WGB_LOWER;
@@ -102,9 +104,9 @@ __global__ __launch_bounds__(256) void triangle_copy_kernel(int64_t order,
   for (int64_t col = blockIdx.y; col < order; col += gridDim.y) {
     // does any of rows row .. row+nr-1 lie in the triangle (diagonal included)?
     const bool any = lower ? row + nr - 1 >= col : row <= col;
-    F4 v = F4(0.f);
+    F4 v = F4((T)0);
     if (any) {
-      const float *a = A + row + col * lda;
+      const T *a = A + row + col * lda;
       if (VEC && nr == 4) {
         v = *reinterpret_cast<const F4 *>(a);
       } else {
@@ -115,12 +117,12 @@ __global__ __launch_bounds__(256) void triangle_copy_kernel(int64_t order,
       for (int c = 0; c < 4; ++c) {
         const int64_t r = row + c;
         if (r == col)
-          v[c] = unit ? 1.f : v[c];
+          v[c] = unit ? (T)1 : v[c];
         else if (!(lower ? r > col : r < col))
-          v[c] = 0.f;  // the other triangle: never used, whatever it holds
+          v[c] = (T)0;  // the other triangle: never used, whatever it holds
       }
     }
-    float *w = W + row + col * ldw;
+    T *w = W + row + col * ldw;
     if (nr == 4) {
       *reinterpret_cast<F4 *>(w) = v;
     } else {
@@ -540,9 +542,24 @@ int check_tri(int side, int uplo, int transA, int diag, int64_t m, int64_t n, co
 
 }  // namespace
 
-extern "C" int wgb_ssyr2k(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t n, int64_t k,
-                          float alpha, const float *A, int64_t lda, const float *B, int64_t ldb,
-                          float beta, float *C, int64_t ldc) {
+namespace {
+
+template <typename T>
+int gemm_t(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64_t n, int64_t k,
+           T alpha, const T *A, int64_t lda, const T *B, int64_t ldb, T beta, T *C, int64_t ldc,
+           int band) {
+  if constexpr (sizeof(T) == 4)
+    return wgb::gemm_f32(ctx, uplo, transA, transB, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc,
+                         band);
+  else
+    return wgb::gemm_f64(ctx, uplo, transA, transB, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc);
+}
+
+// ssyr2k / dsyr2k. fp64 keeps reference BLAS's quick return
+// (src/dsyr2k/dsyr2k.mjs:172-174): alpha = 0 or k = 0 with beta = 1 leaves C.
+template <typename T>
+int syr2k(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t n, int64_t k, T alpha,
+          const T *A, int64_t lda, const T *B, int64_t ldb, T beta, T *C, int64_t ldc) {
   int st = wgb::enter(ctx);
   if (st) return st;
   if (transA != WGB_NO_TRANS && transA != WGB_TRANS)
@@ -554,23 +571,26 @@ extern "C" int wgb_ssyr2k(wgb_ctx *ctx, int uplo, int transA, int transB, int64_
   const int tBt = transB == WGB_NO_TRANS ? WGB_TRANS : WGB_NO_TRANS;
   if ((st = wgb::check_gemm(uplo, true, transA, tBt, n, n, k, A, lda, B, ldb, C, ldc))) return st;
   if (n == 0) return WGB_OK;
+  if (sizeof(T) == 8 && (alpha == (T)0 || k == 0) && beta == (T)1) return WGB_OK;
   wgb::timing_begin(ctx);
   // pass 1: alpha op(A) op(B)^T + beta C; pass 2: alpha op(B) op(A)^T + C
   // (src/ssyr2k/ssyr2k.mjs:206-262), one timed span
-  if ((st = wgb::gemm_f32(ctx, uplo, transA, tBt, n, n, k, alpha, A, lda, B, ldb, beta, C, ldc,
-                          wgb::kBandNone)))
+  if ((st = gemm_t<T>(ctx, uplo, transA, tBt, n, n, k, alpha, A, lda, B, ldb, beta, C, ldc,
+                      wgb::kBandNone)))
     return st;
-  if (alpha != 0.f && k != 0 &&
-      (st = wgb::gemm_f32(ctx, uplo, transB, tAt, n, n, k, alpha, B, ldb, A, lda, 1.f, C, ldc,
-                          wgb::kBandNone)))
+  if (alpha != (T)0 && k != 0 &&
+      (st = gemm_t<T>(ctx, uplo, transB, tAt, n, n, k, alpha, B, ldb, A, lda, (T)1, C, ldc,
+                      wgb::kBandNone)))
     return st;
   wgb::timing_end(ctx);
   return WGB_OK;
 }
 
-extern "C" int wgb_ssymm(wgb_ctx *ctx, int side, int uplo, int transB, int64_t m, int64_t n,
-                         float alpha, const float *A, int64_t lda, const float *B, int64_t ldb,
-                         float beta, float *C, int64_t ldc) {
+// ssymm / dsymm. fp64 keeps reference BLAS's quick return
+// (src/dsymm/dsymm.mjs:143-145): alpha = 0 with beta = 1 leaves C.
+template <typename T>
+int symm(wgb_ctx *ctx, int side, int uplo, int transB, int64_t m, int64_t n, T alpha, const T *A,
+         int64_t lda, const T *B, int64_t ldb, T beta, T *C, int64_t ldc) {
   int st = wgb::enter(ctx);
   if (st) return st;
   if (side != WGB_LEFT && side != WGB_RIGHT)
@@ -588,67 +608,115 @@ extern "C" int wgb_ssymm(wgb_ctx *ctx, int side, int uplo, int transB, int64_t m
     return fail(WGB_ERR_INVALID_VALUE, "ldb must be >= max(1, rows of B)");
   if (ldc < imax(1, m)) return fail(WGB_ERR_INVALID_VALUE, "ldc must be >= max(1, m)");
   if (m == 0 || n == 0) return WGB_OK;
-  if (!C || (alpha != 0.f && (!A || !B))) return fail(WGB_ERR_INVALID_VALUE, "A, B or C is null");
+  if (!C || (alpha != (T)0 && (!A || !B))) return fail(WGB_ERR_INVALID_VALUE, "A, B or C is null");
+  if (sizeof(T) == 8 && alpha == (T)0 && beta == (T)1) return WGB_OK;
   wgb::timing_begin(ctx);
-  if (alpha == 0.f) {
+  if (alpha == (T)0) {
     // C <- beta C, reading neither A nor B
-    st = wgb::gemm_f32(ctx, 0, WGB_NO_TRANS, WGB_NO_TRANS, m, n, 0, 0.f, nullptr, 1, nullptr, 1,
-                       beta, C, ldc, wgb::kBandNone);
+    st = gemm_t<T>(ctx, 0, WGB_NO_TRANS, WGB_NO_TRANS, m, n, 0, (T)0, nullptr, 1, nullptr, 1, beta,
+                   C, ldc, wgb::kBandNone);
   } else {
     const int64_t ldw = round4(order);
-    if ((st = wgb::ensure_op_workspace(ctx, (size_t)ldw * order * sizeof(float)))) return st;
-    float *W = static_cast<float *>(ctx->op_ws);
+    if ((st = wgb::ensure_op_workspace(ctx, (size_t)ldw * order * sizeof(T)))) return st;
+    T *W = static_cast<T *>(ctx->op_ws);
     const int64_t tiles = (order + kTile - 1) / kTile;
-    symmetrize_kernel<<<dim3((unsigned)tiles, (unsigned)tiles), 256, 0, ctx->stream>>>(order, A, lda,
-                                                                                      uplo, W, ldw);
+    symmetrize_kernel<T><<<dim3((unsigned)tiles, (unsigned)tiles), 256, 0, ctx->stream>>>(
+        order, A, lda, uplo, W, ldw);
     WGB_CHECK_LAUNCH("symmetrize_kernel");
     st = side == WGB_LEFT
-             ? wgb::gemm_f32(ctx, 0, WGB_NO_TRANS, transB, m, n, m, alpha, W, ldw, B, ldb, beta, C,
-                             ldc, wgb::kBandNone)
-             : wgb::gemm_f32(ctx, 0, transB, WGB_NO_TRANS, m, n, n, alpha, B, ldb, W, ldw, beta, C,
-                             ldc, wgb::kBandNone);
+             ? gemm_t<T>(ctx, 0, WGB_NO_TRANS, transB, m, n, m, alpha, W, ldw, B, ldb, beta, C, ldc,
+                         wgb::kBandNone)
+             : gemm_t<T>(ctx, 0, transB, WGB_NO_TRANS, m, n, n, alpha, B, ldb, W, ldw, beta, C, ldc,
+                         wgb::kBandNone);
   }
   if (st) return st;
   wgb::timing_end(ctx);
   return WGB_OK;
 }
 
-extern "C" int wgb_strmm(wgb_ctx *ctx, int side, int uplo, int transA, int diag, int64_t m,
-                         int64_t n, float alpha, const float *A, int64_t lda, float *B,
-                         int64_t ldb) {
+// strmm / dtrmm: the triangle copied with zeros elsewhere, B copied, one
+// GEMM. The fp32 GEMM runs only the k-tiles the triangle reaches (banded
+// tiles); fp64 multiplies the whole copy, as wgblas's dtrmm does
+// (src/dtrmm/dtrmm.mjs:21-27).
+template <typename T>
+int trmm(wgb_ctx *ctx, int side, int uplo, int transA, int diag, int64_t m, int64_t n, T alpha,
+         const T *A, int64_t lda, T *B, int64_t ldb) {
   int st = wgb::enter(ctx);
   if (st) return st;
   if ((st = check_tri(side, uplo, transA, diag, m, n, A, lda, B, ldb))) return st;
   if (m == 0 || n == 0) return WGB_OK;
   wgb::timing_begin(ctx);
-  if (alpha == 0.f) {
-    st = zero_b(ctx, m, n, B, ldb);
+  if (alpha == (T)0) {
+    // B <- 0, reading neither A nor B
+    st = gemm_t<T>(ctx, 0, WGB_NO_TRANS, WGB_NO_TRANS, m, n, 0, (T)0, nullptr, 1, nullptr, 1, (T)0,
+                   B, ldb, wgb::kBandNone);
   } else {
     const bool left = side == WGB_LEFT;
     const int64_t order = left ? m : n;
     const int64_t ldw = round4(order), ldbc = round4(m);
-    if ((st = wgb::ensure_op_workspace(ctx, (size_t)(ldw * order + ldbc * n) * sizeof(float)))) return st;
-    float *W = static_cast<float *>(ctx->op_ws);
-    float *Bc = W + ldw * order;  // 16-byte aligned: ldw is a multiple of 4
+    if ((st = wgb::ensure_op_workspace(ctx, (size_t)(ldw * order + ldbc * n) * sizeof(T)))) return st;
+    T *W = static_cast<T *>(ctx->op_ws);
+    T *Bc = W + ldw * order;  // 16-byte aligned: ldw is a multiple of 4
     const int64_t gy = order < 4096 ? order : 4096;
     const dim3 grid((unsigned)((order + 1023) / 1024), (unsigned)gy);
-    if (lda % 4 == 0 && wgb::aligned16(A))
-      triangle_copy_kernel<true><<<grid, 256, 0, ctx->stream>>>(order, A, lda, uplo, diag == WGB_UNIT, W, ldw);
+    // VEC loads 4 elements at once: A aligned to 4 elements (16 or 32 bytes)
+    if (lda % 4 == 0 && ((uintptr_t)A % (4 * sizeof(T))) == 0)
+      triangle_copy_kernel<T, true><<<grid, 256, 0, ctx->stream>>>(order, A, lda, uplo,
+                                                                   diag == WGB_UNIT, W, ldw);
     else
-      triangle_copy_kernel<false><<<grid, 256, 0, ctx->stream>>>(order, A, lda, uplo, diag == WGB_UNIT, W, ldw);
+      triangle_copy_kernel<T, false><<<grid, 256, 0, ctx->stream>>>(order, A, lda, uplo,
+                                                                    diag == WGB_UNIT, W, ldw);
     WGB_CHECK_LAUNCH("triangle_copy_kernel");
-    WGB_CHECK_HIP(hipMemcpy2DAsync(Bc, (size_t)ldbc * sizeof(float), B, (size_t)ldb * sizeof(float),
-                                   (size_t)m * sizeof(float), (size_t)n, hipMemcpyDeviceToDevice,
+    WGB_CHECK_HIP(hipMemcpy2DAsync(Bc, (size_t)ldbc * sizeof(T), B, (size_t)ldb * sizeof(T),
+                                   (size_t)m * sizeof(T), (size_t)n, hipMemcpyDeviceToDevice,
                                    ctx->stream));
     const bool op_lower = (uplo == WGB_LOWER) != (transA == WGB_TRANS);
-    st = left ? wgb::gemm_f32(ctx, 0, transA, WGB_NO_TRANS, m, n, m, alpha, W, ldw, Bc, ldbc, 0.f, B,
-                              ldb, op_lower ? wgb::kBandALower : wgb::kBandAUpper)
-              : wgb::gemm_f32(ctx, 0, WGB_NO_TRANS, transA, m, n, n, alpha, Bc, ldbc, W, ldw, 0.f, B,
-                              ldb, op_lower ? wgb::kBandBLower : wgb::kBandBUpper);
+    st = left ? gemm_t<T>(ctx, 0, transA, WGB_NO_TRANS, m, n, m, alpha, W, ldw, Bc, ldbc, (T)0, B,
+                          ldb, op_lower ? wgb::kBandALower : wgb::kBandAUpper)
+              : gemm_t<T>(ctx, 0, WGB_NO_TRANS, transA, m, n, n, alpha, Bc, ldbc, W, ldw, (T)0, B,
+                          ldb, op_lower ? wgb::kBandBLower : wgb::kBandBUpper);
   }
   if (st) return st;
   wgb::timing_end(ctx);
   return WGB_OK;
+}
+
+}  // namespace
+
+extern "C" int wgb_ssyr2k(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t n, int64_t k,
+                          float alpha, const float *A, int64_t lda, const float *B, int64_t ldb,
+                          float beta, float *C, int64_t ldc) {
+  return syr2k<float>(ctx, uplo, transA, transB, n, k, alpha, A, lda, B, ldb, beta, C, ldc);
+}
+
+extern "C" int wgb_dsyr2k(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t n, int64_t k,
+                          double alpha, const double *A, int64_t lda, const double *B, int64_t ldb,
+                          double beta, double *C, int64_t ldc) {
+  return syr2k<double>(ctx, uplo, transA, transB, n, k, alpha, A, lda, B, ldb, beta, C, ldc);
+}
+
+extern "C" int wgb_ssymm(wgb_ctx *ctx, int side, int uplo, int transB, int64_t m, int64_t n,
+                         float alpha, const float *A, int64_t lda, const float *B, int64_t ldb,
+                         float beta, float *C, int64_t ldc) {
+  return symm<float>(ctx, side, uplo, transB, m, n, alpha, A, lda, B, ldb, beta, C, ldc);
+}
+
+extern "C" int wgb_dsymm(wgb_ctx *ctx, int side, int uplo, int transB, int64_t m, int64_t n,
+                         double alpha, const double *A, int64_t lda, const double *B, int64_t ldb,
+                         double beta, double *C, int64_t ldc) {
+  return symm<double>(ctx, side, uplo, transB, m, n, alpha, A, lda, B, ldb, beta, C, ldc);
+}
+
+extern "C" int wgb_strmm(wgb_ctx *ctx, int side, int uplo, int transA, int diag, int64_t m,
+                         int64_t n, float alpha, const float *A, int64_t lda, float *B,
+                         int64_t ldb) {
+  return trmm<float>(ctx, side, uplo, transA, diag, m, n, alpha, A, lda, B, ldb);
+}
+
+extern "C" int wgb_dtrmm(wgb_ctx *ctx, int side, int uplo, int transA, int diag, int64_t m,
+                         int64_t n, double alpha, const double *A, int64_t lda, double *B,
+                         int64_t ldb) {
+  return trmm<double>(ctx, side, uplo, transA, diag, m, n, alpha, A, lda, B, ldb);
 }
 
 extern "C" int wgb_strsm(wgb_ctx *ctx, int side, int uplo, int transA, int diag, int64_t m,

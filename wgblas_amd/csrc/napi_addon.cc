@@ -344,8 +344,15 @@ napi_value Ssyr2k(napi_env env, napi_callback_info info) {
       !get_i64(env, a.v[10], &ldb) || !get_f64(env, a.v[11], &beta) || !get_ptr(env, a.v[12], &C) ||
       !get_i64(env, a.v[13], &ldc))
     return nullptr;
-  WGB_OK_OR_THROW(wgb_ssyr2k(ctx, uplo, ta, tb, n, k, (float)alpha, (const float *)A, lda,
-                             (const float *)B, ldb, (float)beta, (float *)C, ldc), "wgb_ssyr2k");
+  bool f64 = false;  // optional 15th argument: dsyr2k
+  if (a.n > 14 && napi_get_value_bool(env, a.v[14], &f64) != napi_ok) f64 = false;
+  if (f64) {
+    WGB_OK_OR_THROW(wgb_dsyr2k(ctx, uplo, ta, tb, n, k, alpha, (const double *)A, lda,
+                               (const double *)B, ldb, beta, (double *)C, ldc), "wgb_dsyr2k");
+  } else {
+    WGB_OK_OR_THROW(wgb_ssyr2k(ctx, uplo, ta, tb, n, k, (float)alpha, (const float *)A, lda,
+                               (const float *)B, ldb, (float)beta, (float *)C, ldc), "wgb_ssyr2k");
+  }
   return nullptr;
 }
 
@@ -365,13 +372,20 @@ napi_value Ssymm(napi_env env, napi_callback_info info) {
       !get_i64(env, a.v[10], &ldb) || !get_f64(env, a.v[11], &beta) || !get_ptr(env, a.v[12], &C) ||
       !get_i64(env, a.v[13], &ldc))
     return nullptr;
-  WGB_OK_OR_THROW(wgb_ssymm(ctx, side, uplo, tb, m, n, (float)alpha, (const float *)A, lda,
-                            (const float *)B, ldb, (float)beta, (float *)C, ldc), "wgb_ssymm");
+  bool f64 = false;  // optional 15th argument: dsymm
+  if (a.n > 14 && napi_get_value_bool(env, a.v[14], &f64) != napi_ok) f64 = false;
+  if (f64) {
+    WGB_OK_OR_THROW(wgb_dsymm(ctx, side, uplo, tb, m, n, alpha, (const double *)A, lda,
+                              (const double *)B, ldb, beta, (double *)C, ldc), "wgb_dsymm");
+  } else {
+    WGB_OK_OR_THROW(wgb_ssymm(ctx, side, uplo, tb, m, n, (float)alpha, (const float *)A, lda,
+                              (const float *)B, ldb, (float)beta, (float *)C, ldc), "wgb_ssymm");
+  }
   return nullptr;
 }
 
 // tri(kind, ctx, side, uplo, transA, diag, m, n, alpha, A, lda, B, ldb);
-// kind: 0 strmm, 1 strsm.
+// kind: 0 strmm, 1 strsm, 2 dtrmm.
 napi_value Tri(napi_env env, napi_callback_info info) {
   Args a;
   if (!get_args(env, info, a, 13)) return nullptr;
@@ -390,6 +404,9 @@ napi_value Tri(napi_env env, napi_callback_info info) {
   if (kind == 0) {
     WGB_OK_OR_THROW(wgb_strmm(ctx, side, uplo, trans, diag, m, n, (float)alpha, (const float *)A,
                               lda, (float *)B, ldb), "wgb_strmm");
+  } else if (kind == 2) {
+    WGB_OK_OR_THROW(wgb_dtrmm(ctx, side, uplo, trans, diag, m, n, alpha, (const double *)A, lda,
+                              (double *)B, ldb), "wgb_dtrmm");
   } else {
     WGB_OK_OR_THROW(wgb_strsm(ctx, side, uplo, trans, diag, m, n, (float)alpha, (const float *)A,
                               lda, (float *)B, ldb), "wgb_strsm");

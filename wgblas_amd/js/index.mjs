@@ -15,6 +15,9 @@ export { dsyrk } from "./src/dsyrk.mjs";
 export { ssyr2k } from "./src/ssyr2k.mjs";
 export { ssymm } from "./src/ssymm.mjs";
 export { strmm } from "./src/strmm.mjs";
+export { dsyr2k } from "./src/dsyr2k.mjs";
+export { dsymm } from "./src/dsymm.mjs";
+export { dtrmm } from "./src/dtrmm.mjs";
 export { strsm } from "./src/strsm.mjs";
 export { sgemv } from "./src/sgemv.mjs";
 export { sdot } from "./src/sdot.mjs";

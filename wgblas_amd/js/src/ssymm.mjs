@@ -12,11 +12,20 @@ import { native } from "./native.mjs";
 
 export async function ssymm(device, side, uplo, m, n, alpha, A, lda, B, ldb, beta, C, ldc,
                             layout = "row-major") {
+  return symm("ssymm", device, side, uplo, m, n, alpha, A, lda, B, ldb, beta, C, ldc, layout);
+}
+
+/** ssymm, or dsymm (routine "dsymm": Float64Array operands, reference
+ * BLAS's quick return, wgblas src/dsymm/dsymm.mjs:26-381 with the same
+ * checks and messages). */
+export async function symm(routine, device, side, uplo, m, n, alpha, A, lda, B, ldb, beta, C, ldc,
+                           layout) {
+  const F = routine === "dsymm" ? Float64Array : Float32Array;
   const AIsGpu = A instanceof GpuMatrix;
   const BIsGpu = B instanceof GpuMatrix;
   const CIsGpu = C instanceof GpuMatrix;
   requireGpuDevice(device);
-  requireSameDevice(device, "ssymm", { A, B, C });
+  requireSameDevice(device, routine, { A, B, C });
   checkSide(side);
   checkUplo(uplo);
   checkLayout(layout);
@@ -24,12 +33,12 @@ export async function ssymm(device, side, uplo, m, n, alpha, A, lda, B, ldb, bet
   checkScalar("beta", beta);
   for (const v of [m, n, lda, ldb, ldc])
     if (!Number.isInteger(v)) throw new Error("m, n, lda, ldb, and ldc must be integers.");
-  if (!AIsGpu && !(A instanceof Float32Array)) throw new Error("A must be a Float32Array or GpuMatrix.");
-  if (!BIsGpu && !(B instanceof Float32Array)) throw new Error("B must be a Float32Array or GpuMatrix.");
-  if (!CIsGpu && !(C instanceof Float32Array)) throw new Error("C must be a Float32Array or GpuMatrix.");
-  checkResidentDtype("A", A, AIsGpu, Float32Array);
-  checkResidentDtype("B", B, BIsGpu, Float32Array);
-  checkResidentDtype("C", C, CIsGpu, Float32Array);
+  if (!AIsGpu && !(A instanceof F)) throw new Error(`A must be a ${F.name} or GpuMatrix.`);
+  if (!BIsGpu && !(B instanceof F)) throw new Error(`B must be a ${F.name} or GpuMatrix.`);
+  if (!CIsGpu && !(C instanceof F)) throw new Error(`C must be a ${F.name} or GpuMatrix.`);
+  checkResidentDtype("A", A, AIsGpu, F);
+  checkResidentDtype("B", B, BIsGpu, F);
+  checkResidentDtype("C", C, CIsGpu, F);
   if ((AIsGpu || BIsGpu) && !CIsGpu) throw new Error("C must be a GpuMatrix when A or B is a GpuMatrix.");
   if (CIsGpu && (!AIsGpu || !BIsGpu)) throw new Error("A and B must be GpuMatrix when C is a GpuMatrix.");
   if (m < 0 || n < 0) throw new Error("m and n must be non-negative.");
@@ -57,7 +66,9 @@ export async function ssymm(device, side, uplo, m, n, alpha, A, lda, B, ldb, bet
   let [mm, nn] = [m, n];
   if (layoutC !== "column-major") [s, mm, nn] = [3 - s, n, m];
   const tB = layoutB === layoutC ? NO_TRANS : TRANS;
-  return execute(device, [A, B], C, CIsGpu, Float32Array, (ctx, p, pC) =>
-    native().ssymm(ctx, s, u, tB, mm, nn, alpha, p[0], lda, p[1], ldb, beta, pC, ldc),
+  // Reference BLAS quick return in fp64 (dsymm.mjs:143-145): C as it is.
+  if (F === Float64Array && alpha === 0 && beta === 1) return CIsGpu ? {} : { C };
+  return execute(device, [A, B], C, CIsGpu, F, (ctx, p, pC) =>
+    native().ssymm(ctx, s, u, tB, mm, nn, alpha, p[0], lda, p[1], ldb, beta, pC, ldc, F === Float64Array),
   );
 }

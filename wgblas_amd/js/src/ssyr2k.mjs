@@ -12,11 +12,20 @@ import { native } from "./native.mjs";
 
 export async function ssyr2k(device, uplo, trans, n, k, alpha, A, lda, B, ldb, beta, C, ldc,
                              layout = "row-major") {
+  return syr2k("ssyr2k", device, uplo, trans, n, k, alpha, A, lda, B, ldb, beta, C, ldc, layout);
+}
+
+/** ssyr2k, or dsyr2k (routine "dsyr2k": Float64Array operands, reference
+ * BLAS's quick return, wgblas src/dsyr2k/dsyr2k.mjs:24-331 with the same
+ * checks and messages). */
+export async function syr2k(routine, device, uplo, trans, n, k, alpha, A, lda, B, ldb, beta, C, ldc,
+                            layout) {
+  const F = routine === "dsyr2k" ? Float64Array : Float32Array;
   const AIsGpu = A instanceof GpuMatrix;
   const BIsGpu = B instanceof GpuMatrix;
   const CIsGpu = C instanceof GpuMatrix;
   requireGpuDevice(device);
-  requireSameDevice(device, "ssyr2k", { A, B, C });
+  requireSameDevice(device, routine, { A, B, C });
   checkUplo(uplo);
   checkTrans("trans", trans);
   checkLayout(layout);
@@ -24,12 +33,12 @@ export async function ssyr2k(device, uplo, trans, n, k, alpha, A, lda, B, ldb, b
   checkScalar("beta", beta);
   for (const v of [n, k, lda, ldb, ldc])
     if (!Number.isInteger(v)) throw new Error("n, k, lda, ldb, and ldc must be integers.");
-  if (!AIsGpu && !(A instanceof Float32Array)) throw new Error("A must be a Float32Array or GpuMatrix.");
-  if (!BIsGpu && !(B instanceof Float32Array)) throw new Error("B must be a Float32Array or GpuMatrix.");
-  if (!CIsGpu && !(C instanceof Float32Array)) throw new Error("C must be a Float32Array or GpuMatrix.");
-  checkResidentDtype("A", A, AIsGpu, Float32Array);
-  checkResidentDtype("B", B, BIsGpu, Float32Array);
-  checkResidentDtype("C", C, CIsGpu, Float32Array);
+  if (!AIsGpu && !(A instanceof F)) throw new Error(`A must be a ${F.name} or GpuMatrix.`);
+  if (!BIsGpu && !(B instanceof F)) throw new Error(`B must be a ${F.name} or GpuMatrix.`);
+  if (!CIsGpu && !(C instanceof F)) throw new Error(`C must be a ${F.name} or GpuMatrix.`);
+  checkResidentDtype("A", A, AIsGpu, F);
+  checkResidentDtype("B", B, BIsGpu, F);
+  checkResidentDtype("C", C, CIsGpu, F);
   if ((AIsGpu || BIsGpu) && !CIsGpu) throw new Error("C must be a GpuMatrix when A or B is a GpuMatrix.");
   if (CIsGpu && (!AIsGpu || !BIsGpu)) throw new Error("A and B must be GpuMatrix when C is a GpuMatrix.");
   if (n < 0 || k < 0) throw new Error("n and k must be non-negative.");
@@ -53,9 +62,11 @@ export async function ssyr2k(device, uplo, trans, n, k, alpha, A, lda, B, ldb, b
   const tB = (trans === "transpose") !== (layoutB !== "column-major") ? TRANS : NO_TRANS;
   let u = UPLO[uplo];
   if (layoutC !== "column-major") u = u === 1 ? 2 : 1;
+  // Reference BLAS quick return in fp64 (dsyr2k.mjs:172-174): C as it is.
+  if (F === Float64Array && (alpha === 0 || k === 0) && beta === 1) return CIsGpu ? {} : { C };
   // A and B of different storage orders (GpuMatrix operands) get different
   // flags: one native call either way (one gpuTimeMs span).
-  return execute(device, [A, B], C, CIsGpu, Float32Array, (ctx, p, pC) =>
-    native().ssyr2k(ctx, u, tA, tB, n, k, alpha, p[0], lda, p[1], ldb, beta, pC, ldc),
+  return execute(device, [A, B], C, CIsGpu, F, (ctx, p, pC) =>
+    native().ssyr2k(ctx, u, tA, tB, n, k, alpha, p[0], lda, p[1], ldb, beta, pC, ldc, F === Float64Array),
   );
 }

@@ -1,6 +1,7 @@
-// Shared checks and the column-major mapping of strmm and strsm (wgblas
-// src/strmm/strmm.mjs:46-129, src/strsm/strsm.mjs:162-247: the same checks,
-// in the same order, with the same messages), and ssymm's side check.
+// Shared checks and the column-major mapping of strmm, strsm and dtrmm
+// (wgblas src/strmm/strmm.mjs:46-129, src/strsm/strsm.mjs:162-247,
+// src/dtrmm/dtrmm.mjs:45-113: the same checks, in the same order, with the
+// same messages), and ssymm's side check.
 import { GpuMatrix } from "./classes/GpuMatrix.mjs";
 import { requireGpuDevice, requireSameDevice } from "./device.mjs";
 import {
@@ -15,12 +16,14 @@ export function checkSide(side) {
 }
 
 /**
- * strmm (kind 0) / strsm (kind 1): validation, then one device call on the
- * column-major frame. Returns { B } (a new Float32Array) for host arrays, {}
- * when B is a GpuMatrix (updated in place).
+ * strmm (kind 0) / strsm (kind 1) / dtrmm (kind 2, Float64Array operands,
+ * wgblas src/dtrmm/dtrmm.mjs:28-400 with the same checks): validation, then
+ * one device call on the column-major frame. Returns { B } (a new typed
+ * array) for host arrays, {} when B is a GpuMatrix (updated in place).
  */
 export function runTri(kind, routine, device, side, uplo, transA, diag, m, n, alpha, A, lda, B, ldb,
                        layout) {
+  const F = kind === 2 ? Float64Array : Float32Array;
   const AIsGpu = A instanceof GpuMatrix;
   const BIsGpu = B instanceof GpuMatrix;
   const isUnit = diag === "unit";
@@ -36,11 +39,11 @@ export function runTri(kind, routine, device, side, uplo, transA, diag, m, n, al
   if (!Number.isFinite(alpha)) throw new Error("alpha must be finite.");
   for (const v of [m, n, lda, ldb])
     if (!Number.isInteger(v)) throw new Error("m, n, lda, and ldb must be integers.");
-  if (!AIsGpu && !(A instanceof Float32Array)) throw new Error("A must be a Float32Array or GpuMatrix.");
-  if (!BIsGpu && !(B instanceof Float32Array)) throw new Error("B must be a Float32Array or GpuMatrix.");
-  checkResidentDtype("A", A, AIsGpu, Float32Array);
-  checkResidentDtype("B", B, BIsGpu, Float32Array);
-  if (AIsGpu !== BIsGpu) throw new Error("A and B must both be GpuMatrix or both be Float32Array.");
+  if (!AIsGpu && !(A instanceof F)) throw new Error(`A must be a ${F.name} or GpuMatrix.`);
+  if (!BIsGpu && !(B instanceof F)) throw new Error(`B must be a ${F.name} or GpuMatrix.`);
+  checkResidentDtype("A", A, AIsGpu, F);
+  checkResidentDtype("B", B, BIsGpu, F);
+  if (AIsGpu !== BIsGpu) throw new Error(`A and B must both be GpuMatrix or both be ${F.name}.`);
   if (m < 0 || n < 0) throw new Error("m and n must be non-negative.");
   if (m === 0 || n === 0) return BIsGpu ? {} : { B };
   const layoutA = AIsGpu ? A.layout : layout;
@@ -65,6 +68,6 @@ export function runTri(kind, routine, device, side, uplo, transA, diag, m, n, al
   let s = SIDE[side];
   let [mm, nn] = [m, n];
   if (bRow) [s, mm, nn] = [3 - s, n, m];
-  return execute(device, [A], B, BIsGpu, Float32Array, (ctx, p, pB) =>
+  return execute(device, [A], B, BIsGpu, F, (ctx, p, pB) =>
     native().tri(kind, ctx, s, u, t, isUnit ? 1 : 0, mm, nn, alpha, p[0], lda, pB, ldb), "B");
 }

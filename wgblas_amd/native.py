@@ -62,6 +62,12 @@ _SIGNATURES = {
                   C.c_float, _ptr, _i64],
     "wgb_strmm": [_ptr, C.c_int, C.c_int, C.c_int, C.c_int, _i64, _i64, C.c_float, _ptr, _i64,
                   _ptr, _i64],
+    "wgb_dsyr2k": [_ptr, C.c_int, C.c_int, C.c_int, _i64, _i64, C.c_double, _ptr, _i64, _ptr, _i64,
+                   C.c_double, _ptr, _i64],
+    "wgb_dsymm": [_ptr, C.c_int, C.c_int, C.c_int, _i64, _i64, C.c_double, _ptr, _i64, _ptr, _i64,
+                  C.c_double, _ptr, _i64],
+    "wgb_dtrmm": [_ptr, C.c_int, C.c_int, C.c_int, C.c_int, _i64, _i64, C.c_double, _ptr, _i64,
+                  _ptr, _i64],
     "wgb_strsm": [_ptr, C.c_int, C.c_int, C.c_int, C.c_int, _i64, _i64, C.c_float, _ptr, _i64,
                   _ptr, _i64],
     "wgb_sgemv": [_ptr, C.c_int, _i64, _i64, C.c_float, _ptr, _i64, _ptr, _i64, C.c_float, _ptr,
@@ -289,6 +295,20 @@ class Context:
     def strmm(self, side, uplo, transA, diag, m, n, alpha, A, lda, B, ldb):
         _check(self.lib.wgb_strmm(self.handle, side, uplo, transA, diag, m, n, alpha, _p(A), lda,
                                   _p(B), ldb), "wgb_strmm")
+
+    def dsyr2k(self, uplo, trans, n, k, alpha, A, lda, B, ldb, beta, C_, ldc, transB=None):
+        """`trans` applies to A, and to B unless `transB` is given."""
+        tb = trans if transB is None else transB
+        _check(self.lib.wgb_dsyr2k(self.handle, uplo, trans, tb, n, k, alpha, _p(A), lda, _p(B),
+                                   ldb, beta, _p(C_), ldc), "wgb_dsyr2k")
+
+    def dsymm(self, side, uplo, m, n, alpha, A, lda, B, ldb, beta, C_, ldc, transB=NO_TRANS):
+        _check(self.lib.wgb_dsymm(self.handle, side, uplo, transB, m, n, alpha, _p(A), lda, _p(B),
+                                  ldb, beta, _p(C_), ldc), "wgb_dsymm")
+
+    def dtrmm(self, side, uplo, transA, diag, m, n, alpha, A, lda, B, ldb):
+        _check(self.lib.wgb_dtrmm(self.handle, side, uplo, transA, diag, m, n, alpha, _p(A), lda,
+                                  _p(B), ldb), "wgb_dtrmm")
 
     def strsm(self, side, uplo, transA, diag, m, n, alpha, A, lda, B, ldb):
         _check(self.lib.wgb_strsm(self.handle, side, uplo, transA, diag, m, n, alpha, _p(A), lda,

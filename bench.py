@@ -17,7 +17,8 @@ Also reported under "components", each timed the same way: sgemm 512^3
 n = 8192, k = 4096, 10 chained resident calls (config 5), and sdot / sasum /
 snrm2 / isamax at n = 2^28 plus the incx = 3, n = 2^26 variants (config 2),
 sgemmtr on config 5's operands, ssyr2k / ssymm / strmm / strsm at order 8192
-(strsm also 4096), sgemv 16384 x 16384 in both forms, and ddot / dasum /
+(strsm also 4096), dsyr2k / dsymm / dtrmm at order 4096, sgemv 16384 x 16384
+in both forms, and ddot / dasum /
 dnrm2 / idamax at n = 2^27
 (the same bytes as config 2's fp32 vectors; uniform[-1, 1) inputs, seeds 1
 and 2, as wgblas's randomFloat64Array).
@@ -271,6 +272,7 @@ def bench_components(ctx, ev, quick):
     dB.free()
     dC.free()
     comps.update(bench_level3(ctx, reps))
+    comps.update(bench_level3_f64(ctx, reps))
 
     # sgemv, 16384 x 16384 (1 GiB of A, read once: the HBM roof), both forms
     n = 16384
@@ -396,6 +398,39 @@ def bench_level3(ctx, reps):
     return comps
 
 
+def bench_level3_f64(ctx, reps):
+    """dsyr2k (k = n), dsymm and dtrmm at order 4096 (dgemm's size; left
+    side, lower, no transpose, alpha 1, beta 0: wgblas's benchmarks/<routine>
+    defaults), with those benchmarks' flop conventions (dsyr2k 2n(n+1)k,
+    dsymm 2mn*order + 2mn, dtrmm 2mn*order + mn); `frac_fp64_peak` uses the
+    arithmetic the routine must do (dtrmm: the triangle's mn*order)."""
+    from wgblas_amd import LEFT, LOWER, NON_UNIT, NO_TRANS
+
+    comps = {}
+    n = 4096
+    dA, dB, dC = (ctx.empty(n * n, np.float64) for _ in range(3))
+    ctx.fill_uniform(dA, -1.0, 1.0, 7)
+    ctx.fill_uniform(dB, -1.0, 1.0, 8)
+    ctx.fill_uniform(dC, -1.0, 1.0, 9)
+    f = lambda: ctx.dsyr2k(LOWER, NO_TRANS, n, n, 1.0, dA, n, dB, n, 0.0, dC, n)
+    ms = per_launch_ms(ctx, f, reps, warm=True)
+    fl = 2.0 * n * (n + 1) * n
+    comps["dsyr2k_4096"] = {"ms": ms, "tflops": fl / ms / 1e9, "frac_fp64_peak": fl / ms / 1e-3 / PEAK_FP64}
+    f = lambda: ctx.dsymm(LEFT, LOWER, n, n, 1.0, dA, n, dB, n, 0.0, dC, n)
+    ms = per_launch_ms(ctx, f, reps, warm=True)
+    fl = 2.0 * n * n * n + 2.0 * n * n
+    comps["dsymm_4096"] = {"ms": ms, "tflops": fl / ms / 1e9, "frac_fp64_peak": fl / ms / 1e-3 / PEAK_FP64}
+    f = lambda: ctx.dtrmm(LEFT, LOWER, NO_TRANS, NON_UNIT, n, n, 1.0, dA, n, dB, n)
+    ms = per_launch_ms(ctx, f, reps, warm=True)
+    fl_ref, fl = 2.0 * n * n * n + 1.0 * n * n, 1.0 * n * n * n
+    comps["dtrmm_4096"] = {"ms": ms, "tflops": fl_ref / ms / 1e9, "tflops_triangle": fl / ms / 1e9,
+                           "frac_fp64_peak": fl / ms / 1e-3 / PEAK_FP64}
+    dA.free()
+    dB.free()
+    dC.free()
+    return comps
+
+
 def run_only(ctx, name, reps):
     """One workload alone, `reps` launches, for counter runs (rocprofv3
     --pmc): copy (1 GiB device-to-device, the traffic calibration),
@@ -462,6 +497,23 @@ def run_only(ctx, name, reps):
                 ctx.strsm(LEFT, LOWER, NO_TRANS, NON_UNIT, n, n, 1.0, dA, n, dB, n)
         ctx.synchronize()
         return {"algorithmic_bytes": 4 * 3 * n * n}
+    if name in ("dsyr2k_4096", "dsymm_4096", "dtrmm_4096"):
+        from wgblas_amd import LEFT, NON_UNIT
+
+        n = 4096
+        dA, dB, dC = (ctx.empty(n * n, np.float64) for _ in range(3))
+        ctx.fill_uniform(dA, -1.0, 1.0, 7)
+        ctx.fill_uniform(dC, -1.0, 1.0, 9)
+        for _ in range(reps):
+            ctx.fill_uniform(dB, -1.0, 1.0, 8)
+            if name == "dsyr2k_4096":
+                ctx.dsyr2k(LOWER, NO_TRANS, n, n, 1.0, dA, n, dB, n, 0.0, dC, n)
+            elif name == "dsymm_4096":
+                ctx.dsymm(LEFT, LOWER, n, n, 1.0, dA, n, dB, n, 0.0, dC, n)
+            else:
+                ctx.dtrmm(LEFT, LOWER, NO_TRANS, NON_UNIT, n, n, 1.0, dA, n, dB, n)
+        ctx.synchronize()
+        return {"algorithmic_bytes": 8 * 3 * n * n}
     n = 1 << 28
     dx, dy = ctx.empty(n, np.float32), ctx.empty(n, np.float32)
     ctx.fill_normal(dx, 1)
@@ -610,7 +662,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default=None,
                     help="run one workload alone (copy, sgemm_8192_{NN,NT,TN,TT}, dgemm_4096, ssyrk_8192, "
-                         "ssyr2k_8192, ssymm_8192, strmm_8192, strsm_8192, sdot, sasum, snrm2, "
+                         "ssyr2k_8192, ssymm_8192, strmm_8192, strsm_8192, dsyr2k_4096, dsymm_4096, dtrmm_4096, "
+                         "sdot, sasum, snrm2, "
                          "isamax) for counter and kernel-trace collection")
     ap.add_argument("--reps", type=int, default=3)
     ap.add_argument("--no-vendor", action="store_true",

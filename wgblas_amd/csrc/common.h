@@ -70,11 +70,10 @@ enum { kBandNone = 0, kBandALower = 1, kBandAUpper = 2, kBandBLower = 3, kBandBU
 int gemm_f32(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64_t n, int64_t k,
              float alpha, const float *A, int64_t lda, const float *B, int64_t ldb, float beta,
              float *C, int64_t ldc, int band);
-// The same in fp64 (the band is not used: fp64 has no banded kernels, the
-// product runs over every k-tile).
+// The same in fp64.
 int gemm_f64(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64_t n, int64_t k,
              double alpha, const double *A, int64_t lda, const double *B, int64_t ldb,
-             double beta, double *C, int64_t ldc);
+             double beta, double *C, int64_t ldc, int band);
 // wgb_sgemm_noalloc's fixed per-GPU split-k workspace (noalloc.hip): its
 // size, and its device address on ctx's device (current on entry), looked
 // up on the first call for that device.

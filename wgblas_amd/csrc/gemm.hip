@@ -1328,9 +1328,7 @@ KernelFn<T> pick_layout(bool akc, bool bkc, bool vec) {
 // Banded (paired-tile) kernels exist for fp32 only: strmm is their caller.
 template <typename T, int BT>
 KernelFn<T> pick_kernel(bool akc, bool bkc, bool vec, bool pair) {
-  if constexpr (sizeof(T) == 4) {
-    if (pair) return pick_layout<T, BT, true>(akc, bkc, vec);
-  }
+  if (pair) return pick_layout<T, BT, true>(akc, bkc, vec);
   return pick_layout<T, BT, false>(akc, bkc, vec);
 }
 
@@ -1390,7 +1388,7 @@ struct WsSource {
 template <typename T, int BT>
 int launch_tier(wgb_ctx *ctx, GemmArgs<T> &a, bool akc, bool bkc, bool vec, WsSource wsrc) {
   constexpr int BK = 128 / (int)sizeof(T);
-  const bool pair = sizeof(T) == 4 && a.band != wgb::kBandNone;
+  const bool pair = a.band != wgb::kBandNone;
   KernelFn<T> fn = pick_kernel<T, BT>(akc, bkc, vec, pair);
   const int64_t cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
   const int64_t slots =
@@ -1583,9 +1581,9 @@ int gemm_f32(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64_t 
 
 int gemm_f64(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64_t n, int64_t k,
              double alpha, const double *A, int64_t lda, const double *B, int64_t ldb,
-             double beta, double *C, int64_t ldc) {
+             double beta, double *C, int64_t ldc, int band) {
   return gemm_launch<double>(ctx, uplo, transA, transB, m, n, k, alpha, A, lda, B, ldb, beta, C,
-                             ldc, wgb::kBandNone);
+                             ldc, band);
 }
 
 int check_gemm(int uplo, bool want_uplo, int transA, int transB, int64_t m, int64_t n, int64_t k,

@@ -552,7 +552,8 @@ int gemm_t(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64_t n,
     return wgb::gemm_f32(ctx, uplo, transA, transB, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc,
                          band);
   else
-    return wgb::gemm_f64(ctx, uplo, transA, transB, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc);
+    return wgb::gemm_f64(ctx, uplo, transA, transB, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc,
+                         band);
 }
 
 // ssyr2k / dsyr2k. fp64 keeps reference BLAS's quick return
@@ -635,9 +636,8 @@ int symm(wgb_ctx *ctx, int side, int uplo, int transB, int64_t m, int64_t n, T a
 }
 
 // strmm / dtrmm: the triangle copied with zeros elsewhere, B copied, one
-// GEMM. The fp32 GEMM runs only the k-tiles the triangle reaches (banded
-// tiles); fp64 multiplies the whole copy, as wgblas's dtrmm does
-// (src/dtrmm/dtrmm.mjs:21-27).
+// GEMM whose tiles run only the k-tiles the triangle reaches (banded tiles;
+// wgblas's dtrmm multiplies the whole copy, src/dtrmm/dtrmm.mjs:21-27).
 template <typename T>
 int trmm(wgb_ctx *ctx, int side, int uplo, int transA, int diag, int64_t m, int64_t n, T alpha,
          const T *A, int64_t lda, T *B, int64_t ldb) {

@@ -244,8 +244,9 @@ int wgb_strmm(wgb_ctx *ctx, int side, int uplo, int transA, int diag,
               float *B, int64_t ldb);
 
 /* Native-FP64 dtrmm: wgb_strmm's operation in fp64 (alpha == 0 sets B to
- * zero). The GEMM multiplies the whole zero-filled triangle copy, as
- * wgblas's dtrmm does. Replaces dtrmm (src/dtrmm/dtrmm.mjs:28-400:
+ * zero); like wgb_strmm, the GEMM runs only the k-tiles the triangle
+ * reaches (wgblas's dtrmm multiplies the whole zero-filled copy). Replaces
+ * dtrmm (src/dtrmm/dtrmm.mjs:28-400:
  * triangularize.wgsl on both halves, then dgemm_small). */
 int wgb_dtrmm(wgb_ctx *ctx, int side, int uplo, int transA, int diag,
               int64_t m, int64_t n, double alpha, const double *A, int64_t lda,

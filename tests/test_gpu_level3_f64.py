@@ -185,7 +185,7 @@ def test_dsyr2k_ieee_special_values(ctx, uplo, n):
 @pytest.mark.parametrize("uplo", ["lower", "upper"])
 @pytest.mark.parametrize("n", [7, 150])
 def test_dsyr2k_f64_exponent_range(ctx, uplo, n):
-    # the inputs of test.dsyr2k.js:474-557, in f64's range: 1e300 and 1e-50
+    # the inputs of test.dsyr2k.js:474-554, in f64's range: 1e300 and 1e-50
     # are read as they are and a result past 3.4e38 stays finite
     c = dict(layout="row-major", uplo=uplo, trans="no-transpose", n=n, k=n, alpha=1.5, beta=0.5,
              A=orc.random_f64(n * n, -1, 1, 1), lda=n, B=orc.random_f64(n * n, -1, 1, 2), ldb=n,
@@ -467,7 +467,7 @@ def test_dtrmm_unstored_triangle_and_unit_diagonal_not_read(ctx, uplo, transA):
 @pytest.mark.parametrize("side", ["left", "right"])
 @pytest.mark.parametrize("n", [7, 150])
 def test_dtrmm_f64_exponent_range(ctx, side, n):
-    # the inputs of test.dtrmm.js:378-425 in f64's range
+    # the inputs of test.dtrmm.js:378-423 in f64's range
     c = tri_case("row-major", side, "lower", "no-transpose", "non-unit", n, n, 0, seeds=(1, 2))
     c["A"][at(n, 4, 2)], c["A"][at(n, 5, 5)] = 1e300, 1e-50
     got = check_trmm(ctx, rc.tri_call(c, F64))

@@ -241,6 +241,37 @@ void run_level3(Twin &w) {
   }
 }
 
+// dsyr2k (k = n), dsymm and dtrmm at order 4096: bench.py's fp64 level-3
+// components (left, lower, no transpose, alpha 1, beta 0)
+void run_level3_f64(Twin &w) {
+  const int n = 4096;
+  double *A = w.f64((int64_t)n * n, 7), *B = w.f64((int64_t)n * n, 8), *C = w.f64((int64_t)n * n, 9);
+  const double one = 1.0, zero = 0.0;
+  double ms = w.median_ms(
+      [&] {
+        RB_OK(rocblas_dsyr2k(w.h, rocblas_fill_lower, op('N'), n, n, &one, A, n, B, n, &zero, C, n));
+      },
+      2, 10);
+  emit("dsyr2k_4096", "lower N n = k = 4096 beta 0", ms, 2.0 * n * (n + 1) * (double)n, "TFLOP/s");
+  ms = w.median_ms(
+      [&] {
+        RB_OK(rocblas_dsymm(w.h, rocblas_side_left, rocblas_fill_lower, n, n, &one, A, n, B, n, &zero, C,
+                            n));
+      },
+      2, 10);
+  emit("dsymm_4096", "left lower 4096^2 beta 0", ms, 2.0 * n * n * (double)n + 2.0 * n * n, "TFLOP/s");
+  // out of place, as strmm above: B and C distinct
+  ms = w.median_ms(
+      [&] {
+        RB_OK(rocblas_dtrmm(w.h, rocblas_side_left, rocblas_fill_lower, op('N'), rocblas_diagonal_non_unit,
+                            n, n, &one, A, n, B, n, C, n));
+      },
+      2, 10);
+  emit("dtrmm_4096", "left lower N non-unit 4096^2 (TFLOP/s of the triangle, n^3)", ms,
+       (double)n * n * n, "TFLOP/s");
+  w.release();
+}
+
 void run_gemv(Twin &w) {
   const int n = 16384;
   float *A = w.f32((int64_t)n * n, 12), *x = w.f32(n, 13), *y = w.f32(n, 14);
@@ -307,6 +338,7 @@ int main(int argc, char **argv) {
     void (*fn)(Twin &);
   } items[] = {{"sgemm_8192", run_gemm8192}, {"sgemm_512", run_gemm512},  {"sgemm_ragged", run_ragged},
                {"dgemm_4096", run_dgemm},    {"syrk", run_syrk_family},    {"level3", run_level3},
+               {"level3_f64", run_level3_f64},
                {"sgemv", run_gemv},          {"level1", run_level1}};
   for (const Item &it : items) {
     bool want = argc < 2;

@@ -17,8 +17,8 @@ Also reported under "components", each timed the same way: sgemm 512^3
 n = 8192, k = 4096, 10 chained resident calls (config 5), and sdot / sasum /
 snrm2 / isamax at n = 2^28 plus the incx = 3, n = 2^26 variants (config 2),
 sgemmtr on config 5's operands, ssyr2k / ssymm / strmm / strsm at order 8192
-(strsm also 4096), dsyr2k / dsymm / dtrmm at order 4096, sgemv 16384 x 16384
-in both forms, and ddot / dasum /
+(strsm also 4096), dsyr2k / dsymm / dtrmm at order 4096, sgemv and dgemv
+16384 x 16384 in both forms, and ddot / dasum /
 dnrm2 / idamax at n = 2^27
 (the same bytes as config 2's fp32 vectors; uniform[-1, 1) inputs, seeds 1
 and 2, as wgblas's randomFloat64Array).
@@ -286,6 +286,20 @@ def bench_components(ctx, ev, quick):
         ms = per_launch_ms(ctx, f, 5 * reps, warm=True)
         gbs = 4.0 * (n * n + 3 * n) / ms / 1e6
         comps[f"sgemv_{tname}_16384"] = {"ms": ms, "GB/s": gbs, "frac_hbm_peak": gbs * 1e9 / PEAK_HBM}
+    dA.free()
+    dx.free()
+    dy.free()
+    # dgemv on the same shape (2 GiB of A)
+    dA = ctx.empty(n * n, np.float64)
+    ctx.fill_uniform(dA, -1.0, 1.0, 12)
+    dx, dy = ctx.empty(n, np.float64), ctx.empty(n, np.float64)
+    ctx.fill_uniform(dx, -1.0, 1.0, 13)
+    ctx.fill_uniform(dy, -1.0, 1.0, 14)
+    for t, tname in ((NO_TRANS, "N"), (TRANS, "T")):
+        f = lambda: ctx.dgemv(t, n, n, 1.0, dA, n, dx, 1, 0.5, dy, 1)
+        ms = per_launch_ms(ctx, f, 5 * reps, warm=True)
+        gbs = 8.0 * (n * n + 3 * n) / ms / 1e6
+        comps[f"dgemv_{tname}_16384"] = {"ms": ms, "GB/s": gbs, "frac_hbm_peak": gbs * 1e9 / PEAK_HBM}
     dA.free()
     dx.free()
     dy.free()

@@ -276,6 +276,14 @@ int wgb_sgemv(wgb_ctx *ctx, int trans, int64_t m, int64_t n, float alpha,
               const float *A, int64_t lda, const float *x, int64_t incx,
               float beta, float *y, int64_t incy);
 
+/* Native-FP64 dgemv: wgb_sgemv's operation and rules in fp64 (alpha == 0
+ * with beta == 1 returns without a kernel, src/dgemv/dgemv.mjs:126).
+ * Replaces dgemv (src/dgemv/dgemv.mjs:23-341, src/shaders/dgemv_n.wgsl,
+ * dgemv_t.wgsl, reduce_partials_f64.wgsl in double-double). */
+int wgb_dgemv(wgb_ctx *ctx, int trans, int64_t m, int64_t n, double alpha,
+              const double *A, int64_t lda, const double *x, int64_t incx,
+              double beta, double *y, int64_t incy);
+
 /* ---- level 1 reductions --------------------------------------------------- */
 /* n <= 0 returns 0 (index -1) without touching the device. incx, incy must be
  * positive. The host-result forms block until the value is on the host; the
@@ -315,7 +323,7 @@ int wgb_isamax_dev(wgb_ctx *ctx, int64_t n, const float *x, int64_t incx,
 
 /* The fp64 reductions, accumulated in native float64 with the same rules as
  * their fp32 counterparts (wgblas computes them in double-double:
- * src/shaders/{ddot,dasum,dnrm2,idamax}.wgsl, src/shaders/reduction/*F64.wgsl).
+ * src/shaders/{ddot,dasum,dnrm2,idamax}.wgsl, src/shaders/reduction/(name)F64.wgsl).
  * ddot replaces src/ddot/ddot.mjs:19-174; dasum src/dasum/dasum.mjs:18-138;
  * dnrm2 src/dnrm2/dnrm2.mjs:22-149 (Blue's algorithm with LAPACK 3.10's
  * dnrm2 thresholds for IEEE double; NaN gives NaN, Inf gives Inf); idamax

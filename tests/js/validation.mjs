@@ -398,6 +398,27 @@ async function main() {
     layout: loadParam("layout"),
   }, (a) => wg.sgemv(a.device, a.trans, a.m, a.n, a.alpha, a.A, a.lda, a.x, a.incx, a.beta, a.y, a.incy,
     a.layout), device);
+  // dgemv: wgblas's tests/dgemv/src/test.dgemv.js composition (alpha64 /
+  // beta64 / A64 / x64 / y64)
+  register("dgemv", {
+    device: loadParam("device"),
+    trans: loadParam("trans"),
+    m: loadParam("m"),
+    n: Object.assign({}, nS, {
+      edge: nS.edge.filter((e) => e.value !== -1),
+      invalid: nS.invalid.concat([{ value: -1, error: "n must be non-negative", label: "negative" }]),
+    }),
+    alpha: loadParam("alpha64"),
+    beta: loadParam("beta64"),
+    lda: loadParam("lda"),
+    A: loadParam("A64"),
+    x: loadParam("x64"),
+    incx: loadParam("incx"),
+    y: loadParam("y64"),
+    incy: loadParam("incy"),
+    layout: loadParam("layout"),
+  }, (a) => wg.dgemv(a.device, a.trans, a.m, a.n, a.alpha, a.A, a.lda, a.x, a.incx, a.beta, a.y, a.incy,
+    a.layout), device);
   register("sdot", {
     device: loadParam("device"), n: loadParam("n"), incx: loadParam("incx"), incy: loadParam("incy"),
     x: loadParam("x"), y: loadParam("y"),

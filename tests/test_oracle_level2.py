@@ -10,9 +10,11 @@ from oracle import orc
 from tests import refcases as rc
 
 
+@pytest.mark.parametrize("routine", ["sgemv", "dgemv"])
 @pytest.mark.parametrize("cm", [False, True])
-def test_edge_cases_against_numpy(cm):
-    for c in rc.load("sgemv", cm):
+def test_edge_cases_against_numpy(routine, cm):
+    # dgemv (tests/dgemv/edge-cases*.json) runs the same restatement on doubles
+    for c in rc.load(routine, cm):
         call = rc.gemv_call(c, np.float64)
         out, _ = orc.sgemv_ld(*call)
         assert np.array_equal(out, rc.numpy_gemv(*call)), c["label"]

@@ -1,17 +1,19 @@
 // sgemv (wgblas src/sgemv/sgemv.mjs:19-254, shaders sgemv_n.wgsl,
-// sgemv_t.wgsl, reduce_partials.wgsl), column-major as in BLAS:
+// sgemv_t.wgsl, reduce_partials.wgsl) and its native-fp64 form dgemv
+// (src/dgemv/dgemv.mjs:23-341), column-major as in BLAS:
 //   trans = N: y (m) <- alpha A x + beta y, x of length n;
 //   trans = T: y (n) <- alpha A^T x + beta y, x of length m.
 //
-// Both forms read A once and are HBM-bound.
+// Both forms read A once and are HBM-bound. A lane's loads are 4 consecutive
+// elements (16 bytes in fp32, 32 in fp64).
 //   N: a lane owns 4 consecutive rows in each of kGroupsN 1024-row groups
-//      (a 16-byte load per group and column, kStepN columns per step), and a
+//      (one 4-element load per group and column, kStepN columns per step), and a
 //      block walks a long run of columns (few, deep blocks); the
 //      columns are walked in order and a column whose x entry is zero is
 //      skipped, as reference BLAS does for this form (so 0 * Inf or 0 * NaN
 //      in that column never reaches y).
 //   T: a wave owns 8 columns (4 for short columns) and walks the rows 512
-//      at a time (2 x 4 per lane, 16-byte loads), keeping each x chunk in
+//      at a time (2 x 4 per lane, 4-element loads), keeping each x chunk in
 //      registers for all of its columns;
 //      the dot products are folded with wave shuffles. No zero skipping: the
 //      dot-product form of reference BLAS takes every term.
@@ -53,33 +55,43 @@ constexpr int kTargetBlocks = 2048;  // T form: blocks that keep HBM streaming
 int64_t imax(int64_t a, int64_t b) { return a > b ? a : b; }
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
-typedef float f4 __attribute__((ext_vector_type(4)));
+template <typename T>
+using vec4 = T __attribute__((ext_vector_type(4)));
 
-// A is streamed once: non-temporal 16-byte loads keep it from displacing x
+// A is streamed once: non-temporal 4-element loads keep it from displacing x
 // and the partial sums in the caches.
-__device__ __forceinline__ f4 ld_nt(const float *p) {
-  return __builtin_nontemporal_load(reinterpret_cast<const f4 *>(p));
+template <typename T>
+__device__ __forceinline__ vec4<T> ld_nt(const T *p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const vec4<T> *>(p));
+}
+
+// p aligned to 4 elements (the vector loads' alignment)
+template <typename T>
+bool aligned4(const T *p) {
+  return ((uintptr_t)p % (4 * sizeof(T))) == 0;
 }
 
 // Writes one output element: alpha * acc + beta * y (beta == 0 never reads y).
-__device__ __forceinline__ void store_y(float *y, int64_t idx, float acc, float alpha,
-                                        float beta) {
-  float v = alpha * acc;
-  if (beta != 0.f) v = fmaf(beta, y[idx], v);
+template <typename T>
+__device__ __forceinline__ void store_y(T *y, int64_t idx, T acc, T alpha, T beta) {
+  T v = alpha * acc;
+  if (beta != (T)0) v = fma(beta, y[idx], v);
   y[idx] = v;
 }
 
 // N form. Block b, split s: columns [s*cps, min(n, (s+1)*cps)); rows in
 // kGroupsN groups of 1024, lane t of group g owning rows
 // [b*1024*kGroupsN + g*1024 + 4t, +4) (every load instruction of a wave
-// reads 1 KB of one column). VEC: lda % 4 == 0 and A 16-byte aligned.
-template <bool VEC>
+// reads 256 elements of one column). VEC: lda % 4 == 0 and A aligned to 4
+// elements.
+template <typename T, bool VEC>
 __global__ __launch_bounds__(kThreads) void gemv_n_kernel(int64_t m, int64_t n,
-                                                          const float *__restrict__ A, int64_t lda,
-                                                          const float *__restrict__ x, int64_t incx,
-                                                          int64_t cps, float *__restrict__ part,
-                                                          float alpha, float beta,
-                                                          float *__restrict__ y, int64_t incy) {
+                                                          const T *__restrict__ A, int64_t lda,
+                                                          const T *__restrict__ x, int64_t incx,
+                                                          int64_t cps, T *__restrict__ part,
+                                                          T alpha, T beta,
+                                                          T *__restrict__ y, int64_t incy) {
+  typedef vec4<T> f4;
   constexpr int G = kGroupsN;
   const int64_t rb = (int64_t)blockIdx.x * (4 * kThreads * G) + 4 * threadIdx.x;
   const int64_t j0 = (int64_t)blockIdx.y * cps;
@@ -95,19 +107,19 @@ __global__ __launch_bounds__(kThreads) void gemv_n_kernel(int64_t m, int64_t n,
 #pragma unroll
     for (int q = 0; q < 4; ++q) ir[g][q] = i0 + q < m ? i0 + q : m - 1;
   }
-  float acc[G][4];
+  T acc[G][4];
 #pragma unroll
   for (int g = 0; g < G; ++g)
 #pragma unroll
-    for (int q = 0; q < 4; ++q) acc[g][q] = 0.f;
-  auto load = [&](const float *col, int g) -> f4 {
+    for (int q = 0; q < 4; ++q) acc[g][q] = (T)0;
+  auto load = [&](const T *col, int g) -> f4 {
     if (VEC && full[g]) return ld_nt(col + ir[g][0]);
     return f4{col[ir[g][0]], col[ir[g][1]], col[ir[g][2]], col[ir[g][3]]};
   };
   int64_t j = j0;
   // kStepN columns per step, every load issued before the arithmetic
   for (; j + kStepN <= j1; j += kStepN) {
-    float xv[kStepN];
+    T xv[kStepN];
     f4 av[kStepN][G];
 #pragma unroll
     for (int c = 0; c < kStepN; ++c) xv[c] = x[(j + c) * incx];
@@ -117,24 +129,24 @@ __global__ __launch_bounds__(kThreads) void gemv_n_kernel(int64_t m, int64_t n,
       for (int g = 0; g < G; ++g) av[c][g] = load(A + (j + c) * lda, g);
 #pragma unroll
     for (int c = 0; c < kStepN; ++c) {
-      if (xv[c] != 0.f) {
+      if (xv[c] != (T)0) {
 #pragma unroll
         for (int g = 0; g < G; ++g)
 #pragma unroll
-          for (int q = 0; q < 4; ++q) acc[g][q] = fmaf(av[c][g][q], xv[c], acc[g][q]);
+          for (int q = 0; q < 4; ++q) acc[g][q] = fma(av[c][g][q], xv[c], acc[g][q]);
       }
     }
   }
   for (; j < j1; ++j) {
-    const float xj = x[j * incx];
+    const T xj = x[j * incx];
     f4 a[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) a[g] = load(A + j * lda, g);
-    if (xj != 0.f) {
+    if (xj != (T)0) {
 #pragma unroll
       for (int g = 0; g < G; ++g)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) acc[g][q] = fmaf(a[g][q], xj, acc[g][q]);
+        for (int q = 0; q < 4; ++q) acc[g][q] = fma(a[g][q], xj, acc[g][q]);
     }
   }
 #pragma unroll
@@ -153,26 +165,27 @@ __global__ __launch_bounds__(kThreads) void gemv_n_kernel(int64_t m, int64_t n,
 // T form. Wave w (4 per block) owns columns [CPW w, CPW w + CPW) of split s, rows
 // [s*rps, min(m, (s+1)*rps)). VEC: lda % 4 == 0, A 16-byte aligned, incx == 1
 // and x 16-byte aligned (rps is a multiple of 4, so every 4-row group of a
-// split starts 16-byte aligned).
-template <bool VEC, int CPW>
+// split starts aligned).
+template <typename T, bool VEC, int CPW>
 __global__ __launch_bounds__(kThreads) void gemv_t_kernel(int64_t m, int64_t n,
-                                                          const float *__restrict__ A, int64_t lda,
-                                                          const float *__restrict__ x, int64_t incx,
-                                                          int64_t rps, float *__restrict__ part,
-                                                          float alpha, float beta,
-                                                          float *__restrict__ y, int64_t incy) {
+                                                          const T *__restrict__ A, int64_t lda,
+                                                          const T *__restrict__ x, int64_t incx,
+                                                          int64_t rps, T *__restrict__ part,
+                                                          T alpha, T beta,
+                                                          T *__restrict__ y, int64_t incy) {
+  typedef vec4<T> f4;
   const int lane = threadIdx.x & 63;
   const int64_t col0 = ((int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6)) * CPW;
   if (col0 >= n) return;  // wave-uniform
   const int64_t r0 = (int64_t)blockIdx.y * rps;
   const int64_t r1 = r0 + rps < m ? r0 + rps : m;
   // columns past n repeat column n-1 (in bounds) and are never stored
-  const float *col[CPW];
+  const T *col[CPW];
 #pragma unroll
   for (int c = 0; c < CPW; ++c) col[c] = A + (col0 + c < n ? col0 + c : n - 1) * lda;
-  float acc[CPW];
+  T acc[CPW];
 #pragma unroll
-  for (int c = 0; c < CPW; ++c) acc[c] = 0.f;
+  for (int c = 0; c < CPW; ++c) acc[c] = (T)0;
   int64_t i = r0 + 4 * lane;
   if (VEC) {
     // two 256-row groups per step: 16 loads of A in flight per lane
@@ -185,14 +198,18 @@ __global__ __launch_bounds__(kThreads) void gemv_t_kernel(int64_t m, int64_t n,
         av0[c] = ld_nt(col[c] + i);
         av1[c] = ld_nt(col[c] + i + 256);
       }
+      // fp64: every load of the step is issued before the arithmetic. Left
+      // to itself the scheduler placed each 16-byte load just before its
+      // FMAs and waited for it (one load in flight: 16384^2 at 3.5 TB/s).
+      if constexpr (sizeof(T) == 8) __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int c = 0; c < CPW; ++c)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) acc[c] = fmaf(av0[c][q], xv0[q], acc[c]);
+        for (int q = 0; q < 4; ++q) acc[c] = fma(av0[c][q], xv0[q], acc[c]);
 #pragma unroll
       for (int c = 0; c < CPW; ++c)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) acc[c] = fmaf(av1[c][q], xv1[q], acc[c]);
+        for (int q = 0; q < 4; ++q) acc[c] = fma(av1[c][q], xv1[q], acc[c]);
     }
   }
   for (; i < r1; i += 256) {
@@ -204,13 +221,13 @@ __global__ __launch_bounds__(kThreads) void gemv_t_kernel(int64_t m, int64_t n,
 #pragma unroll
       for (int c = 0; c < CPW; ++c)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) acc[c] = fmaf(av[c][q], xv[q], acc[c]);
+        for (int q = 0; q < 4; ++q) acc[c] = fma(av[c][q], xv[q], acc[c]);
     } else {
       const int cnt = r1 - i < 4 ? (int)(r1 - i) : 4;
       for (int q = 0; q < cnt; ++q) {
-        const float xv = x[(i + q) * incx];
+        const T xv = x[(i + q) * incx];
 #pragma unroll
-        for (int c = 0; c < CPW; ++c) acc[c] = fmaf(col[c][i + q], xv, acc[c]);
+        for (int c = 0; c < CPW; ++c) acc[c] = fma(col[c][i + q], xv, acc[c]);
       }
     }
   }
@@ -220,7 +237,7 @@ __global__ __launch_bounds__(kThreads) void gemv_t_kernel(int64_t m, int64_t n,
     for (int off = 32; off > 0; off >>= 1) acc[c] += __shfl_xor(acc[c], off, 64);
   }
   if (lane < CPW && col0 + lane < n) {
-    float v = acc[0];
+    T v = acc[0];
 #pragma unroll
     for (int c = 1; c < CPW; ++c) v = lane == c ? acc[c] : v;
     if (part)
@@ -236,19 +253,20 @@ __global__ __launch_bounds__(kThreads) void gemv_t_kernel(int64_t m, int64_t n,
 // none is guarded). The last pass (one group) writes alpha * sum + beta * y;
 // earlier ones write the group sums to out[g*len + i] for the next pass.
 constexpr int kFold = 32;
+template <typename T>
 __global__ __launch_bounds__(kThreads) void gemv_fold_kernel(int64_t len, int64_t splits,
-                                                             const float *__restrict__ part,
-                                                             float *__restrict__ out, float alpha,
-                                                             float beta, float *__restrict__ y,
+                                                             const T *__restrict__ part,
+                                                             T *__restrict__ out, T alpha,
+                                                             T beta, T *__restrict__ y,
                                                              int64_t incy) {
   const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
   if (i >= len) return;
   const int64_t s0 = (int64_t)blockIdx.y * kFold;
   const int64_t last = (s0 + kFold < splits ? s0 + kFold : splits) - 1;
-  float v[kFold];
+  T v[kFold];
 #pragma unroll
   for (int q = 0; q < kFold; ++q) v[q] = part[(s0 + q < last ? s0 + q : last) * len + i];
-  float sum = v[0];
+  T sum = v[0];
 #pragma unroll
   for (int q = 1; q < kFold; ++q)
     if (s0 + q <= last) sum += v[q];
@@ -259,19 +277,21 @@ __global__ __launch_bounds__(kThreads) void gemv_fold_kernel(int64_t len, int64_
 }
 
 // y <- beta * y over len elements (0 when beta == 0): alpha == 0.
-__global__ __launch_bounds__(kThreads) void scale_y_kernel(int64_t len, float beta, float *y,
+template <typename T>
+__global__ __launch_bounds__(kThreads) void scale_y_kernel(int64_t len, T beta, T *y,
                                                            int64_t incy) {
   const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  if (i < len) y[i * incy] = beta == 0.f ? 0.f : beta * y[i * incy];
+  if (i < len) y[i * incy] = beta == (T)0 ? (T)0 : beta * y[i * incy];
 }
 
-using wgb::aligned16;
-
-}  // namespace
-
-extern "C" int wgb_sgemv(wgb_ctx *ctx, int trans, int64_t m, int64_t n, float alpha,
-                         const float *A, int64_t lda, const float *x, int64_t incx, float beta,
-                         float *y, int64_t incy) {
+// sgemv / dgemv on the kernels above. dgemv keeps reference BLAS's quick
+// return for alpha == 0 with beta == 1 (src/dgemv/dgemv.mjs:126: no
+// kernel, y untouched bit for bit); sgemv times an empty span there, as
+// wgblas runs a kernel (src/sgemv/sgemv.mjs:85 returns early only for m or
+// n == 0).
+template <typename T>
+int gemv(wgb_ctx *ctx, int trans, int64_t m, int64_t n, T alpha, const T *A, int64_t lda,
+         const T *x, int64_t incx, T beta, T *y, int64_t incy) {
   int st = wgb::enter(ctx);
   if (st) return st;
   if (trans != WGB_NO_TRANS && trans != WGB_TRANS)
@@ -281,28 +301,28 @@ extern "C" int wgb_sgemv(wgb_ctx *ctx, int trans, int64_t m, int64_t n, float al
   if (incx <= 0 || incy <= 0) return fail(WGB_ERR_INVALID_VALUE, "incx and incy must be positive");
   // reference BLAS quick return: nothing to do, y untouched
   if (m == 0 || n == 0) return WGB_OK;
-  if (alpha == 0.f && beta == 1.f) {
-    // y untouched as well, but wgblas runs (and times) a kernel here
-    // (src/sgemv/sgemv.mjs:85 returns early only for m or n == 0): record
-    // this call's empty span so per-call timing reports it, not an older call
+  if (alpha == (T)0 && beta == (T)1) {
+    if (sizeof(T) == 8) return WGB_OK;
+    // y untouched; this call's empty span, so per-call timing reports it
+    // rather than an older call
     wgb::timing_begin(ctx);
     wgb::timing_end(ctx);
     return WGB_OK;
   }
-  if (!y || (alpha != 0.f && (!A || !x))) return fail(WGB_ERR_INVALID_VALUE, "A, x or y is null");
+  if (!y || (alpha != (T)0 && (!A || !x))) return fail(WGB_ERR_INVALID_VALUE, "A, x or y is null");
   const bool nt = trans == WGB_NO_TRANS;
   const int64_t len = nt ? m : n;  // length of y
   wgb::timing_begin(ctx);
-  if (alpha == 0.f) {
-    scale_y_kernel<<<(unsigned)cdiv(len, kThreads), kThreads, 0, ctx->stream>>>(len, beta, y, incy);
+  if (alpha == (T)0) {
+    scale_y_kernel<T><<<(unsigned)cdiv(len, kThreads), kThreads, 0, ctx->stream>>>(len, beta, y, incy);
     WGB_CHECK_LAUNCH("scale_y_kernel");
     wgb::timing_end(ctx);
     return WGB_OK;
   }
-  const bool vecA = lda % 4 == 0 && aligned16(A);
+  const bool vecA = lda % 4 == 0 && aligned4(A);
   // blocks along the output; split the contraction dimension until about
   // the target block count streams A (N: >= kMinColsN columns per split; T: >= 256
-  // rows, a multiple of 256 so every split starts 16-byte aligned)
+  // rows, a multiple of 256 so every split starts aligned)
   const int cpw = m <= kShortColsRows ? kColsPerWaveShort : kColsPerWave;  // T form
   const int64_t bx = nt ? cdiv(m, 4 * kThreads * kGroupsN) : cdiv(cdiv(n, cpw), kThreads / 64);
   const int64_t target = nt ? kTargetBlocksN : kTargetBlocks;
@@ -313,53 +333,67 @@ extern "C" int wgb_sgemv(wgb_ctx *ctx, int trans, int64_t m, int64_t n, float al
   if (want < 1) want = 1;
   const int64_t per = nt ? cdiv(n, want) : cdiv(cdiv(m, want), 256) * 256;
   const int64_t splits = nt ? cdiv(n, per) : cdiv(m, per);
-  float *part = nullptr;
+  T *part = nullptr;
   if (splits > 1) {
     // partials, then the fold passes' group sums after them
     const int64_t groups = cdiv(splits, kFold);
-    if ((st = wgb::ensure_op_workspace(ctx, (size_t)((splits + groups) * len) * sizeof(float))))
+    if ((st = wgb::ensure_op_workspace(ctx, (size_t)((splits + groups) * len) * sizeof(T))))
       return st;
-    part = static_cast<float *>(ctx->op_ws);
+    part = static_cast<T *>(ctx->op_ws);
   }
   dim3 grid((unsigned)bx, (unsigned)splits);
   if (nt) {
     if (vecA)
-      gemv_n_kernel<true><<<grid, kThreads, 0, ctx->stream>>>(m, n, A, lda, x, incx, per, part,
+      gemv_n_kernel<T, true><<<grid, kThreads, 0, ctx->stream>>>(m, n, A, lda, x, incx, per, part,
                                                                alpha, beta, y, incy);
     else
-      gemv_n_kernel<false><<<grid, kThreads, 0, ctx->stream>>>(m, n, A, lda, x, incx, per, part,
+      gemv_n_kernel<T, false><<<grid, kThreads, 0, ctx->stream>>>(m, n, A, lda, x, incx, per, part,
                                                                 alpha, beta, y, incy);
     WGB_CHECK_LAUNCH("gemv_n_kernel");
   } else {
-    const bool vec = vecA && incx == 1 && aligned16(x);
+    const bool vec = vecA && incx == 1 && aligned4(x);
     auto launch = [&](auto kern) {
       kern<<<grid, kThreads, 0, ctx->stream>>>(m, n, A, lda, x, incx, per, part, alpha, beta, y, incy);
     };
     if (cpw == kColsPerWaveShort)
-      launch(vec ? gemv_t_kernel<true, kColsPerWaveShort> : gemv_t_kernel<false, kColsPerWaveShort>);
+      launch(vec ? gemv_t_kernel<T, true, kColsPerWaveShort> : gemv_t_kernel<T, false, kColsPerWaveShort>);
     else
-      launch(vec ? gemv_t_kernel<true, kColsPerWave> : gemv_t_kernel<false, kColsPerWave>);
+      launch(vec ? gemv_t_kernel<T, true, kColsPerWave> : gemv_t_kernel<T, false, kColsPerWave>);
     WGB_CHECK_LAUNCH("gemv_t_kernel");
   }
   if (part) {
     // fold passes until one group of at most kFold remains; each pass
     // alternates between the two halves of the workspace
-    float *src = part, *dst = part + splits * len;
+    T *src = part, *dst = part + splits * len;
     int64_t k = splits;
     while (k > kFold) {
       const int64_t groups = cdiv(k, kFold);
-      gemv_fold_kernel<<<dim3((unsigned)cdiv(len, kThreads), (unsigned)groups), kThreads, 0,
+      gemv_fold_kernel<T><<<dim3((unsigned)cdiv(len, kThreads), (unsigned)groups), kThreads, 0,
                          ctx->stream>>>(len, k, src, dst, alpha, beta, y, incy);
       WGB_CHECK_LAUNCH("gemv_fold_kernel");
-      float *t = src;
+      T *t = src;
       src = dst;
       dst = t;
       k = groups;
     }
-    gemv_fold_kernel<<<dim3((unsigned)cdiv(len, kThreads), 1), kThreads, 0, ctx->stream>>>(
+    gemv_fold_kernel<T><<<dim3((unsigned)cdiv(len, kThreads), 1), kThreads, 0, ctx->stream>>>(
         len, k, src, nullptr, alpha, beta, y, incy);
     WGB_CHECK_LAUNCH("gemv_fold_kernel");
   }
   wgb::timing_end(ctx);
   return WGB_OK;
+}
+
+}  // namespace
+
+extern "C" int wgb_sgemv(wgb_ctx *ctx, int trans, int64_t m, int64_t n, float alpha,
+                         const float *A, int64_t lda, const float *x, int64_t incx, float beta,
+                         float *y, int64_t incy) {
+  return gemv<float>(ctx, trans, m, n, alpha, A, lda, x, incx, beta, y, incy);
+}
+
+extern "C" int wgb_dgemv(wgb_ctx *ctx, int trans, int64_t m, int64_t n, double alpha,
+                         const double *A, int64_t lda, const double *x, int64_t incx, double beta,
+                         double *y, int64_t incy) {
+  return gemv<double>(ctx, trans, m, n, alpha, A, lda, x, incx, beta, y, incy);
 }

@@ -416,7 +416,8 @@ napi_value Tri(napi_env env, napi_callback_info info) {
 
 // ---- level 2 ---------------------------------------------------------------
 
-// sgemv(ctx, trans, m, n, alpha, A, lda, x, incx, beta, y, incy)
+// sgemv(ctx, trans, m, n, alpha, A, lda, x, incx, beta, y, incy[, f64]):
+// sgemv, or dgemv when f64 is true
 napi_value Sgemv(napi_env env, napi_callback_info info) {
   Args a;
   if (!get_args(env, info, a, 12)) return nullptr;
@@ -431,8 +432,15 @@ napi_value Sgemv(napi_env env, napi_callback_info info) {
       !get_ptr(env, a.v[7], &x) || !get_i64(env, a.v[8], &incx) || !get_f64(env, a.v[9], &beta) ||
       !get_ptr(env, a.v[10], &y) || !get_i64(env, a.v[11], &incy))
     return nullptr;
-  WGB_OK_OR_THROW(wgb_sgemv(ctx, trans, m, n, (float)alpha, (const float *)A, lda, (const float *)x,
-                            incx, (float)beta, (float *)y, incy), "wgb_sgemv");
+  bool f64 = false;
+  if (a.n > 12 && napi_get_value_bool(env, a.v[12], &f64) != napi_ok) f64 = false;
+  if (f64) {
+    WGB_OK_OR_THROW(wgb_dgemv(ctx, trans, m, n, alpha, (const double *)A, lda, (const double *)x,
+                              incx, beta, (double *)y, incy), "wgb_dgemv");
+  } else {
+    WGB_OK_OR_THROW(wgb_sgemv(ctx, trans, m, n, (float)alpha, (const float *)A, lda,
+                              (const float *)x, incx, (float)beta, (float *)y, incy), "wgb_sgemv");
+  }
   return nullptr;
 }
 

@@ -284,6 +284,16 @@ void run_gemv(Twin &w) {
     emit(name, "16384^2, 1 GiB of A", ms, 4.0 * ((double)n * n + 3.0 * n), "GB/s");
   }
   w.release();
+  double *Ad = w.f64((int64_t)n * n, 12), *xd = w.f64(n, 13), *yd = w.f64(n, 14);
+  const double oned = 1.0, halfd = 0.5;
+  for (char t : {'N', 'T'}) {
+    const double ms = w.median_ms(
+        [&] { RB_OK(rocblas_dgemv(w.h, op(t), n, n, &oned, Ad, n, xd, 1, &halfd, yd, 1)); }, 5, 20);
+    char name[32];
+    std::snprintf(name, sizeof name, "dgemv_%c_16384", t);
+    emit(name, "16384^2, 2 GiB of A", ms, 8.0 * ((double)n * n + 3.0 * n), "GB/s");
+  }
+  w.release();
 }
 
 void run_level1(Twin &w) {

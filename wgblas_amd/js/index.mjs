@@ -20,6 +20,7 @@ export { dsymm } from "./src/dsymm.mjs";
 export { dtrmm } from "./src/dtrmm.mjs";
 export { strsm } from "./src/strsm.mjs";
 export { sgemv } from "./src/sgemv.mjs";
+export { dgemv } from "./src/dgemv.mjs";
 export { sdot } from "./src/sdot.mjs";
 export { sasum } from "./src/sasum.mjs";
 export { snrm2 } from "./src/snrm2.mjs";

@@ -1,7 +1,8 @@
 // sgemv: y <- alpha*op(A)*x + beta*y (wgblas src/sgemv/sgemv.mjs:19-254), on
-// wgb_sgemv. Argument checks keep wgblas's order and messages
-// (sgemv.mjs:36-121). Returns { y } (a new Float32Array) for host arrays, {}
-// when y is a GpuVector (updated in place); plus gpuTimeMs when
+// wgb_sgemv; dgemv (src/dgemv/dgemv.mjs:23-341) on wgb_dgemv through the same
+// function. Argument checks keep wgblas's order and messages
+// (sgemv.mjs:36-121, dgemv.mjs:36-124). Returns { y } (a new array) for host
+// arrays, {} when y is a GpuVector (updated in place); plus gpuTimeMs when
 // init({benchmark:true}).
 import { GpuMatrix } from "./classes/GpuMatrix.mjs";
 import { GpuVector } from "./classes/GpuVector.mjs";
@@ -11,11 +12,21 @@ import { native } from "./native.mjs";
 
 export async function sgemv(device, trans, m, n, alpha, A, lda, x, incx, beta, y, incy,
                             layout = "row-major") {
+  return gemv("sgemv", device, trans, m, n, alpha, A, lda, x, incx, beta, y, incy, layout);
+}
+
+/** sgemv, or dgemv (routine "dgemv": Float64Array operands, reference BLAS's
+ * alpha = 0, beta = 1 quick return before any device work,
+ * dgemv.mjs:126). */
+export async function gemv(routine, device, trans, m, n, alpha, A, lda, x, incx, beta, y, incy,
+                           layout = "row-major") {
+  const F = routine === "dgemv" ? Float64Array : Float32Array;
+  const FN = F === Float64Array ? "Float64Array" : "Float32Array";
   const AIsGpu = A instanceof GpuMatrix;
   const xIsGpu = x instanceof GpuVector;
   const yIsGpu = y instanceof GpuVector;
   requireGpuDevice(device);
-  requireSameDevice(device, "sgemv", { A, x, y });
+  requireSameDevice(device, routine, { A, x, y });
   checkTrans("trans", trans);
   checkLayout(layout);
   checkScalar("alpha", alpha);
@@ -23,14 +34,15 @@ export async function sgemv(device, trans, m, n, alpha, A, lda, x, incx, beta, y
   for (const v of [m, n, incx, incy, lda])
     if (!Number.isInteger(v)) throw new Error("m, n, incx, incy, and lda must be integers.");
   if (incx <= 0 || incy <= 0) throw new Error("incx and incy must be positive.");
-  if (!AIsGpu && !(A instanceof Float32Array)) throw new Error("A must be a Float32Array or GpuMatrix.");
-  if (!xIsGpu && !(x instanceof Float32Array)) throw new Error("x must be a Float32Array or GpuVector.");
-  if (!yIsGpu && !(y instanceof Float32Array)) throw new Error("y must be a Float32Array or GpuVector.");
-  checkResidentDtype("A", A, AIsGpu, Float32Array);
-  checkResidentDtype("x", x, xIsGpu, Float32Array, "GpuVector");
-  checkResidentDtype("y", y, yIsGpu, Float32Array, "GpuVector");
+  if (!AIsGpu && !(A instanceof F)) throw new Error(`A must be a ${FN} or GpuMatrix.`);
+  if (F === Float64Array) checkResidentDtype("A", A, AIsGpu, F);
+  if (!xIsGpu && !(x instanceof F)) throw new Error(`x must be a ${FN} or GpuVector.`);
+  if (!yIsGpu && !(y instanceof F)) throw new Error(`y must be a ${FN} or GpuVector.`);
+  if (F === Float32Array) checkResidentDtype("A", A, AIsGpu, F);
+  checkResidentDtype("x", x, xIsGpu, F, "GpuVector");
+  checkResidentDtype("y", y, yIsGpu, F, "GpuVector");
   if (xIsGpu !== yIsGpu)
-    throw new Error("x and y must be the same type (both Float32Array or both GpuVector).");
+    throw new Error(`x and y must be the same type (both ${FN} or both GpuVector).`);
   if (xIsGpu && !AIsGpu) throw new Error("A must be a GpuMatrix when x and y are GpuVectors.");
   if (AIsGpu && !xIsGpu) throw new Error("x and y must be GpuVectors when A is a GpuMatrix.");
   if (xIsGpu && x._buf === y._buf)
@@ -57,7 +69,10 @@ export async function sgemv(device, trans, m, n, alpha, A, lda, x, incx, beta, y
     throw new Error("y does not have enough elements for the given dimensions and incy.");
   // The row-major mr x nr frame matrix read column-major is its nr x mr
   // transpose: op flips.
+  // dgemv: reference BLAS's quick return, no device work (dgemv.mjs:126)
+  if (F === Float64Array && alpha === 0 && beta === 1) return yIsGpu ? {} : { y };
   const t = isNoTrans ? 1 : 0;
-  return execute(device, [A, x], y, yIsGpu, Float32Array, (ctx, p, py) =>
-    native().sgemv(ctx, t, nr, mr, alpha, p[0], lda, p[1], incx, beta, py, incy), "y");
+  return execute(device, [A, x], y, yIsGpu, F, (ctx, p, py) =>
+    native().sgemv(ctx, t, nr, mr, alpha, p[0], lda, p[1], incx, beta, py, incy, F === Float64Array),
+  "y");
 }

@@ -72,6 +72,8 @@ _SIGNATURES = {
                   _ptr, _i64],
     "wgb_sgemv": [_ptr, C.c_int, _i64, _i64, C.c_float, _ptr, _i64, _ptr, _i64, C.c_float, _ptr,
                   _i64],
+    "wgb_dgemv": [_ptr, C.c_int, _i64, _i64, C.c_double, _ptr, _i64, _ptr, _i64, C.c_double, _ptr,
+                  _i64],
     "wgb_sdot": [_ptr, _i64, _ptr, _i64, _ptr, _i64, C.POINTER(C.c_float)],
     "wgb_sdot_dev": [_ptr, _i64, _ptr, _i64, _ptr, _i64, _ptr],
     "wgb_sasum": [_ptr, _i64, _ptr, _i64, C.POINTER(C.c_float)],
@@ -318,6 +320,10 @@ class Context:
     def sgemv(self, trans, m, n, alpha, A, lda, x, incx, beta, y, incy):
         _check(self.lib.wgb_sgemv(self.handle, trans, m, n, alpha, _p(A), lda, _p(x), incx, beta,
                                   _p(y), incy), "wgb_sgemv")
+
+    def dgemv(self, trans, m, n, alpha, A, lda, x, incx, beta, y, incy):
+        _check(self.lib.wgb_dgemv(self.handle, trans, m, n, alpha, _p(A), lda, _p(x), incx, beta,
+                                  _p(y), incy), "wgb_dgemv")
 
     # ---- level 1 ----
     def sdot(self, n, x, incx, y, incy):

@@ -18,7 +18,7 @@ n = 8192, k = 4096, 10 chained resident calls (config 5), and sdot / sasum /
 snrm2 / isamax at n = 2^28 plus the incx = 3, n = 2^26 variants (config 2),
 sgemmtr on config 5's operands, ssyr2k / ssymm / strmm / strsm at order 8192
 (strsm also 4096), dsyr2k / dsymm / dtrmm at order 4096, sgemv and dgemv
-16384 x 16384 in both forms, and ddot / dasum /
+16384 x 16384 in both forms, sger and dger on 16384 x 16384, and ddot / dasum /
 dnrm2 / idamax at n = 2^27
 (the same bytes as config 2's fp32 vectors; uniform[-1, 1) inputs, seeds 1
 and 2, as wgblas's randomFloat64Array).
@@ -303,6 +303,22 @@ def bench_components(ctx, ev, quick):
     dA.free()
     dx.free()
     dy.free()
+
+    # sger / dger on the same shape: A read and written once, alpha 1e-3
+    for dt, name, es in ((np.float32, "sger", 4.0), (np.float64, "dger", 8.0)):
+        dA = ctx.empty(n * n, dt)
+        ctx.fill_uniform(dA, -1.0, 1.0, 15)
+        dx, dy = ctx.empty(n, dt), ctx.empty(n, dt)
+        ctx.fill_uniform(dx, -1.0, 1.0, 16)
+        ctx.fill_uniform(dy, -1.0, 1.0, 17)
+        fn = getattr(ctx, name)
+        f = lambda: fn(n, n, 1e-3, dx, 1, dy, 1, dA, n)
+        ms = per_launch_ms(ctx, f, 5 * reps, warm=True)
+        gbs = es * (2 * n * n + 2 * n) / ms / 1e6
+        comps[f"{name}_16384"] = {"ms": ms, "GB/s": gbs, "frac_hbm_peak": gbs * 1e9 / PEAK_HBM}
+        dA.free()
+        dx.free()
+        dy.free()
 
     # config 2: reductions at n = 2^28 (normal seed 1 / 2, planted duplicate max)
     n = 1 << 28

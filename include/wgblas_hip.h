@@ -276,6 +276,22 @@ int wgb_sgemv(wgb_ctx *ctx, int trans, int64_t m, int64_t n, float alpha,
               const float *A, int64_t lda, const float *x, int64_t incx,
               float beta, float *y, int64_t incy);
 
+/* A <- alpha*x*y^T + A, A m-by-n column-major, x of length m, y of length
+ * n. Reference BLAS rules: m == 0, n == 0 or alpha == 0 leave A untouched
+ * and read neither x nor y; a column whose y entry is zero is skipped (its
+ * A entries are neither computed nor written, so Inf / NaN in x never meets
+ * that zero); otherwise A(i,j) = fma(x(i), alpha*y(j), A(i,j)). Replaces
+ * sger (src/sger/sger.mjs:17-176, src/shaders/sger.wgsl; its row-major
+ * frame skips rows where x is zero, this column-major y after the layout
+ * swap of sger.mjs:56-64). */
+int wgb_sger(wgb_ctx *ctx, int64_t m, int64_t n, float alpha, const float *x,
+             int64_t incx, const float *y, int64_t incy, float *A, int64_t lda);
+
+/* Native-FP64 dger: wgb_sger in fp64. Replaces dger (src/dger/dger.mjs:21-238,
+ * src/shaders/dger.wgsl in double-double). */
+int wgb_dger(wgb_ctx *ctx, int64_t m, int64_t n, double alpha, const double *x,
+             int64_t incx, const double *y, int64_t incy, double *A, int64_t lda);
+
 /* Native-FP64 dgemv: wgb_sgemv's operation and rules in fp64 (alpha == 0
  * with beta == 1 returns without a kernel, src/dgemv/dgemv.mjs:126).
  * Replaces dgemv (src/dgemv/dgemv.mjs:23-341, src/shaders/dgemv_n.wgsl,

@@ -686,3 +686,24 @@ void orc_sgemv_ld(int trans, int64_t m, int64_t n, double alpha, const double *A
     if (absdot) absdot[i] = (double)a;
   }
 }
+
+/* ---- level 2: sger / dger (src/sger/sger.mjs:17-176, src/dger/dger.mjs) --
+ * A <- alpha x y^T + A, A m x n column-major, in long double, with reference
+ * BLAS's column order, which the reference's tests hold it to through stdlib
+ * (tests/sger/src/test.sger.js:141-178, 219-298): m == 0, n == 0 or
+ * alpha == 0 leave A untouched (x and y unread); column j is skipped when
+ * y[j] is zero (so Infinity or NaN in x never meets that zero), otherwise
+ * A(i, j) += x[i] * (alpha * y[j]) for every row, zeros in x included. In
+ * the reference's row-major frame the skipped vector is x (sger.wgsl:38-44),
+ * which is this column-major y after its layout swap (sger.mjs:56-64). */
+void orc_sger_ld(int64_t m, int64_t n, double alpha, const double *x, int64_t incx,
+                 const double *y, int64_t incy, double *A, int64_t lda) {
+  if (m == 0 || n == 0 || alpha == 0.0) return;
+  for (int64_t j = 0; j < n; ++j) {
+    long double yj = y[j * incy];
+    if (yj == 0.0L) continue;
+    long double t = (long double)alpha * yj;
+    for (int64_t i = 0; i < m; ++i)
+      A[i + j * lda] = (double)((long double)A[i + j * lda] + (long double)x[i * incx] * t);
+  }
+}

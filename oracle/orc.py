@@ -47,6 +47,7 @@ _SIG = {
                             _i64, _f64p, _i64]),
     "orc_sgemv_ld": (None, [C.c_int, _i64, _i64, C.c_double, _f64p, _i64, _f64p, _i64, C.c_double,
                             _f64p, _i64, _f64p]),
+    "orc_sger_ld": (None, [_i64, _i64, C.c_double, _f64p, _i64, _f64p, _i64, _f64p, _i64]),
 }
 
 _lib = None
@@ -245,6 +246,16 @@ def strsm_ld(side, uplo, trans, unit, m, n, alpha, A, lda, B, ldb):
     lib().orc_strsm_ld(side, uplo, trans, unit, m, n, alpha, Ap, lda,
                        out.ctypes.data_as(_f64p), ldb)
     return out
+
+
+def sger_ld(m, n, alpha, x, incx, y, incy, A, lda):
+    """Returns the whole updated A buffer: alpha x y^T + A in long double
+    (reference BLAS's column order and zero-y skip), column-major."""
+    x, xp = _f64(x if x is not None and len(x) else np.zeros(1))
+    y, yp = _f64(y if y is not None and len(y) else np.zeros(1))
+    out = np.array(A if A is not None and len(A) else np.zeros(1), dtype=np.float64, copy=True)
+    lib().orc_sger_ld(m, n, alpha, xp, incx, yp, incy, out.ctypes.data_as(_f64p), lda)
+    return out[: len(A)] if A is not None else out
 
 
 def sgemv_ld(trans, m, n, alpha, A, lda, x, incx, beta, y, incy):

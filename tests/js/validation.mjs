@@ -82,6 +82,9 @@ function minLength(dependsOn, dims) {
   if ((dependsOn || []).includes("trans") && (dependsOn || []).includes("m") && dims.m !== undefined) {
     const noTrans = (dims.trans || "no-transpose") === "no-transpose";
     len = noTrans === isX ? dims.n : dims.m;
+  } else if ((dependsOn || []).includes("m") && !(dependsOn || []).includes("n")) {
+    // a vector sized by m alone (sger's x)
+    len = dims.m;
   }
   return (len - 1) * inc + 1;
 }
@@ -419,6 +422,27 @@ async function main() {
     layout: loadParam("layout"),
   }, (a) => wg.dgemv(a.device, a.trans, a.m, a.n, a.alpha, a.A, a.lda, a.x, a.incx, a.beta, a.y, a.incy,
     a.layout), device);
+  // sger / dger: wgblas's tests/sger/src/test.sger.js and test.dger.js
+  // compositions (x sized by m, y by n; dger with the 64-bit specs)
+  for (const [r, f64] of [["sger", false], ["dger", true]]) {
+    const v = (name) => loadParam(f64 ? name + "64" : name);
+    register(r, {
+      device: loadParam("device"),
+      m: loadParam("m"),
+      n: Object.assign({}, nS, {
+        edge: nS.edge.filter((e) => e.value !== -1),
+        invalid: nS.invalid.concat([{ value: -1, error: "n must be non-negative", label: "negative" }]),
+      }),
+      alpha: v("alpha"),
+      x: Object.assign({}, v("x"), { dependsOn: ["m", "incx"] }),
+      incx: loadParam("incx"),
+      y: Object.assign({}, v("y"), { dependsOn: ["n", "incy"] }),
+      incy: loadParam("incy"),
+      A: v("A"),
+      lda: loadParam("lda"),
+      layout: loadParam("layout"),
+    }, (a) => wg[r](a.device, a.m, a.n, a.alpha, a.x, a.incx, a.y, a.incy, a.A, a.lda, a.layout), device);
+  }
   register("sdot", {
     device: loadParam("device"), n: loadParam("n"), incx: loadParam("incx"), incy: loadParam("incy"),
     x: loadParam("x"), y: loadParam("y"),

@@ -220,6 +220,32 @@ def gemv_call(case, dtype=np.float32):
     return (1 - t, n, m, case["alpha"], A, case["lda"], x, case["incx"], case["beta"], y, case["incy"])
 
 
+def ger_call(case, dtype=np.float32):
+    """Column-major (m, n, alpha, x, incx, y, incy, A, lda) for sger / dger.
+    A row-major m x n A read column-major is A^T (n x m), and the transpose
+    of a rank-1 update swaps its vectors (src/sger/sger.mjs:56-64)."""
+    layout = case.get("layout", "row-major")
+    m, n = case["m"], case["n"]
+    x, y, A = (np.array(case[k], dtype) for k in ("x", "y", "A"))
+    if layout == "column-major":
+        return (m, n, case["alpha"], x, case["incx"], y, case["incy"], A, case["lda"])
+    return (n, m, case["alpha"], y, case["incy"], x, case["incx"], A, case["lda"])
+
+
+def numpy_ger(m, n, alpha, x, incx, y, incy, A, lda):
+    """Column-major A + alpha x y^T by numpy (float64), with reference BLAS's
+    quick returns and its skipping of columns whose y entry is zero."""
+    out = np.array(A, np.float64, copy=True)
+    if m == 0 or n == 0 or alpha == 0:
+        return out
+    xv = np.asarray(x, np.float64)[np.arange(m) * incx]
+    yv = np.asarray(y, np.float64)[np.arange(n) * incy]
+    for j in np.nonzero(yv != 0)[0]:
+        col = out[j * lda: j * lda + m]
+        col += xv * (alpha * yv[j])
+    return out
+
+
 def numpy_gemv(trans, m, n, alpha, A, lda, x, incx, beta, y, incy):
     """Column-major sgemv by numpy (float64), with reference BLAS's quick
     returns and the no-transpose form's skipping of zero x entries."""

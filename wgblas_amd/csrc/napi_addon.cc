@@ -444,6 +444,32 @@ napi_value Sgemv(napi_env env, napi_callback_info info) {
   return nullptr;
 }
 
+// ger(ctx, m, n, alpha, x, incx, y, incy, A, lda, f64): sger, or dger when
+// f64 is true
+napi_value Ger(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 11)) return nullptr;
+  wgb_ctx *ctx = ctx_of(env, a.v[0]);
+  if (!ctx) return nullptr;
+  int64_t m, n, incx, incy, lda;
+  double alpha;
+  void *x, *y, *A;
+  bool f64 = false;
+  if (!get_i64(env, a.v[1], &m) || !get_i64(env, a.v[2], &n) || !get_f64(env, a.v[3], &alpha) ||
+      !get_ptr(env, a.v[4], &x) || !get_i64(env, a.v[5], &incx) || !get_ptr(env, a.v[6], &y) ||
+      !get_i64(env, a.v[7], &incy) || !get_ptr(env, a.v[8], &A) || !get_i64(env, a.v[9], &lda) ||
+      napi_get_value_bool(env, a.v[10], &f64) != napi_ok)
+    return nullptr;
+  if (f64) {
+    WGB_OK_OR_THROW(wgb_dger(ctx, m, n, alpha, (const double *)x, incx, (const double *)y, incy,
+                             (double *)A, lda), "wgb_dger");
+  } else {
+    WGB_OK_OR_THROW(wgb_sger(ctx, m, n, (float)alpha, (const float *)x, incx, (const float *)y,
+                             incy, (float *)A, lda), "wgb_sger");
+  }
+  return nullptr;
+}
+
 // ---- level 1 ---------------------------------------------------------------
 
 // reduce(kind, ctx, n, x, incx[, y, incy]) -> number; kind: 0 sdot, 1 sasum,
@@ -493,7 +519,7 @@ napi_value ModuleInit(napi_env env, napi_value exports) {
       {"synchronize", Synchronize}, {"malloc", Malloc}, {"free", Free},
       {"upload", Upload}, {"download", Download}, {"gemm", Gemm},
       {"ssyrk", Ssyrk}, {"ssyr2k", Ssyr2k}, {"ssymm", Ssymm},
-      {"tri", Tri}, {"sgemv", Sgemv}, {"reduce", Reduce},
+      {"tri", Tri}, {"sgemv", Sgemv}, {"ger", Ger}, {"reduce", Reduce},
   };
   for (const Fn &f : fns) {
     napi_value v;

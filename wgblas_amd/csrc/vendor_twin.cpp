@@ -294,6 +294,21 @@ void run_gemv(Twin &w) {
     emit(name, "16384^2, 2 GiB of A", ms, 8.0 * ((double)n * n + 3.0 * n), "GB/s");
   }
   w.release();
+  // sger / dger on the same shape (A read and written), alpha 1e-3
+  {
+    float *A = w.f32((int64_t)n * n, 15), *x = w.f32(n, 16), *y = w.f32(n, 17);
+    const float a = 1e-3f;
+    const double ms = w.median_ms([&] { RB_OK(rocblas_sger(w.h, n, n, &a, x, 1, y, 1, A, n)); }, 5, 20);
+    emit("sger_16384", "16384^2, A read and written", ms, 4.0 * (2.0 * n * n + 2.0 * n), "GB/s");
+    w.release();
+  }
+  {
+    double *A = w.f64((int64_t)n * n, 15), *x = w.f64(n, 16), *y = w.f64(n, 17);
+    const double a = 1e-3;
+    const double ms = w.median_ms([&] { RB_OK(rocblas_dger(w.h, n, n, &a, x, 1, y, 1, A, n)); }, 5, 20);
+    emit("dger_16384", "16384^2, A read and written", ms, 8.0 * (2.0 * n * n + 2.0 * n), "GB/s");
+    w.release();
+  }
 }
 
 void run_level1(Twin &w) {

@@ -21,6 +21,8 @@ export { dtrmm } from "./src/dtrmm.mjs";
 export { strsm } from "./src/strsm.mjs";
 export { sgemv } from "./src/sgemv.mjs";
 export { dgemv } from "./src/dgemv.mjs";
+export { sger } from "./src/sger.mjs";
+export { dger } from "./src/dger.mjs";
 export { sdot } from "./src/sdot.mjs";
 export { sasum } from "./src/sasum.mjs";
 export { snrm2 } from "./src/snrm2.mjs";

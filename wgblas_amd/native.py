@@ -72,6 +72,8 @@ _SIGNATURES = {
                   _ptr, _i64],
     "wgb_sgemv": [_ptr, C.c_int, _i64, _i64, C.c_float, _ptr, _i64, _ptr, _i64, C.c_float, _ptr,
                   _i64],
+    "wgb_sger": [_ptr, _i64, _i64, C.c_float, _ptr, _i64, _ptr, _i64, _ptr, _i64],
+    "wgb_dger": [_ptr, _i64, _i64, C.c_double, _ptr, _i64, _ptr, _i64, _ptr, _i64],
     "wgb_dgemv": [_ptr, C.c_int, _i64, _i64, C.c_double, _ptr, _i64, _ptr, _i64, C.c_double, _ptr,
                   _i64],
     "wgb_sdot": [_ptr, _i64, _ptr, _i64, _ptr, _i64, C.POINTER(C.c_float)],
@@ -320,6 +322,14 @@ class Context:
     def sgemv(self, trans, m, n, alpha, A, lda, x, incx, beta, y, incy):
         _check(self.lib.wgb_sgemv(self.handle, trans, m, n, alpha, _p(A), lda, _p(x), incx, beta,
                                   _p(y), incy), "wgb_sgemv")
+
+    def sger(self, m, n, alpha, x, incx, y, incy, A, lda):
+        _check(self.lib.wgb_sger(self.handle, m, n, alpha, _p(x), incx, _p(y), incy, _p(A), lda),
+               "wgb_sger")
+
+    def dger(self, m, n, alpha, x, incx, y, incy, A, lda):
+        _check(self.lib.wgb_dger(self.handle, m, n, alpha, _p(x), incx, _p(y), incy, _p(A), lda),
+               "wgb_dger")
 
     def dgemv(self, trans, m, n, alpha, A, lda, x, incx, beta, y, incy):
         _check(self.lib.wgb_dgemv(self.handle, trans, m, n, alpha, _p(A), lda, _p(x), incx, beta,

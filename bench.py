@@ -18,7 +18,8 @@ n = 8192, k = 4096, 10 chained resident calls (config 5), and sdot / sasum /
 snrm2 / isamax at n = 2^28 plus the incx = 3, n = 2^26 variants (config 2),
 sgemmtr on config 5's operands, ssyr2k / ssymm / strmm / strsm at order 8192
 (strsm also 4096), dsyr2k / dsymm / dtrmm at order 4096, sgemv and dgemv
-16384 x 16384 in both forms, sger and dger on 16384 x 16384, and ddot / dasum /
+16384 x 16384 in both forms, sger / dger and ssyr / dsyr / ssyr2 / dsyr2 (lower)
+at 16384, and ddot / dasum /
 dnrm2 / idamax at n = 2^27
 (the same bytes as config 2's fp32 vectors; uniform[-1, 1) inputs, seeds 1
 and 2, as wgblas's randomFloat64Array).
@@ -316,6 +317,24 @@ def bench_components(ctx, ev, quick):
         ms = per_launch_ms(ctx, f, 5 * reps, warm=True)
         gbs = es * (2 * n * n + 2 * n) / ms / 1e6
         comps[f"{name}_16384"] = {"ms": ms, "GB/s": gbs, "frac_hbm_peak": gbs * 1e9 / PEAK_HBM}
+        dA.free()
+        dx.free()
+        dy.free()
+
+    # ssyr / dsyr, ssyr2 / dsyr2 (lower) on the same order: the triangle read
+    # and written once
+    for dt, pre, es in ((np.float32, "s", 4.0), (np.float64, "d", 8.0)):
+        dA = ctx.empty(n * n, dt)
+        ctx.fill_uniform(dA, -1.0, 1.0, 15)
+        dx, dy = ctx.empty(n, dt), ctx.empty(n, dt)
+        ctx.fill_uniform(dx, -1.0, 1.0, 16)
+        ctx.fill_uniform(dy, -1.0, 1.0, 17)
+        for name, f, vec in ((pre + "syr", lambda: getattr(ctx, pre + "syr")(LOWER, n, 1e-3, dx, 1, dA, n), 1),
+                             (pre + "syr2", lambda: getattr(ctx, pre + "syr2")(LOWER, n, 1e-3, dx, 1, dy, 1,
+                                                                             dA, n), 2)):
+            ms = per_launch_ms(ctx, f, 5 * reps, warm=True)
+            gbs = es * (n * (n + 1) + vec * n) / ms / 1e6
+            comps[f"{name}_16384"] = {"ms": ms, "GB/s": gbs, "frac_hbm_peak": gbs * 1e9 / PEAK_HBM}
         dA.free()
         dx.free()
         dy.free()

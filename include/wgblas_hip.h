@@ -292,6 +292,37 @@ int wgb_sger(wgb_ctx *ctx, int64_t m, int64_t n, float alpha, const float *x,
 int wgb_dger(wgb_ctx *ctx, int64_t m, int64_t n, double alpha, const double *x,
              int64_t incx, const double *y, int64_t incy, double *A, int64_t lda);
 
+/* The uplo triangle (WGB_LOWER: i >= j, WGB_UPPER: i <= j) of the n-by-n
+ * column-major A <- alpha*x*x^T + A; the other triangle is never written
+ * (its values never reach the result). Reference BLAS rules: n == 0 or alpha == 0 leave A untouched and
+ * read no vector; a column whose x entry is zero is skipped (Inf / NaN in x
+ * never meets it); otherwise A(i,j) = fma(x(i), alpha*x(j), A(i,j)).
+ * Replaces ssyr (src/ssyr/ssyr.mjs:17-143, src/shaders/ssyr.wgsl; its
+ * row-major frame skips rows, this column after the uplo flip of
+ * ssyr.mjs:68-71). */
+int wgb_ssyr(wgb_ctx *ctx, int uplo, int64_t n, float alpha, const float *x,
+             int64_t incx, float *A, int64_t lda);
+
+/* Native-FP64 dsyr: wgb_ssyr in fp64. Replaces dsyr
+ * (src/dsyr/dsyr.mjs:21-196, double-double in dsyr.wgsl). */
+int wgb_dsyr(wgb_ctx *ctx, int uplo, int64_t n, double alpha, const double *x,
+             int64_t incx, double *A, int64_t lda);
+
+/* The uplo triangle of A <- alpha*x*y^T + alpha*y*x^T + A (n-by-n,
+ * column-major); column j is skipped when x(j) and y(j) are both zero,
+ * otherwise A(i,j) = fma(y(i), alpha*x(j), fma(x(i), alpha*y(j), A(i,j))).
+ * n == 0 or alpha == 0 leave A untouched. Replaces ssyr2
+ * (src/ssyr2/ssyr2.mjs:17-184, src/shaders/ssyr2.wgsl). */
+int wgb_ssyr2(wgb_ctx *ctx, int uplo, int64_t n, float alpha, const float *x,
+              int64_t incx, const float *y, int64_t incy, float *A,
+              int64_t lda);
+
+/* Native-FP64 dsyr2: wgb_ssyr2 in fp64. Replaces dsyr2
+ * (src/dsyr2/dsyr2.mjs:21-260, double-double in dsyr2.wgsl). */
+int wgb_dsyr2(wgb_ctx *ctx, int uplo, int64_t n, double alpha,
+              const double *x, int64_t incx, const double *y, int64_t incy,
+              double *A, int64_t lda);
+
 /* Native-FP64 dgemv: wgb_sgemv's operation and rules in fp64 (alpha == 0
  * with beta == 1 returns without a kernel, src/dgemv/dgemv.mjs:126).
  * Replaces dgemv (src/dgemv/dgemv.mjs:23-341, src/shaders/dgemv_n.wgsl,

@@ -707,3 +707,32 @@ void orc_sger_ld(int64_t m, int64_t n, double alpha, const double *x, int64_t in
       A[i + j * lda] = (double)((long double)A[i + j * lda] + (long double)x[i * incx] * t);
   }
 }
+
+/* ---- level 2: ssyr / dsyr, ssyr2 / dsyr2 (src/ssyr/ssyr.mjs:17-143,
+ * src/ssyr2/ssyr2.mjs:17-184 and their fp64 forms) ------------------------
+ * The uplo triangle (1 lower: i >= j, 2 upper: i <= j) of the n x n
+ * column-major A <- alpha x x^T + A (syr), or alpha x y^T + alpha y x^T + A
+ * (syr2), in long double, in reference BLAS's column order, which the
+ * reference's tests hold it to through stdlib (tests/ssyr/src/test.ssyr.js:
+ * 111-128, 165-230; test.ssyr2.js:142-161, 202-283): n == 0 or alpha == 0
+ * leave A untouched (vectors unread); column j is skipped when x[j] (syr2:
+ * x[j] and y[j]) is zero; otherwise A(i, j) += x[i] (alpha x[j]) (syr2:
+ * + x[i] (alpha y[j]) + y[i] (alpha x[j])) over the triangle's rows. The
+ * other triangle is never touched. In the reference's row-major frame the
+ * skipped index is the row (ssyr.wgsl:38-44), this column after its uplo
+ * flip (ssyr.mjs:68-71). */
+void orc_ssyr2_ld(int uplo, int64_t n, double alpha, const double *x, int64_t incx,
+                  const double *y, int64_t incy, int two, double *A, int64_t lda) {
+  if (n == 0 || alpha == 0.0) return;
+  for (int64_t j = 0; j < n; ++j) {
+    long double xj = x[j * incx], yj = two ? y[j * incy] : xj;
+    if (xj == 0.0L && (!two || yj == 0.0L)) continue;
+    long double t1 = (long double)alpha * yj, t2 = (long double)alpha * xj;
+    int64_t lo = uplo == 1 ? j : 0, hi = uplo == 1 ? n : j + 1;
+    for (int64_t i = lo; i < hi; ++i) {
+      long double v = (long double)A[i + j * lda] + (long double)x[i * incx] * t1;
+      if (two) v += (long double)y[i * incy] * t2;
+      A[i + j * lda] = (double)v;
+    }
+  }
+}

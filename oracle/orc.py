@@ -48,6 +48,7 @@ _SIG = {
     "orc_sgemv_ld": (None, [C.c_int, _i64, _i64, C.c_double, _f64p, _i64, _f64p, _i64, C.c_double,
                             _f64p, _i64, _f64p]),
     "orc_sger_ld": (None, [_i64, _i64, C.c_double, _f64p, _i64, _f64p, _i64, _f64p, _i64]),
+    "orc_ssyr2_ld": (None, [C.c_int, _i64, C.c_double, _f64p, _i64, _f64p, _i64, C.c_int, _f64p, _i64]),
 }
 
 _lib = None
@@ -256,6 +257,23 @@ def sger_ld(m, n, alpha, x, incx, y, incy, A, lda):
     out = np.array(A if A is not None and len(A) else np.zeros(1), dtype=np.float64, copy=True)
     lib().orc_sger_ld(m, n, alpha, xp, incx, yp, incy, out.ctypes.data_as(_f64p), lda)
     return out[: len(A)] if A is not None else out
+
+
+def ssyr_ld(uplo, n, alpha, x, incx, A, lda):
+    """The whole updated A buffer: the uplo triangle (1 lower, 2 upper) of
+    alpha x x^T + A in long double (zero-x column skip), column-major."""
+    return ssyr2_ld(uplo, n, alpha, x, incx, None, 1, A, lda)
+
+
+def ssyr2_ld(uplo, n, alpha, x, incx, y, incy, A, lda):
+    """ssyr2 (y given) or ssyr (y None): the uplo triangle of
+    alpha x y^T + alpha y x^T + A in long double, column-major."""
+    two = y is not None
+    x, xp = _f64(x if x is not None and len(x) else np.zeros(1))
+    y, yp = _f64(y if two and len(y) else np.zeros(1))
+    out = np.array(A if len(A) else np.zeros(1), dtype=np.float64, copy=True)
+    lib().orc_ssyr2_ld(uplo, n, alpha, xp, incx, yp, incy, int(two), out.ctypes.data_as(_f64p), lda)
+    return out[: len(A)]
 
 
 def sgemv_ld(trans, m, n, alpha, A, lda, x, incx, beta, y, incy):

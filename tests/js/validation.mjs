@@ -443,6 +443,33 @@ async function main() {
       layout: loadParam("layout"),
     }, (a) => wg[r](a.device, a.m, a.n, a.alpha, a.x, a.incx, a.y, a.incy, a.A, a.lda, a.layout), device);
   }
+  // ssyr / dsyr, ssyr2 / dsyr2: wgblas's tests/{ssyr,dsyr,ssyr2,dsyr2}/src
+  // compositions (x and y sized by n, A n x n)
+  for (const [r, f64, two] of [["ssyr", false, false], ["dsyr", true, false], ["ssyr2", false, true],
+    ["dsyr2", true, true]]) {
+    const v = (name) => loadParam(f64 ? name + "64" : name);
+    const specs = {
+      device: loadParam("device"),
+      uplo: loadParam("uplo"),
+      n: Object.assign({}, nS, {
+        edge: nS.edge.filter((e) => e.value !== -1),
+        invalid: nS.invalid.concat([{ value: -1, error: "n must be non-negative", label: "negative" }]),
+      }),
+      alpha: v("alpha"),
+      x: Object.assign({}, v("x"), { dependsOn: ["n", "incx"] }),
+      incx: loadParam("incx"),
+      A: Object.assign({}, v("A"), { dependsOn: ["n", "lda"] }),
+      lda: loadParam("lda"),
+      layout: loadParam("layout"),
+    };
+    if (two) {
+      specs.y = Object.assign({}, v("y"), { dependsOn: ["n", "incy"] });
+      specs.incy = loadParam("incy");
+    }
+    register(r, specs, two
+      ? (a) => wg[r](a.device, a.uplo, a.n, a.alpha, a.x, a.incx, a.y, a.incy, a.A, a.lda, a.layout)
+      : (a) => wg[r](a.device, a.uplo, a.n, a.alpha, a.x, a.incx, a.A, a.lda, a.layout), device);
+  }
   register("sdot", {
     device: loadParam("device"), n: loadParam("n"), incx: loadParam("incx"), incy: loadParam("incy"),
     x: loadParam("x"), y: loadParam("y"),

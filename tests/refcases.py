@@ -246,6 +246,41 @@ def numpy_ger(m, n, alpha, x, incx, y, incy, A, lda):
     return out
 
 
+def syr_call(case, dtype=np.float32):
+    """Column-major (uplo, n, alpha, x, incx, A, lda) for ssyr / dsyr, or
+    (uplo, n, alpha, x, incx, y, incy, A, lda) for ssyr2 / dsyr2 (a case with
+    y). A symmetric row-major A read column-major stores the other triangle:
+    uplo flips (src/ssyr/ssyr.mjs:68-71)."""
+    uplo = UPLO[case["uplo"]]
+    if case.get("layout", "row-major") != "column-major":
+        uplo = flip_uplo(uplo)
+    x, A = np.array(case["x"], dtype), np.array(case["A"], dtype)
+    if "y" in case:
+        return (uplo, case["n"], case["alpha"], x, case["incx"], np.array(case["y"], dtype), case["incy"],
+                A, case["lda"])
+    return (uplo, case["n"], case["alpha"], x, case["incx"], A, case["lda"])
+
+
+def numpy_syr2(uplo, n, alpha, x, incx, y, incy, A, lda):
+    """Column-major ssyr2 (y given) / ssyr (y None) by numpy (float64): the
+    uplo triangle of A + alpha (x y^T + y x^T) (or + alpha x x^T), with the
+    quick returns and the skip of columns whose x (and y) entry is zero."""
+    out = np.array(A, np.float64, copy=True)
+    if n == 0 or alpha == 0:
+        return out
+    xv = np.asarray(x, np.float64)[np.arange(n) * incx]
+    yv = xv if y is None else np.asarray(y, np.float64)[np.arange(n) * incy]
+    for j in range(n):
+        if xv[j] == 0 and (y is None or yv[j] == 0):
+            continue
+        rows = np.arange(j, n) if uplo == 1 else np.arange(0, j + 1)
+        upd = xv[rows] * (alpha * yv[j])
+        if y is not None:
+            upd = upd + yv[rows] * (alpha * xv[j])
+        out[rows + j * lda] += upd
+    return out
+
+
 def numpy_gemv(trans, m, n, alpha, A, lda, x, incx, beta, y, incy):
     """Column-major sgemv by numpy (float64), with reference BLAS's quick
     returns and the no-transpose form's skipping of zero x entries."""

@@ -1,8 +1,8 @@
 // sgemv (wgblas src/sgemv/sgemv.mjs:19-254, shaders sgemv_n.wgsl,
 // sgemv_t.wgsl, reduce_partials.wgsl) and its native-fp64 form dgemv
-// (src/dgemv/dgemv.mjs:23-341), column-major as in BLAS, and the rank-1
-// updates sger / dger (src/sger/sger.mjs:17-176, src/dger/dger.mjs) further
-// down. gemv:
+// (src/dgemv/dgemv.mjs:23-341), column-major as in BLAS, and further down
+// the rank-1 / rank-2 updates sger / dger, ssyr / dsyr, ssyr2 / dsyr2
+// (src/{sger,dger,ssyr,dsyr,ssyr2,dsyr2}/*.mjs). gemv:
 //   trans = N: y (m) <- alpha A x + beta y, x of length n;
 //   trans = T: y (n) <- alpha A^T x + beta y, x of length m.
 //
@@ -286,36 +286,78 @@ __global__ __launch_bounds__(kThreads) void scale_y_kernel(int64_t len, T beta, 
   if (i < len) y[i * incy] = beta == (T)0 ? (T)0 : beta * y[i * incy];
 }
 
-// sger / dger: A <- alpha x y^T + A, A m x n column-major. Block (b, c): rows
-// [1024 b, +1024) (4 consecutive rows per lane, its x entries held in
-// registers), columns [c cpb, min(n, (c+1) cpb)), kStepG at a time with all
-// of a step's A loads in flight. Column j takes t = alpha y[j] and
-// A(i, j) = fma(x[i], t, A(i, j)); a column whose y entry is zero is neither
-// computed nor written (reference BLAS's skip: Infinity or NaN in x never
-// meets that zero). VEC: lda % 4 == 0 and A aligned to 4 elements. A is read
-// and written once: HBM-bound, 2 m n elements of traffic.
+// Rank-1 and rank-2 updates, A m x n column-major:
+//   ger  (UPLO 0, !TWO): A += alpha x y^T;
+//   syr  (UPLO 1 / 2, !TWO, y = x): the lower (i >= j) / upper (i <= j)
+//        triangle of A += alpha x x^T;
+//   syr2 (UPLO 1 / 2, TWO): that triangle of A += alpha x y^T + alpha y x^T.
+// Block (b, c): rows [1024 b, +1024) (4 consecutive rows per lane, its x
+// (and y) entries held in registers), columns [c cpb, min(n, (c+1) cpb)),
+// kStepG at a time with all of a step's A loads in flight. Column j takes
+// t1 = alpha y[j] (and t2 = alpha x[j]) and A(i, j) = fma(x[i], t1, A(i, j))
+// (then fma(y[i], t2, .)); a column whose y entry (for syr2: both entries)
+// is zero is neither computed nor written, reference BLAS's skip: Infinity or
+// NaN in the row vector never meets that zero. A is read and written once:
+// HBM-bound, 2 m n elements of traffic (half that for a triangle).
 constexpr int kStepG = 8;
-template <typename T, bool VEC>
-__global__ __launch_bounds__(kThreads) void ger_kernel(int64_t m, int64_t n, T alpha,
-                                                       const T *__restrict__ x, int64_t incx,
-                                                       const T *__restrict__ y, int64_t incy,
-                                                       T *__restrict__ A, int64_t lda, int64_t cpb) {
+template <typename T, bool VEC, int UPLO, bool TWO>
+__global__ __launch_bounds__(kThreads) void rank_update_kernel(
+    int64_t m, int64_t n, T alpha, const T *__restrict__ x, int64_t incx, const T *__restrict__ y,
+    int64_t incy, T *__restrict__ A, int64_t lda, int64_t cpb) {
   typedef vec4<T> f4;
-  const int64_t i0 = (int64_t)blockIdx.x * (4 * kThreads) + 4 * threadIdx.x;
+  const int64_t r0 = (int64_t)blockIdx.x * (4 * kThreads);
+  const int64_t i0 = r0 + 4 * threadIdx.x;
   if (i0 >= m) return;
   const int rows = i0 + 4 <= m ? 4 : (int)(m - i0);
-  f4 xv;
+  f4 xv, yv;
 #pragma unroll
-  for (int q = 0; q < 4; ++q) xv[q] = q < rows ? x[(i0 + q) * incx] : (T)0;
-  const int64_t j0 = (int64_t)blockIdx.y * cpb;
-  const int64_t j1 = j0 + cpb < n ? j0 + cpb : n;
-  // FULL: every row of the block is inside m (a block-uniform choice), so
-  // the loads and stores are whole vectors with no per-lane branch between
-  // them and a step's loads all issue together; otherwise element accesses
-  // with clamped rows. (A per-lane choice between the two, measured at
-  // 16384^2 with 512 blocks on one box: fp32 5.0 against 5.5 TB/s.)
-  auto walk = [&](auto full_tag) {
+  for (int q = 0; q < 4; ++q) {
+    xv[q] = q < rows ? x[(i0 + q) * incx] : (T)0;
+    yv[q] = TWO && q < rows ? y[(i0 + q) * incy] : (T)0;
+  }
+  int64_t j0 = (int64_t)blockIdx.y * cpb;
+  int64_t j1 = j0 + cpb < n ? j0 + cpb : n;
+  // triangle: the block's columns split into whole ones (every row of the
+  // block inside the triangle) and diagonal ones (rows masked per element)
+  const int64_t rlast = r0 + 4 * kThreads - 1;  // the block's last row
+  int64_t d0 = j0, d1 = j0;                     // diagonal columns [d0, d1)
+  if (UPLO == 1) {                              // lower: i >= j
+    if (j1 > rlast + 1) j1 = rlast + 1;
+    d0 = j0 > r0 + 1 ? j0 : r0 + 1;
+    d1 = j1;
+    if (d0 > d1) d0 = d1;
+  } else if (UPLO == 2) {  // upper: i <= j
+    if (j0 < r0) j0 = r0;
+    d0 = j0;
+    d1 = j1 < rlast ? j1 : rlast;
+    if (d1 < d0) d1 = d0;
+  }
+  // update of one column's 4 rows (masked rows keep their value)
+  auto column_scalars = [&](int64_t j, T &t1, T &t2) -> bool {
+    const T c1 = y[j * incy];
+    const T c2 = TWO ? x[j * incx] : (T)0;
+    t1 = alpha * c1;
+    t2 = alpha * c2;
+    return c1 != (T)0 || (TWO && c2 != (T)0);
+  };
+  auto update = [&](f4 &a, T t1, T t2) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      a[q] = fma(xv[q], t1, a[q]);
+      if (TWO) a[q] = fma(yv[q], t2, a[q]);
+    }
+  };
+  // FULL: every row of the block inside m (a block-uniform choice): whole
+  // non-temporal vectors with no per-lane branch between them, a step's
+  // loads all issued together; otherwise element accesses with clamped rows.
+  // (A per-lane choice between the two, measured for ger at 16384^2 with
+  // 512 blocks on one box: fp32 5.0 against 5.5 TB/s.) MASK (the diagonal
+  // columns of a triangle): the same loads and arithmetic, and each lane
+  // stores only its rows inside the triangle (whole vectors where all four
+  // are).
+  auto walk = [&](auto full_tag, auto mask_tag, int64_t ja, int64_t jb) {
     constexpr bool FULL = decltype(full_tag)::value;
+    constexpr bool MASK = decltype(mask_tag)::value;
     auto load = [&](const T *col) -> f4 {
       if constexpr (FULL) return ld_nt(col + i0);
       f4 v;
@@ -323,78 +365,119 @@ __global__ __launch_bounds__(kThreads) void ger_kernel(int64_t m, int64_t n, T a
       for (int q = 0; q < 4; ++q) v[q] = col[i0 + (q < rows ? q : 0)];
       return v;
     };
-    auto store = [&](T *col, const f4 &v) {
+    auto store = [&](T *col, const f4 &v, int64_t j) {
+      if constexpr (MASK) {
+        const bool all = UPLO == 1 ? i0 >= j : i0 + rows - 1 <= j;
+        if (!all) {
+          for (int q = 0; q < rows; ++q) {
+            const int64_t i = i0 + q;
+            if (UPLO == 1 ? i >= j : i <= j) col[i] = v[q];
+          }
+          return;
+        }
+      }
       if constexpr (FULL) {
         __builtin_nontemporal_store(v, reinterpret_cast<f4 *>(col + i0));
       } else {
         for (int q = 0; q < rows; ++q) col[i0 + q] = v[q];
       }
     };
-    int64_t j = j0;
-    for (; j + kStepG <= j1; j += kStepG) {
-      T t[kStepG];
+    int64_t j = ja;
+    for (; j + kStepG <= jb; j += kStepG) {
+      T t1[kStepG], t2[kStepG];
+      bool live[kStepG];
       f4 a[kStepG];
 #pragma unroll
-      for (int c = 0; c < kStepG; ++c) t[c] = y[(j + c) * incy];
+      for (int c = 0; c < kStepG; ++c) live[c] = column_scalars(j + c, t1[c], t2[c]);
 #pragma unroll
       for (int c = 0; c < kStepG; ++c) a[c] = load(A + (j + c) * lda);
 #pragma unroll
       for (int c = 0; c < kStepG; ++c) {
-        if (t[c] != (T)0) {  // uniform: the column's y entry
-          const T tc = alpha * t[c];
-#pragma unroll
-          for (int q = 0; q < 4; ++q) a[c][q] = fma(xv[q], tc, a[c][q]);
-          store(A + (j + c) * lda, a[c]);
+        if (live[c]) {  // uniform: the column's entries
+          update(a[c], t1[c], t2[c]);
+          store(A + (j + c) * lda, a[c], j + c);
         }
       }
     }
-    for (; j < j1; ++j) {
-      const T yj = y[j * incy];
-      if (yj != (T)0) {
-        const T tc = alpha * yj;
+    for (; j < jb; ++j) {
+      T t1, t2;
+      if (column_scalars(j, t1, t2)) {
         f4 a = load(A + j * lda);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) a[q] = fma(xv[q], tc, a[q]);
-        store(A + j * lda, a);
+        update(a, t1, t2);
+        store(A + j * lda, a, j);
       }
     }
   };
-  if (VEC && (int64_t)(blockIdx.x + 1) * (4 * kThreads) <= m)
-    walk(std::true_type{});
+  const bool whole_rows = VEC && rlast < m;
+  auto walk_range = [&](auto mask_tag, int64_t ja, int64_t jb) {
+    if (ja >= jb) return;
+    if (whole_rows)
+      walk(std::true_type{}, mask_tag, ja, jb);
+    else
+      walk(std::false_type{}, mask_tag, ja, jb);
+  };
+  if (UPLO == 0) {
+    walk_range(std::false_type{}, j0, j1);
+    return;
+  }
+  // whole columns, then the diagonal ones: row i of column j is stored
+  // where i >= j (lower) or i <= j (upper)
+  if (UPLO == 1)
+    walk_range(std::false_type{}, j0, d0);
   else
-    walk(std::false_type{});
+    walk_range(std::false_type{}, d1, j1);
+  walk_range(std::true_type{}, d0, d1);
 }
 
+// ger (uplo 0, y given), syr (uplo 1 / 2, y == x, !two), syr2 (uplo 1 / 2,
+// two): argument checks, reference BLAS's quick returns (m or n zero, alpha
+// zero: A untouched, vectors unread; src/sger/sger.mjs:86, 103,
+// src/ssyr/ssyr.mjs:59, 75), one launch.
 template <typename T>
-int ger(wgb_ctx *ctx, int64_t m, int64_t n, T alpha, const T *x, int64_t incx, const T *y,
-        int64_t incy, T *A, int64_t lda) {
+int rank_update(wgb_ctx *ctx, int uplo, bool two, int64_t m, int64_t n, T alpha, const T *x,
+                int64_t incx, const T *y, int64_t incy, T *A, int64_t lda) {
   int st = wgb::enter(ctx);
   if (st) return st;
+  if (uplo != 0 && uplo != WGB_LOWER && uplo != WGB_UPPER)
+    return fail(WGB_ERR_INVALID_VALUE, "uplo must be WGB_LOWER or WGB_UPPER");
   if (m < 0 || n < 0) return fail(WGB_ERR_INVALID_VALUE, "m and n must be non-negative");
-  if (lda < imax(1, m)) return fail(WGB_ERR_INVALID_VALUE, "lda must be >= max(1, m)");
+  if (lda < imax(1, m)) return fail(WGB_ERR_INVALID_VALUE, "lda must be >= max(1, rows of A)");
   if (incx <= 0 || incy <= 0) return fail(WGB_ERR_INVALID_VALUE, "incx and incy must be positive");
-  // reference BLAS quick returns: A untouched, x and y unread
-  // (src/sger/sger.mjs:86, 103)
   if (m == 0 || n == 0 || alpha == (T)0) return WGB_OK;
   if (!A || !x || !y) return fail(WGB_ERR_INVALID_VALUE, "A, x or y is null");
   wgb::timing_begin(ctx);
   const int64_t bx = cdiv(m, 4 * kThreads);
-  // column chunks: about one block per CU in all (each a long run of
+  // column chunks: about one block per CU in all for ger (each a long run of
   // columns), at least kStepG columns each. Measured at 16384^2 on one box,
   // blocks in all against TB/s (fp32 / fp64): 128 3.5 / 3.7, 256 5.7 / 5.2,
-  // 384 5.7 / 4.1, 512 5.5 / 4.9, 2048 4.8 / 4.7.
-  const int64_t target = ctx->num_cus > 0 ? ctx->num_cus : 256;
+  // 384 5.7 / 4.1, 512 5.5 / 4.9, 2048 4.8 / 4.7. A triangle's blocks do
+  // work that varies with their row; for fp32, four times as many, shorter
+  // blocks even it out (lower 16384, blocks per CU 1 / 2 / 4 / 8 / 16: ssyr
+  // 2.4 / 3.4 / 3.5 / 3.6 / 3.3 TB/s), fp64 kept one per CU (dsyr 3.4 / 3.0 /
+  // 3.1 / 3.1 / 3.2).
+  const int64_t cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
+  const int64_t target = uplo == 0 || sizeof(T) == 8 ? cus : 4 * cus;
   int64_t chunks = cdiv(target, bx);
   if (chunks > cdiv(n, kStepG)) chunks = cdiv(n, kStepG);
   if (chunks > 65535) chunks = 65535;
   if (chunks < 1) chunks = 1;
   const int64_t cpb = cdiv(n, chunks);
   const dim3 grid((unsigned)bx, (unsigned)cdiv(n, cpb));
-  if (lda % 4 == 0 && aligned4(A))
-    ger_kernel<T, true><<<grid, kThreads, 0, ctx->stream>>>(m, n, alpha, x, incx, y, incy, A, lda, cpb);
+  const bool vec = lda % 4 == 0 && aligned4(A);
+  auto launch = [&](auto kern) {
+    kern<<<grid, kThreads, 0, ctx->stream>>>(m, n, alpha, x, incx, y, incy, A, lda, cpb);
+  };
+  if (uplo == 0)
+    launch(vec ? rank_update_kernel<T, true, 0, false> : rank_update_kernel<T, false, 0, false>);
+  else if (uplo == WGB_LOWER && !two)
+    launch(vec ? rank_update_kernel<T, true, 1, false> : rank_update_kernel<T, false, 1, false>);
+  else if (!two)
+    launch(vec ? rank_update_kernel<T, true, 2, false> : rank_update_kernel<T, false, 2, false>);
+  else if (uplo == WGB_LOWER)
+    launch(vec ? rank_update_kernel<T, true, 1, true> : rank_update_kernel<T, false, 1, true>);
   else
-    ger_kernel<T, false><<<grid, kThreads, 0, ctx->stream>>>(m, n, alpha, x, incx, y, incy, A, lda, cpb);
-  WGB_CHECK_LAUNCH("ger_kernel");
+    launch(vec ? rank_update_kernel<T, true, 2, true> : rank_update_kernel<T, false, 2, true>);
+  WGB_CHECK_LAUNCH("rank_update_kernel");
   wgb::timing_end(ctx);
   return WGB_OK;
 }
@@ -509,12 +592,36 @@ extern "C" int wgb_sgemv(wgb_ctx *ctx, int trans, int64_t m, int64_t n, float al
 
 extern "C" int wgb_sger(wgb_ctx *ctx, int64_t m, int64_t n, float alpha, const float *x,
                         int64_t incx, const float *y, int64_t incy, float *A, int64_t lda) {
-  return ger<float>(ctx, m, n, alpha, x, incx, y, incy, A, lda);
+  return rank_update<float>(ctx, 0, false, m, n, alpha, x, incx, y, incy, A, lda);
 }
 
 extern "C" int wgb_dger(wgb_ctx *ctx, int64_t m, int64_t n, double alpha, const double *x,
                         int64_t incx, const double *y, int64_t incy, double *A, int64_t lda) {
-  return ger<double>(ctx, m, n, alpha, x, incx, y, incy, A, lda);
+  return rank_update<double>(ctx, 0, false, m, n, alpha, x, incx, y, incy, A, lda);
+}
+
+extern "C" int wgb_ssyr(wgb_ctx *ctx, int uplo, int64_t n, float alpha, const float *x,
+                        int64_t incx, float *A, int64_t lda) {
+  if (uplo == 0) return fail(WGB_ERR_INVALID_VALUE, "uplo must be WGB_LOWER or WGB_UPPER");
+  return rank_update<float>(ctx, uplo, false, n, n, alpha, x, incx, x, incx, A, lda);
+}
+
+extern "C" int wgb_dsyr(wgb_ctx *ctx, int uplo, int64_t n, double alpha, const double *x,
+                        int64_t incx, double *A, int64_t lda) {
+  if (uplo == 0) return fail(WGB_ERR_INVALID_VALUE, "uplo must be WGB_LOWER or WGB_UPPER");
+  return rank_update<double>(ctx, uplo, false, n, n, alpha, x, incx, x, incx, A, lda);
+}
+
+extern "C" int wgb_ssyr2(wgb_ctx *ctx, int uplo, int64_t n, float alpha, const float *x,
+                         int64_t incx, const float *y, int64_t incy, float *A, int64_t lda) {
+  if (uplo == 0) return fail(WGB_ERR_INVALID_VALUE, "uplo must be WGB_LOWER or WGB_UPPER");
+  return rank_update<float>(ctx, uplo, true, n, n, alpha, x, incx, y, incy, A, lda);
+}
+
+extern "C" int wgb_dsyr2(wgb_ctx *ctx, int uplo, int64_t n, double alpha, const double *x,
+                         int64_t incx, const double *y, int64_t incy, double *A, int64_t lda) {
+  if (uplo == 0) return fail(WGB_ERR_INVALID_VALUE, "uplo must be WGB_LOWER or WGB_UPPER");
+  return rank_update<double>(ctx, uplo, true, n, n, alpha, x, incx, y, incy, A, lda);
 }
 
 extern "C" int wgb_dgemv(wgb_ctx *ctx, int trans, int64_t m, int64_t n, double alpha,

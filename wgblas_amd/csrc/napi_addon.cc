@@ -470,6 +470,40 @@ napi_value Ger(napi_env env, napi_callback_info info) {
   return nullptr;
 }
 
+// syr(ctx, uplo, n, alpha, x, incx, y, incy, A, lda, f64): ssyr2 / dsyr2, or
+// ssyr / dsyr when y is null
+napi_value Syr(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 11)) return nullptr;
+  wgb_ctx *ctx = ctx_of(env, a.v[0]);
+  if (!ctx) return nullptr;
+  int uplo;
+  int64_t n, incx, incy, lda;
+  double alpha;
+  void *x, *A, *y;
+  bool f64 = false;
+  if (!get_i32(env, a.v[1], &uplo) || !get_i64(env, a.v[2], &n) || !get_f64(env, a.v[3], &alpha) ||
+      !get_ptr(env, a.v[4], &x) || !get_i64(env, a.v[5], &incx) || !get_ptr(env, a.v[6], &y) ||
+      !get_i64(env, a.v[7], &incy) || !get_ptr(env, a.v[8], &A) || !get_i64(env, a.v[9], &lda) ||
+      napi_get_value_bool(env, a.v[10], &f64) != napi_ok)
+    return nullptr;
+  if (y == nullptr) {
+    if (f64)
+      WGB_OK_OR_THROW(wgb_dsyr(ctx, uplo, n, alpha, (const double *)x, incx, (double *)A, lda),
+                      "wgb_dsyr");
+    else
+      WGB_OK_OR_THROW(wgb_ssyr(ctx, uplo, n, (float)alpha, (const float *)x, incx, (float *)A, lda),
+                      "wgb_ssyr");
+  } else if (f64) {
+    WGB_OK_OR_THROW(wgb_dsyr2(ctx, uplo, n, alpha, (const double *)x, incx, (const double *)y, incy,
+                              (double *)A, lda), "wgb_dsyr2");
+  } else {
+    WGB_OK_OR_THROW(wgb_ssyr2(ctx, uplo, n, (float)alpha, (const float *)x, incx, (const float *)y,
+                              incy, (float *)A, lda), "wgb_ssyr2");
+  }
+  return nullptr;
+}
+
 // ---- level 1 ---------------------------------------------------------------
 
 // reduce(kind, ctx, n, x, incx[, y, incy]) -> number; kind: 0 sdot, 1 sasum,
@@ -519,7 +553,7 @@ napi_value ModuleInit(napi_env env, napi_value exports) {
       {"synchronize", Synchronize}, {"malloc", Malloc}, {"free", Free},
       {"upload", Upload}, {"download", Download}, {"gemm", Gemm},
       {"ssyrk", Ssyrk}, {"ssyr2k", Ssyr2k}, {"ssymm", Ssymm},
-      {"tri", Tri}, {"sgemv", Sgemv}, {"ger", Ger}, {"reduce", Reduce},
+      {"tri", Tri}, {"sgemv", Sgemv}, {"ger", Ger}, {"syr", Syr}, {"reduce", Reduce},
   };
   for (const Fn &f : fns) {
     napi_value v;

@@ -309,6 +309,33 @@ void run_gemv(Twin &w) {
     emit("dger_16384", "16384^2, A read and written", ms, 8.0 * (2.0 * n * n + 2.0 * n), "GB/s");
     w.release();
   }
+  // ssyr / ssyr2 / dsyr / dsyr2 (lower): the triangle read and written
+  {
+    float *A = w.f32((int64_t)n * n, 15), *x = w.f32(n, 16), *y = w.f32(n, 17);
+    const float a = 1e-3f;
+    double ms = w.median_ms(
+        [&] { RB_OK(rocblas_ssyr(w.h, rocblas_fill_lower, n, &a, x, 1, A, n)); }, 5, 20);
+    emit("ssyr_16384", "lower 16384, triangle read and written", ms,
+         4.0 * ((double)n * (n + 1) + n), "GB/s");
+    ms = w.median_ms(
+        [&] { RB_OK(rocblas_ssyr2(w.h, rocblas_fill_lower, n, &a, x, 1, y, 1, A, n)); }, 5, 20);
+    emit("ssyr2_16384", "lower 16384, triangle read and written", ms,
+         4.0 * ((double)n * (n + 1) + 2.0 * n), "GB/s");
+    w.release();
+  }
+  {
+    double *A = w.f64((int64_t)n * n, 15), *x = w.f64(n, 16), *y = w.f64(n, 17);
+    const double a = 1e-3;
+    double ms = w.median_ms(
+        [&] { RB_OK(rocblas_dsyr(w.h, rocblas_fill_lower, n, &a, x, 1, A, n)); }, 5, 20);
+    emit("dsyr_16384", "lower 16384, triangle read and written", ms,
+         8.0 * ((double)n * (n + 1) + n), "GB/s");
+    ms = w.median_ms(
+        [&] { RB_OK(rocblas_dsyr2(w.h, rocblas_fill_lower, n, &a, x, 1, y, 1, A, n)); }, 5, 20);
+    emit("dsyr2_16384", "lower 16384, triangle read and written", ms,
+         8.0 * ((double)n * (n + 1) + 2.0 * n), "GB/s");
+    w.release();
+  }
 }
 
 void run_level1(Twin &w) {

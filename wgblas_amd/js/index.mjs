@@ -23,6 +23,10 @@ export { sgemv } from "./src/sgemv.mjs";
 export { dgemv } from "./src/dgemv.mjs";
 export { sger } from "./src/sger.mjs";
 export { dger } from "./src/dger.mjs";
+export { ssyr } from "./src/ssyr.mjs";
+export { dsyr } from "./src/dsyr.mjs";
+export { ssyr2 } from "./src/ssyr2.mjs";
+export { dsyr2 } from "./src/dsyr2.mjs";
 export { sdot } from "./src/sdot.mjs";
 export { sasum } from "./src/sasum.mjs";
 export { snrm2 } from "./src/snrm2.mjs";

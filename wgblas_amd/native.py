@@ -74,6 +74,10 @@ _SIGNATURES = {
                   _i64],
     "wgb_sger": [_ptr, _i64, _i64, C.c_float, _ptr, _i64, _ptr, _i64, _ptr, _i64],
     "wgb_dger": [_ptr, _i64, _i64, C.c_double, _ptr, _i64, _ptr, _i64, _ptr, _i64],
+    "wgb_ssyr": [_ptr, C.c_int, _i64, C.c_float, _ptr, _i64, _ptr, _i64],
+    "wgb_dsyr": [_ptr, C.c_int, _i64, C.c_double, _ptr, _i64, _ptr, _i64],
+    "wgb_ssyr2": [_ptr, C.c_int, _i64, C.c_float, _ptr, _i64, _ptr, _i64, _ptr, _i64],
+    "wgb_dsyr2": [_ptr, C.c_int, _i64, C.c_double, _ptr, _i64, _ptr, _i64, _ptr, _i64],
     "wgb_dgemv": [_ptr, C.c_int, _i64, _i64, C.c_double, _ptr, _i64, _ptr, _i64, C.c_double, _ptr,
                   _i64],
     "wgb_sdot": [_ptr, _i64, _ptr, _i64, _ptr, _i64, C.POINTER(C.c_float)],
@@ -330,6 +334,20 @@ class Context:
     def dger(self, m, n, alpha, x, incx, y, incy, A, lda):
         _check(self.lib.wgb_dger(self.handle, m, n, alpha, _p(x), incx, _p(y), incy, _p(A), lda),
                "wgb_dger")
+
+    def ssyr(self, uplo, n, alpha, x, incx, A, lda):
+        _check(self.lib.wgb_ssyr(self.handle, uplo, n, alpha, _p(x), incx, _p(A), lda), "wgb_ssyr")
+
+    def dsyr(self, uplo, n, alpha, x, incx, A, lda):
+        _check(self.lib.wgb_dsyr(self.handle, uplo, n, alpha, _p(x), incx, _p(A), lda), "wgb_dsyr")
+
+    def ssyr2(self, uplo, n, alpha, x, incx, y, incy, A, lda):
+        _check(self.lib.wgb_ssyr2(self.handle, uplo, n, alpha, _p(x), incx, _p(y), incy, _p(A), lda),
+               "wgb_ssyr2")
+
+    def dsyr2(self, uplo, n, alpha, x, incx, y, incy, A, lda):
+        _check(self.lib.wgb_dsyr2(self.handle, uplo, n, alpha, _p(x), incx, _p(y), incy, _p(A), lda),
+               "wgb_dsyr2")
 
     def dgemv(self, trans, m, n, alpha, A, lda, x, incx, beta, y, incy):
         _check(self.lib.wgb_dgemv(self.handle, trans, m, n, alpha, _p(A), lda, _p(x), incx, beta,

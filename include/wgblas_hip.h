@@ -323,6 +323,24 @@ int wgb_dsyr2(wgb_ctx *ctx, int uplo, int64_t n, double alpha,
               const double *x, int64_t incx, const double *y, int64_t incy,
               double *A, int64_t lda);
 
+/* y <- alpha*S*x + beta*y, S the n-by-n symmetric matrix whose uplo
+ * triangle (WGB_LOWER / WGB_UPPER) the column-major A holds; the other
+ * triangle is never read. Reference BLAS rules: n == 0, or alpha == 0 with
+ * beta == 1, leave y untouched; alpha == 0 reads neither A nor x; beta == 0
+ * never reads y; every term is taken. The triangle is read once; partial
+ * sums are folded in a fixed order (deterministic). Replaces ssymv
+ * (src/ssymv/ssymv.mjs:17-216, src/shaders/ssymv.wgsl, reduce_partials.wgsl). */
+int wgb_ssymv(wgb_ctx *ctx, int uplo, int64_t n, float alpha, const float *A,
+              int64_t lda, const float *x, int64_t incx, float beta, float *y,
+              int64_t incy);
+
+/* Native-FP64 dsymv: wgb_ssymv in fp64, alpha == 0 with beta == 1 returning
+ * without a kernel (src/dsymv/dsymv.mjs:116). Replaces dsymv
+ * (src/dsymv/dsymv.mjs:25-336, double-double in dsymv.wgsl). */
+int wgb_dsymv(wgb_ctx *ctx, int uplo, int64_t n, double alpha, const double *A,
+              int64_t lda, const double *x, int64_t incx, double beta,
+              double *y, int64_t incy);
+
 /* Native-FP64 dgemv: wgb_sgemv's operation and rules in fp64 (alpha == 0
  * with beta == 1 returns without a kernel, src/dgemv/dgemv.mjs:126).
  * Replaces dgemv (src/dgemv/dgemv.mjs:23-341, src/shaders/dgemv_n.wgsl,

@@ -736,3 +736,36 @@ void orc_ssyr2_ld(int uplo, int64_t n, double alpha, const double *x, int64_t in
     }
   }
 }
+
+/* ---- level 2: ssymv / dsymv (src/ssymv/ssymv.mjs:17-216,
+ * src/dsymv/dsymv.mjs) ----------------------------------------------------
+ * y <- alpha S x + beta y, S the n x n symmetric matrix whose uplo triangle
+ * (1 lower, 2 upper) the column-major A holds, in long double, with
+ * reference BLAS's rules, which the reference's tests hold it to through
+ * stdlib (tests/ssymv/src/test.ssymv.js:147-171, 258-297): n == 0, or
+ * alpha == 0 with beta == 1, leave y untouched; alpha == 0 reads neither A
+ * nor x; beta == 0 never reads y; every term is taken (no zero skipping).
+ * absdot (may be NULL, length n) gets sum_j |S(i, j) x(j)|. */
+void orc_ssymv_ld(int uplo, int64_t n, double alpha, const double *A, int64_t lda,
+                  const double *x, int64_t incx, double beta, double *y, int64_t incy,
+                  double *absdot) {
+  if (absdot)
+    for (int64_t i = 0; i < n; ++i) absdot[i] = 0.0;
+  if (n == 0 || (alpha == 0.0 && beta == 1.0)) return;
+  for (int64_t i = 0; i < n; ++i) {
+    long double s = 0, a = 0;
+    if (alpha != 0.0) {
+      for (int64_t j = 0; j < n; ++j) {
+        int stored = uplo == 1 ? i >= j : i <= j;
+        long double sij = stored ? A[i + j * lda] : A[j + i * lda];
+        long double t = sij * (long double)x[j * incx];
+        s += t;
+        a += fabsl(t);
+      }
+    }
+    long double v = (long double)alpha * s;
+    if (beta != 0.0) v += (long double)beta * y[i * incy];
+    y[i * incy] = (double)v;
+    if (absdot) absdot[i] = (double)a;
+  }
+}

@@ -48,6 +48,8 @@ _SIG = {
     "orc_sgemv_ld": (None, [C.c_int, _i64, _i64, C.c_double, _f64p, _i64, _f64p, _i64, C.c_double,
                             _f64p, _i64, _f64p]),
     "orc_sger_ld": (None, [_i64, _i64, C.c_double, _f64p, _i64, _f64p, _i64, _f64p, _i64]),
+    "orc_ssymv_ld": (None, [C.c_int, _i64, C.c_double, _f64p, _i64, _f64p, _i64, C.c_double, _f64p,
+                            _i64, _f64p]),
     "orc_ssyr2_ld": (None, [C.c_int, _i64, C.c_double, _f64p, _i64, _f64p, _i64, C.c_int, _f64p, _i64]),
 }
 
@@ -257,6 +259,19 @@ def sger_ld(m, n, alpha, x, incx, y, incy, A, lda):
     out = np.array(A if A is not None and len(A) else np.zeros(1), dtype=np.float64, copy=True)
     lib().orc_sger_ld(m, n, alpha, xp, incx, yp, incy, out.ctypes.data_as(_f64p), lda)
     return out[: len(A)] if A is not None else out
+
+
+def ssymv_ld(uplo, n, alpha, A, lda, x, incx, beta, y, incy):
+    """Returns (y_out, absdot): y_out the whole updated y buffer (alpha S x +
+    beta y in long double, S from A's uplo triangle; reference BLAS's
+    rules), absdot per output element."""
+    A, Ap = _f64(A if A is not None and len(A) else np.zeros(1))
+    x, xp = _f64(x if x is not None and len(x) else np.zeros(1))
+    out = np.array(y, dtype=np.float64, copy=True)
+    ad = np.zeros(max(n, 1))
+    lib().orc_ssymv_ld(uplo, n, alpha, Ap, lda, xp, incx, beta, out.ctypes.data_as(_f64p), incy,
+                       ad.ctypes.data_as(_f64p))
+    return out, ad
 
 
 def ssyr_ld(uplo, n, alpha, x, incx, A, lda):

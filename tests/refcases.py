@@ -281,6 +281,33 @@ def numpy_syr2(uplo, n, alpha, x, incx, y, incy, A, lda):
     return out
 
 
+def symv_call(case, dtype=np.float32):
+    """Column-major (uplo, n, alpha, A, lda, x, incx, beta, y, incy) for
+    ssymv / dsymv: a symmetric row-major A read column-major stores the
+    other triangle, so uplo flips (src/ssymv/ssymv.mjs:96-99)."""
+    uplo = UPLO[case["uplo"]]
+    if case.get("layout", "row-major") != "column-major":
+        uplo = flip_uplo(uplo)
+    A, x, y = (np.array(case[k], dtype) for k in ("A", "x", "y"))
+    return (uplo, case["n"], case["alpha"], A, case["lda"], x, case["incx"], case["beta"], y, case["incy"])
+
+
+def numpy_symv(uplo, n, alpha, A, lda, x, incx, beta, y, incy):
+    """Column-major symv by numpy (float64): S from A's uplo triangle, with
+    reference BLAS's quick returns."""
+    out = np.array(y, np.float64, copy=True)
+    if n == 0 or (alpha == 0 and beta == 1):
+        return out
+    Ad = dense_op(A, n, n, lda, 0)
+    S = np.tril(Ad) + np.tril(Ad, -1).T if uplo == 1 else np.triu(Ad) + np.triu(Ad, 1).T
+    xv = np.asarray(x, np.float64)[np.arange(n) * incx]
+    prod = S @ xv if alpha != 0 else np.zeros(n)
+    idx = np.arange(n) * incy
+    yin = out[idx]
+    out[idx] = alpha * prod + (beta * yin if beta != 0 else 0.0)
+    return out
+
+
 def numpy_gemv(trans, m, n, alpha, A, lda, x, incx, beta, y, incy):
     """Column-major sgemv by numpy (float64), with reference BLAS's quick
     returns and the no-transpose form's skipping of zero x entries."""

@@ -482,6 +482,208 @@ int rank_update(wgb_ctx *ctx, int uplo, bool two, int64_t m, int64_t n, T alpha,
   return WGB_OK;
 }
 
+// ssymv / dsymv: y <- alpha S x + beta y, S the n x n symmetric matrix whose
+// uplo triangle A holds (column-major). The triangle is read once: block
+// (r, p) takes rows [1024 r, +1024) (4 per lane, their x entries in
+// registers) and panel p, columns [128 p, +128), 8 at a time with all of a
+// step's loads in flight, and uses each stored element twice: A(i, j) x(j)
+// for row i and, off the diagonal, A(i, j) x(i) for its mirror, row j. The
+// row sums of a panel go to rowpart[p][i]; the mirror sums of a column are
+// folded across each wave (shuffles) and, once at the end of the block,
+// across its 4 waves (LDS) into colpart[r][j]. symv_fold_kernel then adds, for each j, exactly the slots
+// the triangle's blocks wrote, in a fixed order (deterministic), and applies
+// alpha and beta. Every term is taken (no zero skipping, as reference BLAS's
+// symv). Blocks that cross the diagonal mask elements outside the triangle
+// by selecting their terms away (never multiplying them).
+constexpr int kSymvRows = 4 * kThreads;  // rows per block
+constexpr int kSymvPanel = 128;          // columns per block
+template <typename T, bool VEC, int UPLO>
+__global__ __launch_bounds__(kThreads) void symv_kernel(int64_t n, const T *__restrict__ A, int64_t lda,
+                                                        const T *__restrict__ x, int64_t incx,
+                                                        T *__restrict__ rowpart,
+                                                        T *__restrict__ colpart) {
+  typedef vec4<T> f4;
+  const int64_t r0 = (int64_t)blockIdx.x * kSymvRows;
+  const int64_t c0 = (int64_t)blockIdx.y * kSymvPanel;
+  const int64_t rlast = r0 + kSymvRows - 1;
+  // does the block hold any element of the triangle? (block-uniform)
+  if (UPLO == 1 ? rlast < c0 : r0 > c0 + kSymvPanel - 1) return;
+  const int64_t cend = c0 + kSymvPanel < n ? c0 + kSymvPanel : n;
+  // a block strictly below (lower) / above (upper) the diagonal needs no
+  // masks: every element stored, none on the diagonal
+  const bool cross = UPLO == 1 ? r0 < cend : rlast >= c0;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t i0 = r0 + 4 * threadIdx.x;
+  const int rows = i0 >= n ? 0 : (i0 + 4 <= n ? 4 : (int)(n - i0));
+  const bool whole = VEC && rlast < n;  // every lane's 4 rows inside n
+  const int64_t ib = rows > 0 ? i0 : 0;  // a row inside the matrix
+  f4 xv;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) xv[q] = q < rows ? x[(i0 + q) * incx] : (T)0;
+  T racc[4] = {(T)0, (T)0, (T)0, (T)0};
+  // per-wave column sums of every step, added across the waves once at the
+  // end: no barrier between steps, so a step's loads never wait on the
+  // previous step's reduction
+  __shared__ T red[kSymvPanel / kStepG][4][kStepG];
+  // the step loop, compiled once per (WHOLE, CROSS): with either as a
+  // run-time test the loads sat in separate branches and issued one by one
+  auto steps = [&](auto whole_tag, auto cross_tag) {
+    constexpr bool WHOLE = decltype(whole_tag)::value;
+    constexpr bool CROSS = decltype(cross_tag)::value;
+    int step = 0;
+    for (int64_t j = c0; j < cend; j += kStepG, ++step) {
+      const int cols = cend - j < kStepG ? (int)(cend - j) : kStepG;
+      f4 a[kStepG];
+      T xc[kStepG];
+#pragma unroll
+      for (int c = 0; c < kStepG; ++c) {
+        const int64_t jc = j + (c < cols ? c : 0);  // clamped: every load in bounds
+        const T xj = x[jc * incx];
+        xc[c] = c < cols ? xj : (T)0;
+        const T *col = A + jc * lda;
+        if constexpr (WHOLE) {
+          a[c] = ld_nt(col + i0);
+        } else {
+          // rows past n read row ib (inside the matrix) and are never used;
+          // a lane with no rows (i0 >= n, kept for the block's final
+          // barrier) reads row 0
+#pragma unroll
+          for (int q = 0; q < 4; ++q) a[c][q] = col[ib + (q < rows ? q : 0)];
+        }
+      }
+      T cacc[kStepG];
+#pragma unroll
+      for (int c = 0; c < kStepG; ++c) {
+        cacc[c] = (T)0;
+        const int64_t jc = j + c;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int64_t i = i0 + q;
+          bool in = c < cols && q < rows;  // stored element (i, jc)
+          bool mirror = in;                // ... off the diagonal
+          if constexpr (CROSS) {
+            in = in && (UPLO == 1 ? i >= jc : i <= jc);
+            mirror = in && i != jc;
+          }
+          racc[q] = in ? fma(a[c][q], xc[c], racc[q]) : racc[q];
+          cacc[c] = mirror ? fma(a[c][q], xv[q], cacc[c]) : cacc[c];
+        }
+      }
+      // the step's column sums across the wave
+#pragma unroll
+      for (int c = 0; c < kStepG; ++c) {
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) cacc[c] += __shfl_xor(cacc[c], off, 64);
+      }
+      if (lane < kStepG) {
+        T v = cacc[0];
+#pragma unroll
+        for (int c = 1; c < kStepG; ++c) v = lane == c ? cacc[c] : v;
+        red[step][wave][lane] = v;
+      }
+    }
+  };
+  if (whole && !cross)
+    steps(std::true_type{}, std::false_type{});
+  else if (whole)
+    steps(std::true_type{}, std::true_type{});
+  else
+    steps(std::false_type{}, std::true_type{});
+  for (int q = 0; q < rows; ++q) rowpart[(int64_t)blockIdx.y * n + i0 + q] = racc[q];
+  __syncthreads();
+  if (threadIdx.x < cend - c0) {
+    const int st = threadIdx.x / kStepG, c = threadIdx.x % kStepG;
+    const T v = ((red[st][0][c] + red[st][1][c]) + red[st][2][c]) + red[st][3][c];
+    colpart[(int64_t)blockIdx.x * n + c0 + threadIdx.x] = v;
+  }
+}
+
+// y(j) <- alpha (sum of the row sums of the panels that reach row j + sum of
+// the mirror sums of the row chunks that reach column j) + beta y(j): the
+// slots symv_kernel wrote for j, lower (UPLO 1): panels 0 .. j/128, chunks
+// from the one holding row 128 (j/128) on; upper: panels j/128 .. P-1, chunks
+// up to the one holding row 128 (j/128) + 127. beta == 0 never reads y.
+template <typename T, int UPLO>
+__global__ __launch_bounds__(kThreads) void symv_fold_kernel(int64_t n, const T *__restrict__ rowpart,
+                                                             const T *__restrict__ colpart, T alpha,
+                                                             T beta, T *__restrict__ y, int64_t incy) {
+  const int64_t j = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (j >= n) return;
+  const int64_t np = (n + kSymvPanel - 1) / kSymvPanel, nr = (n + kSymvRows - 1) / kSymvRows;
+  const int64_t pj = j / kSymvPanel;
+  const int64_t p0 = UPLO == 1 ? 0 : pj, p1 = UPLO == 1 ? pj + 1 : np;
+  const int64_t ra = UPLO == 1 ? (pj * kSymvPanel) / kSymvRows : 0;
+  const int64_t rb = UPLO == 1 ? nr : (pj * kSymvPanel + kSymvPanel - 1) / kSymvRows + 1;
+  T s = (T)0;
+  int64_t p = p0;
+  for (; p + 8 <= p1; p += 8) {
+    T v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = rowpart[(p + u) * n + j];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) s += v[u];
+  }
+  for (; p < p1; ++p) s += rowpart[p * n + j];
+  for (int64_t r = ra; r < (rb < nr ? rb : nr); ++r) s += colpart[r * n + j];
+  T v = alpha * s;
+  if (beta != (T)0) v = fma(beta, y[j * incy], v);
+  y[j * incy] = v;
+}
+
+template <typename T>
+int symv(wgb_ctx *ctx, int uplo, int64_t n, T alpha, const T *A, int64_t lda, const T *x, int64_t incx,
+         T beta, T *y, int64_t incy) {
+  int st = wgb::enter(ctx);
+  if (st) return st;
+  if (uplo != WGB_LOWER && uplo != WGB_UPPER)
+    return fail(WGB_ERR_INVALID_VALUE, "uplo must be WGB_LOWER or WGB_UPPER");
+  if (n < 0) return fail(WGB_ERR_INVALID_VALUE, "n must be non-negative");
+  if (lda < imax(1, n)) return fail(WGB_ERR_INVALID_VALUE, "lda must be >= max(1, n)");
+  if (incx <= 0 || incy <= 0) return fail(WGB_ERR_INVALID_VALUE, "incx and incy must be positive");
+  if (n == 0) return WGB_OK;
+  if (alpha == (T)0 && beta == (T)1) {
+    // dsymv: reference BLAS's quick return, no kernel (src/dsymv/dsymv.mjs:116);
+    // ssymv runs (and times) its kernels there (src/ssymv/ssymv.mjs): an
+    // empty span, y untouched
+    if (sizeof(T) == 8) return WGB_OK;
+    wgb::timing_begin(ctx);
+    wgb::timing_end(ctx);
+    return WGB_OK;
+  }
+  if (!y || (alpha != (T)0 && (!A || !x))) return fail(WGB_ERR_INVALID_VALUE, "A, x or y is null");
+  wgb::timing_begin(ctx);
+  if (alpha == (T)0) {
+    scale_y_kernel<T><<<(unsigned)cdiv(n, kThreads), kThreads, 0, ctx->stream>>>(n, beta, y, incy);
+    WGB_CHECK_LAUNCH("scale_y_kernel");
+    wgb::timing_end(ctx);
+    return WGB_OK;
+  }
+  const int64_t nr = cdiv(n, kSymvRows), np = cdiv(n, kSymvPanel);
+  if (np > 65535) return fail(WGB_ERR_INVALID_VALUE, "n too large for one launch");
+  if ((st = wgb::ensure_op_workspace(ctx, (size_t)((np + nr) * n) * sizeof(T)))) return st;
+  T *rowpart = static_cast<T *>(ctx->op_ws);
+  T *colpart = rowpart + np * n;
+  const dim3 grid((unsigned)nr, (unsigned)np);
+  const bool vec = lda % 4 == 0 && aligned4(A);
+  auto launch = [&](auto kern) {
+    kern<<<grid, kThreads, 0, ctx->stream>>>(n, A, lda, x, incx, rowpart, colpart);
+  };
+  if (uplo == WGB_LOWER)
+    launch(vec ? symv_kernel<T, true, 1> : symv_kernel<T, false, 1>);
+  else
+    launch(vec ? symv_kernel<T, true, 2> : symv_kernel<T, false, 2>);
+  WGB_CHECK_LAUNCH("symv_kernel");
+  if (uplo == WGB_LOWER)
+    symv_fold_kernel<T, 1><<<(unsigned)cdiv(n, kThreads), kThreads, 0, ctx->stream>>>(
+        n, rowpart, colpart, alpha, beta, y, incy);
+  else
+    symv_fold_kernel<T, 2><<<(unsigned)cdiv(n, kThreads), kThreads, 0, ctx->stream>>>(
+        n, rowpart, colpart, alpha, beta, y, incy);
+  WGB_CHECK_LAUNCH("symv_fold_kernel");
+  wgb::timing_end(ctx);
+  return WGB_OK;
+}
+
 // sgemv / dgemv on the kernels above. dgemv keeps reference BLAS's quick
 // return for alpha == 0 with beta == 1 (src/dgemv/dgemv.mjs:126: no
 // kernel, y untouched bit for bit); sgemv times an empty span there, as
@@ -622,6 +824,18 @@ extern "C" int wgb_dsyr2(wgb_ctx *ctx, int uplo, int64_t n, double alpha, const 
                          int64_t incx, const double *y, int64_t incy, double *A, int64_t lda) {
   if (uplo == 0) return fail(WGB_ERR_INVALID_VALUE, "uplo must be WGB_LOWER or WGB_UPPER");
   return rank_update<double>(ctx, uplo, true, n, n, alpha, x, incx, y, incy, A, lda);
+}
+
+extern "C" int wgb_ssymv(wgb_ctx *ctx, int uplo, int64_t n, float alpha, const float *A,
+                         int64_t lda, const float *x, int64_t incx, float beta, float *y,
+                         int64_t incy) {
+  return symv<float>(ctx, uplo, n, alpha, A, lda, x, incx, beta, y, incy);
+}
+
+extern "C" int wgb_dsymv(wgb_ctx *ctx, int uplo, int64_t n, double alpha, const double *A,
+                         int64_t lda, const double *x, int64_t incx, double beta, double *y,
+                         int64_t incy) {
+  return symv<double>(ctx, uplo, n, alpha, A, lda, x, incx, beta, y, incy);
 }
 
 extern "C" int wgb_dgemv(wgb_ctx *ctx, int trans, int64_t m, int64_t n, double alpha,

@@ -504,6 +504,33 @@ napi_value Syr(napi_env env, napi_callback_info info) {
   return nullptr;
 }
 
+// symv(ctx, uplo, n, alpha, A, lda, x, incx, beta, y, incy, f64): ssymv, or
+// dsymv when f64 is true
+napi_value Symv(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 12)) return nullptr;
+  wgb_ctx *ctx = ctx_of(env, a.v[0]);
+  if (!ctx) return nullptr;
+  int uplo;
+  int64_t n, lda, incx, incy;
+  double alpha, beta;
+  void *A, *x, *y;
+  bool f64 = false;
+  if (!get_i32(env, a.v[1], &uplo) || !get_i64(env, a.v[2], &n) || !get_f64(env, a.v[3], &alpha) ||
+      !get_ptr(env, a.v[4], &A) || !get_i64(env, a.v[5], &lda) || !get_ptr(env, a.v[6], &x) ||
+      !get_i64(env, a.v[7], &incx) || !get_f64(env, a.v[8], &beta) || !get_ptr(env, a.v[9], &y) ||
+      !get_i64(env, a.v[10], &incy) || napi_get_value_bool(env, a.v[11], &f64) != napi_ok)
+    return nullptr;
+  if (f64) {
+    WGB_OK_OR_THROW(wgb_dsymv(ctx, uplo, n, alpha, (const double *)A, lda, (const double *)x, incx,
+                              beta, (double *)y, incy), "wgb_dsymv");
+  } else {
+    WGB_OK_OR_THROW(wgb_ssymv(ctx, uplo, n, (float)alpha, (const float *)A, lda, (const float *)x,
+                              incx, (float)beta, (float *)y, incy), "wgb_ssymv");
+  }
+  return nullptr;
+}
+
 // ---- level 1 ---------------------------------------------------------------
 
 // reduce(kind, ctx, n, x, incx[, y, incy]) -> number; kind: 0 sdot, 1 sasum,
@@ -553,7 +580,7 @@ napi_value ModuleInit(napi_env env, napi_value exports) {
       {"synchronize", Synchronize}, {"malloc", Malloc}, {"free", Free},
       {"upload", Upload}, {"download", Download}, {"gemm", Gemm},
       {"ssyrk", Ssyrk}, {"ssyr2k", Ssyr2k}, {"ssymm", Ssymm},
-      {"tri", Tri}, {"sgemv", Sgemv}, {"ger", Ger}, {"syr", Syr}, {"reduce", Reduce},
+      {"tri", Tri}, {"sgemv", Sgemv}, {"ger", Ger}, {"syr", Syr}, {"symv", Symv}, {"reduce", Reduce},
   };
   for (const Fn &f : fns) {
     napi_value v;

@@ -336,6 +336,25 @@ void run_gemv(Twin &w) {
          8.0 * ((double)n * (n + 1) + 2.0 * n), "GB/s");
     w.release();
   }
+  // ssymv / dsymv (lower): the triangle read once
+  {
+    float *A = w.f32((int64_t)n * n, 18), *x = w.f32(n, 19), *y = w.f32(n, 20);
+    const float one = 1.f, half = 0.5f;
+    const double ms = w.median_ms(
+        [&] { RB_OK(rocblas_ssymv(w.h, rocblas_fill_lower, n, &one, A, n, x, 1, &half, y, 1)); }, 5, 20);
+    emit("ssymv_16384", "lower 16384, triangle read once", ms, 4.0 * ((double)n * (n + 1) / 2 + 3.0 * n),
+         "GB/s");
+    w.release();
+  }
+  {
+    double *A = w.f64((int64_t)n * n, 18), *x = w.f64(n, 19), *y = w.f64(n, 20);
+    const double one = 1.0, half = 0.5;
+    const double ms = w.median_ms(
+        [&] { RB_OK(rocblas_dsymv(w.h, rocblas_fill_lower, n, &one, A, n, x, 1, &half, y, 1)); }, 5, 20);
+    emit("dsymv_16384", "lower 16384, triangle read once", ms, 8.0 * ((double)n * (n + 1) / 2 + 3.0 * n),
+         "GB/s");
+    w.release();
+  }
 }
 
 void run_level1(Twin &w) {

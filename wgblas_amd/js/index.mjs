@@ -27,6 +27,8 @@ export { ssyr } from "./src/ssyr.mjs";
 export { dsyr } from "./src/dsyr.mjs";
 export { ssyr2 } from "./src/ssyr2.mjs";
 export { dsyr2 } from "./src/dsyr2.mjs";
+export { ssymv } from "./src/ssymv.mjs";
+export { dsymv } from "./src/dsymv.mjs";
 export { sdot } from "./src/sdot.mjs";
 export { sasum } from "./src/sasum.mjs";
 export { snrm2 } from "./src/snrm2.mjs";

@@ -78,6 +78,8 @@ _SIGNATURES = {
     "wgb_dsyr": [_ptr, C.c_int, _i64, C.c_double, _ptr, _i64, _ptr, _i64],
     "wgb_ssyr2": [_ptr, C.c_int, _i64, C.c_float, _ptr, _i64, _ptr, _i64, _ptr, _i64],
     "wgb_dsyr2": [_ptr, C.c_int, _i64, C.c_double, _ptr, _i64, _ptr, _i64, _ptr, _i64],
+    "wgb_ssymv": [_ptr, C.c_int, _i64, C.c_float, _ptr, _i64, _ptr, _i64, C.c_float, _ptr, _i64],
+    "wgb_dsymv": [_ptr, C.c_int, _i64, C.c_double, _ptr, _i64, _ptr, _i64, C.c_double, _ptr, _i64],
     "wgb_dgemv": [_ptr, C.c_int, _i64, _i64, C.c_double, _ptr, _i64, _ptr, _i64, C.c_double, _ptr,
                   _i64],
     "wgb_sdot": [_ptr, _i64, _ptr, _i64, _ptr, _i64, C.POINTER(C.c_float)],
@@ -348,6 +350,14 @@ class Context:
     def dsyr2(self, uplo, n, alpha, x, incx, y, incy, A, lda):
         _check(self.lib.wgb_dsyr2(self.handle, uplo, n, alpha, _p(x), incx, _p(y), incy, _p(A), lda),
                "wgb_dsyr2")
+
+    def ssymv(self, uplo, n, alpha, A, lda, x, incx, beta, y, incy):
+        _check(self.lib.wgb_ssymv(self.handle, uplo, n, alpha, _p(A), lda, _p(x), incx, beta, _p(y), incy),
+               "wgb_ssymv")
+
+    def dsymv(self, uplo, n, alpha, A, lda, x, incx, beta, y, incy):
+        _check(self.lib.wgb_dsymv(self.handle, uplo, n, alpha, _p(A), lda, _p(x), incx, beta, _p(y), incy),
+               "wgb_dsymv")
 
     def dgemv(self, trans, m, n, alpha, A, lda, x, incx, beta, y, incy):
         _check(self.lib.wgb_dgemv(self.handle, trans, m, n, alpha, _p(A), lda, _p(x), incx, beta,

@@ -484,8 +484,8 @@ int rank_update(wgb_ctx *ctx, int uplo, bool two, int64_t m, int64_t n, T alpha,
 
 // ssymv / dsymv: y <- alpha S x + beta y, S the n x n symmetric matrix whose
 // uplo triangle A holds (column-major). The triangle is read once: block
-// (r, p) takes rows [1024 r, +1024) (4 per lane, their x entries in
-// registers) and panel p, columns [128 p, +128), 8 at a time with all of a
+// (r, p) takes rows [1024 r, +1024) (4 per lane in each row group, their x
+// entries in registers) and panel p, columns [128 p, +128), 8 at a time with all of a
 // step's loads in flight, and uses each stored element twice: A(i, j) x(j)
 // for row i and, off the diagonal, A(i, j) x(i) for its mirror, row j. The
 // row sums of a panel go to rowpart[p][i]; the mirror sums of a column are
@@ -495,14 +495,22 @@ int rank_update(wgb_ctx *ctx, int uplo, bool two, int64_t m, int64_t n, T alpha,
 // alpha and beta. Every term is taken (no zero skipping, as reference BLAS's
 // symv). Blocks that cross the diagonal mask elements outside the triangle
 // by selecting their terms away (never multiplying them).
-constexpr int kSymvRows = 4 * kThreads;  // rows per block
-constexpr int kSymvPanel = 128;          // columns per block
+// Measured at 16384 / 8192 (lower, TB/s of triangle traffic, fp32 / fp64):
+// 1 row group and 128-column panels 3.5 / 3.1 and 2.1 / 2.7; 2 groups 2.8 /
+// 2.9 and 1.4 / 1.8, 4 groups (4 columns a step) 2.7 / 2.3 and 0.8 / 1.0
+// (fewer blocks); 64-column panels 3.3 / 3.0 and 2.5 / 2.6, 32-column 3.2 /
+// 2.8 and 2.4 / 2.5.
+constexpr int kSymvGroups = 1;                         // 1024-row groups per block
+constexpr int kSymvRows = kSymvGroups * 4 * kThreads;  // rows per block
+constexpr int kSymvPanel = 128;                        // columns per block
+constexpr int kSymvStep = 8;                           // columns per step
 template <typename T, bool VEC, int UPLO>
 __global__ __launch_bounds__(kThreads) void symv_kernel(int64_t n, const T *__restrict__ A, int64_t lda,
                                                         const T *__restrict__ x, int64_t incx,
                                                         T *__restrict__ rowpart,
                                                         T *__restrict__ colpart) {
   typedef vec4<T> f4;
+  constexpr int G = kSymvGroups, S = kSymvStep;
   const int64_t r0 = (int64_t)blockIdx.x * kSymvRows;
   const int64_t c0 = (int64_t)blockIdx.y * kSymvPanel;
   const int64_t rlast = r0 + kSymvRows - 1;
@@ -513,72 +521,87 @@ __global__ __launch_bounds__(kThreads) void symv_kernel(int64_t n, const T *__re
   // masks: every element stored, none on the diagonal
   const bool cross = UPLO == 1 ? r0 < cend : rlast >= c0;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t i0 = r0 + 4 * threadIdx.x;
-  const int rows = i0 >= n ? 0 : (i0 + 4 <= n ? 4 : (int)(n - i0));
-  const bool whole = VEC && rlast < n;  // every lane's 4 rows inside n
-  const int64_t ib = rows > 0 ? i0 : 0;  // a row inside the matrix
-  f4 xv;
+  const bool whole = VEC && rlast < n;  // every lane's rows inside n
+  // group g: this lane's 4 rows i0[g] .. i0[g]+3 (rows[g] of them inside n)
+  int64_t i0[G], ib[G];
+  int rows[G];
+  f4 xv[G];
+  T racc[G][4];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) xv[q] = q < rows ? x[(i0 + q) * incx] : (T)0;
-  T racc[4] = {(T)0, (T)0, (T)0, (T)0};
+  for (int g = 0; g < G; ++g) {
+    i0[g] = r0 + (int64_t)g * 4 * kThreads + 4 * threadIdx.x;
+    rows[g] = i0[g] >= n ? 0 : (i0[g] + 4 <= n ? 4 : (int)(n - i0[g]));
+    ib[g] = rows[g] > 0 ? i0[g] : 0;  // a row inside the matrix
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      xv[g][q] = q < rows[g] ? x[(i0[g] + q) * incx] : (T)0;
+      racc[g][q] = (T)0;
+    }
+  }
   // per-wave column sums of every step, added across the waves once at the
   // end: no barrier between steps, so a step's loads never wait on the
   // previous step's reduction
-  __shared__ T red[kSymvPanel / kStepG][4][kStepG];
+  __shared__ T red[kSymvPanel / S][4][S];
   // the step loop, compiled once per (WHOLE, CROSS): with either as a
   // run-time test the loads sat in separate branches and issued one by one
   auto steps = [&](auto whole_tag, auto cross_tag) {
     constexpr bool WHOLE = decltype(whole_tag)::value;
     constexpr bool CROSS = decltype(cross_tag)::value;
     int step = 0;
-    for (int64_t j = c0; j < cend; j += kStepG, ++step) {
-      const int cols = cend - j < kStepG ? (int)(cend - j) : kStepG;
-      f4 a[kStepG];
-      T xc[kStepG];
+    for (int64_t j = c0; j < cend; j += S, ++step) {
+      const int cols = cend - j < S ? (int)(cend - j) : S;
+      f4 a[S][G];
+      T xc[S];
 #pragma unroll
-      for (int c = 0; c < kStepG; ++c) {
+      for (int c = 0; c < S; ++c) {
         const int64_t jc = j + (c < cols ? c : 0);  // clamped: every load in bounds
         const T xj = x[jc * incx];
         xc[c] = c < cols ? xj : (T)0;
         const T *col = A + jc * lda;
-        if constexpr (WHOLE) {
-          a[c] = ld_nt(col + i0);
-        } else {
-          // rows past n read row ib (inside the matrix) and are never used;
-          // a lane with no rows (i0 >= n, kept for the block's final
-          // barrier) reads row 0
 #pragma unroll
-          for (int q = 0; q < 4; ++q) a[c][q] = col[ib + (q < rows ? q : 0)];
+        for (int g = 0; g < G; ++g) {
+          if constexpr (WHOLE) {
+            a[c][g] = ld_nt(col + i0[g]);
+          } else {
+            // rows past n read row ib (inside the matrix) and are never
+            // used; a lane with no rows in a group (kept for the block's
+            // final barrier) reads row 0
+#pragma unroll
+            for (int q = 0; q < 4; ++q) a[c][g][q] = col[ib[g] + (q < rows[g] ? q : 0)];
+          }
         }
       }
-      T cacc[kStepG];
+      T cacc[S];
 #pragma unroll
-      for (int c = 0; c < kStepG; ++c) {
+      for (int c = 0; c < S; ++c) {
         cacc[c] = (T)0;
         const int64_t jc = j + c;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int64_t i = i0 + q;
-          bool in = c < cols && q < rows;  // stored element (i, jc)
-          bool mirror = in;                // ... off the diagonal
-          if constexpr (CROSS) {
-            in = in && (UPLO == 1 ? i >= jc : i <= jc);
-            mirror = in && i != jc;
+        for (int g = 0; g < G; ++g) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int64_t i = i0[g] + q;
+            bool in = c < cols && q < rows[g];  // stored element (i, jc)
+            bool mirror = in;                   // ... off the diagonal
+            if constexpr (CROSS) {
+              in = in && (UPLO == 1 ? i >= jc : i <= jc);
+              mirror = in && i != jc;
+            }
+            racc[g][q] = in ? fma(a[c][g][q], xc[c], racc[g][q]) : racc[g][q];
+            cacc[c] = mirror ? fma(a[c][g][q], xv[g][q], cacc[c]) : cacc[c];
           }
-          racc[q] = in ? fma(a[c][q], xc[c], racc[q]) : racc[q];
-          cacc[c] = mirror ? fma(a[c][q], xv[q], cacc[c]) : cacc[c];
         }
       }
       // the step's column sums across the wave
 #pragma unroll
-      for (int c = 0; c < kStepG; ++c) {
+      for (int c = 0; c < S; ++c) {
 #pragma unroll
         for (int off = 32; off > 0; off >>= 1) cacc[c] += __shfl_xor(cacc[c], off, 64);
       }
-      if (lane < kStepG) {
+      if (lane < S) {
         T v = cacc[0];
 #pragma unroll
-        for (int c = 1; c < kStepG; ++c) v = lane == c ? cacc[c] : v;
+        for (int c = 1; c < S; ++c) v = lane == c ? cacc[c] : v;
         red[step][wave][lane] = v;
       }
     }
@@ -589,10 +612,12 @@ __global__ __launch_bounds__(kThreads) void symv_kernel(int64_t n, const T *__re
     steps(std::true_type{}, std::true_type{});
   else
     steps(std::false_type{}, std::true_type{});
-  for (int q = 0; q < rows; ++q) rowpart[(int64_t)blockIdx.y * n + i0 + q] = racc[q];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+    for (int q = 0; q < rows[g]; ++q) rowpart[(int64_t)blockIdx.y * n + i0[g] + q] = racc[g][q];
   __syncthreads();
   if (threadIdx.x < cend - c0) {
-    const int st = threadIdx.x / kStepG, c = threadIdx.x % kStepG;
+    const int st = threadIdx.x / S, c = threadIdx.x % S;
     const T v = ((red[st][0][c] + red[st][1][c]) + red[st][2][c]) + red[st][3][c];
     colpart[(int64_t)blockIdx.x * n + c0 + threadIdx.x] = v;
   }

@@ -19,7 +19,7 @@ snrm2 / isamax at n = 2^28 plus the incx = 3, n = 2^26 variants (config 2),
 sgemmtr on config 5's operands, ssyr2k / ssymm / strmm / strsm at order 8192
 (strsm also 4096), dsyr2k / dsymm / dtrmm at order 4096, sgemv and dgemv
 16384 x 16384 in both forms, sger / dger and ssyr / dsyr / ssyr2 / dsyr2 / ssymv /
-dsymv (lower) at 16384, and ddot / dasum /
+dsymv (lower) at 16384, strmv / dtrmv (lower, N and T) at 16384, and ddot / dasum /
 dnrm2 / idamax at n = 2^27
 (the same bytes as config 2's fp32 vectors; uniform[-1, 1) inputs, seeds 1
 and 2, as wgblas's randomFloat64Array).
@@ -350,6 +350,22 @@ def bench_components(ctx, ev, quick):
         ms = per_launch_ms(ctx, f, 5 * reps, warm=True)
         gbs = es * (n * (n + 1) / 2 + 3 * n) / ms / 1e6
         comps[f"{pre}symv_16384"] = {"ms": ms, "GB/s": gbs, "frac_hbm_peak": gbs * 1e9 / PEAK_HBM}
+        dA.free()
+        dx.free()
+        dy.free()
+
+    # strmv / dtrmv (lower, both forms) on the same order: the triangle read
+    # once, x read and y written
+    for dt, pre, es in ((np.float32, "s", 4.0), (np.float64, "d", 8.0)):
+        dA = ctx.empty(n * n, dt)
+        ctx.fill_uniform(dA, -1.0, 1.0, 21)
+        dx, dy = ctx.empty(n, dt), ctx.empty(n, dt)
+        ctx.fill_uniform(dx, -1.0, 1.0, 22)
+        for t, tname in ((0, "N"), (1, "T")):
+            f = lambda: getattr(ctx, pre + "trmv")(LOWER, t, 0, n, dA, n, dx, 1, dy, 1)
+            ms = per_launch_ms(ctx, f, 5 * reps, warm=True)
+            gbs = es * (n * (n + 1) / 2 + 2 * n) / ms / 1e6
+            comps[f"{pre}trmv_{tname}_16384"] = {"ms": ms, "GB/s": gbs, "frac_hbm_peak": gbs * 1e9 / PEAK_HBM}
         dA.free()
         dx.free()
         dy.free()

@@ -341,6 +341,25 @@ int wgb_dsymv(wgb_ctx *ctx, int uplo, int64_t n, double alpha, const double *A,
               int64_t lda, const double *x, int64_t incx, double beta,
               double *y, int64_t incy);
 
+/* strmv: y <- op(T) x out of place, T the n x n uplo triangle of the
+ * column-major A (lda >= max(1, n)), op(T) = T (WGB_NO_TRANS) or T^T
+ * (WGB_TRANS), diag WGB_UNIT taking the diagonal as 1 (never read); incx,
+ * incy > 0; y is written, never read, and must not overlap A or x. The
+ * WGB_NO_TRANS form skips a column whose x entry is zero (reference BLAS's
+ * column form), the transposed one takes every term. One pass over the
+ * triangle (row or column sums of 1024 x 128 blocks), then a fixed-order
+ * fold (deterministic). Replaces strmv (src/strmv/strmv.mjs:20-259,
+ * src/shaders/strmv.wgsl, strmv_t.wgsl, reduce_partials.wgsl). */
+int wgb_strmv(wgb_ctx *ctx, int uplo, int trans, int diag, int64_t n,
+              const float *A, int64_t lda, const float *x, int64_t incx,
+              float *y, int64_t incy);
+
+/* Native-FP64 dtrmv: wgb_strmv in fp64. Replaces dtrmv
+ * (src/dtrmv/dtrmv.mjs:24-355, double-double in dtrmv.wgsl, dtrmv_t.wgsl). */
+int wgb_dtrmv(wgb_ctx *ctx, int uplo, int trans, int diag, int64_t n,
+              const double *A, int64_t lda, const double *x, int64_t incx,
+              double *y, int64_t incy);
+
 /* Native-FP64 dgemv: wgb_sgemv's operation and rules in fp64 (alpha == 0
  * with beta == 1 returns without a kernel, src/dgemv/dgemv.mjs:126).
  * Replaces dgemv (src/dgemv/dgemv.mjs:23-341, src/shaders/dgemv_n.wgsl,

@@ -769,3 +769,34 @@ void orc_ssymv_ld(int uplo, int64_t n, double alpha, const double *A, int64_t ld
     if (absdot) absdot[i] = (double)a;
   }
 }
+
+/* ---- level 2: strmv / dtrmv (src/strmv/strmv.mjs:20-259,
+ * src/dtrmv/dtrmv.mjs:24-355) ----------------------------------------------------
+ * y <- op(T) x out of place, T the n x n triangle (uplo 1 lower, 2 upper) of
+ * the column-major A, op(T) = T (trans 0) or T^T (trans 1), the diagonal
+ * taken as 1 when unit (its stored value never read), in long double. The
+ * column form (trans 0 here, the reference's row-major transposed kernel,
+ * src/shaders/strmv_t.wgsl:44-55) skips a column whose x entry is +-0, so
+ * 0 * Inf / NaN of that column never happens; the dot form (trans 1, the
+ * row kernel src/shaders/strmv.wgsl:35-47) takes every term. y is written,
+ * never read (only its strided slots). absdot (may be NULL, length n) gets
+ * sum_j |op(T)(i, j) x(j)| over the terms taken. */
+void orc_strmv_ld(int uplo, int trans, int unit, int64_t n, const double *A, int64_t lda,
+                  const double *x, int64_t incx, double *y, int64_t incy, double *absdot) {
+  for (int64_t i = 0; i < n; ++i) {
+    long double s = 0, a = 0;
+    for (int64_t j = 0; j < n; ++j) {
+      /* element (r, c) of T read for op(T)(i, j) */
+      int64_t r = trans ? j : i, c = trans ? i : j;
+      int stored = uplo == 1 ? r >= c : r <= c;
+      if (!stored) continue;
+      double xj = x[j * incx];
+      if (!trans && xj == 0.0) continue;
+      long double t = (unit && r == c ? 1.0L : (long double)A[r + c * lda]) * (long double)xj;
+      s += t;
+      a += fabsl(t);
+    }
+    y[i * incy] = (double)s;
+    if (absdot) absdot[i] = (double)a;
+  }
+}

@@ -48,6 +48,7 @@ _SIG = {
     "orc_sgemv_ld": (None, [C.c_int, _i64, _i64, C.c_double, _f64p, _i64, _f64p, _i64, C.c_double,
                             _f64p, _i64, _f64p]),
     "orc_sger_ld": (None, [_i64, _i64, C.c_double, _f64p, _i64, _f64p, _i64, _f64p, _i64]),
+    "orc_strmv_ld": (None, [C.c_int, C.c_int, C.c_int, _i64, _f64p, _i64, _f64p, _i64, _f64p, _i64, _f64p]),
     "orc_ssymv_ld": (None, [C.c_int, _i64, C.c_double, _f64p, _i64, _f64p, _i64, C.c_double, _f64p,
                             _i64, _f64p]),
     "orc_ssyr2_ld": (None, [C.c_int, _i64, C.c_double, _f64p, _i64, _f64p, _i64, C.c_int, _f64p, _i64]),
@@ -270,6 +271,20 @@ def ssymv_ld(uplo, n, alpha, A, lda, x, incx, beta, y, incy):
     out = np.array(y, dtype=np.float64, copy=True)
     ad = np.zeros(max(n, 1))
     lib().orc_ssymv_ld(uplo, n, alpha, Ap, lda, xp, incx, beta, out.ctypes.data_as(_f64p), incy,
+                       ad.ctypes.data_as(_f64p))
+    return out, ad
+
+
+def strmv_ld(uplo, trans, unit, n, A, lda, x, incx, y, incy):
+    """Returns (y_out, absdot): y_out the whole y buffer with op(T) x written
+    to its strided slots (long double; T the uplo triangle of the
+    column-major A, unit diagonal taken as 1, trans 0's column form skipping
+    zero x entries), absdot per output element."""
+    A, Ap = _f64(A if A is not None and len(A) else np.zeros(1))
+    x, xp = _f64(x if x is not None and len(x) else np.zeros(1))
+    out = np.array(y if len(y) else np.zeros(1), dtype=np.float64, copy=True)
+    ad = np.zeros(max(n, 1))
+    lib().orc_strmv_ld(uplo, trans, unit, n, Ap, lda, xp, incx, out.ctypes.data_as(_f64p), incy,
                        ad.ctypes.data_as(_f64p))
     return out, ad
 

@@ -493,6 +493,29 @@ async function main() {
     }, (a) => wg[r](a.device, a.uplo, a.n, a.alpha, a.A, a.lda, a.x, a.incx, a.beta, a.y, a.incy, a.layout),
     device);
   }
+  // strmv / dtrmv: wgblas's tests/strmv/src/test.strmv.js composition
+  // (dtrmv with the 64-bit specs)
+  for (const [r, f64] of [["strmv", false], ["dtrmv", true]]) {
+    const v = (name) => loadParam(f64 ? name + "64" : name);
+    register(r, {
+      device: loadParam("device"),
+      uplo: loadParam("uplo"),
+      trans: loadParam("trans"),
+      diag: loadParam("diag"),
+      n: Object.assign({}, nS, {
+        edge: nS.edge.filter((e) => e.value !== -1),
+        invalid: nS.invalid.concat([{ value: -1, error: "n must be non-negative", label: "negative" }]),
+      }),
+      A: Object.assign({}, v("A"), { dependsOn: ["n", "lda"] }),
+      lda: loadParam("lda"),
+      x: Object.assign({}, v("x"), { dependsOn: ["n", "incx"] }),
+      incx: loadParam("incx"),
+      y: Object.assign({}, v("y"), { dependsOn: ["n", "incy"] }),
+      incy: loadParam("incy"),
+      layout: loadParam("layout"),
+    }, (a) => wg[r](a.device, a.uplo, a.trans, a.diag, a.n, a.A, a.lda, a.x, a.incx, a.y, a.incy, a.layout),
+    device);
+  }
   register("sdot", {
     device: loadParam("device"), n: loadParam("n"), incx: loadParam("incx"), incy: loadParam("incy"),
     x: loadParam("x"), y: loadParam("y"),

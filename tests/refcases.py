@@ -328,3 +328,37 @@ def numpy_gemv(trans, m, n, alpha, A, lda, x, incx, beta, y, incy):
     yin = out[idx]
     out[idx] = alpha * prod + (beta * yin if beta != 0 else 0.0)
     return out
+
+
+def trmv_call(case, dtype=np.float32):
+    """Column-major (uplo, trans, diag, n, A, lda, x, incx, y, incy) for
+    strmv / dtrmv: a row-major A read column-major is A^T, so uplo and trans
+    both flip (src/strmv/strmv.mjs:97-103). y is output only; it is sized
+    from n and incy where the case holds none."""
+    uplo, trans = UPLO[case["uplo"]], TRANS[case["trans"]]
+    if case.get("layout", "row-major") != "column-major":
+        uplo, trans = flip_uplo(uplo), 1 - trans
+    A, x = (np.array(case[k], dtype) for k in ("A", "x"))
+    n, incy = case["n"], case["incy"]
+    y = np.array(case["y"], dtype) if "y" in case else np.zeros(max(n - 1, 0) * incy + 1, dtype)
+    return (uplo, trans, DIAG[case["diag"]], n, A, case["lda"], x, case["incx"], y, incy)
+
+
+def numpy_trmv(uplo, trans, diag, n, A, lda, x, incx, y, incy):
+    """Column-major strmv by numpy (float64): op(T) x into y's strided slots,
+    T the uplo triangle of A (unit diagonal 1); the no-transpose column form
+    drops the columns where x is zero."""
+    out = np.array(y, np.float64, copy=True)
+    if n == 0:
+        return out
+    Ad = dense_op(A, n, n, lda, 0)
+    T = np.tril(Ad) if uplo == 1 else np.triu(Ad)
+    if diag == 1:
+        np.fill_diagonal(T, 1.0)
+    xv = np.asarray(x, np.float64)[np.arange(n) * incx]
+    if trans == 0:
+        keep = xv != 0
+        out[np.arange(n) * incy] = T[:, keep] @ xv[keep]
+    else:
+        out[np.arange(n) * incy] = T.T @ xv
+    return out

@@ -504,7 +504,11 @@ constexpr int kSymvGroups = 1;                         // 1024-row groups per bl
 constexpr int kSymvRows = kSymvGroups * 4 * kThreads;  // rows per block
 constexpr int kSymvPanel = 128;                        // columns per block
 constexpr int kSymvStep = 8;                           // columns per step
-template <typename T, bool VEC, int UPLO>
+// MODE 0: symv (row and mirror sums); 1: strmv without transpose (row sums
+// over the triangle, diagonal included, a column skipped where x is zero);
+// 2: strmv transposed (column sums over the triangle, diagonal included, no
+// skipping). UNIT: the diagonal taken as 1, its stored value never used.
+template <typename T, bool VEC, int UPLO, int MODE = 0, bool UNIT = false>
 __global__ __launch_bounds__(kThreads) void symv_kernel(int64_t n, const T *__restrict__ A, int64_t lda,
                                                         const T *__restrict__ x, int64_t incx,
                                                         T *__restrict__ rowpart,
@@ -587,11 +591,21 @@ __global__ __launch_bounds__(kThreads) void symv_kernel(int64_t n, const T *__re
               in = in && (UPLO == 1 ? i >= jc : i <= jc);
               mirror = in && i != jc;
             }
-            racc[g][q] = in ? fma(a[c][g][q], xc[c], racc[g][q]) : racc[g][q];
-            cacc[c] = mirror ? fma(a[c][g][q], xv[g][q], cacc[c]) : cacc[c];
+            T av = a[c][g][q];
+            if constexpr (UNIT && CROSS) av = i == jc ? (T)1 : av;  // only a crossing block holds the diagonal
+            if constexpr (MODE == 0) {
+              racc[g][q] = in ? fma(av, xc[c], racc[g][q]) : racc[g][q];
+              cacc[c] = mirror ? fma(av, xv[g][q], cacc[c]) : cacc[c];
+            } else if constexpr (MODE == 1) {
+              // reference BLAS's column form: a zero x entry skips its column
+              racc[g][q] = in && xc[c] != (T)0 ? fma(av, xc[c], racc[g][q]) : racc[g][q];
+            } else {
+              cacc[c] = in ? fma(av, xv[g][q], cacc[c]) : cacc[c];
+            }
           }
         }
       }
+      if constexpr (MODE == 1) continue;  // row sums only
       // the step's column sums across the wave
 #pragma unroll
       for (int c = 0; c < S; ++c) {
@@ -612,9 +626,12 @@ __global__ __launch_bounds__(kThreads) void symv_kernel(int64_t n, const T *__re
     steps(std::true_type{}, std::true_type{});
   else
     steps(std::false_type{}, std::true_type{});
+  if (MODE != 2) {
 #pragma unroll
-  for (int g = 0; g < G; ++g)
-    for (int q = 0; q < rows[g]; ++q) rowpart[(int64_t)blockIdx.y * n + i0[g] + q] = racc[g][q];
+    for (int g = 0; g < G; ++g)
+      for (int q = 0; q < rows[g]; ++q) rowpart[(int64_t)blockIdx.y * n + i0[g] + q] = racc[g][q];
+  }
+  if (MODE == 1) return;  // uniform, after the last use of red
   __syncthreads();
   if (threadIdx.x < cend - c0) {
     const int st = threadIdx.x / S, c = threadIdx.x % S;
@@ -628,7 +645,7 @@ __global__ __launch_bounds__(kThreads) void symv_kernel(int64_t n, const T *__re
 // slots symv_kernel wrote for j, lower (UPLO 1): panels 0 .. j/128, chunks
 // from the one holding row 128 (j/128) on; upper: panels j/128 .. P-1, chunks
 // up to the one holding row 128 (j/128) + 127. beta == 0 never reads y.
-template <typename T, int UPLO>
+template <typename T, int UPLO, int MODE = 0>
 __global__ __launch_bounds__(kThreads) void symv_fold_kernel(int64_t n, const T *__restrict__ rowpart,
                                                              const T *__restrict__ colpart, T alpha,
                                                              T beta, T *__restrict__ y, int64_t incy) {
@@ -640,16 +657,19 @@ __global__ __launch_bounds__(kThreads) void symv_fold_kernel(int64_t n, const T 
   const int64_t ra = UPLO == 1 ? (pj * kSymvPanel) / kSymvRows : 0;
   const int64_t rb = UPLO == 1 ? nr : (pj * kSymvPanel + kSymvPanel - 1) / kSymvRows + 1;
   T s = (T)0;
-  int64_t p = p0;
-  for (; p + 8 <= p1; p += 8) {
-    T v[8];
+  if (MODE != 2) {  // row sums (symv, strmv without transpose)
+    int64_t p = p0;
+    for (; p + 8 <= p1; p += 8) {
+      T v[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = rowpart[(p + u) * n + j];
+      for (int u = 0; u < 8; ++u) v[u] = rowpart[(p + u) * n + j];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) s += v[u];
+      for (int u = 0; u < 8; ++u) s += v[u];
+    }
+    for (; p < p1; ++p) s += rowpart[p * n + j];
   }
-  for (; p < p1; ++p) s += rowpart[p * n + j];
-  for (int64_t r = ra; r < (rb < nr ? rb : nr); ++r) s += colpart[r * n + j];
+  if (MODE != 1)  // column sums (symv's mirrors, strmv transposed)
+    for (int64_t r = ra; r < (rb < nr ? rb : nr); ++r) s += colpart[r * n + j];
   T v = alpha * s;
   if (beta != (T)0) v = fma(beta, y[j * incy], v);
   y[j * incy] = v;
@@ -704,6 +724,79 @@ int symv(wgb_ctx *ctx, int uplo, int64_t n, T alpha, const T *A, int64_t lda, co
   else
     symv_fold_kernel<T, 2><<<(unsigned)cdiv(n, kThreads), kThreads, 0, ctx->stream>>>(
         n, rowpart, colpart, alpha, beta, y, incy);
+  WGB_CHECK_LAUNCH("symv_fold_kernel");
+  wgb::timing_end(ctx);
+  return WGB_OK;
+}
+
+// strmv / dtrmv: y <- op(T) x, T the n x n triangle (uplo) of A, unit
+// diagonal taken as 1 where diag is WGB_UNIT; on symv_kernel's row sums
+// (no transpose, with the column form's zero skip) or column sums
+// (transpose), folded as symv's. x and y must not overlap.
+template <typename T>
+int trmv(wgb_ctx *ctx, int uplo, int trans, int diag, int64_t n, const T *A, int64_t lda, const T *x,
+         int64_t incx, T *y, int64_t incy) {
+  int st = wgb::enter(ctx);
+  if (st) return st;
+  if (uplo != WGB_LOWER && uplo != WGB_UPPER)
+    return fail(WGB_ERR_INVALID_VALUE, "uplo must be WGB_LOWER or WGB_UPPER");
+  if (trans != WGB_NO_TRANS && trans != WGB_TRANS)
+    return fail(WGB_ERR_INVALID_VALUE, "trans must be WGB_NO_TRANS or WGB_TRANS");
+  if (diag != WGB_NON_UNIT && diag != WGB_UNIT)
+    return fail(WGB_ERR_INVALID_VALUE, "diag must be WGB_NON_UNIT or WGB_UNIT");
+  if (n < 0) return fail(WGB_ERR_INVALID_VALUE, "n must be non-negative");
+  if (lda < imax(1, n)) return fail(WGB_ERR_INVALID_VALUE, "lda must be >= max(1, n)");
+  if (incx <= 0 || incy <= 0) return fail(WGB_ERR_INVALID_VALUE, "incx and incy must be positive");
+  if (n == 0) return WGB_OK;
+  if (!A || !x || !y) return fail(WGB_ERR_INVALID_VALUE, "A, x or y is null");
+  const int64_t nr = cdiv(n, kSymvRows), np = cdiv(n, kSymvPanel);
+  if (np > 65535) return fail(WGB_ERR_INVALID_VALUE, "n too large for one launch");
+  if ((st = wgb::ensure_op_workspace(ctx, (size_t)((np + nr) * n) * sizeof(T)))) return st;
+  T *rowpart = static_cast<T *>(ctx->op_ws);
+  T *colpart = rowpart + np * n;
+  wgb::timing_begin(ctx);
+  const dim3 grid((unsigned)nr, (unsigned)np);
+  const bool vec = lda % 4 == 0 && aligned4(A);
+  const bool lower = uplo == WGB_LOWER, nt = trans == WGB_NO_TRANS, unit = diag == WGB_UNIT;
+  auto launch = [&](auto kern) {
+    kern<<<grid, kThreads, 0, ctx->stream>>>(n, A, lda, x, incx, rowpart, colpart);
+  };
+  // one instantiation per (vector loads, uplo, form, unit)
+  auto pick = [&](auto vec_tag, auto lower_tag, auto mode_tag, auto unit_tag) {
+    launch(symv_kernel<T, decltype(vec_tag)::value, decltype(lower_tag)::value ? 1 : 2,
+                       decltype(mode_tag)::value, decltype(unit_tag)::value>);
+  };
+  auto by_unit = [&](auto v, auto l, auto m) {
+    if (unit)
+      pick(v, l, m, std::true_type{});
+    else
+      pick(v, l, m, std::false_type{});
+  };
+  auto by_mode = [&](auto v, auto l) {
+    if (nt)
+      by_unit(v, l, std::integral_constant<int, 1>{});
+    else
+      by_unit(v, l, std::integral_constant<int, 2>{});
+  };
+  auto by_lower = [&](auto v) {
+    if (lower)
+      by_mode(v, std::true_type{});
+    else
+      by_mode(v, std::false_type{});
+  };
+  if (vec)
+    by_lower(std::true_type{});
+  else
+    by_lower(std::false_type{});
+  WGB_CHECK_LAUNCH("symv_kernel");
+  auto fold = [&](auto kern) {
+    kern<<<(unsigned)cdiv(n, kThreads), kThreads, 0, ctx->stream>>>(n, rowpart, colpart, (T)1, (T)0, y,
+                                                                    incy);
+  };
+  if (lower)
+    fold(nt ? symv_fold_kernel<T, 1, 1> : symv_fold_kernel<T, 1, 2>);
+  else
+    fold(nt ? symv_fold_kernel<T, 2, 1> : symv_fold_kernel<T, 2, 2>);
   WGB_CHECK_LAUNCH("symv_fold_kernel");
   wgb::timing_end(ctx);
   return WGB_OK;
@@ -861,6 +954,16 @@ extern "C" int wgb_dsymv(wgb_ctx *ctx, int uplo, int64_t n, double alpha, const 
                          int64_t lda, const double *x, int64_t incx, double beta, double *y,
                          int64_t incy) {
   return symv<double>(ctx, uplo, n, alpha, A, lda, x, incx, beta, y, incy);
+}
+
+extern "C" int wgb_strmv(wgb_ctx *ctx, int uplo, int trans, int diag, int64_t n, const float *A,
+                         int64_t lda, const float *x, int64_t incx, float *y, int64_t incy) {
+  return trmv<float>(ctx, uplo, trans, diag, n, A, lda, x, incx, y, incy);
+}
+
+extern "C" int wgb_dtrmv(wgb_ctx *ctx, int uplo, int trans, int diag, int64_t n, const double *A,
+                         int64_t lda, const double *x, int64_t incx, double *y, int64_t incy) {
+  return trmv<double>(ctx, uplo, trans, diag, n, A, lda, x, incx, y, incy);
 }
 
 extern "C" int wgb_dgemv(wgb_ctx *ctx, int trans, int64_t m, int64_t n, double alpha,

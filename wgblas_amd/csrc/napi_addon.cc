@@ -531,6 +531,32 @@ napi_value Symv(napi_env env, napi_callback_info info) {
   return nullptr;
 }
 
+// trmv(ctx, uplo, trans, diag, n, A, lda, x, incx, y, incy, f64): strmv, or
+// dtrmv when f64 is true
+napi_value Trmv(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 12)) return nullptr;
+  wgb_ctx *ctx = ctx_of(env, a.v[0]);
+  if (!ctx) return nullptr;
+  int uplo, trans, diag;
+  int64_t n, lda, incx, incy;
+  void *A, *x, *y;
+  bool f64 = false;
+  if (!get_i32(env, a.v[1], &uplo) || !get_i32(env, a.v[2], &trans) || !get_i32(env, a.v[3], &diag) ||
+      !get_i64(env, a.v[4], &n) || !get_ptr(env, a.v[5], &A) || !get_i64(env, a.v[6], &lda) ||
+      !get_ptr(env, a.v[7], &x) || !get_i64(env, a.v[8], &incx) || !get_ptr(env, a.v[9], &y) ||
+      !get_i64(env, a.v[10], &incy) || napi_get_value_bool(env, a.v[11], &f64) != napi_ok)
+    return nullptr;
+  if (f64) {
+    WGB_OK_OR_THROW(wgb_dtrmv(ctx, uplo, trans, diag, n, (const double *)A, lda, (const double *)x, incx,
+                              (double *)y, incy), "wgb_dtrmv");
+  } else {
+    WGB_OK_OR_THROW(wgb_strmv(ctx, uplo, trans, diag, n, (const float *)A, lda, (const float *)x, incx,
+                              (float *)y, incy), "wgb_strmv");
+  }
+  return nullptr;
+}
+
 // ---- level 1 ---------------------------------------------------------------
 
 // reduce(kind, ctx, n, x, incx[, y, incy]) -> number; kind: 0 sdot, 1 sasum,
@@ -580,7 +606,7 @@ napi_value ModuleInit(napi_env env, napi_value exports) {
       {"synchronize", Synchronize}, {"malloc", Malloc}, {"free", Free},
       {"upload", Upload}, {"download", Download}, {"gemm", Gemm},
       {"ssyrk", Ssyrk}, {"ssyr2k", Ssyr2k}, {"ssymm", Ssymm},
-      {"tri", Tri}, {"sgemv", Sgemv}, {"ger", Ger}, {"syr", Syr}, {"symv", Symv}, {"reduce", Reduce},
+      {"tri", Tri}, {"sgemv", Sgemv}, {"ger", Ger}, {"syr", Syr}, {"symv", Symv}, {"trmv", Trmv}, {"reduce", Reduce},
   };
   for (const Fn &f : fns) {
     napi_value v;

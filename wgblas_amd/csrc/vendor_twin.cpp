@@ -355,6 +355,29 @@ void run_gemv(Twin &w) {
          "GB/s");
     w.release();
   }
+  // strmv / dtrmv (lower, both forms; rocBLAS's is in place, x <- op(T) x,
+  // the same bytes): the triangle read once, x read and written
+  for (int t = 0; t < 2; ++t) {
+    const rocblas_operation op = t ? rocblas_operation_transpose : rocblas_operation_none;
+    {
+      float *A = w.f32((int64_t)n * n, 21), *x = w.f32(n, 22);
+      const double ms = w.median_ms(
+          [&] { RB_OK(rocblas_strmv(w.h, rocblas_fill_lower, op, rocblas_diagonal_non_unit, n, A, n, x, 1)); },
+          5, 20);
+      emit(t ? "strmv_T_16384" : "strmv_N_16384", "lower 16384, triangle read once", ms,
+           4.0 * ((double)n * (n + 1) / 2 + 2.0 * n), "GB/s");
+      w.release();
+    }
+    {
+      double *A = w.f64((int64_t)n * n, 21), *x = w.f64(n, 22);
+      const double ms = w.median_ms(
+          [&] { RB_OK(rocblas_dtrmv(w.h, rocblas_fill_lower, op, rocblas_diagonal_non_unit, n, A, n, x, 1)); },
+          5, 20);
+      emit(t ? "dtrmv_T_16384" : "dtrmv_N_16384", "lower 16384, triangle read once", ms,
+           8.0 * ((double)n * (n + 1) / 2 + 2.0 * n), "GB/s");
+      w.release();
+    }
+  }
 }
 
 void run_level1(Twin &w) {

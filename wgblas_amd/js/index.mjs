@@ -29,6 +29,8 @@ export { ssyr2 } from "./src/ssyr2.mjs";
 export { dsyr2 } from "./src/dsyr2.mjs";
 export { ssymv } from "./src/ssymv.mjs";
 export { dsymv } from "./src/dsymv.mjs";
+export { strmv } from "./src/strmv.mjs";
+export { dtrmv } from "./src/dtrmv.mjs";
 export { sdot } from "./src/sdot.mjs";
 export { sasum } from "./src/sasum.mjs";
 export { snrm2 } from "./src/snrm2.mjs";

@@ -78,6 +78,8 @@ _SIGNATURES = {
     "wgb_dsyr": [_ptr, C.c_int, _i64, C.c_double, _ptr, _i64, _ptr, _i64],
     "wgb_ssyr2": [_ptr, C.c_int, _i64, C.c_float, _ptr, _i64, _ptr, _i64, _ptr, _i64],
     "wgb_dsyr2": [_ptr, C.c_int, _i64, C.c_double, _ptr, _i64, _ptr, _i64, _ptr, _i64],
+    "wgb_strmv": [_ptr, C.c_int, C.c_int, C.c_int, _i64, _ptr, _i64, _ptr, _i64, _ptr, _i64],
+    "wgb_dtrmv": [_ptr, C.c_int, C.c_int, C.c_int, _i64, _ptr, _i64, _ptr, _i64, _ptr, _i64],
     "wgb_ssymv": [_ptr, C.c_int, _i64, C.c_float, _ptr, _i64, _ptr, _i64, C.c_float, _ptr, _i64],
     "wgb_dsymv": [_ptr, C.c_int, _i64, C.c_double, _ptr, _i64, _ptr, _i64, C.c_double, _ptr, _i64],
     "wgb_dgemv": [_ptr, C.c_int, _i64, _i64, C.c_double, _ptr, _i64, _ptr, _i64, C.c_double, _ptr,
@@ -358,6 +360,14 @@ class Context:
     def dsymv(self, uplo, n, alpha, A, lda, x, incx, beta, y, incy):
         _check(self.lib.wgb_dsymv(self.handle, uplo, n, alpha, _p(A), lda, _p(x), incx, beta, _p(y), incy),
                "wgb_dsymv")
+
+    def strmv(self, uplo, trans, diag, n, A, lda, x, incx, y, incy):
+        _check(self.lib.wgb_strmv(self.handle, uplo, trans, diag, n, _p(A), lda, _p(x), incx, _p(y), incy),
+               "wgb_strmv")
+
+    def dtrmv(self, uplo, trans, diag, n, A, lda, x, incx, y, incy):
+        _check(self.lib.wgb_dtrmv(self.handle, uplo, trans, diag, n, _p(A), lda, _p(x), incx, _p(y), incy),
+               "wgb_dtrmv")
 
     def dgemv(self, trans, m, n, alpha, A, lda, x, incx, beta, y, incy):
         _check(self.lib.wgb_dgemv(self.handle, trans, m, n, alpha, _p(A), lda, _p(x), incx, beta,

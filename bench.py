@@ -690,6 +690,8 @@ def reference_cpu_adapter_probe():
     info["runnable"] = not missing
     if missing:
         info["reason"] = "missing " + ", ".join(missing) + "; nothing can be installed (no network)"
+    if not info["vulkan_icds"]:
+        del info["vulkan_icds"]  # keeps the line's end short; `reason` names what is missing
     return info
 
 
@@ -801,9 +803,46 @@ def main():
         line["roof_probe"] = roofs
     if rank == 0 and not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline()
+    if comps:
+        line["summary"] = summary(line)
     if rank == 0:
         print(json.dumps(line))
     return 0
+
+
+def summary(line):
+    """Every BASELINE configuration's figure in a few hundred bytes, the last
+    key of the line (a reader that keeps only the end of the output still
+    sees all of them): c1 sgemm 512^3 (us per call), c2 the reductions at
+    2^28 (GB/s) and their incx = 3 forms at 2^26 (GB/s of span), c3 the
+    8192^3 layouts and the ragged 8191x8193x4097 layouts (TFLOP/s), c4 dgemm
+    4096^3 per layout (TFLOP/s), c5 ssyrk / sgemmtr 8192 k 4096 (TFLOP/s),
+    and the level-3 callers as fractions of their peak."""
+    c = line["components"]
+    r1 = lambda x: round(x, 1)
+    flops = 2.0 * 8192 ** 3
+    s = {"c1_sgemm512_us": r1(c["sgemm_512"]["ms"] * 1e3)}
+    red = ("sdot", "sasum", "snrm2", "isamax")
+    s["c2_GBps"] = {r: round(c[f"{r}_2^28"]["GB/s"]) for r in red}
+    s["c2_inc3_span_GBps"] = {r: round(c[f"{r}_2^26_incx3"]["GB/s_span"]) for r in red}
+    c3 = {"mean": r1(line["value"])}
+    c3.update({lay: r1(flops / ms / 1e9) for lay, ms in line["sgemm_launch_ms"].items()})
+    s["c3_TF"] = c3
+    s["c3_ragged_TF"] = {lay: r1(v["tflops"])
+                         for lay, v in c["sgemm_ragged_8191x8193x4097"]["per_layout"].items()}
+    s["c4_dgemm_TF"] = {lay: r1(v["tflops"]) for lay, v in c["dgemm_4096"]["per_layout"].items()}
+    s["c5_TF"] = {"ssyrk": r1(c["ssyrk_8192x4096_x10"]["tflops"]),
+                  "sgemmtr": r1(c["sgemmtr_8192x4096_x10"]["tflops"])}
+    fr = {}
+    for key, name in (("ssyr2k_8192x4096", "ssyr2k"), ("ssymm_8192", "ssymm"), ("strmm_8192", "strmm"),
+                      ("strsm_4096", "strsm4k"), ("strsm_8192", "strsm8k"), ("dsyr2k_4096", "dsyr2k"),
+                      ("dsymm_4096", "dsymm"), ("dtrmm_4096", "dtrmm")):
+        if key in c:
+            v = c[key]
+            fr[name] = round(v.get("frac_fp32_peak", v.get("frac_fp64_peak", 0.0)), 3)
+    s["l3_frac_of_peak"] = fr
+    s["headline_frac"] = round(line["roofline"]["frac"], 3)
+    return s
 
 
 if __name__ == "__main__":

@@ -28,6 +28,12 @@
 extern "C" {
 #endif
 
+/* Version of this interface: raised whenever an entry point's signature or
+ * meaning changes (3: wgb_ssyr2k takes a trans flag per operand and
+ * wgb_ssymm / wgb_dsymm one for B). A caller compares wgb_abi_version()
+ * with the WGB_ABI_VERSION it was built against before its first call. */
+#define WGB_ABI_VERSION 3
+
 typedef enum wgb_status {
   WGB_OK = 0,
   WGB_ERR_INVALID_VALUE = -1, /* bad argument (see wgb_last_error) */
@@ -48,6 +54,11 @@ enum { WGB_LEFT = 1, WGB_RIGHT = 2 };
 enum { WGB_NON_UNIT = 0, WGB_UNIT = 1 };
 
 typedef struct wgb_ctx wgb_ctx;
+
+/* WGB_ABI_VERSION of the built library (no device work; callable before
+ * wgb_init). No counterpart in the reference, whose JavaScript API has no
+ * compiled boundary to version. */
+int wgb_abi_version(void);
 
 /* ---- device / context ---------------------------------------------------- */
 
@@ -136,6 +147,10 @@ int wgb_sgemm(wgb_ctx *ctx, int transA, int transB, int64_t m, int64_t n,
  * same bits on the same inputs), with its split-k workspace taken from a
  * fixed 32 MiB device array of the library instead of a buffer grown with
  * hipMalloc; the call makes no hipMalloc, hipFree or other allocation.
+ * The first call on each device (not under graph capture) looks the array
+ * up, which makes the HIP runtime load its code object and place the array
+ * on that device: that one-time load is the only device memory the entry
+ * point ever causes to be reserved; every later call allocates nothing.
  * No counterpart in the reference: it is for callers that cannot allocate
  * (code under HIP graph capture, tight serving loops, harnesses that forbid
  * allocation). Each GPU holds one copy of the array until the process ends,

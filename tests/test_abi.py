@@ -28,6 +28,14 @@ def test_header_declares_the_path():
         assert required in names
 
 
+def test_abi_version_matches_the_header_and_the_binding():
+    text = open(HEADER).read()
+    version = int(re.search(r"#define WGB_ABI_VERSION (\d+)", text).group(1))
+    assert native.library().wgb_abi_version() == version == native.ABI_VERSION
+    addon = open(os.path.join(ROOT, "wgblas_amd", "csrc", "napi_addon.cc")).read()
+    assert "wgb_abi_version() != WGB_ABI_VERSION" in addon
+
+
 def test_library_exports_every_declared_symbol():
     lib = native.library()
     out = subprocess.run(["nm", "-D", "--defined-only", native.LIB_PATH], capture_output=True,

@@ -1,7 +1,8 @@
 """Runs the JavaScript-layer suites (tests/js/*.mjs) with node.
 
-CPU: the reference's validation specs (invalid cases) against the JS API and
-the seeded generators against the reference's golden vectors.
+CPU: the reference's validation specs (invalid cases) against the JS API, the
+seeded generators against the reference's golden vectors, and the package's
+subpath exports with their TypeScript declarations.
 GPU: the validation edge cases (valid calls must run) and the end-to-end
 API suite through the Node-API addon and libwgblas_hip.
 """
@@ -33,6 +34,11 @@ def test_js_validation_specs():
 
 def test_js_random_matches_reference_golden():
     run_node("random.mjs")
+
+
+def test_js_package_subpaths_resolve_with_declarations():
+    out = run_node("package_exports.mjs")
+    assert int(out.strip().splitlines()[-1].split()[0]) > 30
 
 
 @pytest.mark.gpu

@@ -16,8 +16,12 @@ Each case is two calls in a row on the one array, the second with a smaller
 input, so the second call runs over whatever the first left in the array.
 Every result is also checked on sampled columns against a float64 product
 under the reference's forward-error bound (tests/sgemm/helpers.js:1-57), and
-C's ld padding is bit-checked.
+C's ld padding is bit-checked. On a fresh context, repeated split-k calls
+leave the device's free memory (hipMemGetInfo) unchanged, while wgb_sgemm's
+first split-k call on that context lowers it by its workspace.
 """
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -114,6 +118,56 @@ def test_noalloc_paths_without_split(ctx):
     print("noalloc case small kernel 300x200x100 and alpha = 0", flush=True)
     _run_pair(ctx, 0, 0, 300, 200, 100, 1.25, -0.5, 301, 35)
     _run_pair(ctx, 1, 1, 256, 128, 64, 0.0, 2.0, 256, 36)
+
+
+def _free_device_bytes():
+    """hipMemGetInfo's free bytes on the current device (device 0)."""
+    hip = ctypes.CDLL("libamdhip64.so")
+    free, total = ctypes.c_size_t(), ctypes.c_size_t()
+    assert hip.hipMemGetInfo(ctypes.byref(free), ctypes.byref(total)) == 0
+    return free.value
+
+
+def test_noalloc_allocates_nothing_on_a_fresh_context():
+    """The entry point called first on a new context (no wgb_sgemm before
+    it, so no context workspace exists): once its array is loaded (the
+    first call on the device), further split-k calls of two shapes change
+    the device's free memory by nothing; wgb_sgemm's first split-k call on
+    the same context then lowers it by its hipMalloc'd workspace, which
+    shows the measure sees allocations of that size."""
+    from wgblas_amd import Context
+
+    print("noalloc case fresh context, free-memory check", flush=True)
+    c = Context(0)
+    bufs = []
+    try:
+        shapes = [(3072, 4096, 1024, 40), (2944, 2944, 2048, 41)]
+        ops = []
+        for (m, n, k, seed) in shapes:
+            A, lda, B, ldb, C0 = _make(c, 0, 1, m, n, k, m, seed)
+            bufs += [A, B, C0]
+            ops.append((m, n, k, A, lda, B, ldb, C0))
+        call = lambda op: c.sgemm_noalloc(0, 1, op[0], op[1], op[2], 1.0, op[3], op[4], op[5], op[6], 0.5,
+                                          op[7], op[0])
+        call(ops[0])  # loads the array on this device if no call has yet
+        c.synchronize()
+        before = _free_device_bytes()
+        for _ in range(3):
+            for op in ops:
+                call(op)
+        c.synchronize()
+        after = _free_device_bytes()
+        assert after == before, f"free device memory moved by {before - after} bytes across noalloc calls"
+        m, n, k, A, lda, B, ldb, C0 = ops[0]
+        c.sgemm(0, 1, m, n, k, 1.0, A, lda, B, ldb, 0.5, C0, m)
+        c.synchronize()
+        grown = _free_device_bytes()
+        assert before - grown >= 16 << 20, \
+            f"wgb_sgemm's workspace did not show in hipMemGetInfo ({before - grown} bytes)"
+    finally:
+        for x in bufs:
+            x.free()
+        c.close()
 
 
 def test_noalloc_rejects_bad_arguments(ctx):

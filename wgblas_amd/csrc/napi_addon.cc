@@ -8,6 +8,7 @@
 
 #include <cstdint>
 #include <cstring>
+#include <set>
 #include <string>
 
 #include "wgblas_hip.h"
@@ -134,6 +135,23 @@ wgb_ctx *ctx_of(napi_env env, napi_value v) {
 
 // ---- device ----------------------------------------------------------------
 
+// Contexts created through this addon and not yet destroyed. The JavaScript
+// layer releases them in cleanup(); any still open when the Node environment
+// is torn down (a program that never called cleanup()) are destroyed by the
+// environment's cleanup hook, which Node runs before the process's exit
+// handlers, so no stream, event or buffer of the library is left for the
+// HIP runtime's own exit-time teardown.
+std::set<wgb_ctx *> &live_contexts() {
+  static std::set<wgb_ctx *> live;
+  return live;
+}
+
+void destroy_live_contexts(void *) {
+  std::set<wgb_ctx *> &live = live_contexts();
+  for (wgb_ctx *ctx : live) (void)wgb_destroy(ctx);
+  live.clear();
+}
+
 napi_value DeviceCount(napi_env env, napi_callback_info) {
   int c = 0;
   WGB_OK_OR_THROW(wgb_device_count(&c), "wgb_device_count");
@@ -147,6 +165,7 @@ napi_value Init(napi_env env, napi_callback_info info) {
   if (!get_i32(env, a.v[0], &dev)) return nullptr;
   wgb_ctx *ctx = nullptr;
   WGB_OK_OR_THROW(wgb_init(dev, &ctx), "wgb_init");
+  live_contexts().insert(ctx);
   return make_external(env, ctx);
 }
 
@@ -155,6 +174,9 @@ napi_value Destroy(napi_env env, napi_callback_info info) {
   if (!get_args(env, info, a, 1)) return nullptr;
   void *p;
   if (!get_ptr(env, a.v[0], &p)) return nullptr;
+  // Only contexts this addon created and has not destroyed yet: a second
+  // destroy of the same handle is a no-op instead of a double free.
+  if (live_contexts().erase((wgb_ctx *)p) == 0) return nullptr;
   WGB_OK_OR_THROW(wgb_destroy((wgb_ctx *)p), "wgb_destroy");
   return nullptr;
 }
@@ -597,6 +619,13 @@ napi_value Reduce(napi_env env, napi_callback_info info) {
 }
 
 napi_value ModuleInit(napi_env env, napi_value exports) {
+  if (wgb_abi_version() != WGB_ABI_VERSION) {
+    std::string msg = "wgblas_hip addon: libwgblas_hip implements C ABI version " +
+                      std::to_string(wgb_abi_version()) + ", the addon was built for " +
+                      std::to_string(WGB_ABI_VERSION) + " (rebuild with `python -m wgblas_amd.build`)";
+    napi_throw_error(env, nullptr, msg.c_str());
+    return nullptr;
+  }
   struct Fn {
     const char *name;
     napi_callback cb;
@@ -614,6 +643,7 @@ napi_value ModuleInit(napi_env env, napi_value exports) {
         napi_set_named_property(env, exports, f.name, v) != napi_ok)
       return nullptr;
   }
+  if (napi_add_env_cleanup_hook(env, destroy_live_contexts, nullptr) != napi_ok) return nullptr;
   return exports;
 }
 

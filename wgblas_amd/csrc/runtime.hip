@@ -65,6 +65,8 @@ using wgb::fail;
 
 extern "C" const char *wgb_last_error(void) { return wgb::t_last_error.c_str(); }
 
+extern "C" int wgb_abi_version(void) { return WGB_ABI_VERSION; }
+
 extern "C" const char *wgb_status_string(int status) {
   switch (status) {
     case WGB_OK: return "ok";

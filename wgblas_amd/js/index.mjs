@@ -5,7 +5,7 @@
 export { init, cleanup, gpuName, HipDevice } from "./src/init.mjs";
 export { GpuVector } from "./src/classes/GpuVector.mjs";
 export { GpuMatrix } from "./src/classes/GpuMatrix.mjs";
-export { randomFloat32Array, randomFloat64Array } from "./src/random.mjs";
+export { randomFloat32Array, randomFloat64Array, randomTriangularFloat32Array } from "./src/random.mjs";
 export { sgemm } from "./src/sgemm.mjs";
 export { sgemmtr } from "./src/sgemmtr.mjs";
 export { ssyrk } from "./src/ssyrk.mjs";

@@ -23,7 +23,7 @@ export class GpuMatrix {
    * GpuMatrix.from([device,] data, rows, cols, lda?, layout = 'row-major').
    * lda defaults to cols (row-major) or rows (column-major); data must hold
    * at least outer*lda elements. Argument checks and their messages follow
-   * wgblas's (src/classes/GpuMatrix.mjs:149-185).
+   * wgblas's (src/classes/GpuMatrix.mjs:43-79).
    */
   static from(deviceOrData, ...rest) {
     const explicit = deviceOrData instanceof HipDevice;

@@ -1,0 +1,46 @@
+// TypeScript declarations for dgemv (src/dgemv.mjs).
+import { HipDevice } from "./init.mjs";
+import { GpuMatrix } from "./classes/GpuMatrix.mjs";
+import { GpuVector } from "./classes/GpuVector.mjs";
+import type { Layout, Timed, Trans } from "./types.mjs";
+
+/**
+ * y = alpha op(A) x + beta y.
+ * Host arrays: `layout` (default row-major) gives their storage order; the
+ * result comes back as a new Float64Array under `y` (the input is not modified).
+ */
+export declare function dgemv(
+  device: HipDevice,
+  trans: Trans,
+  m: number,
+  n: number,
+  alpha: number,
+  A: Float64Array,
+  lda: number,
+  x: Float64Array,
+  incx: number,
+  beta: number,
+  y: Float64Array,
+  incy: number,
+  layout?: Layout,
+): Promise<{ y: Float64Array } & Timed>;
+
+/**
+ * y = alpha op(A) x + beta y.
+ * Resident operands: each GpuMatrix's own layout applies and `y` is
+ * updated in place on the device.
+ */
+export declare function dgemv(
+  device: HipDevice,
+  trans: Trans,
+  m: number,
+  n: number,
+  alpha: number,
+  A: GpuMatrix,
+  lda: number,
+  x: GpuVector,
+  incx: number,
+  beta: number,
+  y: GpuVector,
+  incy: number,
+): Promise<Timed>;

@@ -3,7 +3,7 @@
 // (wgblas src/dsymm/dsymm.mjs:26-381: symmetrize.wgsl on both halves, then
 // dgemm_small in double-double), on wgb_dsymm. Checks and messages follow
 // dsymm.mjs:46-142.
-import { symm } from "./ssymm.mjs";
+import { symm } from "./impl/symm.mjs";
 
 export async function dsymm(device, side, uplo, m, n, alpha, A, lda, B, ldb, beta, C, ldc,
                             layout = "row-major") {

@@ -1,0 +1,47 @@
+// TypeScript declarations for dsyr2k (src/dsyr2k.mjs).
+import { HipDevice } from "./init.mjs";
+import { GpuMatrix } from "./classes/GpuMatrix.mjs";
+import type { Layout, Timed, Trans, Uplo } from "./types.mjs";
+
+/**
+ * The uplo triangle of C = alpha (op(A) op(B)^T + op(B) op(A)^T) + beta C.
+ * Host arrays: `layout` (default row-major) gives their storage order; the
+ * result comes back as a new Float64Array under `C` (the input is not modified).
+ */
+export declare function dsyr2k(
+  device: HipDevice,
+  uplo: Uplo,
+  trans: Trans,
+  n: number,
+  k: number,
+  alpha: number,
+  A: Float64Array,
+  lda: number,
+  B: Float64Array,
+  ldb: number,
+  beta: number,
+  C: Float64Array,
+  ldc: number,
+  layout?: Layout,
+): Promise<{ C: Float64Array } & Timed>;
+
+/**
+ * The uplo triangle of C = alpha (op(A) op(B)^T + op(B) op(A)^T) + beta C.
+ * Resident operands: each GpuMatrix's own layout applies and `C` is
+ * updated in place on the device.
+ */
+export declare function dsyr2k(
+  device: HipDevice,
+  uplo: Uplo,
+  trans: Trans,
+  n: number,
+  k: number,
+  alpha: number,
+  A: GpuMatrix,
+  lda: number,
+  B: GpuMatrix,
+  ldb: number,
+  beta: number,
+  C: GpuMatrix,
+  ldc: number,
+): Promise<Timed>;

@@ -1,0 +1,45 @@
+// TypeScript declarations for dtrmm (src/dtrmm.mjs).
+import { HipDevice } from "./init.mjs";
+import { GpuMatrix } from "./classes/GpuMatrix.mjs";
+import type { Diag, Layout, Side, Timed, Trans, Uplo } from "./types.mjs";
+
+/**
+ * B = alpha op(A) B (side left) or alpha B op(A) (right), A triangular.
+ * Host arrays: `layout` (default row-major) gives their storage order; the
+ * result comes back as a new Float64Array under `B` (the input is not modified).
+ */
+export declare function dtrmm(
+  device: HipDevice,
+  side: Side,
+  uplo: Uplo,
+  transA: Trans,
+  diag: Diag,
+  m: number,
+  n: number,
+  alpha: number,
+  A: Float64Array,
+  lda: number,
+  B: Float64Array,
+  ldb: number,
+  layout?: Layout,
+): Promise<{ B: Float64Array } & Timed>;
+
+/**
+ * B = alpha op(A) B (side left) or alpha B op(A) (right), A triangular.
+ * Resident operands: each GpuMatrix's own layout applies and `B` is
+ * updated in place on the device.
+ */
+export declare function dtrmm(
+  device: HipDevice,
+  side: Side,
+  uplo: Uplo,
+  transA: Trans,
+  diag: Diag,
+  m: number,
+  n: number,
+  alpha: number,
+  A: GpuMatrix,
+  lda: number,
+  B: GpuMatrix,
+  ldb: number,
+): Promise<Timed>;

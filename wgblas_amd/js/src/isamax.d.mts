@@ -1,0 +1,12 @@
+// TypeScript declarations for isamax (src/isamax.mjs).
+import { HipDevice } from "./init.mjs";
+import { GpuVector } from "./classes/GpuVector.mjs";
+import type { Timed } from "./types.mjs";
+
+/** The 0-based index of the first largest |x_i| (NaN skipped); -1 when n <= 0. The vectors are all host arrays or all GpuVectors. */
+export declare function isamax(
+  device: HipDevice,
+  n: number,
+  x: Float32Array | GpuVector,
+  incx: number,
+): Promise<{ index: number } & Timed>;

@@ -1,0 +1,42 @@
+// TypeScript declarations for sger (src/sger.mjs).
+import { HipDevice } from "./init.mjs";
+import { GpuMatrix } from "./classes/GpuMatrix.mjs";
+import { GpuVector } from "./classes/GpuVector.mjs";
+import type { Layout, Timed } from "./types.mjs";
+
+/**
+ * A = alpha x y^T + A.
+ * Host arrays: `layout` (default row-major) gives their storage order; the
+ * result comes back as a new Float32Array under `A` (the input is not modified).
+ */
+export declare function sger(
+  device: HipDevice,
+  m: number,
+  n: number,
+  alpha: number,
+  x: Float32Array,
+  incx: number,
+  y: Float32Array,
+  incy: number,
+  A: Float32Array,
+  lda: number,
+  layout?: Layout,
+): Promise<{ A: Float32Array } & Timed>;
+
+/**
+ * A = alpha x y^T + A.
+ * Resident operands: each GpuMatrix's own layout applies and `A` is
+ * updated in place on the device.
+ */
+export declare function sger(
+  device: HipDevice,
+  m: number,
+  n: number,
+  alpha: number,
+  x: GpuVector,
+  incx: number,
+  y: GpuVector,
+  incy: number,
+  A: GpuMatrix,
+  lda: number,
+): Promise<Timed>;

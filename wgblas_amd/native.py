@@ -33,6 +33,7 @@ _SIGNATURES = {
     "wgb_synchronize": [_ptr],
     "wgb_stream": [_ptr],
     "wgb_last_error": [],
+    "wgb_abi_version": [],
     "wgb_status_string": [C.c_int],
     "wgb_malloc": [_ptr, C.c_size_t, C.POINTER(_ptr)],
     "wgb_free": [_ptr, _ptr],
@@ -109,6 +110,9 @@ _RESTYPES = {
 
 _lib = None
 
+# WGB_ABI_VERSION of include/wgblas_hip.h that these signatures follow.
+ABI_VERSION = 3
+
 
 class WgblasError(RuntimeError):
     def __init__(self, status, where, message):
@@ -129,6 +133,9 @@ def library():
             fn = getattr(lib, name)
             fn.argtypes = argtypes
             fn.restype = _RESTYPES.get(name, C.c_int)
+        if lib.wgb_abi_version() != ABI_VERSION:
+            raise RuntimeError(f"{LIB_PATH} implements C ABI version {lib.wgb_abi_version()}, this binding "
+                               f"expects {ABI_VERSION}: rebuild with `python -m wgblas_amd.build`")
         _lib = lib
     return _lib
 

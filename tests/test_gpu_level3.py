@@ -461,6 +461,67 @@ def test_strsm_special_path_matches(ctx, side, uplo, trans):
             assert bits_equal(rhs(X, r), rhs(Xs, r)), r
 
 
+def _blocks_of_condition(order, lda, seed, weak, scale):
+    """Column-major A (lda x order): off-diagonals in [-1/order, 1/order),
+    diagonal 2, except that every 256-order diagonal block listed in `weak`
+    holds off-diagonals in [-scale, scale) and a unit diagonal. With scale
+    0.1 such a block's condition number ||M||_1 ||M^-1||_1 is about 260, far
+    above what the inverse path accepts (16), with every entry of its inverse
+    still of order 1; with 0.02 it is about 14, just below."""
+    A = orc.random_f32(lda * order, -1.0 / order, 1.0 / order, seed)
+    A[np.arange(order) * (lda + 1)] = 2.0
+    W = orc.random_f32(256 * 256, -scale, scale, seed + 1)
+    for b in weak:
+        lo = 256 * b
+        nb = min(256, order - lo)
+        for j in range(nb):
+            col = (lo + j) * lda + lo
+            A[col:col + nb] = W[j * 256:j * 256 + nb]
+            A[col + j] = 1.0
+    return A
+
+
+@pytest.mark.parametrize("weak,scale", [((1,), 0.1), ((0, 2), 0.1), ((0, 1, 2), 0.02), ((), 0.1)])
+@pytest.mark.parametrize("side,uplo,trans", [(1, 1, 0), (1, 2, 1), (2, 1, 1), (2, 2, 0)])
+def test_strsm_node_path_block_conditions(ctx, weak, scale, side, uplo, trans):
+    # Order 700: nodes [0, 512) (two diagonal blocks, the inverse path with
+    # its coupling block) and [512, 700) (one partial block). A diagonal
+    # block whose condition estimate exceeds the inverse path's limit is
+    # solved by substitution, the others by their inverses, in either solve
+    # direction and on either side; the backward residual bound holds
+    # throughout (ill-conditioned blocks included) and ld padding stays
+    # untouched. alpha 1.25 exercises the scaling on both paths.
+    order, other = 700, 40
+    m, n = (order, other) if side == 1 else (other, order)
+    lda, ldb = order + 3, m + 2
+    A = _blocks_of_condition(order, lda, 131, weak, scale)
+    B = orc.random_f32(ldb * n, -1, 1, 132)
+    check_trsm(ctx, (side, uplo, trans, 0, m, n, 1.25, A, lda, B, ldb))
+
+
+@pytest.mark.parametrize("side", [1, 2])
+def test_strsm_node_path_rhs_independent_of_batch(ctx, side):
+    # Order 600 (the node path), a mix of blocks solved by inverse and by
+    # substitution: each right-hand side's solution is bit-equal to solving
+    # it alone (one right-hand side per call), so neither path mixes
+    # right-hand sides or depends on how many are solved together.
+    order, other = 600, 21
+    m, n = (order, other) if side == 1 else (other, order)
+    lda, ldb = order + 1, m
+    A = _blocks_of_condition(order, lda, 141, (1,), 0.1)
+    B = orc.random_f32(ldb * n, -1, 1, 142)
+    X = run_trsm(ctx, (side, 1, 0, 0, m, n, 0.5, A, lda, B, ldb))
+    for r in (0, 7, 20):
+        if side == 1:
+            Br = np.asarray(B, F32)[r * ldb:r * ldb + order]
+            Xr = run_trsm(ctx, (side, 1, 0, 0, order, 1, 0.5, A, lda, Br, order))
+            assert bits_equal(Xr, np.asarray(X, F32)[r * ldb:r * ldb + order]), r
+        else:
+            Br = np.asarray(B, F32)[r::ldb][:order]
+            Xr = run_trsm(ctx, (side, 1, 0, 0, 1, order, 0.5, A, lda, Br, 1))
+            assert bits_equal(Xr, np.asarray(X, F32)[r::ldb][:order]), r
+
+
 # ------------------------------------------- operands of different storage orders
 def _cm_transpose(X, rows, cols, ld):
     """Column-major rows x cols (leading dimension ld) -> its transpose as a

@@ -657,12 +657,20 @@ __device__ __forceinline__ void node_load_panels(const float *__restrict__ BF, i
   }
 }
 
-// x[u] into panel rows 16 t + 4 g .. + 3 of right-hand side i16.
+// Row block (16 frame rows) u = 0..3 of wave W in the node kernel: W,
+// 7 - W, 8 + W, 15 - W, so every wave applies 34 of an inverse's 136
+// tiles (row block t has t + 1 of them).
+__host__ __device__ constexpr int node_rb(int u, int W) {
+  return u == 0 ? W : u == 1 ? 7 - W : u == 2 ? 8 + W : 15 - W;
+}
+
+// x[u] into panel rows 16 t + 4 g .. + 3 (t = node_rb(u, W)) of right-hand
+// side i16.
 template <int W>
 __device__ __forceinline__ void node_to_panel(const Vec4 (&x)[4], float (*panel)[kLeaf + 4], int lane) {
   const int g = lane >> 4, i16 = lane & 15;
 #pragma unroll
-  for (int u = 0; u < 4; ++u) *reinterpret_cast<Vec4 *>(&panel[i16][16 * (4 * u + W) + 4 * g]) = x[u];
+  for (int u = 0; u < 4; ++u) *reinterpret_cast<Vec4 *>(&panel[i16][16 * node_rb(u, W) + 4 * g]) = x[u];
 }
 
 // Bit i16 of *bad for any non-finite value among this lane's x.
@@ -687,7 +695,7 @@ __device__ __forceinline__ void node_store(const Vec4 (&x)[4], float *__restrict
   for (int u = 0; u < 4; ++u)
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      const int f = 16 * (4 * u + W) + 4 * g + c;
+      const int f = 16 * node_rb(u, W) + 4 * g + c;
       if (f < nb) B[node_act(0, nb, rev, f) * vi + (r0 + i16) * vr] = x[u][c];
     }
 }
@@ -725,8 +733,8 @@ __device__ __forceinline__ bool node_usable(const float *__restrict__ slot) {
   return m * v <= kCondMax;
 }
 
-// The fast path's products for wave W as one stream of NS = 16 (F alone) or
-// 48 k-tile steps: X_F = inv_F P[0] (steps 0-15), T = P[1] - M[S, F] X_F
+// The fast path's products for wave W (row blocks node_rb(u, W)) as one
+// stream of NS = 16 (F alone) or 48 k-tile steps: X_F = inv_F P[0] (steps 0-15), T = P[1] - M[S, F] X_F
 // (16-31), X_S = inv_S T (32-47), with the panel hand-offs between them.
 // Each step's A operands are loaded kAhead steps before it (a register
 // ring), across the phase boundaries too: one wave per SIMD leaves the
@@ -748,11 +756,12 @@ __device__ __forceinline__ void node_stream(const NodeArgs &a, int lane, float (
   const Vec4 *ivS = reinterpret_cast<const Vec4 *>(a.invS);
   const Vec4 *cp = reinterpret_cast<const Vec4 *>(a.cpl);
   Vec4 ring[kAhead + 1][4];
+  Vec4 bcur;
   // whether step s has a tile for row block u, and the load of it
   auto issue = [&](auto sc) {
     constexpr int st = decltype(sc)::value, ph = st / kSub, kb = st % kSub, slot = st % (kAhead + 1);
     static_for<4>([&](auto uc) {
-      constexpr int u = decltype(uc)::value, t = 4 * u + W;
+      constexpr int u = decltype(uc)::value, t = node_rb(u, W);
       if constexpr (ph == 0 && t >= kb) ring[slot][u] = ivF[inv_at(t, kb) / 4 + lane];
       if constexpr (ph == 1) ring[slot][u] = cp[64 * (16 * t + kb) + lane];
       if constexpr (ph == 2 && t >= kb) ring[slot][u] = ivS[inv_at(t, kb) / 4 + lane];
@@ -773,7 +782,7 @@ __device__ __forceinline__ void node_stream(const NodeArgs &a, int lane, float (
     if constexpr (ph == 1 && kb == 0) {
 #pragma unroll
       for (int u = 0; u < 4; ++u)
-        xt[u] = *reinterpret_cast<const Vec4 *>(&P[1][i16][16 * (4 * u + W) + 4 * g]);
+        xt[u] = *reinterpret_cast<const Vec4 *>(&P[1][i16][16 * node_rb(u, W) + 4 * g]);
     }
     if constexpr (ph == 2 && kb == 0) {
 #pragma unroll
@@ -781,14 +790,20 @@ __device__ __forceinline__ void node_stream(const NodeArgs &a, int lane, float (
     }
     Vec4(&acc)[4] = ph == 0 ? xf : ph == 1 ? xt : xs;
     const float(*src)[kLeaf + 4] = ph == 2 ? P[1] : P[0];
-    const Vec4 b4 = *reinterpret_cast<const Vec4 *>(&src[i16][16 * kb + 4 * g]);
+    // B operands: this step's were read one step earlier (inside a phase;
+    // a phase's first step reads its own, after the hand-off barriers)
+    if constexpr (kb == 0) bcur = *reinterpret_cast<const Vec4 *>(&src[i16][4 * g]);
+    Vec4 bnext;
+    if constexpr (kb + 1 < kSub) bnext = *reinterpret_cast<const Vec4 *>(&src[i16][16 * (kb + 1) + 4 * g]);
+    const Vec4 b4 = bcur;
 #pragma unroll
     for (int c = 0; c < 4; ++c)
       static_for<4>([&](auto uc) {
         constexpr int u = decltype(uc)::value;
-        if constexpr (ph == 1 || 4 * u + W >= kb)
+        if constexpr (ph == 1 || node_rb(u, W) >= kb)
           acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(ring[slot][u][c], b4[c], acc[u], 0, 0, 0);
       });
+    if constexpr (kb + 1 < kSub) bcur = bnext;
     if constexpr (kb == kSub - 1 && ph == 0) {
       node_flag(xf, lane, &flag[0]);
       __syncthreads();  // every wave has read B_F's panel
@@ -821,14 +836,14 @@ __device__ __forceinline__ void node_recompute(const NodeArgs &a, int lane, floa
   const Vec4 *iv = reinterpret_cast<const Vec4 *>(a.invS);
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
-    xt[u] = *reinterpret_cast<const Vec4 *>(&P[1][i16][16 * (4 * u + W) + 4 * g]);
+    xt[u] = *reinterpret_cast<const Vec4 *>(&P[1][i16][16 * node_rb(u, W) + 4 * g]);
     xs[u] = Vec4{0.f, 0.f, 0.f, 0.f};
   }
 #pragma unroll 1
   for (int kb = 0; kb < kSub; ++kb) {
     Vec4 a4[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) a4[u] = cp[64 * (16 * (4 * u + W) + kb) + lane];
+    for (int u = 0; u < 4; ++u) a4[u] = cp[64 * (16 * node_rb(u, W) + kb) + lane];
     const Vec4 b4 = *reinterpret_cast<const Vec4 *>(&P[0][i16][16 * kb + 4 * g]);
 #pragma unroll
     for (int c = 0; c < 4; ++c)
@@ -844,13 +859,13 @@ __device__ __forceinline__ void node_recompute(const NodeArgs &a, int lane, floa
     Vec4 a4[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u)
-      if (4 * u + W >= kb) a4[u] = iv[inv_at(4 * u + W, kb) / 4 + lane];
+      if (node_rb(u, W) >= kb) a4[u] = iv[inv_at(node_rb(u, W), kb) / 4 + lane];
     const Vec4 b4 = *reinterpret_cast<const Vec4 *>(&P[1][i16][16 * kb + 4 * g]);
 #pragma unroll
     for (int c = 0; c < 4; ++c)
 #pragma unroll
       for (int u = 0; u < 4; ++u)
-        if (4 * u + W >= kb) xs[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(a4[u][c], b4[c], xs[u], 0, 0, 0);
+        if (node_rb(u, W) >= kb) xs[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(a4[u][c], b4[c], xs[u], 0, 0, 0);
   }
   node_flag(xs, lane, &flag[2]);
 }

@@ -511,61 +511,66 @@ def bench_level3_f64(ctx, reps):
     return comps
 
 
-def run_only(ctx, name, reps):
-    """One workload alone, `reps` launches, for counter runs (rocprofv3
-    --pmc): copy (1 GiB device-to-device, the traffic calibration),
-    sgemm_8192 (NN), dgemm_4096, ssyrk_8192, sdot / sasum / snrm2 / isamax
-    at n = 2^28."""
+def run_only(ctx, name, reps, warm=False):
+    """One workload alone, `reps` launches, for counter and kernel-trace runs
+    (rocprofv3): copy (1 GiB device-to-device, the traffic calibration),
+    sgemm_8192_{NN,NT,TN,TT}, dgemm_4096_{NN,NT,TN,TT} (bare dgemm_4096: NT),
+    ssyrk_8192, ssyr2k / ssymm / strmm / strsm at 8192 (strsm also 4096),
+    dsyr2k / dsymm / dtrmm at 4096, sdot / sasum / snrm2 / isamax at
+    n = 2^28. With `warm`, about 30 ms of the same calls run first (the
+    clocks settle under load), so the traced launches match bench.py's."""
     from wgblas_amd import LOWER, NO_TRANS, TRANS
+
+    def go(work, info):
+        if warm:
+            warm_up(ctx, work)
+        for _ in range(reps):
+            work()
+        ctx.synchronize()
+        return info
+
+    def layout(lay):
+        return (TRANS if lay[0] == "T" else NO_TRANS), (TRANS if lay[1] == "T" else NO_TRANS)
 
     if name == "copy":
         n = 1 << 28
         a, b = ctx.empty(n, np.float32), ctx.empty(n, np.float32)
-        for _ in range(reps):
-            ctx.lib.wgb_memcpy_d2d(ctx.handle, b.ptr, a.ptr, 4 * n)
-        ctx.synchronize()
-        return {"bytes_read": 4 * n, "bytes_written": 4 * n}
+        return go(lambda: ctx.lib.wgb_memcpy_d2d(ctx.handle, b.ptr, a.ptr, 4 * n),
+                  {"bytes_read": 4 * n, "bytes_written": 4 * n})
     if name.startswith("sgemm_8192"):
-        # sgemm_8192_NN / _NT / _TN / _TT: one headline launch (bare name: NN)
-        lay = name[len("sgemm_8192_"):] or "NN"
-        ta, tb = (TRANS if lay[0] == "T" else NO_TRANS), (TRANS if lay[1] == "T" else NO_TRANS)
+        # one headline launch per call (bare name: NN)
+        ta, tb = layout(name[len("sgemm_8192_"):] or "NN")
         n = 8192
         buf = ctx.empty(3 * n * n, np.float32)
         ctx.fill_uniform(buf, -1.0, 1.0, 2)
-        for _ in range(reps):
-            ctx.sgemm(ta, tb, n, n, n, 1.5, buf.offset(0), n, buf.offset(n * n), n, 0.5,
-                      buf.offset(2 * n * n), n)
-        ctx.synchronize()
-        return {"algorithmic_bytes": 4 * 4 * n * n}
-    if name == "dgemm_4096":
+        return go(lambda: ctx.sgemm(ta, tb, n, n, n, 1.5, buf.offset(0), n, buf.offset(n * n), n, 0.5,
+                                    buf.offset(2 * n * n), n), {"algorithmic_bytes": 4 * 4 * n * n})
+    if name.startswith("dgemm_4096"):
+        ta, tb = layout(name[len("dgemm_4096_"):] or "NT")
         n = 4096
         buf = ctx.empty(3 * n * n, np.float64)
         ctx.fill_uniform(buf, -1.0, 1.0, 3)
-        for _ in range(reps):
-            ctx.dgemm(NO_TRANS, TRANS, n, n, n, 1.0, buf.offset(0), n, buf.offset(n * n), n, 1.0,
-                      buf.offset(2 * n * n), n)
-        ctx.synchronize()
-        return {"algorithmic_bytes": 8 * 4 * n * n}
+        return go(lambda: ctx.dgemm(ta, tb, n, n, n, 1.0, buf.offset(0), n, buf.offset(n * n), n, 1.0,
+                                    buf.offset(2 * n * n), n), {"algorithmic_bytes": 8 * 4 * n * n})
     if name == "ssyrk_8192":
         n, k = 8192, 4096
         dA, dC = ctx.empty(n * k, np.float32), ctx.empty(n * n, np.float32)
         ctx.fill_normal(dA, 4)
         ctx.fill_uniform(dC, -1.0, 1.0, 5)
-        for _ in range(reps):
-            ctx.ssyrk(LOWER, NO_TRANS, n, k, 1.0, dA, n, 0.25, dC, n)
-        ctx.synchronize()
-        return {"algorithmic_bytes": 4 * (n * k + n * (n + 1))}
-    if name in ("ssyr2k_8192", "ssymm_8192", "strmm_8192", "strsm_8192"):
+        return go(lambda: ctx.ssyrk(LOWER, NO_TRANS, n, k, 1.0, dA, n, 0.25, dC, n),
+                  {"algorithmic_bytes": 4 * (n * k + n * (n + 1))})
+    if name in ("ssyr2k_8192", "ssymm_8192", "strmm_8192", "strsm_8192", "strsm_4096"):
         from wgblas_amd import LEFT, NON_UNIT
 
-        n = 8192
+        n = int(name.split("_")[1])
         dA, dB, dC = (ctx.empty(n * n, np.float32) for _ in range(3))
         ctx.fill_uniform(dA, -1.0 / n, 1.0 / n, 10)
         ctx.fill_uniform(dC, -1.0, 1.0, 9)
         diag = np.full(1, 2.0, np.float32)
         for i in range(n):
             ctx.h2d(dA.offset(i * n + i), diag)
-        for _ in range(reps):
+
+        def work():
             ctx.fill_uniform(dB, -1.0, 1.0, 11)
             if name == "ssyr2k_8192":
                 ctx.ssyr2k(LOWER, NO_TRANS, n, n // 2, 1.0, dA, n, dB, n, 0.25, dC, n)
@@ -575,8 +580,8 @@ def run_only(ctx, name, reps):
                 ctx.strmm(LEFT, LOWER, NO_TRANS, NON_UNIT, n, n, 1.0, dA, n, dB, n)
             else:
                 ctx.strsm(LEFT, LOWER, NO_TRANS, NON_UNIT, n, n, 1.0, dA, n, dB, n)
-        ctx.synchronize()
-        return {"algorithmic_bytes": 4 * 3 * n * n}
+
+        return go(work, {"algorithmic_bytes": 4 * 3 * n * n})
     if name in ("dsyr2k_4096", "dsymm_4096", "dtrmm_4096"):
         from wgblas_amd import LEFT, NON_UNIT
 
@@ -584,7 +589,8 @@ def run_only(ctx, name, reps):
         dA, dB, dC = (ctx.empty(n * n, np.float64) for _ in range(3))
         ctx.fill_uniform(dA, -1.0, 1.0, 7)
         ctx.fill_uniform(dC, -1.0, 1.0, 9)
-        for _ in range(reps):
+
+        def work():
             ctx.fill_uniform(dB, -1.0, 1.0, 8)
             if name == "dsyr2k_4096":
                 ctx.dsyr2k(LOWER, NO_TRANS, n, n, 1.0, dA, n, dB, n, 0.0, dC, n)
@@ -592,8 +598,8 @@ def run_only(ctx, name, reps):
                 ctx.dsymm(LEFT, LOWER, n, n, 1.0, dA, n, dB, n, 0.0, dC, n)
             else:
                 ctx.dtrmm(LEFT, LOWER, NO_TRANS, NON_UNIT, n, n, 1.0, dA, n, dB, n)
-        ctx.synchronize()
-        return {"algorithmic_bytes": 8 * 3 * n * n}
+
+        return go(work, {"algorithmic_bytes": 8 * 3 * n * n})
     n = 1 << 28
     dx, dy = ctx.empty(n, np.float32), ctx.empty(n, np.float32)
     ctx.fill_normal(dx, 1)
@@ -601,10 +607,7 @@ def run_only(ctx, name, reps):
     out, iout = ctx.empty(4, np.float32), ctx.empty(1, np.int64)
     fns = {"sdot": lambda: ctx.sdot_dev(n, dx, 1, dy, 1, out), "sasum": lambda: ctx.sasum_dev(n, dx, 1, out),
            "snrm2": lambda: ctx.snrm2_dev(n, dx, 1, out), "isamax": lambda: ctx.isamax_dev(n, dx, 1, iout)}
-    for _ in range(reps):
-        fns[name]()
-    ctx.synchronize()
-    return {"algorithmic_bytes": (8 if name == "sdot" else 4) * n}
+    return go(fns[name], {"algorithmic_bytes": (8 if name == "sdot" else 4) * n})
 
 
 def vendor_twin():
@@ -743,11 +746,13 @@ def main():
     ap.add_argument("--no-components", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default=None,
-                    help="run one workload alone (copy, sgemm_8192_{NN,NT,TN,TT}, dgemm_4096, ssyrk_8192, "
-                         "ssyr2k_8192, ssymm_8192, strmm_8192, strsm_8192, dsyr2k_4096, dsymm_4096, dtrmm_4096, "
+                    help="run one workload alone (copy, sgemm_8192_{NN,NT,TN,TT}, dgemm_4096[_{NN,NT,TN,TT}], ssyrk_8192, "
+                         "ssyr2k_8192, ssymm_8192, strmm_8192, strsm_8192, strsm_4096, dsyr2k_4096, dsymm_4096, dtrmm_4096, "
                          "sdot, sasum, snrm2, "
                          "isamax) for counter and kernel-trace collection")
     ap.add_argument("--reps", type=int, default=3)
+    ap.add_argument("--warm", action="store_true",
+                    help="with --only: about 30 ms of untimed calls before the reps")
     ap.add_argument("--no-vendor", action="store_true",
                     help="skip the rocBLAS twin (wgblas_amd/lib/vendor_twin) of the components "
                          "and the roof probe (wgblas_amd/lib/roof_probe)")
@@ -762,7 +767,7 @@ def main():
 
     ctx = Context(0)
     if args.only:
-        info = run_only(ctx, args.only, args.reps)
+        info = run_only(ctx, args.only, args.reps, args.warm)
         ctx.close()
         print(json.dumps({"only": args.only, "reps": args.reps, **info}))
         return 0

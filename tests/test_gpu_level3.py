@@ -206,6 +206,65 @@ def test_ssyr2k_large_tier_padded(ctx, uplo, trans):
     check_syr2k(ctx, call)
 
 
+def syr2k_sampled(ctx, uplo, trans, n, k, alpha, beta, ld, ldc, seed, dt=np.float32):
+    """ssyr2k / dsyr2k with lda == ldb, the shape of the one-launch path
+    (both products over one two-part k range when k is whole k-tiles),
+    with inputs generated on the device. Sampled columns of the triangle
+    are checked against float64 products under the reference's bound, and
+    C's other triangle and ld padding must come back bit-identical."""
+    from tests.helpers import EPS_DD
+
+    f64 = dt == np.float64
+    cols = n if trans else k
+    A, B = ctx.empty(ld * cols, dt), ctx.empty(ld * cols, dt)
+    C = ctx.empty(ldc * n, dt)
+    try:
+        for i, X in enumerate((A, B, C)):
+            ctx.fill_uniform(X, -1.0, 1.0, seed + i)
+        ctx.synchronize()
+        a, b, cin = A.to_host(), B.to_host(), C.to_host()
+        (ctx.dsyr2k if f64 else ctx.ssyr2k)(uplo, trans, n, k, alpha, A, ld, B, ld, beta, C, ldc)
+        got = C.to_host()
+    finally:
+        for X in (A, B):
+            X.free()
+        C.free()
+
+    def op(x):  # op(X) as n x k float64
+        return (x.reshape(n, ld)[:, :k] if trans else x.reshape(k, ld)[:, :n].T).astype(np.float64)
+
+    oa, ob = op(a), op(b)
+    keep = np.ones(len(cin), bool)
+    keep[region(n, n, ldc, uplo)] = False
+    assert bits_equal(got[keep], cin[keep]), "other triangle or ld padding written"
+    rng = np.random.default_rng(seed)
+    sel = np.unique(np.concatenate([[0, n - 1, n // 2, min(n - 1, 128), min(n - 1, 127)],
+                                    rng.integers(0, n, 20)]))
+    eps, c1, c2, c3 = (EPS_DD, 2, 1, 2) if f64 else (EPS32, 3, 2, 3)
+    for j in sel:
+        rows = np.arange(j, n) if uplo == 1 else np.arange(0, j + 1)
+        cj = cin[j * ldc + rows].astype(np.float64)
+        ref = alpha * (oa[rows] @ ob[j] + ob[rows] @ oa[j]) + beta * cj
+        d1 = np.abs(oa[rows]) @ np.abs(ob[j])
+        d2 = np.abs(ob[rows]) @ np.abs(oa[j])
+        bound = eps * ((k + c1) * abs(alpha) * d1 + (k + c2) * abs(alpha) * d2 + c3 * abs(beta) * np.abs(cj))
+        err = np.abs(got[j * ldc + rows].astype(np.float64) - ref)
+        assert np.all(err <= bound), f"column {j}: max err/bound {np.max(err / bound)}"
+
+
+@pytest.mark.parametrize("uplo", [1, 2])
+@pytest.mark.parametrize("trans", [0, 1])
+@pytest.mark.parametrize("n,k", [(4224, 544), (2900, 320), (1100, 96)])
+def test_ssyr2k_one_launch(ctx, uplo, trans, n, k):
+    # lda == ldb and k a multiple of 32: one launch over (A, B) then (B, A).
+    # 4224 / 544: 561 tiles of 128 on the 128 tier, a split-k tail whose
+    # k-slices straddle the switch from (A, B) to (B, A) (k-tile 17 of 34);
+    # 2900 / 320: 128 tier with edge tiles; 1100 / 96: 64 tier, edge tiles
+    print(f"ssyr2k one launch uplo={uplo} trans={trans} n={n} k={k}", flush=True)
+    ld = (k if trans else n) + 4
+    syr2k_sampled(ctx, uplo, trans, n, k, 0.75, -0.5, ld, n + 2, 1000 + n)
+
+
 # ------------------------------------------------------------ ssymm
 def symm_case(layout, side, uplo, N, OTHER, pad, alpha=1.5, beta=0.5, seeds=(91, 92, 93)):
     # tests/ssymm/src/test.ssymm.js:236-297

@@ -130,6 +130,20 @@ def test_dsyr2k_multi_tile(ctx, layout, N, uplo, trans):
 
 
 @pytest.mark.parametrize("uplo", [1, 2])
+@pytest.mark.parametrize("trans", [0, 1])
+@pytest.mark.parametrize("n,k", [(4224, 272), (1100, 48)])
+def test_dsyr2k_one_launch(ctx, uplo, trans, n, k):
+    # lda == ldb and k a multiple of 16: one launch over (A, B) then (B, A).
+    # 4224 / 272: 561 tiles of 128, a split-k tail whose k-slices straddle
+    # the switch (k-tile 17 of 34); 1100 / 48: 64 tier with edge tiles
+    from tests.test_gpu_level3 import syr2k_sampled
+
+    print(f"dsyr2k one launch uplo={uplo} trans={trans} n={n} k={k}", flush=True)
+    ld = (k if trans else n) + 2
+    syr2k_sampled(ctx, uplo, trans, n, k, 0.75, -0.5, ld, n + 1, 2000 + n, np.float64)
+
+
+@pytest.mark.parametrize("uplo", [1, 2])
 def test_dsyr2k_k0_is_beta_c(ctx, uplo):
     # test.dsyr2k.js:267-319: k = 0 gives beta C on the triangle (exact in
     # fp64), the other triangle unchanged

@@ -74,6 +74,16 @@ int gemm_f32(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64_t 
 int gemm_f64(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64_t n, int64_t k,
              double alpha, const double *A, int64_t lda, const double *B, int64_t ldb,
              double beta, double *C, int64_t ldc, int band);
+// C = alpha (op(A) op(B) + op(A2) op(B2)) + beta C on the uplo part of C,
+// the second pair at the first pair's leading dimensions and transposes:
+// one launch over both k ranges where the kernels allow it (ssyr2k /
+// dsyr2k), else two.
+int gemm2_f32(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64_t n, int64_t k,
+              float alpha, const float *A, const float *A2, int64_t lda, const float *B,
+              const float *B2, int64_t ldb, float beta, float *C, int64_t ldc);
+int gemm2_f64(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64_t n, int64_t k,
+              double alpha, const double *A, const double *A2, int64_t lda, const double *B,
+              const double *B2, int64_t ldb, double beta, double *C, int64_t ldc);
 // wgb_sgemm_noalloc's fixed per-GPU split-k workspace (noalloc.hip): its
 // size, and its device address on ctx's device (current on entry), looked
 // up on the first call for that device.

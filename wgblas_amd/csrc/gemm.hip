@@ -113,6 +113,11 @@ struct GemmArgs {
   // and split_fixup adds them. nregular == ntiles: no split.
   int nregular, splits, kt_split;
   T *ws;
+  // Two-part k range (K2 kernels, ssyr2k / dsyr2k as one launch): k-tiles
+  // kt >= kt_switch read A2 in place of A and B2 in place of B, at the same
+  // leading dimensions and at k-tile kt - kt_switch of those.
+  const T *A2, *B2;
+  int kt_switch;
 };
 
 constexpr int kThreads = 256;
@@ -145,7 +150,7 @@ __device__ __forceinline__ int kc_swz(int row) { return row & 7; }
 // KC: k-contiguous in memory, staged [row][k] (row stride BK, chunks
 //     swizzled by kc_swz).
 // !KC: row-contiguous in memory, staged [k][row] (row stride BT).
-template <typename T, int BT, bool KC, bool VEC, int NT = kThreads>
+template <typename T, int BT, bool KC, bool VEC, int NT = kThreads, bool K2 = false>
 struct Stager {
   typedef typename Ty<T>::v16 V;
   static constexpr int VW = Ty<T>::VW;
@@ -183,6 +188,21 @@ struct Stager {
   const T *origin;
   uint32_t voff[LOADS];
   int copy_shift;  // elements from this thread's register-path vector to its copy source
+  // K2: from k-tile ksw on, every address moves by dsw bytes: k-tile kt of
+  // the first operand's addressing becomes k-tile kt - kt_switch of the
+  // second operand (same leading dimension, so the same offsets from it).
+  int ksw;
+  int64_t dsw;
+
+  // After init (k_step set), before advance.
+  __device__ void set_switch(const T *P, const T *P2, int kt_switch) {
+    ksw = kt_switch;
+    dsw = ((const char *)P2 - (const char *)P) - (int64_t)kt_switch * k_step * (int64_t)sizeof(T);
+  }
+  __device__ const T *sel(const T *q, int kt) const {
+    if constexpr (K2) return kt < ksw ? q : (const T *)((const char *)q + dsw);
+    return q;
+  }
 
   __device__ void init(const T *P, int64_t ld, int64_t row0, int t, int64_t rows_total_,
                        int64_t K_) {
@@ -219,6 +239,7 @@ struct Stager {
     base += (int64_t)kt0 * k_step;
     origin += (int64_t)kt0 * k_step;
     K -= (int64_t)kt0 * BK;
+    if constexpr (K2) ksw -= kt0;
   }
 
   // Edge-tile fields (after init and advance): see the members above.
@@ -254,16 +275,16 @@ struct Stager {
   // otherwise a whole k-tile, with EDGE for tiles that cross rows_total.
   template <bool GUARD, bool EDGE = false>
   __device__ void load(V (&regs)[LOADS], int kt) const {
-    const T *p = base + (int64_t)kt * k_step;
+    const T *p = sel(base + (int64_t)kt * k_step, kt);
 #pragma unroll
     for (int r = 0; r < LOADS; ++r) {
       const T *q = p + r * r_step;
       if (!GUARD && !EDGE) {
         regs[r] = load_full(q);
       } else if (!GUARD && KC) {
-        regs[r] = load_full(r < nvr ? q : fb + (int64_t)kt * k_step);
+        regs[r] = load_full(r < nvr ? q : sel(fb + (int64_t)kt * k_step, kt));
       } else if (!GUARD) {
-        regs[r] = load_full(vok ? q : fb + (int64_t)kt * k_step + r * r_step);
+        regs[r] = load_full(vok ? q : sel(fb + (int64_t)kt * k_step, kt) + r * r_step);
       } else if (KC) {
         int64_t row = row_first + 32 * r;
         int64_t nv = K - ((int64_t)kt * BK + k_first);
@@ -308,7 +329,7 @@ struct Stager {
     static_assert(sizeof(V) == 16, "LDS copies move 16 bytes per lane");
     T *dst = stage + wave * 64 * VW;
     if constexpr (SCALAR_BASE) {
-      const uint64_t o64 = (uint64_t)(origin + (int64_t)kt * k_step);
+      const uint64_t o64 = (uint64_t)sel(origin + (int64_t)kt * k_step, kt);
       uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)o64);
       uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(o64 >> 32));
       asm volatile("" : "+s"(lo), "+s"(hi));
@@ -320,12 +341,12 @@ struct Stager {
         copy16_to_lds(o + v, dst + r * lds_r_step);
       }
     } else {
-      const T *p = base + (int64_t)kt * k_step;
+      const T *p = sel(base + (int64_t)kt * k_step, kt);
 #pragma unroll
       for (int r = 0; r < LOADS; ++r) {
         const T *q = p + r * r_step;
-        if (EDGE && KC) q = r < nvr ? q : fb + (int64_t)kt * k_step;
-        if (EDGE && !KC) q = vok ? q : fb + (int64_t)kt * k_step + r * r_step;
+        if (EDGE && KC) q = r < nvr ? q : sel(fb + (int64_t)kt * k_step, kt);
+        if (EDGE && !KC) q = vok ? q : sel(fb + (int64_t)kt * k_step, kt) + r * r_step;
         copy16_to_lds(q + copy_shift, dst + r * lds_r_step);
       }
     }
@@ -549,7 +570,7 @@ __device__ __forceinline__ void copies_landed_sync() {
 // loop and the epilogue (unit >= 0: a split-k unit's raw partial to ws).
 // NT = 256 threads (2 x 2 waves); every wave owns a square WT x WT part of
 // the tile.
-template <typename T, int BTM, int BTN, int NT, bool AKC, bool BKC, bool VEC>
+template <typename T, int BTM, int BTN, int NT, bool AKC, bool BKC, bool VEC, bool K2 = false>
 __device__ __forceinline__ void gemm_tile(const GemmArgs<T> &p, int tm, int tn, int unit, int kt0,
                                           int nkt, T *smem, const int t) {
   typedef typename Ty<T>::acc Acc;
@@ -561,8 +582,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs<T> &p, int tm, int tn, 
   constexpr int WT = BTM / WGM;
   static_assert(WT == BTN / (NT / 64 / WGM), "square wave tiles");
   constexpr int MB = WT / 16;
-  typedef Stager<T, BTM, AKC, VEC, NT> SA;
-  typedef Stager<T, BTN, BKC, VEC, NT> SB;
+  typedef Stager<T, BTM, AKC, VEC, NT, K2> SA;
+  typedef Stager<T, BTN, BKC, VEC, NT, K2> SB;
   constexpr int STAGE = SA::ELEMS + SB::ELEMS;
   const int64_t m0 = (int64_t)tm * BTM, n0 = (int64_t)tn * BTN;
   const int lane = t & 63, wave = t >> 6;
@@ -574,6 +595,10 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs<T> &p, int tm, int tn, 
   SB sb;
   sa.init(p.A, p.lda, m0, t, p.m, p.k);
   sb.init(p.B, p.ldb, n0, t, p.n, p.k);
+  if constexpr (K2) {
+    sa.set_switch(p.A, p.A2, p.kt_switch);
+    sb.set_switch(p.B, p.B2, p.kt_switch);
+  }
   sa.advance(kt0);
   sb.advance(kt0);
   const bool interior = (m0 + BTM <= p.m) && (n0 + BTN <= p.n);
@@ -1059,7 +1084,10 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs<T> &p, int tm, int tn, 
 // column's) k range grows with its index, so block b takes the tile pair
 // (r, c) and (tiles-1-r, c) (columns for a band on op(B)) and every block
 // does the same work, whatever order the dispatcher fills the CUs in.
-template <typename T, int BT, bool AKC, bool BKC, bool VEC, bool PAIR>
+//
+// K2: the two-part k range of GemmArgs (k-tiles from kt_switch on read A2 and
+// B2); no PAIR.
+template <typename T, int BT, bool AKC, bool BKC, bool VEC, bool PAIR, bool K2 = false>
 __global__ __launch_bounds__(kThreads, (VEC || (AKC && BKC) ||
                                        ((PAIR || sizeof(T) == 8) && (AKC || BKC)))
                                           ? 2
@@ -1087,7 +1115,7 @@ __global__ __launch_bounds__(kThreads, (VEC || (AKC && BKC) ||
     // (nkt >= 1: k > 0 here, and the host never plans an empty split; an
     // explicit nkt check costs the fp32 loop ~60 VGPRs of scheduling freedom.)
     if (tm < 0 || tn < 0 || tm >= p.tiles_m || tn >= p.tiles_n) return;  // block-uniform
-    gemm_tile<T, BT, BT, kThreads, AKC, BKC, VEC>(p, tm, tn, unit, kt0, nkt, smem, (int)threadIdx.x);
+    gemm_tile<T, BT, BT, kThreads, AKC, BKC, VEC, K2>(p, tm, tn, unit, kt0, nkt, smem, (int)threadIdx.x);
   } else {
     const int nkt_all = (int)((p.k + BK - 1) / BK);
     const bool on_rows = p.band == wgb::kBandALower || p.band == wgb::kBandAUpper;
@@ -1325,9 +1353,14 @@ KernelFn<T> pick_layout(bool akc, bool bkc, bool vec) {
   return bkc ? gemm_kernel<T, BT, false, true, false, PAIR> : gemm_kernel<T, BT, false, false, false, PAIR>;
 }
 
-// Banded (paired-tile) kernels exist for fp32 only: strmm is their caller.
+// Banded (paired-tile) kernels serve strmm / dtrmm. Two-part k kernels
+// (ssyr2k / dsyr2k) exist for 16-byte aligned operands in the layouts
+// op(A) op(B)^T (both mn-contiguous) and op(A)^T op(B) (both k-contiguous):
+// the host plans one only there.
 template <typename T, int BT>
-KernelFn<T> pick_kernel(bool akc, bool bkc, bool vec, bool pair) {
+KernelFn<T> pick_kernel(bool akc, bool bkc, bool vec, bool pair, bool k2) {
+  if (k2) return akc ? gemm_kernel<T, BT, true, true, true, false, true>
+                     : gemm_kernel<T, BT, false, false, true, false, true>;
   if (pair) return pick_layout<T, BT, true>(akc, bkc, vec);
   return pick_layout<T, BT, false>(akc, bkc, vec);
 }
@@ -1336,7 +1369,7 @@ KernelFn<T> pick_kernel(bool akc, bool bkc, bool vec, bool pair) {
 // cached per (tier, operand layout) slot; 0 = not yet queried.
 template <typename T, int BT>
 int blocks_per_cu(KernelFn<T> fn, int slot) {
-  static int cache[16] = {0};
+  static int cache[32] = {0};
   if (cache[slot] == 0) {
     int nb = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, reinterpret_cast<const void *>(fn),
@@ -1389,10 +1422,11 @@ template <typename T, int BT>
 int launch_tier(wgb_ctx *ctx, GemmArgs<T> &a, bool akc, bool bkc, bool vec, WsSource wsrc) {
   constexpr int BK = 128 / (int)sizeof(T);
   const bool pair = a.band != wgb::kBandNone;
-  KernelFn<T> fn = pick_kernel<T, BT>(akc, bkc, vec, pair);
+  const bool k2 = a.kt_switch < (int)((a.k + BK - 1) / BK);
+  KernelFn<T> fn = pick_kernel<T, BT>(akc, bkc, vec, pair, k2);
   const int64_t cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
-  const int64_t slots =
-      cus * blocks_per_cu<T, BT>(fn, (pair ? 8 : 0) + (akc ? 4 : 0) + (bkc ? 2 : 0) + (vec ? 1 : 0));
+  const int64_t slots = cus * blocks_per_cu<T, BT>(fn, (k2 ? 16 : 0) + (pair ? 8 : 0) + (akc ? 4 : 0) +
+                                                           (bkc ? 2 : 0) + (vec ? 1 : 0));
   const int64_t nkt = (a.k + BK - 1) / BK;
   a.nregular = a.ntiles;
   if (pair) {
@@ -1470,11 +1504,17 @@ int check_gemm_args(int uplo, bool want_uplo, int transA, int transB, int64_t m,
   return WGB_OK;
 }
 
-// Enqueues one GEMM (no argument checks, no timing events).
+// Enqueues one GEMM (no argument checks, no timing events). With A2 / B2:
+// C = alpha (op(A) op(B) + op(A2) op(B2)) + beta C, the second pair at lda /
+// ldb with the same transposes (ssyr2k / dsyr2k): one launch over a two-part
+// k range when both pairs are 16-byte aligned, k is whole k-tiles and op(A),
+// op(B) are both mn-contiguous or both k-contiguous; otherwise two launches,
+// the second with beta = 1.
 template <typename T>
 int gemm_launch(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64_t n, int64_t k,
                 T alpha, const T *A, int64_t lda, const T *B, int64_t ldb, T beta, T *C,
-                int64_t ldc, int band, WsSource wsrc = WsSource()) {
+                int64_t ldc, int band, WsSource wsrc = WsSource(), const T *A2 = nullptr,
+                const T *B2 = nullptr) {
   if (m == 0 || n == 0) return WGB_OK;
   if (alpha == (T)0 || k == 0) {
     dim3 block(256);
@@ -1498,6 +1538,9 @@ int gemm_launch(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64
   a.ldc = ldc;
   a.uplo = uplo;
   a.band = band;
+  a.A2 = nullptr;
+  a.B2 = nullptr;
+  a.kt_switch = INT32_MAX;
   const int VW = Ty<T>::VW;
   a.c_vec = (ldc % VW == 0) && aligned16(C);
   const bool akc = transA == WGB_TRANS;
@@ -1509,7 +1552,7 @@ int gemm_launch(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64
     // across its waves does it in one launch.
     const int64_t t32m = (m + kSmallTile - 1) / kSmallTile, t32n = (n + kSmallTile - 1) / kSmallTile;
     const int64_t t64 = ((m + 63) / 64) * ((n + 63) / 64);
-    if (uplo == 0 && band == wgb::kBandNone && k <= kSmallMaxK && 2 * t64 < fill &&
+    if (uplo == 0 && band == wgb::kBandNone && !A2 && k <= kSmallMaxK && 2 * t64 < fill &&
         t32m * t32n <= 4 * fill) {
       a.tiles_m = (int)t32m;
       a.tiles_n = (int)t32n;
@@ -1531,6 +1574,21 @@ int gemm_launch(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64
   const int64_t off_cap = (int64_t)1 << 31;
   const bool offs32 = 256 * lda * (int64_t)sizeof(T) < off_cap && 256 * ldb * (int64_t)sizeof(T) < off_cap;
   const bool vec = (lda % VW == 0) && (ldb % VW == 0) && aligned16(A) && aligned16(B) && offs32;
+  if (A2) {
+    constexpr int BK = 128 / (int)sizeof(T);
+    if (!(vec && aligned16(A2) && aligned16(B2) && k % BK == 0 && akc == bkc && band == wgb::kBandNone)) {
+      int st = gemm_launch<T>(ctx, uplo, transA, transB, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc,
+                              band, wsrc);
+      if (st) return st;
+      return gemm_launch<T>(ctx, uplo, transA, transB, m, n, k, alpha, A2, lda, B2, ldb, (T)1, C, ldc,
+                            band, wsrc);
+    }
+    if (2 * k > INT32_MAX) return wgb::fail(WGB_ERR_INVALID_VALUE, "k too large for one two-part launch");
+    a.k = 2 * k;
+    a.A2 = A2;
+    a.B2 = B2;
+    a.kt_switch = (int)(k / BK);
+  }
   // Large tier once the 128-tiles alone fill the chip; small tier otherwise.
   auto count = [&](int64_t bt, int64_t &tmn, int64_t &tnn) {
     tmn = (m + bt - 1) / bt;
@@ -1584,6 +1642,20 @@ int gemm_f64(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64_t 
              double beta, double *C, int64_t ldc, int band) {
   return gemm_launch<double>(ctx, uplo, transA, transB, m, n, k, alpha, A, lda, B, ldb, beta, C,
                              ldc, band);
+}
+
+int gemm2_f32(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64_t n, int64_t k,
+              float alpha, const float *A, const float *A2, int64_t lda, const float *B,
+              const float *B2, int64_t ldb, float beta, float *C, int64_t ldc) {
+  return gemm_launch<float>(ctx, uplo, transA, transB, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc,
+                            wgb::kBandNone, WsSource(), A2, B2);
+}
+
+int gemm2_f64(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64_t n, int64_t k,
+              double alpha, const double *A, const double *A2, int64_t lda, const double *B,
+              const double *B2, int64_t ldb, double beta, double *C, int64_t ldc) {
+  return gemm_launch<double>(ctx, uplo, transA, transB, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc,
+                             wgb::kBandNone, WsSource(), A2, B2);
 }
 
 int check_gemm(int uplo, bool want_uplo, int transA, int transB, int64_t m, int64_t n, int64_t k,

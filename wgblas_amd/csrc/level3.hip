@@ -2,7 +2,9 @@
 // strsm (wgblas src/{ssyr2k,ssymm,strmm,strsm}/*.mjs), and the native-fp64
 // dsyr2k, dsymm, dtrmm (src/{dsyr2k,dsymm,dtrmm}/*.mjs) on its fp64 form.
 //
-// ssyr2k: two triangle GEMM launches, the second with beta = 1.
+// ssyr2k: one triangle GEMM launch over a two-part k range, (A, B) then
+//   (B, A), when both products share a layout; else two launches, the
+//   second with beta = 1.
 // ssymm: the symmetric operand is expanded into a dense workspace copy
 //   (LDS-tiled, coalesced both ways), then one GEMM.
 // strmm: A's triangle is copied with zeros elsewhere, B is copied (the GEMM
@@ -1157,6 +1159,20 @@ int syr2k(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t n, int64_t k, 
   if (n == 0) return WGB_OK;
   if (sizeof(T) == 8 && (alpha == (T)0 || k == 0) && beta == (T)1) return WGB_OK;
   wgb::timing_begin(ctx);
+  if (transA == transB && lda == ldb) {
+    // op(A) op(B)^T and op(B) op(A)^T take the same GEMM layout and leading
+    // dimensions: one launch over k-tiles of (A, B) then of (B, A), both
+    // products summed in one accumulator and alpha applied once. (wgblas
+    // runs its GEMM twice, the second pass with beta = 1,
+    // src/ssyr2k/ssyr2k.mjs:206-262: the same products, rounded once more.)
+    if constexpr (sizeof(T) == 4)
+      st = wgb::gemm2_f32(ctx, uplo, transA, tBt, n, n, k, alpha, A, B, lda, B, A, ldb, beta, C, ldc);
+    else
+      st = wgb::gemm2_f64(ctx, uplo, transA, tBt, n, n, k, alpha, A, B, lda, B, A, ldb, beta, C, ldc);
+    if (st) return st;
+    wgb::timing_end(ctx);
+    return WGB_OK;
+  }
   // pass 1: alpha op(A) op(B)^T + beta C; pass 2: alpha op(B) op(A)^T + C
   // (src/ssyr2k/ssyr2k.mjs:206-262), one timed span
   if ((st = gemm_t<T>(ctx, uplo, transA, tBt, n, n, k, alpha, A, lda, B, ldb, beta, C, ldc,

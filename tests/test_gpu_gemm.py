@@ -159,7 +159,7 @@ def test_beta_zero_ignores_nan_in_c(ctx):
 @pytest.mark.parametrize("variant", ["ldc_pad4", "c_misaligned", "beta0_nan"])
 @pytest.mark.parametrize("ta", [0, 1])
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
-@pytest.mark.parametrize("shape", [(1024, 768, 96), (2048, 2304, 40)])  # small / large tier
+@pytest.mark.parametrize("shape", [(1024, 768, 96), (2048, 4608, 40)])  # 64 / 128 tier (576 tiles)
 def test_epilogue_paths(ctx, variant, ta, dtype, shape):
     """Whole-vector C epilogue (ldc multiple of the vector width, C 16-byte
     aligned) against the element-wise one (C one element off alignment), with

@@ -254,12 +254,13 @@ def syr2k_sampled(ctx, uplo, trans, n, k, alpha, beta, ld, ldc, seed, dt=np.floa
 
 @pytest.mark.parametrize("uplo", [1, 2])
 @pytest.mark.parametrize("trans", [0, 1])
-@pytest.mark.parametrize("n,k", [(4224, 544), (2900, 320), (1100, 96)])
+@pytest.mark.parametrize("n,k", [(4224, 544), (4100, 320), (1100, 96)])
 def test_ssyr2k_one_launch(ctx, uplo, trans, n, k):
     # lda == ldb and k a multiple of 32: one launch over (A, B) then (B, A).
     # 4224 / 544: 561 tiles of 128 on the 128 tier, a split-k tail whose
     # k-slices straddle the switch from (A, B) to (B, A) (k-tile 17 of 34);
-    # 2900 / 320: 128 tier with edge tiles; 1100 / 96: 64 tier, edge tiles
+    # 4100 / 320: 561 tiles of 128 with edge tiles (no split: 20 k-tiles);
+    # 1100 / 96: 64 tier, edge tiles
     print(f"ssyr2k one launch uplo={uplo} trans={trans} n={n} k={k}", flush=True)
     ld = (k if trans else n) + 4
     syr2k_sampled(ctx, uplo, trans, n, k, 0.75, -0.5, ld, n + 2, 1000 + n)

@@ -1589,7 +1589,6 @@ int gemm_launch(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64
     a.B2 = B2;
     a.kt_switch = (int)(k / BK);
   }
-  // Large tier once the 128-tiles alone fill the chip; small tier otherwise.
   auto count = [&](int64_t bt, int64_t &tmn, int64_t &tnn) {
     tmn = (m + bt - 1) / bt;
     tnn = (n + bt - 1) / bt;
@@ -1597,9 +1596,16 @@ int gemm_launch(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64
     if (uplo == WGB_UPPER) return triangle_tiles(tnn, tmn);
     return tmn * tnn;
   };
+  // 128-tiles once they fill whole rounds of two blocks per CU, or exactly
+  // one block per CU over a long k; otherwise 64-tiles, whose rounds of
+  // about four blocks per CU leave fewer CUs idle or half loaded. Measured
+  // (TFLOP/s, 128 -> 64 tier): 2048 x 3072 x 4096 (384 tiles) 109.5 -> 126.0,
+  // 1024 x 4096 x 1024 (256) 114.0 -> 119.0, 512 x 8192 x 512 (256) 94.3 ->
+  // 102.6, 2048 x 2048 x 2048 (256) 128.5 -> 129.6; 2048 x 2048 x 8192 (256)
+  // 141.0 -> 138.9 stays on 128-tiles.
   int64_t tm128, tn128;
   int64_t tiles128 = count(128, tm128, tn128);
-  const int bt = tiles128 >= fill ? 128 : 64;
+  const int bt = (tiles128 >= 2 * fill || (tiles128 == fill && k >= 4096)) ? 128 : 64;
   int64_t tmn, tnn;
   int64_t ntiles = count(bt, tmn, tnn);
   if (ntiles > INT32_MAX) return wgb::fail(WGB_ERR_INVALID_VALUE, "problem too large for one launch");

@@ -360,6 +360,70 @@ def test_strmm_large_band(ctx, side, uplo, trans):
     check_trmm(ctx, call)
 
 
+def trmm_sampled(ctx, side, uplo, trans, unit, m, n, alpha, lda, ldb, seed, dt=np.float32):
+    """strmm / dtrmm on device-generated inputs. The unreferenced triangle
+    of A holds NaN, and its diagonal too for a unit triangle, so any of it
+    reaching the product shows. Sampled columns against float64 under the
+    reference's bound; B's ld padding bit-identical."""
+    from tests.helpers import EPS_DD
+
+    order = m if side == 1 else n
+    A, B = ctx.empty(lda * order, dt), ctx.empty(ldb * n, dt)
+    try:
+        ctx.fill_uniform(A, -1.0, 1.0, seed)
+        ctx.fill_uniform(B, -1.0, 1.0, seed + 1)
+        ctx.synchronize()
+        a = A.to_host()
+        M = a.reshape(order, lda)[:, :order].T.astype(np.float64)  # M[i, j] = A(i, j)
+        i, j = np.arange(order)[:, None], np.arange(order)[None, :]
+        stored = (i > j) if uplo == 1 else (i < j)
+        if not unit:
+            stored = stored | (i == j)
+        poison = a.reshape(order, lda).copy()
+        poison[:, :order][~stored.T] = np.nan  # (column-major: row index j of the view = column)
+        ctx.h2d(A.ptr, poison.reshape(-1))
+        bin_ = B.to_host()
+        fn = ctx.dtrmm if dt == np.float64 else ctx.strmm
+        fn(side, uplo, trans, 1 if unit else 0, m, n, alpha, A, lda, B, ldb)
+        got = B.to_host()
+    finally:
+        A.free()
+        B.free()
+    T = np.where(stored, M, 0.0)
+    if unit:
+        T[np.arange(order), np.arange(order)] = 1.0
+    opA = T.T if trans else T
+    Bm = bin_.reshape(n, ldb)[:, :m].T.astype(np.float64)
+    pad = np.ones((n, ldb), bool)
+    pad[:, :m] = False
+    assert bits_equal(got.reshape(n, ldb)[pad], bin_.reshape(n, ldb)[pad])
+    eps = EPS_DD if dt == np.float64 else EPS32
+    rng = np.random.default_rng(seed)
+    cols = np.unique(np.concatenate([[0, n - 1, min(n - 1, 127), min(n - 1, 128)], rng.integers(0, n, 12)]))
+    G = got.reshape(n, ldb)[:, :m].T.astype(np.float64)
+    for c in cols:
+        if side == 1:
+            ref = alpha * (opA @ Bm[:, c])
+            ad = abs(alpha) * (np.abs(opA) @ np.abs(Bm[:, c]))
+        else:
+            ref = alpha * (Bm @ opA[:, c])
+            ad = abs(alpha) * (np.abs(Bm) @ np.abs(opA[:, c]))
+        assert np.all(np.isfinite(G[:, c])), f"column {c}: the unreferenced triangle leaked"
+        assert np.all(np.abs(G[:, c] - ref) <= eps * (order + 2) * ad), f"column {c}"
+
+
+@pytest.mark.parametrize("side,uplo,trans", list(itertools.product([1, 2], [1, 2], [0, 1])))
+@pytest.mark.parametrize("unit", [0, 1])
+@pytest.mark.parametrize("dims", [(3000, 2900), (700, 260)])
+def test_strmm_large_unreferenced_nan(ctx, side, uplo, trans, unit, dims):
+    # 3000 x 2900 puts the banded launch on 128-tiles with edge tiles,
+    # 700 x 260 on 64-tiles; NaN wherever A is not referenced
+    m, n = dims
+    order = m if side == 1 else n
+    print(f"strmm side={side} uplo={uplo} trans={trans} unit={unit} {m}x{n}", flush=True)
+    trmm_sampled(ctx, side, uplo, trans, unit, m, n, 0.75, order + 4, m + 3, 77 + order)
+
+
 # ------------------------------------------------------------ strsm
 def well_conditioned(c, N):
     # tests/strsm/src/test.strsm.js:294-296: off-diagonals in [-1/N, 1/N), diagonal 2

@@ -414,6 +414,20 @@ def test_dtrmm_multi_tile(ctx, N, pad, layout, side, uplo, transA):
     check_trmm(ctx, rc.tri_call(tri_case(layout, side, uplo, transA, diag, N, 72, pad), F64))
 
 
+@pytest.mark.parametrize("side,uplo,trans", list(itertools.product([1, 2], [1, 2], [0, 1])))
+@pytest.mark.parametrize("unit", [0, 1])
+@pytest.mark.parametrize("dims", [(3000, 2900), (700, 260)])
+def test_dtrmm_large_unreferenced_nan(ctx, side, uplo, trans, unit, dims):
+    # 128-tiles with edge tiles, and 64-tiles; NaN wherever A is not
+    # referenced
+    from tests.test_gpu_level3 import trmm_sampled
+
+    m, n = dims
+    order = m if side == 1 else n
+    print(f"dtrmm side={side} uplo={uplo} trans={trans} unit={unit} {m}x{n}", flush=True)
+    trmm_sampled(ctx, side, uplo, trans, unit, m, n, 0.75, order + 2, m + 3, 88 + order, np.float64)
+
+
 @pytest.mark.parametrize("mn", [(0, 4), (4, 0)])
 def test_dtrmm_zero_dimension(ctx, mn):
     # test.dtrmm.js:141-171

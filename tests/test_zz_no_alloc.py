@@ -118,6 +118,10 @@ def test_noalloc_paths_without_split(ctx):
     print("noalloc case small kernel 300x200x100 and alpha = 0", flush=True)
     _run_pair(ctx, 0, 0, 300, 200, 100, 1.25, -0.5, 301, 35)
     _run_pair(ctx, 1, 1, 256, 128, 64, 0.0, 2.0, 256, 36)
+    # the wide tier (whole 256 x 128 tiles filling a round of two blocks per
+    # CU): no workspace either
+    print("noalloc case wide tier 4096x4096x1024", flush=True)
+    _run_pair(ctx, 1, 0, 4096, 4096, 1024, 1.5, 0.5, 4096, 37)
 
 
 def _free_device_bytes():

@@ -11,7 +11,9 @@
 // Block: 256 threads = 4 waves in a 2x2 grid, block tile BT x BT of C
 // (BT = 128 large tier, 64 small tier), k-tile BK = 128 bytes of k (32
 // floats / 16 doubles); tiny fp32 problems take a
-// one-launch kernel of 32x32 tiles (gemm_small_kernel). Each operand tile is
+// one-launch kernel of 32x32 tiles (gemm_small_kernel), and large fp32
+// problems of whole 256 x 128 tiles the wide tier (gemm_wide_kernel: 16-float
+// k-tiles, 128 x 64 wave tiles, two blocks per CU). Each operand tile is
 // staged in LDS, double buffered, in the orientation it has in memory so the
 // global->LDS path is plain 16-byte copies (for 16-byte aligned operands,
 // copies made by global_load_lds_dwordx4 without passing through
@@ -479,28 +481,28 @@ __device__ __forceinline__ int out_col(int b, int lane) {
 //     16 i + 4 g + q, a run of 4 rows.
 // (fp64 with A k-contiguous holds no runs: drow interleaves; it keeps the
 // scalar path.) All C loads of a batch are issued before any store.
-template <typename T, bool AKC, bool BKC, int MB>
+template <typename T, bool AKC, bool BKC, int MA, int MN, bool ONE_COL = false>
 __device__ __forceinline__ void epilogue_vec(const GemmArgs<T> &p,
-                                             const typename Ty<T>::acc (&acc)[MB][MB],
+                                             const typename Ty<T>::acc (&acc)[MA][MN],
                                              int64_t row0, int64_t col0, int lane) {
   constexpr int VW = Ty<T>::VW;
-  constexpr int RW = MB < VW ? MB : VW;
+  constexpr int RW = MA < VW ? MA : VW;
   const int g = lane >> 4;
   const T alpha = p.alpha, beta = p.beta;
   if constexpr (!AKC) {
     typedef T VN __attribute__((ext_vector_type(RW)));
     // fp32 keeps every column block in flight at once; fp64 (accumulators
-    // in VGPRs) goes one column block at a time.
-    constexpr int JB = sizeof(T) == 4 ? MB : 1;
+    // in VGPRs) and ONE_COL go one column block at a time.
+    constexpr int JB = (sizeof(T) == 4 && !ONE_COL) ? MN : 1;
 #pragma unroll
-    for (int j0 = 0; j0 < MB; j0 += JB) {
-      VN cv[JB][MB / RW][4];
-      T *cp[JB][MB / RW][4];
+    for (int j0 = 0; j0 < MN; j0 += JB) {
+      VN cv[JB][MA / RW][4];
+      T *cp[JB][MA / RW][4];
 #pragma unroll
       for (int jj = 0; jj < JB; ++jj) {
-        const int64_t col = col0 + out_col<BKC, MB, VW>(j0 + jj, lane);
+        const int64_t col = col0 + out_col<BKC, MN, VW>(j0 + jj, lane);
 #pragma unroll
-        for (int h = 0; h < MB / RW; ++h)
+        for (int h = 0; h < MA / RW; ++h)
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
             cp[jj][h][q] = p.C + (row0 + 16 * RW * h + RW * Ty<T>::drow(g, q)) + col * p.ldc;
@@ -510,7 +512,7 @@ __device__ __forceinline__ void epilogue_vec(const GemmArgs<T> &p,
 #pragma unroll
       for (int jj = 0; jj < JB; ++jj)
 #pragma unroll
-        for (int h = 0; h < MB / RW; ++h)
+        for (int h = 0; h < MA / RW; ++h)
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
             VN v;
@@ -525,20 +527,44 @@ __device__ __forceinline__ void epilogue_vec(const GemmArgs<T> &p,
   } else {
     static_assert(sizeof(T) == 4, "vector epilogue with k-contiguous A is fp32 only");
     typedef typename Ty<T>::v4 V4;
-    V4 cv[MB][MB];
-    T *cp[MB][MB];
+    if constexpr (ONE_COL) {
 #pragma unroll
-    for (int i = 0; i < MB; ++i)
+      for (int j = 0; j < MN; ++j) {
+        const int64_t col = col0 + out_col<BKC, MN, VW>(j, lane);
+        V4 cv[MA];
+        T *cp[MA];
 #pragma unroll
-      for (int j = 0; j < MB; ++j) {
-        const int64_t col = col0 + out_col<BKC, MB, VW>(j, lane);
+        for (int i = 0; i < MA; ++i) {
+          cp[i] = p.C + (row0 + 16 * i + 4 * g) + col * p.ldc;
+          if (beta != (T)0) cv[i] = *reinterpret_cast<const V4 *>(cp[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < MA; ++i) {
+          V4 v;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            T x = alpha * acc[i][j][q];
+            v[q] = beta != (T)0 ? fma(beta, cv[i][q], x) : x;
+          }
+          *reinterpret_cast<V4 *>(cp[i]) = v;
+        }
+      }
+      return;
+    }
+    V4 cv[MA][MN];
+    T *cp[MA][MN];
+#pragma unroll
+    for (int i = 0; i < MA; ++i)
+#pragma unroll
+      for (int j = 0; j < MN; ++j) {
+        const int64_t col = col0 + out_col<BKC, MN, VW>(j, lane);
         cp[i][j] = p.C + (row0 + 16 * i + 4 * g) + col * p.ldc;
         if (beta != (T)0) cv[i][j] = *reinterpret_cast<const V4 *>(cp[i][j]);
       }
 #pragma unroll
-    for (int i = 0; i < MB; ++i)
+    for (int i = 0; i < MA; ++i)
 #pragma unroll
-      for (int j = 0; j < MB; ++j) {
+      for (int j = 0; j < MN; ++j) {
         V4 v;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -1026,7 +1052,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs<T> &p, int tm, int tn, 
       q.ldc = BTM;
       q.alpha = (T)1;
       q.beta = (T)0;
-      epilogue_vec<T, AKC, BKC, MB>(q, acc, wm, wn, lane);
+      epilogue_vec<T, AKC, BKC, MB, MB>(q, acc, wm, wn, lane);
     } else {
 #pragma unroll
       for (int i = 0; i < MB; ++i)
@@ -1043,7 +1069,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs<T> &p, int tm, int tn, 
   const bool tri_diag = p.uplo != 0 && tm == tn;
   if constexpr (!AKC || sizeof(T) == 4) {
     if (interior && !tri_diag && p.c_vec) {
-      epilogue_vec<T, AKC, BKC, MB>(p, acc, m0 + wm, n0 + wn, lane);
+      epilogue_vec<T, AKC, BKC, MB, MB>(p, acc, m0 + wm, n0 + wn, lane);
       return;
     }
   }
@@ -1149,6 +1175,270 @@ __global__ __launch_bounds__(kThreads, (VEC || (AKC && BKC) ||
       gemm_tile<T, BT, BT, kThreads, AKC, BKC, VEC>(p, tm, tn, -1, lo, hi - lo, smem, t);
     }
   }
+}
+
+// Wide fp32 tier: 256 x 128 tiles of C, two blocks of 4 waves per CU, each
+// wave a 128 x 64 part of the tile (8 x 4 MFMA blocks, 128 accumulator
+// registers), k-tiles of 16 floats in a ring of three 24 KB LDS stages
+// (72 KB per block), copies issued two k-tiles ahead. Per flop it copies
+// 3/4 of the operand bytes of a 128 x 128 tile, and the second block on a
+// CU covers each block's epilogue.
+constexpr int kWideM = 256, kWideN = 128, kWideBK = 16, kWideStages = 3;
+
+// s_waitcnt immediate (gfx9 encoding): at most n vector-memory operations of
+// this wave in flight (vmcnt, bits 3:0 and 15:14), every LDS operation
+// complete (lgkmcnt 0), exports not waited for.
+constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4); }
+
+// Waits until at most VM of this wave's copies are in flight and its LDS
+// reads are done, then joins the block barrier. No memory fence: a fence
+// would wait for every copy in flight (vmcnt 0); the empty asm statements
+// keep the compiler from moving memory accesses across the barrier and the
+// sched_barriers keep the scheduler from moving anything.
+template <int VM>
+__device__ __forceinline__ void wait_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm(VM));
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// Copies of one operand's BT x 16 k-tile, 256 threads, 16 bytes each:
+//   KC (k-contiguous): staged [row][k], 64-byte rows whose four 16-byte
+//     chunks sit at chunk ^ ((row >> 2) & 3): a 16-lane read of one chunk of
+//     16 consecutive rows then touches every bank once;
+//   !KC: staged [k][row], rows of BT floats.
+// Thread t's copy r lands at 16 t bytes + r * 4 KB of the operand's stage
+// (the LDS DMA address rule), so each thread reads the global vector that
+// belongs there.
+template <int BT, bool KC>
+struct WideStager {
+  static constexpr int LOADS = BT / 64;  // 16-byte copies per thread per k-tile
+  static constexpr int ELEMS = BT * kWideBK;
+  const float *origin;  // k-tile 0 of the tile
+  int64_t k_step;       // elements per k-tile
+  uint32_t voff[LOADS];
+  __device__ void init(const float *P, int64_t ld, int64_t row0, int t) {
+    if (KC) {
+      origin = P + row0 * ld;
+      k_step = kWideBK;
+      const int row = t >> 2, pos = t & 3, key = (t >> 4) & 3;
+#pragma unroll
+      for (int r = 0; r < LOADS; ++r)
+        voff[r] = (uint32_t)((((int64_t)(row + 64 * r)) * ld + 4 * (pos ^ key)) * (int64_t)sizeof(float));
+    } else {
+      origin = P + row0;
+      k_step = kWideBK * ld;
+      constexpr int VPK = BT / 4, KROWS = 256 / VPK;
+      const int mv = t % VPK, kk = t / VPK;
+#pragma unroll
+      for (int r = 0; r < LOADS; ++r)
+        voff[r] = (uint32_t)((((int64_t)(kk + KROWS * r)) * ld + 4 * mv) * (int64_t)sizeof(float));
+    }
+  }
+  // The wave-uniform tile origin of k-tile kt.
+  __device__ const char *base(int kt) const {
+    const uint64_t o64 = (uint64_t)(origin + (int64_t)kt * k_step);
+    uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)o64);
+    uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(o64 >> 32));
+    asm volatile("" : "+s"(lo), "+s"(hi));
+    return (const char *)(((uint64_t)hi << 32) | lo);
+  }
+  // Copy r of this thread from origin o into its operand stage.
+  __device__ void copy_one(const char *o, float *stage, int wave, int r) const {
+    uint32_t v = voff[r];
+    asm volatile("" : "+v"(v));
+    copy16_to_lds(o + v, stage + wave * 256 + r * 1024);
+  }
+  __device__ void copy(float *stage, int kt, int wave) const {
+    const char *o = base(kt);
+#pragma unroll
+    for (int r = 0; r < LOADS; ++r) copy_one(o, stage, wave, r);
+  }
+};
+
+// MFMA operands of one 16-k tile for MB 16-row blocks from rows wrow.. of
+// a wide stage (the k order and row placement of fetch_operands).
+template <int BT, bool KC, int MB>
+__device__ __forceinline__ void wide_operands(const float *stage, int wrow, int lane,
+                                              float (&out)[4][MB]) {
+  typedef float V4 __attribute__((ext_vector_type(4)));
+  const int g = lane >> 4, i16 = lane & 15;
+  if (KC) {
+    const int pos = g ^ ((i16 >> 2) & 3);
+#pragma unroll
+    for (int b = 0; b < MB; ++b) {
+      V4 v = *reinterpret_cast<const V4 *>(stage + (wrow + 16 * b + i16) * kWideBK + 4 * pos);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) out[s][b] = v[s];
+    }
+  } else {
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int h = 0; h < MB / 4; ++h) {
+        V4 v = *reinterpret_cast<const V4 *>(stage + (4 * g + s) * BT + wrow + 64 * h + 4 * i16);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) out[s][4 * h + c] = v[c];
+      }
+  }
+}
+
+// Read `idx` of wide_operands' reads (KC: block idx; !KC: step idx / (MB / 4),
+// row group idx % (MB / 4)), so reads can be placed one by one.
+template <int BT, bool KC, int MB>
+__device__ __forceinline__ void wide_read(const float *stage, int wrow, int lane, float (&out)[4][MB],
+                                          int idx) {
+  typedef float V4 __attribute__((ext_vector_type(4)));
+  const int g = lane >> 4, i16 = lane & 15;
+  if (KC) {
+    const int pos = g ^ ((i16 >> 2) & 3);
+    V4 v = *reinterpret_cast<const V4 *>(stage + (wrow + 16 * idx + i16) * kWideBK + 4 * pos);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) out[s][idx] = v[s];
+  } else {
+    const int s = idx / (MB / 4), h = idx % (MB / 4);
+    V4 v = *reinterpret_cast<const V4 *>(stage + (4 * g + s) * BT + wrow + 64 * h + 4 * i16);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) out[s][4 * h + c] = v[c];
+  }
+}
+
+// v_mfma_f32_16x16x4f32 with the accumulator pinned in AGPRs. Left to the
+// builtin at two waves per SIMD, the compiler either took the VGPR form and
+// spilled or kept its AGPRs as spill space (100-230 v_accvgpr moves per
+// k-tile pair). Being volatile, these statements also keep the memory
+// operations between them where the source puts them.
+__device__ __forceinline__ void mfma_agpr(Ty<float>::acc &c, float a, float b) {
+  asm volatile("v_mfma_f32_16x16x4_f32 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+}
+
+// The host launches it only with m % 256 == 0, n % 128 == 0, k a multiple
+// of 16 with at least 3 k-tiles, 16-byte aligned operands with 32-bit copy
+// offsets, a vector-aligned C, full C (no triangle, band or split). Measured
+// at 8192^3 on MI355X against the 128 x 128 tier (A/B, one box): NN 148.9
+// -> 151.3, NT 148.9 -> 150.2, TN 148.9 -> 150.0, TT 148.4 -> 150.3
+// TFLOP/s; timing-only variants put its copies at ~1.5% (2.8% in the 128
+// tier) and its epilogue at ~0.6%.
+template <bool AKC, bool BKC>
+__global__ __launch_bounds__(kThreads, 2) void gemm_wide_kernel(GemmArgs<float> p) {
+  typedef float T;
+  typedef Ty<T>::acc Acc;
+  constexpr int MA = kWideM / 32, MN = kWideN / 32;
+  typedef WideStager<kWideM, AKC> SA;
+  typedef WideStager<kWideN, BKC> SB;
+  constexpr int STAGE = SA::ELEMS + SB::ELEMS;
+  constexpr int NCOPY = SA::LOADS + SB::LOADS;  // copies per thread per k-tile
+  __shared__ __attribute__((aligned(16))) T smem[kWideStages * STAGE];
+
+  int tm, tn;
+  logical_tile(xcd_remap((int)blockIdx.x, p.ntiles), p.tiles_m, p.tiles_n, 0, tm, tn);
+  const int t = (int)threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int wm = (wave & 1) * (kWideM / 2), wn = (wave >> 1) * (kWideN / 2);
+  SA sa;
+  SB sb;
+  sa.init(p.A, p.lda, (int64_t)tm * kWideM, t);
+  sb.init(p.B, p.ldb, (int64_t)tn * kWideN, t);
+  const int nkt = (int)(p.k / kWideBK);
+  auto copy = [&](T *st, int kt) {
+    sa.copy(st, kt, wave);
+    sb.copy(st + SA::ELEMS, kt, wave);
+  };
+  Acc acc[MA][MN];
+#pragma unroll
+  for (int i = 0; i < MA; ++i)
+#pragma unroll
+    for (int j = 0; j < MN; ++j) acc[i][j] = Acc(0);
+  // One copy per 8 MFMAs (5 and 3 measured slower, 10 the same).
+  constexpr int kMfmaPerCopy = 8;
+  static_assert(kMfmaPerCopy * NCOPY <= 2 * MA * MN, "copies fit in half a k-tile");
+  // MFMA q (0..63) of half h of a k-tile: k-step 2h + q / 32, block (i, j) =
+  // ((q % 32) / MN, q % MN); an accumulator recurs every 32 MFMAs.
+  auto mf = [&](const T (&a)[4][MA], const T (&b)[4][MN], int h, int q) {
+    const int st = 2 * h + q / 32, i = (q % 32) / MN, j = q % MN;
+    mfma_agpr(acc[i][j], a[st][i], b[st][j]);
+  };
+  // First half of a k-tile: k-steps 0-1, one copy of k-tile ckt into stage
+  // cst after every kMfmaPerCopy MFMAs.
+  auto half0 = [&](const T (&a)[4][MA], const T (&b)[4][MN], T *cst, int ckt) {
+    ckt = ckt < nkt ? ckt : nkt - 1;
+    const char *oa = sa.base(ckt), *ob = sb.base(ckt);
+#pragma unroll
+    for (int q = 0; q < 64; ++q) {
+      mf(a, b, 0, q);
+      if (q % kMfmaPerCopy == kMfmaPerCopy - 1 && q / kMfmaPerCopy < NCOPY) {
+        const int r = q / kMfmaPerCopy;
+        if (r < SA::LOADS)
+          sa.copy_one(oa, cst, wave, r);
+        else
+          sb.copy_one(ob, cst + SA::ELEMS, wave, r - SA::LOADS);
+      }
+    }
+  };
+  // Second half: k-steps 2-3, the next k-tile's 12 operand reads from stage
+  // rst after the first 12 MFMAs, one per MFMA.
+  auto half1 = [&](const T (&a)[4][MA], const T (&b)[4][MN], const T *rst, T (&na)[4][MA],
+                   T (&nb)[4][MN]) {
+#pragma unroll
+    for (int q = 0; q < 64; ++q) {
+      mf(a, b, 1, q);
+      if (q < MA)
+        wide_read<kWideM, AKC, MA>(rst, wm, lane, na, q);
+      else if (q < MA + MN)
+        wide_read<kWideN, BKC, MN>(rst + SA::ELEMS, wn, lane, nb, q - MA);
+    }
+  };
+
+  copy(smem, 0);
+  copy(smem + STAGE, 1);
+  wait_barrier<NCOPY>();
+  T x[4][MA], xb[4][MN], y[4][MA], yb[4][MN];
+  wide_operands<kWideM, AKC, MA>(smem, wm, lane, x);
+  wide_operands<kWideN, BKC, MN>(smem + SA::ELEMS, wn, lane, xb);
+  // Two k-tiles per iteration (x / xb, then y / yb). For k-tile kt, with
+  // its operands in registers and k-tile kt + 1 in flight or landed:
+  //   copies of k-tile kt + 2 into its stage (which held k-tile kt - 1,
+  //   whose reads every wave finished before the previous barrier) under
+  //   the MFMAs of k-steps 0-1 of k-tile kt;
+  //   wait for k-tile kt + 1 (k-tile kt + 2 may still be in flight),
+  //   barrier, its operands read into the other registers under the MFMAs
+  //   of k-steps 2-3.
+  // Copies past the last k-tile re-copy it (a valid address) into a stage
+  // nobody reads again, so every iteration is the same branch-free code.
+  int s0 = 0, kt = 0;
+  for (; kt + 1 < nkt; kt += 2) {
+    const int s1 = s0 == 2 ? 0 : s0 + 1, s2 = s1 == 2 ? 0 : s1 + 1;
+    half0(x, xb, smem + s2 * STAGE, kt + 2);
+    wait_barrier<NCOPY>();
+    half1(x, xb, smem + s1 * STAGE, y, yb);
+    half0(y, yb, smem + s0 * STAGE, kt + 3);
+    wait_barrier<NCOPY>();
+    half1(y, yb, smem + s2 * STAGE, x, xb);
+    s0 = s2;
+  }
+  if (kt < nkt) {  // an odd k-tile count's last k-tile
+#pragma unroll
+    for (int q = 0; q < 128; ++q) mf(x, xb, q / 64, q % 64);
+  }
+  // The accumulators are read next, by instructions the compiler places
+  // without knowing the asm statements were MFMAs: wait out the last ones
+  // (32 wait states cover an 8-pass MFMA's result), in statements that also
+  // redefine every accumulator, so each later read depends on them.
+  static_assert(MA * MN == 32, "four groups of eight accumulators");
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7"
+               : "+a"(acc[0][0]), "+a"(acc[0][1]), "+a"(acc[0][2]), "+a"(acc[0][3]),
+                 "+a"(acc[1][0]), "+a"(acc[1][1]), "+a"(acc[1][2]), "+a"(acc[1][3]));
+#pragma unroll
+  for (int i = 2; i < MA; i += 2)
+    asm volatile("" : "+a"(acc[i][0]), "+a"(acc[i][1]), "+a"(acc[i][2]), "+a"(acc[i][3]),
+                      "+a"(acc[i + 1][0]), "+a"(acc[i + 1][1]), "+a"(acc[i + 1][2]), "+a"(acc[i + 1][3]));
+  // No copy may land in LDS after the block has ended.
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+  epilogue_vec<T, AKC, BKC, MA, MN, true>(p, acc, (int64_t)tm * kWideM + wm,
+                                          (int64_t)tn * kWideN + wn, lane);
 }
 
 // Small GEMMs (a few hundred 32x32 tiles of C, k <= kSmallMaxK): one block
@@ -1574,6 +1864,32 @@ int gemm_launch(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64
   const int64_t off_cap = (int64_t)1 << 31;
   const bool offs32 = 256 * lda * (int64_t)sizeof(T) < off_cap && 256 * ldb * (int64_t)sizeof(T) < off_cap;
   const bool vec = (lda % VW == 0) && (ldb % VW == 0) && aligned16(A) && aligned16(B) && offs32;
+  if constexpr (sizeof(T) == 4) {
+    // Wide tier: whole 256 x 128 tiles filling whole rounds of two blocks
+    // per CU over a long k (8192^3: 2048 tiles, four rounds), full C only;
+    // everything else (edge tiles, triangles, bands, split-k tails, the
+    // two-part k range) stays on the 128 / 64 tiers.
+    const int64_t wtiles = (m / kWideM) * (n / kWideN);
+    if (vec && a.c_vec && uplo == 0 && band == wgb::kBandNone && !A2 && m % kWideM == 0 &&
+        n % kWideN == 0 && k % kWideBK == 0 && k >= 1024 && wtiles > 0 && wtiles % (2 * fill) == 0 &&
+        wtiles <= INT32_MAX) {
+      a.tiles_m = (int)(m / kWideM);
+      a.tiles_n = (int)(n / kWideN);
+      a.ntiles = (int)wtiles;
+      a.nregular = a.ntiles;
+      a.splits = 1;
+      a.kt_split = (int)(k / kWideBK);
+      a.ws = nullptr;
+      void *args[] = {&a};
+      const void *fn = akc ? (bkc ? reinterpret_cast<const void *>(gemm_wide_kernel<true, true>)
+                                  : reinterpret_cast<const void *>(gemm_wide_kernel<true, false>))
+                           : (bkc ? reinterpret_cast<const void *>(gemm_wide_kernel<false, true>)
+                                  : reinterpret_cast<const void *>(gemm_wide_kernel<false, false>));
+      WGB_CHECK_HIP(hipLaunchKernel(fn, dim3((unsigned)wtiles), dim3(kThreads), args, 0, ctx->stream));
+      WGB_CHECK_LAUNCH("gemm_wide_kernel");
+      return WGB_OK;
+    }
+  }
   if (A2) {
     constexpr int BK = 128 / (int)sizeof(T);
     if (!(vec && aligned16(A2) && aligned16(B2) && k % BK == 0 && akc == bkc && band == wgb::kBandNone)) {

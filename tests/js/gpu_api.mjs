@@ -827,41 +827,57 @@ test("sgemv alpha = 0, beta = 1 in benchmark mode reports this call's gpuTimeMs"
   }
 });
 
-// A GpuMatrix / GpuVector holds native elements of its dtype: the fp32
-// routines reject Float64Array-backed resident operands (they cannot read
-// doubles as floats).
-test("fp32 routines reject Float64Array-backed resident operands", async () => {
-  const M = (dt) => wg.GpuMatrix.from(device, new dt(64).fill(1), 8, 8, 8, "column-major");
-  const V = (dt) => wg.GpuVector.from(device, new dt(8).fill(1));
+// fp32 routines given a Float64Array-backed resident operand compute on its
+// float32 rounding, as wgblas's fp32 routines compute on the `_buf` (float32
+// high half) of such an operand (src/util/f64.mjs:33-63); an output then
+// reads back as the float32 result plus its old low half. Every operand
+// starts at 1 + 2^-30 (high half 1, low half 2^-30), so each call must equal
+// the all-Float32Array call on ones, plus 2^-30 in an f64-backed output.
+test("fp32 routines read Float64Array-backed resident operands as float32", async () => {
+  const v = 1 + 2 ** -30;
+  const M = (dt) => wg.GpuMatrix.from(device, new dt(64).fill(dt === Float64Array ? v : 1), 8, 8, 8, "column-major");
+  const V = (dt) => wg.GpuVector.from(device, new dt(8).fill(dt === Float64Array ? v : 1));
   const N = "no-transpose";
   const cases = [
-    ["sgemm", ["A", "B", "C"], (o) => wg.sgemm(device, N, N, 8, 8, 8, 1, o.A, 8, o.B, 8, 0, o.C, 8)],
-    ["sgemmtr", ["A", "B", "C"], (o) => wg.sgemmtr(device, "lower", N, N, 8, 8, 8, 1, o.A, 8, o.B, 8, 0, o.C, 8)],
-    ["ssyrk", ["A", "C"], (o) => wg.ssyrk(device, "lower", N, 8, 8, 1, o.A, 8, 0, o.C, 8)],
-    ["ssyr2k", ["A", "B", "C"], (o) => wg.ssyr2k(device, "lower", N, 8, 8, 1, o.A, 8, o.B, 8, 0, o.C, 8)],
-    ["ssymm", ["A", "B", "C"], (o) => wg.ssymm(device, "left", "lower", 8, 8, 1, o.A, 8, o.B, 8, 0, o.C, 8)],
-    ["strmm", ["A", "B"], (o) => wg.strmm(device, "left", "lower", N, "non-unit", 8, 8, 1, o.A, 8, o.B, 8)],
-    ["strsm", ["A", "B"], (o) => wg.strsm(device, "left", "lower", N, "non-unit", 8, 8, 1, o.A, 8, o.B, 8)],
-    ["sgemv", ["A", "x", "y"], (o) => wg.sgemv(device, N, 8, 8, 1, o.A, 8, o.x, 1, 0, o.y, 1)],
-    ["sdot", ["x", "y"], (o) => wg.sdot(device, 8, o.x, 1, o.y, 1)],
-    ["sasum", ["x"], (o) => wg.sasum(device, 8, o.x, 1)],
-    ["snrm2", ["x"], (o) => wg.snrm2(device, 8, o.x, 1)],
-    ["isamax", ["x"], (o) => wg.isamax(device, 8, o.x, 1)],
+    ["sgemm", ["A", "B", "C"], "C", (o) => wg.sgemm(device, N, N, 8, 8, 8, 1, o.A, 8, o.B, 8, 0.5, o.C, 8)],
+    ["sgemmtr", ["A", "B", "C"], "C", (o) => wg.sgemmtr(device, "lower", N, N, 8, 8, 8, 1, o.A, 8, o.B, 8, 0.5, o.C, 8)],
+    ["ssyrk", ["A", "C"], "C", (o) => wg.ssyrk(device, "lower", N, 8, 8, 1, o.A, 8, 0.5, o.C, 8)],
+    ["ssyr2k", ["A", "B", "C"], "C", (o) => wg.ssyr2k(device, "lower", N, 8, 8, 1, o.A, 8, o.B, 8, 0.5, o.C, 8)],
+    ["ssymm", ["A", "B", "C"], "C", (o) => wg.ssymm(device, "left", "lower", 8, 8, 1, o.A, 8, o.B, 8, 0.5, o.C, 8)],
+    ["strmm", ["A", "B"], "B", (o) => wg.strmm(device, "left", "lower", N, "non-unit", 8, 8, 1, o.A, 8, o.B, 8)],
+    ["strsm", ["A", "B"], "B", (o) => wg.strsm(device, "left", "lower", N, "non-unit", 8, 8, 1, o.A, 8, o.B, 8)],
+    ["sgemv", ["A", "x", "y"], "y", (o) => wg.sgemv(device, N, 8, 8, 1, o.A, 8, o.x, 1, 0.5, o.y, 1)],
+    ["sdot", ["x", "y"], null, (o) => wg.sdot(device, 8, o.x, 1, o.y, 1)],
+    ["sasum", ["x"], null, (o) => wg.sasum(device, 8, o.x, 1)],
+    ["snrm2", ["x"], null, (o) => wg.snrm2(device, 8, o.x, 1)],
+    ["isamax", ["x"], null, (o) => wg.isamax(device, 8, o.x, 1)],
   ];
-  for (const [routine, names, fn] of cases)
-    for (const bad of names) {
-      const o = {};
-      for (const nm of names) {
-        const dt = nm === bad ? Float64Array : Float32Array;
-        o[nm] = nm === "x" || nm === "y" ? V(dt) : M(dt);
-      }
-      try {
-        const kind = bad === "x" || bad === "y" ? "GpuVector" : "GpuMatrix";
-        await assertRejects(() => fn(o), `${bad} must be a Float32Array-backed ${kind}`, `${routine} ${bad}`);
-      } finally {
-        for (const nm of names) o[nm].destroy();
-      }
+  const runWith = async (names, out, fn, f64name) => {
+    const o = {};
+    for (const nm of names) {
+      const dt = nm === f64name ? Float64Array : Float32Array;
+      o[nm] = nm === "x" || nm === "y" ? V(dt) : M(dt);
     }
+    try {
+      const r = await fn(o);
+      return out === null ? Object.values(r)[0] : Array.from(await o[out].read());
+    } finally {
+      for (const nm of names) o[nm].destroy();
+    }
+  };
+  for (const [routine, names, out, fn] of cases) {
+    const base = await runWith(names, out, fn, null);
+    for (const f64name of names) {
+      const got = await runWith(names, out, fn, f64name);
+      if (out === null) {
+        assertEqual(got, base, `${routine} with ${f64name} f64-backed`);
+        continue;
+      }
+      const lo = f64name === out ? 2 ** -30 : 0;
+      for (let i = 0; i < base.length; i++)
+        assertEqual(got[i], base[i] + lo, `${routine} with ${f64name} f64-backed, element ${i}`);
+    }
+  }
 });
 
 test("GpuMatrix.read strips lda padding; GpuVector round trip", async () => {

@@ -10,11 +10,13 @@
 // tests/<routine>/src/test.<routine>.js.
 //
 //   node tests/js/validation.mjs          # invalid cases, no GPU needed
-//   node tests/js/validation.mjs --gpu    # invalid + edge cases on the GPU
+//   node tests/js/validation.mjs --gpu    # invalid + edge cases on the GPU,
+//                                         # plus resident_gpu.mjs
 import { readFileSync } from "fs";
 import { fileURLToPath } from "url";
 import { dirname, join } from "path";
 import { test, run, assertRejects } from "./harness.mjs";
+import { registerResidentTests } from "./resident_gpu.mjs";
 import * as wg from "../../wgblas_amd/js/index.mjs";
 
 const here = dirname(fileURLToPath(import.meta.url));
@@ -532,6 +534,7 @@ async function main() {
   for (const r of ["dasum", "dnrm2", "idamax"])
     register(r, { device: loadParam("device"), n: loadParam("n"), incx: loadParam("incx"), x: loadParam("x64") },
       (a) => wg[r](a.device, a.n, a.x, a.incx), device);
+  if (GPU) registerResidentTests(wg, device);
   await run();
   if (GPU) wg.cleanup();
 }

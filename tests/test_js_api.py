@@ -3,8 +3,11 @@
 CPU: the reference's validation specs (invalid cases) against the JS API, the
 seeded generators against the reference's golden vectors, and the package's
 subpath exports with their TypeScript declarations.
-GPU: the validation edge cases (valid calls must run) and the end-to-end
-API suite through the Node-API addon and libwgblas_hip.
+GPU: the validation edge cases (valid calls must run) plus the resident-operand
+checks of resident_gpu.mjs (GpuMatrix / GpuVector round trips, routines on
+resident operands, Float64Array-backed operands in the fp32 routines,
+gpuName) on one context, and the end-to-end API suite through the Node-API
+addon and libwgblas_hip.
 """
 import os
 import shutil
@@ -43,7 +46,8 @@ def test_js_package_subpaths_resolve_with_declarations():
 
 @pytest.mark.gpu
 def test_js_validation_edge_cases_on_gpu():
-    run_node("validation.mjs", "--gpu")
+    out = run_node("validation.mjs", "--gpu")
+    assert "ok   resident: fp32 routines read Float64Array-backed operands" in out
 
 
 @pytest.mark.gpu

@@ -16,6 +16,7 @@ import { GpuVector } from "./classes/GpuVector.mjs";
 import { requireGpuDevice, requireSameDevice } from "./device.mjs";
 import { lastGpuTimeMs } from "./init.mjs";
 import { native } from "./native.mjs";
+import { narrowResident, needsNarrowing, widenResident } from "./narrow.mjs";
 
 export const NO_TRANS = 0;
 export const TRANS = 1;
@@ -37,9 +38,13 @@ export function checkScalar(name, v) {
   if (!Number.isFinite(v)) throw new Error(`${name} must be finite.`);
 }
 
-/** A resident operand must hold elements of the routine's type. */
+/** The fp64 routines' check that a resident operand holds doubles (e.g.
+ * src/dsymm/dsymm.mjs:74-79). The fp32 routines check nothing: wgblas binds
+ * a Float64Array-backed operand's float32 half, and execute() reads such an
+ * operand through its float32 rounding (narrow.mjs). */
 export function checkResidentDtype(name, X, isGpu, arr, kind = "GpuMatrix") {
-  if (isGpu && X.dtype !== arr) throw new Error(`${name} must be a ${arr.name}-backed ${kind}.`);
+  if (arr === Float64Array && isGpu && X.dtype !== arr)
+    throw new Error(`${name} must be a ${arr.name}-backed ${kind}.`);
 }
 
 export function checkUplo(uplo) {
@@ -93,10 +98,11 @@ export function checkGemm(device, a, opts) {
   for (const [name, X, isGpu] of [["A", a.A, AIsGpu], ["B", a.B, BIsGpu], ["C", a.C, CIsGpu]]) {
     if (!isGpu && !(X instanceof arr)) throw new Error(`${name} must be a ${arrName} or GpuMatrix.`);
   }
-  // A GpuMatrix holds native elements of its dtype: an fp32 routine cannot
-  // read a Float64Array-backed one, nor an fp64 routine a Float32Array one.
+  // dgemm / dgemmtr need Float64Array-backed GpuMatrix operands
+  // (src/dgemm/dgemm.mjs:73-78); sgemm / sgemmtr read any GpuMatrix through
+  // its float32 values (execute()).
   for (const [name, X, isGpu] of [["A", a.A, AIsGpu], ["B", a.B, BIsGpu], ["C", a.C, CIsGpu]])
-    if (isGpu && X.dtype !== arr) throw new Error(`${name} must be a ${arrName}-backed GpuMatrix.`);
+    checkResidentDtype(name, X, isGpu, arr);
   if ((AIsGpu || BIsGpu) && !CIsGpu) throw new Error("C must be a GpuMatrix when A or B is a GpuMatrix.");
   if (CIsGpu && (!AIsGpu || !BIsGpu)) throw new Error("A and B must be GpuMatrix when C is a GpuMatrix.");
   if (a.m < 0 || a.n < 0 || a.k < 0) throw new Error("m, n, and k must be non-negative.");
@@ -128,7 +134,9 @@ export function toColumnMajor(a, eff, uplo) {
  * buffers (freed before returning) and the output C is read back into a new
  * typed array (the input is not modified), returned under `key` ("C", "B"
  * for strmm / strsm, "y" for sgemv); GpuMatrix / GpuVector operands are used
- * in place.
+ * in place, except a Float64Array-backed one in an fp32 routine, which is
+ * read through a float32 copy and, as the output, written back as wgblas's
+ * read() would return it (narrow.mjs).
  * `launch(ctx, ptrs, ptrC)` issues the call.
  */
 export function execute(device, operands, C, CIsGpu, arrayType, launch, key = "C") {
@@ -136,25 +144,31 @@ export function execute(device, operands, C, CIsGpu, arrayType, launch, key = "C
   const ctx = device.ctx();
   const temps = [];
   const cache = new Map();
+  const narrowed = new Map();
   const upload = (X) => {
     const p = nat.malloc(ctx, X.byteLength);
     temps.push(p);
     nat.upload(ctx, p, X);
     return p;
   };
+  const narrowOf = (X) => {
+    if (!narrowed.has(X)) narrowed.set(X, narrowResident(nat, ctx, X, temps));
+    return narrowed.get(X);
+  };
   // Read-only inputs passed as the same array share one upload; C always
   // gets its own buffer, so an input aliasing C is read unmodified.
   const resident = (X) => X instanceof GpuMatrix || X instanceof GpuVector;
   const ptrOf = (X) => {
-    if (resident(X)) return X._buf;
+    if (resident(X)) return needsNarrowing(X, arrayType) ? narrowOf(X).p : X._buf;
     if (!cache.has(X)) cache.set(X, upload(X));
     return cache.get(X);
   };
   try {
     const ptrs = operands.map(ptrOf);
-    const pC = resident(C) ? C._buf : upload(C);
+    const pC = resident(C) ? ptrOf(C) : upload(C);
     launch(ctx, ptrs, pC);
     const t = lastGpuTimeMs(device);
+    if (CIsGpu && needsNarrowing(C, arrayType)) widenResident(nat, ctx, C, narrowOf(C));
     if (CIsGpu) return t === undefined ? {} : { gpuTimeMs: t };
     const out = new arrayType(C.length);
     nat.download(ctx, pC, out);

@@ -30,8 +30,8 @@ export function syrk(routine, device, uplo, trans, n, k, alpha, A, lda, beta, C,
     if (!Number.isInteger(v)) throw new Error("n, k, lda, and ldc must be integers.");
   if (!AIsGpu && !(A instanceof arr)) throw new Error(`A must be a ${arrName} or GpuMatrix.`);
   if (!CIsGpu && !(C instanceof arr)) throw new Error(`C must be a ${arrName} or GpuMatrix.`);
-  if (AIsGpu && A.dtype !== arr) throw new Error(`A must be a ${arrName}-backed GpuMatrix.`);
-  if (CIsGpu && C.dtype !== arr) throw new Error(`C must be a ${arrName}-backed GpuMatrix.`);
+  if (f64 && AIsGpu && A.dtype !== arr) throw new Error(`A must be a ${arrName}-backed GpuMatrix.`);
+  if (f64 && CIsGpu && C.dtype !== arr) throw new Error(`C must be a ${arrName}-backed GpuMatrix.`);
   if (AIsGpu && !CIsGpu) throw new Error("C must be a GpuMatrix when A is a GpuMatrix.");
   if (CIsGpu && !AIsGpu) throw new Error("A must be a GpuMatrix when C is a GpuMatrix.");
   if (n < 0 || k < 0) throw new Error("n and k must be non-negative.");

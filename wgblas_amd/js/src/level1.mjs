@@ -8,6 +8,7 @@ import { GpuVector } from "./classes/GpuVector.mjs";
 import { requireGpuDevice, requireSameDevice } from "./device.mjs";
 import { lastGpuTimeMs } from "./init.mjs";
 import { native } from "./native.mjs";
+import { narrowResident, needsNarrowing } from "./narrow.mjs";
 
 export const KIND = { sdot: 0, sasum: 1, snrm2: 2, isamax: 3, ddot: 4, dasum: 5, dnrm2: 6, idamax: 7 };
 
@@ -24,12 +25,12 @@ export function reduceOne(routine, device, n, x, incx, emptyValue) {
   if (incx <= 0) throw new Error("incx must be positive.");
   if (!xIsGpu && !(x instanceof (f64 ? Float64Array : Float32Array)))
     throw new Error(`x must be a ${arrName} or GpuVector.`);
-  if (xIsGpu && x.dtype !== (f64 ? Float64Array : Float32Array))
-    throw new Error(`x must be a ${arrName}-backed GpuVector.`);
+  if (f64 && xIsGpu && x.dtype !== Float64Array) throw new Error(`x must be a ${arrName}-backed GpuVector.`);
   if (n <= 0) return { value: emptyValue };
   if (x.length < (n - 1) * incx + 1)
     throw new Error("x does not have enough elements for the given n and incx.");
-  return run(device, [x], (ctx, p) => native().reduce(KIND[routine], ctx, n, p[0], incx));
+  return run(device, [x], f64 ? Float64Array : Float32Array,
+    (ctx, p) => native().reduce(KIND[routine], ctx, n, p[0], incx));
 }
 
 /** The two-vector form (sdot, ddot). */
@@ -46,8 +47,8 @@ export function reduceDot(device, n, x, incx, y, incy, routine = "sdot") {
   if (incx <= 0 || incy <= 0) throw new Error("incx and incy must be positive.");
   if (!xIsGpu && !(x instanceof Arr)) throw new Error(`x must be a ${arrName} or GpuVector.`);
   if (!yIsGpu && !(y instanceof Arr)) throw new Error(`y must be a ${arrName} or GpuVector.`);
-  if (xIsGpu && x.dtype !== Arr) throw new Error(`x must be a ${arrName}-backed GpuVector.`);
-  if (yIsGpu && y.dtype !== Arr) throw new Error(`y must be a ${arrName}-backed GpuVector.`);
+  if (f64 && xIsGpu && x.dtype !== Arr) throw new Error(`x must be a ${arrName}-backed GpuVector.`);
+  if (f64 && yIsGpu && y.dtype !== Arr) throw new Error(`y must be a ${arrName}-backed GpuVector.`);
   if (xIsGpu !== yIsGpu)
     throw new Error(`x and y must be the same type (both ${arrName} or both GpuVector).`);
   if (n <= 0) return { value: 0 };
@@ -55,17 +56,25 @@ export function reduceDot(device, n, x, incx, y, incy, routine = "sdot") {
     throw new Error("x does not have enough elements for the given n and incx.");
   if (y.length < (n - 1) * incy + 1)
     throw new Error("y does not have enough elements for the given n and incy.");
-  return run(device, [x, y], (ctx, p) => native().reduce(KIND[routine], ctx, n, p[0], incx, p[1], incy));
+  return run(device, [x, y], Arr,
+    (ctx, p) => native().reduce(KIND[routine], ctx, n, p[0], incx, p[1], incy));
 }
 
 // Host arrays go to temporary device buffers (freed before returning);
-// GpuVectors are read in place. The scalar result comes back to the host.
-function run(device, vectors, call) {
+// GpuVectors are read in place, a Float64Array-backed one in an fp32
+// routine through its float32 rounding (narrow.mjs: wgblas binds that
+// vector's float32 half). The scalar result comes back to the host.
+function run(device, vectors, arrayType, call) {
   const nat = native();
   const ctx = device.ctx();
   const temps = [];
+  const narrowed = new Map();
   try {
     const ptrs = vectors.map((v) => {
+      if (v instanceof GpuVector && needsNarrowing(v, arrayType)) {
+        if (!narrowed.has(v)) narrowed.set(v, narrowResident(nat, ctx, v, temps).p);
+        return narrowed.get(v);
+      }
       if (v instanceof GpuVector) return v._buf;
       const p = nat.malloc(ctx, v.byteLength);
       temps.push(p);

@@ -2,8 +2,8 @@
 // dger (src/dger/dger.mjs:21-238) on wgb_dger through the same function.
 // Argument checks keep wgblas's order and messages (sger.mjs:30-101,
 // dger.mjs:34-110), the vectors' checks after the layout swap as there. The
-// fp32 routine also rejects a Float64Array-backed resident operand, as every
-// fp32 routine here does. Returns { A } (a new array) for host arrays, {}
+// fp32 routine reads a Float64Array-backed resident operand through its
+// float32 rounding, as every fp32 routine here does (narrow.mjs). Returns { A } (a new array) for host arrays, {}
 // when A is a GpuMatrix (updated in place); plus gpuTimeMs when
 // init({benchmark:true}).
 import { ger } from "./impl/ger.mjs";

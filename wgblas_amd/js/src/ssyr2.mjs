@@ -2,7 +2,8 @@
 // src/ssyr2/ssyr2.mjs:17-184), on wgb_ssyr2; dsyr2 (src/dsyr2/dsyr2.mjs:21-260)
 // on wgb_dsyr2 through the same function. Argument checks keep wgblas's
 // order and messages (ssyr2.mjs:33-91, dsyr2.mjs:37-103); the fp32 routine
-// also rejects Float64Array-backed resident operands. Returns { A } for host
+// reads a Float64Array-backed resident operand through its float32 rounding
+// (narrow.mjs). Returns { A } for host
 // arrays, {} when A is a GpuMatrix; plus gpuTimeMs when
 // init({benchmark:true}).
 import { syr2 } from "./impl/syr2.mjs";

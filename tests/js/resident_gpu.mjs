@@ -34,6 +34,14 @@ const hiOf = (x) => Math.fround(x);
 const loOf = (x) => (Number.isFinite(Math.fround(x)) ? Math.fround(x - Math.fround(x)) : 0);
 
 export function registerResidentTests(wg, device) {
+  test("resident: init() with the same options returns the same device", async () => {
+    // wgblas keys its devices by their options (src/init.mjs:14-41): a
+    // second init() makes no new context
+    const again = await wg.init();
+    assert(again === device, "init() returned another device");
+    assert(again._ctx === device._ctx, "init() made another context");
+  });
+
   test("resident: gpuName names the gfx950 device", async () => {
     const g = wg.gpuName(device);
     assert(typeof g.description === "string" && g.description.length > 0, "description");

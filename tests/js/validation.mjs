@@ -11,7 +11,8 @@
 //
 //   node tests/js/validation.mjs          # invalid cases, no GPU needed
 //   node tests/js/validation.mjs --gpu    # invalid + edge cases on the GPU,
-//                                         # plus resident_gpu.mjs
+//                                         # plus resident_gpu.mjs and
+//                                         # parity_gpu.mjs
 import { readFileSync } from "fs";
 import { fileURLToPath } from "url";
 import { dirname, join } from "path";
@@ -534,7 +535,13 @@ async function main() {
   for (const r of ["dasum", "dnrm2", "idamax"])
     register(r, { device: loadParam("device"), n: loadParam("n"), incx: loadParam("incx"), x: loadParam("x64") },
       (a) => wg[r](a.device, a.n, a.x, a.incx), device);
-  if (GPU) registerResidentTests(wg, device);
+  if (GPU) {
+    registerResidentTests(wg, device);
+    // the JS API's single-context parity cases (fixtures, regressions,
+    // residency) on the same device
+    const parity = await import("./parity_gpu.mjs");
+    parity.setParityDevice(device);
+  }
   await run();
   if (GPU) wg.cleanup();
 }

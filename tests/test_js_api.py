@@ -3,11 +3,15 @@
 CPU: the reference's validation specs (invalid cases) against the JS API, the
 seeded generators against the reference's golden vectors, and the package's
 subpath exports with their TypeScript declarations.
-GPU: the validation edge cases (valid calls must run) plus the resident-operand
-checks of resident_gpu.mjs (GpuMatrix / GpuVector round trips, routines on
-resident operands, Float64Array-backed operands in the fp32 routines,
-gpuName) on one context, and the end-to-end API suite through the Node-API
-addon and libwgblas_hip.
+GPU, in one node process on one context: the validation edge cases (valid
+calls must run), the resident-operand checks of resident_gpu.mjs (GpuMatrix /
+GpuVector round trips, routines on resident operands, Float64Array-backed
+operands in the fp32 routines, init's device cache, gpuName) and the JS API's
+parity cases of parity_gpu.mjs (the reference's edge-case fixtures exactly,
+its regression scenarios, residency forms and layouts), all through the
+Node-API addon and libwgblas_hip. gpu_api.mjs adds the device-handling and
+benchmark-mode cases (a second device, cleanup of one device) to the same
+parity cases; it stays skipped.
 """
 import os
 import shutil
@@ -48,6 +52,9 @@ def test_js_package_subpaths_resolve_with_declarations():
 def test_js_validation_edge_cases_on_gpu():
     out = run_node("validation.mjs", "--gpu")
     assert "ok   resident: fp32 routines read Float64Array-backed operands" in out
+    # the parity cases ran too: fixtures of the GEMM family and of level 3
+    assert "ok   sgemm rm: " in out and "ok   strsm cm: " in out
+    assert int(out.strip().splitlines()[-1].split()[0]) > 2541 + 250
 
 
 @pytest.mark.gpu

@@ -5,7 +5,8 @@
 // gpuName (src/init.mjs:133-143), and Float64Array-backed operands in the
 // fp32 routines, which wgblas computes on the float32 half of their
 // double-double pair (src/util/f64.mjs:33-63). Registered by validation.mjs
-// when it runs with --gpu; every expected value below is exact.
+// when it runs with --gpu (registerCleanupTest after every other case);
+// every expected value below is exact.
 import { test, assert, assertEqual } from "./harness.mjs";
 
 const bitsEqual = (a, b) => {
@@ -190,5 +191,33 @@ export function registerResidentTests(wg, device) {
       gx2.destroy();
       gy2.destroy();
     }
+  });
+}
+
+// Registered last: cleanup() with no argument releases every device
+// (src/init.mjs:110-131); the released device then rejects calls and
+// gpuName() has no device to name. A GpuMatrix made before stays safe to
+// destroy (a no-op once its device is gone).
+export function registerCleanupTest(wg, device) {
+  test("cleanup() releases every device", async () => {
+    const g = wg.GpuMatrix.from(device, new Float32Array([1, 2, 3, 4]), 2, 2);
+    wg.cleanup();
+    assert(device._ctx === null, "device still holds its context");
+    let threw = false;
+    try {
+      wg.gpuName();
+    } catch (e) {
+      threw = /init\(\)/.test(e.message);
+    }
+    assert(threw, "gpuName() after cleanup()");
+    let rejected = false;
+    try {
+      await wg.sdot(device, 2, new Float32Array([1, 2]), 1, new Float32Array([3, 4]), 1);
+    } catch (e) {
+      rejected = /released by cleanup/.test(e.message);
+    }
+    assert(rejected, "a call on the released device");
+    g.destroy();
+    wg.cleanup();  // nothing left: a no-op
   });
 }

@@ -17,7 +17,7 @@ import { readFileSync } from "fs";
 import { fileURLToPath } from "url";
 import { dirname, join } from "path";
 import { test, run, assertRejects } from "./harness.mjs";
-import { registerResidentTests } from "./resident_gpu.mjs";
+import { registerResidentTests, registerCleanupTest } from "./resident_gpu.mjs";
 import * as wg from "../../wgblas_amd/js/index.mjs";
 
 const here = dirname(fileURLToPath(import.meta.url));
@@ -541,6 +541,7 @@ async function main() {
     // residency) on the same device
     const parity = await import("./parity_gpu.mjs");
     parity.setParityDevice(device);
+    registerCleanupTest(wg, device);
   }
   await run();
   if (GPU) wg.cleanup();

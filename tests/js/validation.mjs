@@ -11,8 +11,8 @@
 //
 //   node tests/js/validation.mjs          # invalid cases, no GPU needed
 //   node tests/js/validation.mjs --gpu    # invalid + edge cases on the GPU,
-//                                         # plus resident_gpu.mjs and
-//                                         # parity_gpu.mjs
+//                                         # plus resident_gpu.mjs,
+//                                         # parity_gpu.mjs and fixtures_gpu.mjs
 import { readFileSync } from "fs";
 import { fileURLToPath } from "url";
 import { dirname, join } from "path";
@@ -541,6 +541,9 @@ async function main() {
     // residency) on the same device
     const parity = await import("./parity_gpu.mjs");
     parity.setParityDevice(device);
+    // random fixtures in the shape of the reference's runFixtures
+    const fixtures = await import("./fixtures_gpu.mjs");
+    fixtures.registerFixtureTests(wg, device);
     registerCleanupTest(wg, device);
   }
   await run();

@@ -8,8 +8,10 @@ calls must run), the resident-operand checks of resident_gpu.mjs (GpuMatrix /
 GpuVector round trips, routines on resident operands, Float64Array-backed
 operands in the fp32 routines, init's device cache, gpuName) and the JS API's
 parity cases of parity_gpu.mjs (the reference's edge-case fixtures exactly,
-its regression scenarios, residency forms and layouts), all through the
-Node-API addon and libwgblas_hip. gpu_api.mjs adds the device-handling and
+its regression scenarios, residency forms and layouts) and the random
+fixtures of fixtures_gpu.mjs (100 runs per routine of the path, host and
+GPU-resident, under the reference's metrics), all through the Node-API addon
+and libwgblas_hip. fixtures_selfcheck.mjs checks that checker on the CPU. gpu_api.mjs adds the device-handling and
 benchmark-mode cases (a second device, cleanup of one device) to the same
 parity cases; it stays skipped.
 """
@@ -39,6 +41,25 @@ def test_js_validation_specs():
     assert int(out.strip().splitlines()[-1].split()[0]) > 300
 
 
+@pytest.mark.parametrize("mode,routine", [("beta", "sgemm"), ("trans", "sgemm"), ("tri", "sgemmtr"),
+                                          ("syrk", "ssyrk"), ("dgemm_round", "dgemm"), ("dot", "sdot"),
+                                          ("asum", "sasum"), ("nrm2", "snrm2"), ("amax", "isamax")])
+def test_js_fixture_checker_rejects_planted_mistakes(mode, routine):
+    """fixtures_gpu.mjs's runs and metrics through CPU stand-ins: a mistake
+    planted in one stand-in fails exactly that routine's two fixture cases
+    (host arrays and GPU-resident)."""
+    res = subprocess.run([NODE, os.path.join(ROOT, "tests", "js", "fixtures_selfcheck.mjs"), mode], cwd=ROOT,
+                         capture_output=True, text=True, timeout=300)
+    failed = sorted(ln.split("fixtures: ")[1].split(",")[0] for ln in res.stdout.splitlines()
+                    if ln.startswith("FAIL fixtures: "))
+    assert res.returncode != 0 and failed == [routine, routine], res.stdout[-2000:]
+
+
+def test_js_fixture_checker_passes_exact_stand_ins():
+    out = run_node("fixtures_selfcheck.mjs", "good")
+    assert "16 passed, 0 failed" in out
+
+
 def test_js_random_matches_reference_golden():
     run_node("random.mjs")
 
@@ -54,6 +75,9 @@ def test_js_validation_edge_cases_on_gpu():
     assert "ok   resident: fp32 routines read Float64Array-backed operands" in out
     # the parity cases ran too: fixtures of the GEMM family and of level 3
     assert "ok   sgemm rm: " in out and "ok   strsm cm: " in out
+    # and the random fixtures of every routine on the path, host and resident
+    for r in ("sgemm", "sgemmtr", "ssyrk", "dgemm", "sdot", "sasum", "snrm2", "isamax"):
+        assert f"ok   fixtures: {r}, 100 random runs (GPU-resident)" in out, r
     assert int(out.strip().splitlines()[-1].split()[0]) > 2541 + 250
 
 

@@ -1,8 +1,10 @@
 """Runs the JavaScript-layer suites (tests/js/*.mjs) with node.
 
 CPU: the reference's validation specs (invalid cases) against the JS API, the
-seeded generators against the reference's golden vectors, and the package's
-subpath exports with their TypeScript declarations.
+seeded generators against the reference's golden vectors, the package's
+subpath exports with their TypeScript declarations, the device handling
+(init's cache, cleanup of one device or all) against a stub addon, and the
+random-fixture checker against planted mistakes.
 GPU, in one node process on one context: the validation edge cases (valid
 calls must run), the resident-operand checks of resident_gpu.mjs (GpuMatrix /
 GpuVector round trips, routines on resident operands, Float64Array-backed
@@ -58,6 +60,16 @@ def test_js_fixture_checker_rejects_planted_mistakes(mode, routine):
 def test_js_fixture_checker_passes_exact_stand_ins():
     out = run_node("fixtures_selfcheck.mjs", "good")
     assert "16 passed, 0 failed" in out
+
+
+def test_js_device_handling_against_a_stub_addon():
+    """init()'s cache, cleanup(one) / cleanup(), gpuName's default device and
+    foreign-device operands, through the JS layer with stub_addon.cjs (host
+    memory, no compute calls) in place of the Node-API addon."""
+    env = dict(os.environ, WGBLAS_HIP_ADDON=os.path.join(ROOT, "tests", "js", "stub_addon.cjs"))
+    res = subprocess.run([NODE, os.path.join(ROOT, "tests", "js", "devices_cpu.mjs")], cwd=ROOT, env=env,
+                         capture_output=True, text=True, timeout=120)
+    assert res.returncode == 0 and "3 passed, 0 failed" in res.stdout, res.stdout + res.stderr
 
 
 def test_js_random_matches_reference_golden():

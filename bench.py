@@ -514,7 +514,8 @@ def bench_level3_f64(ctx, reps):
 def run_only(ctx, name, reps, warm=False):
     """One workload alone, `reps` launches, for counter and kernel-trace runs
     (rocprofv3): copy (1 GiB device-to-device, the traffic calibration),
-    sgemm_8192_{NN,NT,TN,TT}, dgemm_4096_{NN,NT,TN,TT} (bare dgemm_4096: NT),
+    sgemm_8192_{NN,NT,TN,TT}, config 3's ragged sgemm_ragged_{NN,NT,TN,TT},
+    dgemm_4096_{NN,NT,TN,TT} (bare dgemm_4096: NT),
     ssyrk_8192, ssyr2k / ssymm / strmm / strsm at 8192 (strsm also 4096),
     dsyr2k / dsymm / dtrmm at 4096, sdot / sasum / snrm2 / isamax at
     n = 2^28. With `warm`, about 30 ms of the same calls run first (the
@@ -545,6 +546,19 @@ def run_only(ctx, name, reps, warm=False):
         ctx.fill_uniform(buf, -1.0, 1.0, 2)
         return go(lambda: ctx.sgemm(ta, tb, n, n, n, 1.5, buf.offset(0), n, buf.offset(n * n), n, 0.5,
                                     buf.offset(2 * n * n), n), {"algorithmic_bytes": 4 * 4 * n * n})
+    if name.startswith("sgemm_ragged"):
+        # config 3's ragged case, one launch per call (bare name: NN)
+        ta, tb = layout(name[len("sgemm_ragged_"):] or "NN")
+        m, n, k = 8191, 8193, 4097
+        ld = lambda r: ((r + 63) // 64) * 64 + 1
+        a_rows, a_cols = (k, m) if ta else (m, k)
+        b_rows, b_cols = (n, k) if tb else (k, n)
+        lda, ldb, ldc = ld(a_rows), ld(b_rows), ld(m)
+        sa, sb, sc = lda * a_cols, ldb * b_cols, ldc * n
+        buf = ctx.empty(sa + sb + sc, np.float32)
+        ctx.fill_uniform(buf, -1.0, 1.0, 2)
+        return go(lambda: ctx.sgemm(ta, tb, m, n, k, 1.5, buf.offset(0), lda, buf.offset(sa), ldb, 0.5,
+                                    buf.offset(sa + sb), ldc), {"algorithmic_bytes": 4 * (sa + sb + 2 * sc)})
     if name.startswith("dgemm_4096"):
         ta, tb = layout(name[len("dgemm_4096_"):] or "NT")
         n = 4096
@@ -746,7 +760,8 @@ def main():
     ap.add_argument("--no-components", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default=None,
-                    help="run one workload alone (copy, sgemm_8192_{NN,NT,TN,TT}, dgemm_4096[_{NN,NT,TN,TT}], ssyrk_8192, "
+                    help="run one workload alone (copy, sgemm_8192_{NN,NT,TN,TT}, sgemm_ragged_{NN,NT,TN,TT}, "
+                         "dgemm_4096[_{NN,NT,TN,TT}], ssyrk_8192, "
                          "ssyr2k_8192, ssymm_8192, strmm_8192, strsm_8192, strsm_4096, dsyr2k_4096, dsymm_4096, dtrmm_4096, "
                          "sdot, sasum, snrm2, "
                          "isamax) for counter and kernel-trace collection")

@@ -10,7 +10,7 @@ import pytest
 
 from oracle import orc
 from tests import refcases
-from tests.helpers import bits_equal, gemm_forward_factor, untouched_mask
+from tests.helpers import EPS32, bits_equal, gemm_forward_factor, untouched_mask
 
 pytestmark = pytest.mark.gpu
 
@@ -231,6 +231,72 @@ def test_odd_leading_dimensions(ctx, ta, tb):
     ld = lambda r: ((r + 63) // 64) * 64 + 1
     check_case(ctx, 0, ta, tb, m, n, k, -0.75, 1.0, lda=ld(k if ta else m), ldb=ld(n if tb else k),
                ldc=ld(m))
+
+
+def _restride(x, rows, cols, ld_from, ld_to):
+    """Column-major rows x cols from leading dimension ld_from to ld_to (new
+    gap cells NaN: they must never be read)."""
+    out = np.full(ld_to * cols, np.nan, x.dtype)
+    out.reshape(cols, ld_to)[:, :rows] = x.reshape(cols, ld_from)[:, :rows]
+    return out
+
+
+@pytest.mark.parametrize("ta", [0, 1])
+@pytest.mark.parametrize("tb", [0, 1])
+@pytest.mark.parametrize("shape", [(1100, 1000, 700), (4100, 4100, 1100)])
+def test_element_aligned_operands_bit_equal_to_aligned(ctx, ta, tb, shape):
+    """fp32 operands that are only element-aligned (ld = 1 mod 64, and a base
+    one float past a 16-byte boundary) take the LDS copies too (the register
+    path for NN); the MFMA sequence does not depend on how a k-tile reaches
+    LDS, so C must equal, bit for bit, the product of the same values stored
+    16-byte aligned (ld a multiple of 64). The shapes put the launch on the
+    64-tile tier and on the 128-tile tier with a split-k tail (1089 tiles:
+    two rounds and 65 tail tiles in k-slices); both include edge tiles and
+    a partial k-tile."""
+    m, n, k = shape
+    a_rows, a_cols = (k, m) if ta else (m, k)
+    b_rows, b_cols = (n, k) if tb else (k, n)
+    up = lambda r: (r + 63) // 64 * 64
+    odd = lambda r: up(r) + 1
+    A = orc.random_f32(up(a_rows) * a_cols, -1, 1, 71)
+    B = orc.random_f32(up(b_rows) * b_cols, -1, 1, 72)
+    C = orc.random_f32(up(m) * n, -1, 1, 73)
+    outs = []
+    for form in ("aligned", "odd_ld", "odd_base"):
+        if form == "aligned":
+            lda, ldb, ldc, shift = up(a_rows), up(b_rows), up(m), 0
+        else:
+            lda, ldb, ldc, shift = odd(a_rows), odd(b_rows), odd(m), (1 if form == "odd_base" else 0)
+            if form == "odd_base":
+                lda, ldb = up(a_rows) + 4, up(b_rows) + 4  # ld a multiple of 4, base misaligned
+        hA = _restride(A, a_rows, a_cols, up(a_rows), lda)
+        hB = _restride(B, b_rows, b_cols, up(b_rows), ldb)
+        hC = _restride(C, m, n, up(m), ldc)
+        pad = lambda h: np.concatenate([np.zeros(shift, np.float32), h])
+        dA, dB, dC = ctx.upload(pad(hA)), ctx.upload(pad(hB)), ctx.upload(hC)
+        try:
+            print(f"element-aligned case {form} ta={ta} tb={tb} {m}x{n}x{k}", flush=True)
+            ctx.sgemm(ta, tb, m, n, k, 1.5, dA.offset(shift), lda, dB.offset(shift), ldb, 0.5, dC, ldc)
+            got = dC.to_host()
+        finally:
+            for d in (dA, dB, dC):
+                d.free()
+        keep = np.ones((n, ldc), bool)
+        keep[:, :m] = False
+        assert bits_equal(got.reshape(n, ldc)[keep], hC.reshape(n, ldc)[keep]), f"{form}: C padding changed"
+        outs.append(got.reshape(n, ldc)[:, :m])
+    assert bits_equal(outs[1], outs[0]), "ld = 1 mod 64 differs from the aligned product"
+    assert bits_equal(outs[2], outs[0]), "misaligned base differs from the aligned product"
+    # and the product itself against the oracle on sampled columns
+    cols = np.unique(np.linspace(0, n - 1, 9).astype(int))
+    opA = (A.reshape(a_cols, up(a_rows))[:, :a_rows].T if not ta
+           else A.reshape(a_cols, up(a_rows))[:, :a_rows]).astype(np.float64)
+    opB = (B.reshape(b_cols, up(b_rows))[:, :b_rows].T if not tb
+           else B.reshape(b_cols, up(b_rows))[:, :b_rows]).astype(np.float64)
+    c0 = C.reshape(n, up(m))[cols, :m].T.astype(np.float64)
+    ref = 1.5 * (opA @ opB[:, cols]) + 0.5 * c0
+    bound = EPS32 * ((k + 1) * 1.5 * (np.abs(opA) @ np.abs(opB[:, cols])) + 0.5 * np.abs(c0))
+    assert np.all(np.abs(outs[0][cols].T.astype(np.float64) - ref) <= bound)
 
 
 @pytest.mark.parametrize("ta", [0, 1])

@@ -264,11 +264,11 @@ struct Stager {
     return v;
   }
 
+  // One 16-byte load for any element-aligned p: CDNA multi-dword global
+  // loads need dword alignment only. Typed with the element's alignment,
+  // since the VEC path also takes fp32 operands that are not 16-byte
+  // aligned.
   __device__ static V load_full(const T *p) {
-    if (VEC) return *reinterpret_cast<const V *>(p);
-    // Only element-aligned (ld not a multiple of VW, or a misaligned base):
-    // CDNA multi-dword global loads need dword alignment only, so this is
-    // still a single 16-byte load.
     typedef T VU __attribute__((ext_vector_type(VW), aligned(sizeof(T))));
     return *reinterpret_cast<const VU *>(p);
   }
@@ -1900,21 +1900,29 @@ int gemm_launch(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64
       return WGB_OK;
     }
   }
-  // VEC: 16-byte aligned operand vectors. That path copies k-tiles straight
-  // into LDS with 32-bit lane offsets from the tile origin, which stay below
-  // 256 * ld * sizeof(T) (a tile spans at most 128 rows or k-rows of ld
-  // elements); larger leading dimensions take the element-aligned register
-  // path (same results, same loads).
+  // VEC: the path that copies k-tiles straight into LDS with 32-bit lane
+  // offsets from the tile origin, which stay below 256 * ld * sizeof(T) (a
+  // tile spans at most 128 rows or k-rows of ld elements); larger leading
+  // dimensions take the register path (same results, same loads). It takes
+  // 16-byte aligned operand vectors, and fp32 operands that are only
+  // element-aligned (ld not a multiple of 4 or a misaligned base: each
+  // 16-byte copy then reads four dword-aligned floats, which CDNA's loads
+  // allow), except NN, whose register path (B staged first) measured
+  // faster there: on config 3's ragged 8191 x 8193 x 4097 (ld = 1 mod 64)
+  // the copies took NT / TN / TT from 4037 / 4015 / 4055 to 3897 / 3879 /
+  // 3895 us per launch and NN from 3992 to 4082.
   const int64_t off_cap = (int64_t)1 << 31;
   const bool offs32 = 256 * lda * (int64_t)sizeof(T) < off_cap && 256 * ldb * (int64_t)sizeof(T) < off_cap;
-  const bool vec = (lda % VW == 0) && (ldb % VW == 0) && aligned16(A) && aligned16(B) && offs32;
+  const bool aligned = (lda % VW == 0) && (ldb % VW == 0) && aligned16(A) && aligned16(B);
+  const bool vec = offs32 && (aligned || (sizeof(T) == 4 && (akc || !bkc)));
   if constexpr (sizeof(T) == 4) {
     // Wide tier: whole 256 x 128 tiles filling whole rounds of two blocks
-    // per CU over a long k (8192^3: 2048 tiles, four rounds), full C only;
+    // per CU over a long k (8192^3: 2048 tiles, four rounds), 16-byte
+    // aligned operands and full C only;
     // everything else (edge tiles, triangles, bands, split-k tails, the
     // two-part k range) stays on the 128 / 64 tiers.
     const int64_t wtiles = (m / kWideM) * (n / kWideN);
-    if (vec && a.c_vec && uplo == 0 && band == wgb::kBandNone && !A2 && m % kWideM == 0 &&
+    if (vec && aligned && a.c_vec && uplo == 0 && band == wgb::kBandNone && !A2 && m % kWideM == 0 &&
         n % kWideN == 0 && k % kWideBK == 0 && k >= 1024 && wtiles > 0 && wtiles % (2 * fill) == 0 &&
         wtiles <= INT32_MAX) {
       a.tiles_m = (int)(m / kWideM);
@@ -1936,7 +1944,8 @@ int gemm_launch(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64
   }
   if (A2) {
     constexpr int BK = 128 / (int)sizeof(T);
-    if (!(vec && aligned16(A2) && aligned16(B2) && k % BK == 0 && akc == bkc && band == wgb::kBandNone)) {
+    if (!(vec && aligned && aligned16(A2) && aligned16(B2) && k % BK == 0 && akc == bkc &&
+          band == wgb::kBandNone)) {
       int st = gemm_launch<T>(ctx, uplo, transA, transB, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc,
                               band, wsrc);
       if (st) return st;

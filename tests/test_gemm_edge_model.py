@@ -9,13 +9,19 @@ element read lies inside the operand matrix for many shapes, leading
 dimensions (down to 1), tile sizes, element types and split-k starting
 tiles: a partly in-range vector overruns its column by at most VW-1 elements
 and at least BK columns follow the last column read this way.
+
+The fp32 LDS copies (Stager::init_copy / load_lds: 16-byte aligned operands,
+and since they also take element-aligned ones, any ld) read the same
+addresses except that a k-contiguous lane reads the 16-byte chunk the LDS
+swizzle places at its slot, chunk kv ^ (row & 7) of its row instead of kv
+(copy_shift); COPY adds that shift.
 """
 import pytest
 
 THREADS = 256
 
 
-def max_read_offset(KC, BT, VW, BK, rows_total, K, ld, kt0):
+def max_read_offset(KC, BT, VW, BK, rows_total, K, ld, kt0, COPY=False):
     """Largest and smallest element offset read by EDGE loads, or None."""
     LOADS, VPK = BT // 32, BT // VW
     KROWS = THREADS // VPK
@@ -33,6 +39,7 @@ def max_read_offset(KC, BT, VW, BK, rows_total, K, ld, kt0):
                 valid = rows_total - row_first
                 nvr = 0 if valid <= 0 else min((valid + 31) // 32, LOADS)
                 fb = base + (rows_total - 1 - row_first) * (r_step // 32)
+                shift = ((kv ^ (row & 7)) - kv) * VW if COPY else 0
             else:
                 mv, kk = t % VPK, t // VPK
                 row_first = row0 + mv * VW
@@ -44,7 +51,7 @@ def max_read_offset(KC, BT, VW, BK, rows_total, K, ld, kt0):
                 for r in range(LOADS):
                     q = base + kt * k_step + r * r_step
                     if KC:
-                        a = q if r < nvr else fb + kt * k_step
+                        a = (q if r < nvr else fb + kt * k_step) + shift
                     else:
                         a = q if vok else fb + kt * k_step + r * r_step
                     lo = a if lo is None else min(lo, a)
@@ -60,13 +67,14 @@ for KC in (True, False):
                 for K in (3 * BK - 1, 4 * BK, 5 * BK + 3):
                     for pad in (0, 1, 64):
                         for kt0 in (0, 1):
-                            CASES.append((KC, BT, VW, BK, rows_total, K, pad, kt0))
+                            for copy in ((False, True) if VW == 4 else (False,)):
+                                CASES.append((KC, BT, VW, BK, rows_total, K, pad, kt0, copy))
 
 
-@pytest.mark.parametrize("KC,BT,VW,BK,rows_total,K,pad,kt0", CASES)
-def test_edge_loads_stay_inside_the_matrix(KC, BT, VW, BK, rows_total, K, pad, kt0):
+@pytest.mark.parametrize("KC,BT,VW,BK,rows_total,K,pad,kt0,copy", CASES)
+def test_edge_loads_stay_inside_the_matrix(KC, BT, VW, BK, rows_total, K, pad, kt0, copy):
     ld = (K if KC else rows_total) + pad
-    lo, hi = max_read_offset(KC, BT, VW, BK, rows_total, K, ld, kt0)
+    lo, hi = max_read_offset(KC, BT, VW, BK, rows_total, K, ld, kt0, copy)
     if lo is None:
         return
     last = (rows_total - 1) * ld + K - 1 if KC else (K - 1) * ld + rows_total - 1

@@ -79,3 +79,20 @@ def test_edge_loads_stay_inside_the_matrix(KC, BT, VW, BK, rows_total, K, pad, k
         return
     last = (rows_total - 1) * ld + K - 1 if KC else (K - 1) * ld + rows_total - 1
     assert lo >= 0 and hi <= last, (lo, hi, last)
+
+
+def copy_chunk(t):
+    """16-byte chunk of its row (0..7 in a 32-float k-tile) that thread t's
+    fp32 LDS copy reads: chunk kv ^ (row & 7) (Stager::init, copy_shift)."""
+    row, kv = t // 8, t % 8
+    return (kv ^ (row & 7))
+
+
+def test_copy_chunks_cover_each_row_k_tile_once():
+    # The 8 lanes of a row copy its 8 chunks of the k-tile, each exactly
+    # once, and never a chunk of another k-tile: so the copies' addresses are
+    # the register path's, permuted inside each row's k-tile (which the
+    # bounds above then cover), and every LDS slot gets its element.
+    for row in range(THREADS // 8):
+        chunks = sorted(copy_chunk(8 * row + kv) for kv in range(8))
+        assert chunks == list(range(8)), (row, chunks)

@@ -161,9 +161,10 @@ def test_beta_zero_ignores_nan_in_c(ctx):
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
 @pytest.mark.parametrize("shape", [(1024, 768, 96), (2048, 4608, 40)])  # 64 / 128 tier (576 tiles)
 def test_epilogue_paths(ctx, variant, ta, dtype, shape):
-    """Whole-vector C epilogue (ldc multiple of the vector width, C 16-byte
-    aligned) against the element-wise one (C one element off alignment), with
-    ld padding kept bit-identical and beta == 0 never reading C."""
+    """C one element off 16-byte alignment against aligned C: fp32 stores
+    whole vectors of rows either way (dword-aligned 16-byte stores), fp64
+    falls back to element-wise stores; ld padding kept bit-identical and
+    beta == 0 never reading C."""
     m, n, k = shape
     ldc = m + 4
     gen = orc.random_f64 if dtype == np.float64 else orc.random_f32

@@ -105,7 +105,7 @@ struct GemmArgs {
   int64_t ldc;
   int tiles_m, tiles_n, ntiles;
   int uplo;   // 0 = full C, WGB_LOWER, WGB_UPPER
-  int c_vec;  // ldc % VW == 0 and C 16-byte aligned: whole-vector C access
+  int c_vec;  // interior tiles store C in vectors (fp32 always; fp64 if C is 16-byte aligned)
   // wgb::kBand*: one operand is triangular (zero outside its triangle), so a
   // tile only needs the k-tiles its nonzero band reaches (never split).
   int band;
@@ -472,8 +472,9 @@ __device__ __forceinline__ int out_col(int b, int lane) {
   return 16 * RW * (b / RW) + RW * i16 + (b % RW);
 }
 
-// Epilogue of a whole interior tile with C accessed in vectors (ldc a
-// multiple of the vector width, C 16-byte aligned). Every lane holds runs of
+// Epilogue of a whole interior tile with C accessed in vectors (fp32: any
+// C; fp64: ldc a multiple of the vector width, C 16-byte aligned; vector
+// types of element alignment). Every lane holds runs of
 // consecutive C rows in one column:
 //   * A mn-contiguous: blocks i = RW h + c (c = 0..RW-1) of register q sit at
 //     rows 16 RW h + RW drow(g, q) + c, a run of RW rows;
@@ -490,7 +491,8 @@ __device__ __forceinline__ void epilogue_vec(const GemmArgs<T> &p,
   const int g = lane >> 4;
   const T alpha = p.alpha, beta = p.beta;
   if constexpr (!AKC) {
-    typedef T VN __attribute__((ext_vector_type(RW)));
+    // element alignment: fp32 C may start anywhere dword-aligned
+    typedef T VN __attribute__((ext_vector_type(RW), aligned(sizeof(T))));
     // fp32 keeps every column block in flight at once; fp64 (accumulators
     // in VGPRs) and ONE_COL go one column block at a time.
     constexpr int JB = (sizeof(T) == 4 && !ONE_COL) ? MN : 1;
@@ -526,7 +528,7 @@ __device__ __forceinline__ void epilogue_vec(const GemmArgs<T> &p,
     }
   } else {
     static_assert(sizeof(T) == 4, "vector epilogue with k-contiguous A is fp32 only");
-    typedef typename Ty<T>::v4 V4;
+    typedef T V4 __attribute__((ext_vector_type(4), aligned(sizeof(T))));
     if constexpr (ONE_COL) {
 #pragma unroll
       for (int j = 0; j < MN; ++j) {
@@ -1876,7 +1878,13 @@ int gemm_launch(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64
   a.B2 = nullptr;
   a.kt_switch = INT32_MAX;
   const int VW = Ty<T>::VW;
-  a.c_vec = (ldc % VW == 0) && aligned16(C);
+  // Interior tiles store C in vectors of consecutive rows. fp32 does so for
+  // any C (a 16-byte store needs dword alignment only, as the loads do);
+  // element-wise stores cost about four times the bytes in partial lines
+  // (config 3's ragged C, ldc = 8193: 1.1 GB written per NN / NT launch
+  // for 0.27 GB of C). fp64 keeps vectors for 16-byte aligned C.
+  const bool c_aligned = (ldc % VW == 0) && aligned16(C);
+  a.c_vec = sizeof(T) == 4 || c_aligned;
   const bool akc = transA == WGB_TRANS;
   const bool bkc = transB == WGB_NO_TRANS;
   const int64_t fill = ctx->num_cus > 0 ? ctx->num_cus : 256;
@@ -1922,7 +1930,7 @@ int gemm_launch(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64
     // everything else (edge tiles, triangles, bands, split-k tails, the
     // two-part k range) stays on the 128 / 64 tiers.
     const int64_t wtiles = (m / kWideM) * (n / kWideN);
-    if (vec && aligned && a.c_vec && uplo == 0 && band == wgb::kBandNone && !A2 && m % kWideM == 0 &&
+    if (vec && aligned && c_aligned && uplo == 0 && band == wgb::kBandNone && !A2 && m % kWideM == 0 &&
         n % kWideN == 0 && k % kWideBK == 0 && k >= 1024 && wtiles > 0 && wtiles % (2 * fill) == 0 &&
         wtiles <= INT32_MAX) {
       a.tiles_m = (int)(m / kWideM);

@@ -64,6 +64,9 @@ int ensure_op_workspace(wgb_ctx *ctx, size_t bytes);
 
 // GEMM k-band: which operand is triangular (zero outside its triangle).
 enum { kBandNone = 0, kBandALower = 1, kBandAUpper = 2, kBandBLower = 3, kBandBUpper = 4 };
+// Order of the diagonal blocks a banded GEMM reads from a side copy
+// (gemm_side_*; trmm's copy of its triangle's diagonal blocks).
+constexpr int kSideBlock = 128;
 
 // One fp32 GEMM on ctx's stream, C = alpha op(A) op(B) + beta C on the uplo
 // part of C (0 = all), without argument checks or timing events.
@@ -74,6 +77,16 @@ int gemm_f32(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64_t 
 int gemm_f64(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64_t n, int64_t k,
              double alpha, const double *A, int64_t lda, const double *B, int64_t ldb,
              double beta, double *C, int64_t ldc, int band);
+// C = alpha op(A) op(B) (beta = 0, full C) with one operand banded (band):
+// that operand's diagonal kSideBlock x kSideBlock blocks are read from
+// `side`, a matrix at the same leading dimension (only those blocks need to
+// hold anything), the rest of it in place. trmm's product.
+int gemm_side_f32(wgb_ctx *ctx, int transA, int transB, int64_t m, int64_t n, int64_t k, float alpha,
+                  const float *A, int64_t lda, const float *B, int64_t ldb, float *C, int64_t ldc,
+                  int band, const float *side);
+int gemm_side_f64(wgb_ctx *ctx, int transA, int transB, int64_t m, int64_t n, int64_t k, double alpha,
+                  const double *A, int64_t lda, const double *B, int64_t ldb, double *C, int64_t ldc,
+                  int band, const double *side);
 // C = alpha (op(A) op(B) + op(A2) op(B2)) + beta C on the uplo part of C,
 // the second pair at the first pair's leading dimensions and transposes:
 // one launch over both k ranges where the kernels allow it (ssyr2k /

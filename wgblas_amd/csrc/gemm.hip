@@ -120,6 +120,13 @@ struct GemmArgs {
   // leading dimensions and at k-tile kt - kt_switch of those.
   const T *A2, *B2;
   int kt_switch;
+  // Banded GEMMs (paired kernels): with band_side set, the banded operand's
+  // diagonal kSideBlock x kSideBlock blocks are read from A2 (band on A) or
+  // B2 (band on B) at the same leading dimension and element coordinates,
+  // everything else from A / B in place (trmm: the caller's triangle stays
+  // where it is; only its diagonal blocks are copied, the other triangle
+  // zeroed in them).
+  int band_side;
 };
 
 constexpr int kThreads = 256;
@@ -190,9 +197,11 @@ struct Stager {
   const T *origin;
   uint32_t voff[LOADS];
   int copy_shift;  // elements from this thread's register-path vector to its copy source
-  // K2: from k-tile ksw on, every address moves by dsw bytes: k-tile kt of
-  // the first operand's addressing becomes k-tile kt - kt_switch of the
-  // second operand (same leading dimension, so the same offsets from it).
+  // K2 (switchable stager): from k-tile ksw on, every address moves by dsw
+  // bytes. Two-part k: k-tile kt of the first operand's addressing becomes
+  // k-tile kt - kt_switch of the second operand (same leading dimension, so
+  // the same offsets from it). Side copy: the same element coordinates in
+  // the second matrix (same leading dimension).
   int ksw;
   int64_t dsw;
 
@@ -200,6 +209,11 @@ struct Stager {
   __device__ void set_switch(const T *P, const T *P2, int kt_switch) {
     ksw = kt_switch;
     dsw = ((const char *)P2 - (const char *)P) - (int64_t)kt_switch * k_step * (int64_t)sizeof(T);
+  }
+  // Side copy: k-tiles from kt_sw on read P2's elements at P's coordinates.
+  __device__ void set_side(const T *P, const T *P2, int kt_sw) {
+    ksw = kt_sw;
+    dsw = (const char *)P2 - (const char *)P;
   }
   __device__ const T *sel(const T *q, int kt) const {
     if constexpr (K2) return kt < ksw ? q : (const T *)((const char *)q + dsw);
@@ -598,7 +612,8 @@ __device__ __forceinline__ void copies_landed_sync() {
 // loop and the epilogue (unit >= 0: a split-k unit's raw partial to ws).
 // NT = 256 threads (2 x 2 waves); every wave owns a square WT x WT part of
 // the tile.
-template <typename T, int BTM, int BTN, int NT, bool AKC, bool BKC, bool VEC, bool K2 = false>
+template <typename T, int BTM, int BTN, int NT, bool AKC, bool BKC, bool VEC, bool K2 = false,
+          bool SIDE = false>
 __device__ __forceinline__ void gemm_tile(const GemmArgs<T> &p, int tm, int tn, int unit, int kt0,
                                           int nkt, T *smem, const int t) {
   typedef typename Ty<T>::acc Acc;
@@ -610,8 +625,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs<T> &p, int tm, int tn, 
   constexpr int WT = BTM / WGM;
   static_assert(WT == BTN / (NT / 64 / WGM), "square wave tiles");
   constexpr int MB = WT / 16;
-  typedef Stager<T, BTM, AKC, VEC, NT, K2> SA;
-  typedef Stager<T, BTN, BKC, VEC, NT, K2> SB;
+  typedef Stager<T, BTM, AKC, VEC, NT, K2 || SIDE> SA;
+  typedef Stager<T, BTN, BKC, VEC, NT, K2 || SIDE> SB;
   constexpr int STAGE = SA::ELEMS + SB::ELEMS;
   const int64_t m0 = (int64_t)tm * BTM, n0 = (int64_t)tn * BTN;
   const int lane = t & 63, wave = t >> 6;
@@ -621,8 +636,39 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs<T> &p, int tm, int tn, 
   // see K - kt0 BK columns.
   SA sa;
   SB sb;
-  sa.init(p.A, p.lda, m0, t, p.m, p.k);
-  sb.init(p.B, p.ldb, n0, t, p.n, p.k);
+  if constexpr (SIDE) {
+    // Banded operand with a side copy of its diagonal blocks: the k-tiles of
+    // this tile's diagonal block come from the copy, the rest in place. A
+    // band that starts at the diagonal (op(A) upper, op(B) lower) reads the
+    // copy first; one that ends there (op(A) lower, op(B) upper) reads it
+    // last. Without a side copy no k-tile switches.
+    constexpr int kSideTiles = wgb::kSideBlock / BK;  // k-tiles per diagonal block
+    const T *PA = p.A, *QA = p.A, *PB = p.B, *QB = p.B;
+    int kswA = INT32_MAX, kswB = INT32_MAX;
+    if (p.band_side) {
+      const int da = (int)(m0 / wgb::kSideBlock), db = (int)(n0 / wgb::kSideBlock);
+      if (p.band == wgb::kBandALower) {
+        QA = p.A2;
+        kswA = da * kSideTiles;
+      } else if (p.band == wgb::kBandAUpper) {
+        PA = p.A2;
+        kswA = (da + 1) * kSideTiles;
+      } else if (p.band == wgb::kBandBLower) {
+        PB = p.B2;
+        kswB = (db + 1) * kSideTiles;
+      } else if (p.band == wgb::kBandBUpper) {
+        QB = p.B2;
+        kswB = db * kSideTiles;
+      }
+    }
+    sa.init(PA, p.lda, m0, t, p.m, p.k);
+    sb.init(PB, p.ldb, n0, t, p.n, p.k);
+    sa.set_side(PA, QA, kswA);
+    sb.set_side(PB, QB, kswB);
+  } else {
+    sa.init(p.A, p.lda, m0, t, p.m, p.k);
+    sb.init(p.B, p.ldb, n0, t, p.n, p.k);
+  }
   if constexpr (K2) {
     sa.set_switch(p.A, p.A2, p.kt_switch);
     sb.set_switch(p.B, p.B2, p.kt_switch);
@@ -1174,7 +1220,7 @@ __global__ __launch_bounds__(kThreads, (VEC || (AKC && BKC) ||
       // out of this loop and held in registers across both tiles.
       int t = (int)threadIdx.x;
       asm volatile("" : "+v"(t));
-      gemm_tile<T, BT, BT, kThreads, AKC, BKC, VEC>(p, tm, tn, -1, lo, hi - lo, smem, t);
+      gemm_tile<T, BT, BT, kThreads, AKC, BKC, VEC, false, true>(p, tm, tn, -1, lo, hi - lo, smem, t);
     }
   }
 }
@@ -1850,7 +1896,7 @@ template <typename T>
 int gemm_launch(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64_t n, int64_t k,
                 T alpha, const T *A, int64_t lda, const T *B, int64_t ldb, T beta, T *C,
                 int64_t ldc, int band, WsSource wsrc = WsSource(), const T *A2 = nullptr,
-                const T *B2 = nullptr) {
+                const T *B2 = nullptr, const T *side = nullptr) {
   if (m == 0 || n == 0) return WGB_OK;
   if (alpha == (T)0 || k == 0) {
     dim3 block(256);
@@ -1877,6 +1923,14 @@ int gemm_launch(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64
   a.A2 = nullptr;
   a.B2 = nullptr;
   a.kt_switch = INT32_MAX;
+  a.band_side = 0;
+  if (side && band != wgb::kBandNone) {
+    // the banded operand's diagonal blocks from `side` (same ld), the rest in place
+    const bool on_a = band == wgb::kBandALower || band == wgb::kBandAUpper;
+    a.band_side = 1;
+    a.A2 = on_a ? side : nullptr;
+    a.B2 = on_a ? nullptr : side;
+  }
   const int VW = Ty<T>::VW;
   // Interior tiles store C in vectors of consecutive rows. fp32 does so for
   // any C (a 16-byte store needs dword alignment only, as the loads do);
@@ -2025,6 +2079,20 @@ int gemm_f64(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64_t 
              double beta, double *C, int64_t ldc, int band) {
   return gemm_launch<double>(ctx, uplo, transA, transB, m, n, k, alpha, A, lda, B, ldb, beta, C,
                              ldc, band);
+}
+
+int gemm_side_f32(wgb_ctx *ctx, int transA, int transB, int64_t m, int64_t n, int64_t k, float alpha,
+                  const float *A, int64_t lda, const float *B, int64_t ldb, float *C, int64_t ldc,
+                  int band, const float *side) {
+  return gemm_launch<float>(ctx, 0, transA, transB, m, n, k, alpha, A, lda, B, ldb, 0.f, C, ldc, band,
+                            WsSource(), nullptr, nullptr, side);
+}
+
+int gemm_side_f64(wgb_ctx *ctx, int transA, int transB, int64_t m, int64_t n, int64_t k, double alpha,
+                  const double *A, int64_t lda, const double *B, int64_t ldb, double *C, int64_t ldc,
+                  int band, const double *side) {
+  return gemm_launch<double>(ctx, 0, transA, transB, m, n, k, alpha, A, lda, B, ldb, 0.0, C, ldc, band,
+                             WsSource(), nullptr, nullptr, side);
 }
 
 int gemm2_f32(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64_t n, int64_t k,

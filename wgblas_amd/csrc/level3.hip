@@ -91,57 +91,36 @@ __global__ __launch_bounds__(256) void symmetrize_kernel(int64_t order, const T 
   }
 }
 
-// W <- A's uplo triangle, zero elsewhere, ones on the diagonal for a unit
-// triangle (src/shaders/triangularize.wgsl builds op(A); W keeps A's own
-// orientation and the GEMM applies transA).
-// A thread writes 4 consecutive rows of W (one 16-byte store in fp32, two
-// in fp64; W's ld is a multiple of 4) in columns blockIdx.y, blockIdx.y + gridDim.y, ...; a row
-// group wholly outside the triangle writes zeros without reading A, and
-// only inside the diagonal kTriBlock x kTriBlock blocks: the banded GEMM
-// that reads W runs each tile row (column) only over the k-tiles up to the
-// end of its diagonal tile, tiles of at most kTriBlock, so the rest of the
-// other triangle is never read (for 4096^2 in fp64 that skips 62 of the
-// 128 MB a full zero fill writes). VEC: lda a multiple of 4 and A aligned
-// to 4 elements (4-element loads).
-constexpr int64_t kTriBlock = 128;
-template <typename T, bool VEC>
-__global__ __launch_bounds__(256) void triangle_copy_kernel(int64_t order,
-                                                            const T *__restrict__ A,
-                                                            int64_t lda, int uplo, int unit,
-                                                            T *__restrict__ W, int64_t ldw) {
-  typedef T F4 __attribute__((ext_vector_type(4)));
-  const int64_t row = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
-  if (row >= order) return;
+// trmm's side copy of its triangle's diagonal blocks (wgblas builds the
+// whole triangle densely, src/shaders/triangularize.wgsl): W (same leading
+// dimension as A, so the banded GEMM reads it at A's element coordinates)
+// receives, inside each kSideBlock x kSideBlock diagonal block only, A's
+// uplo triangle with the other triangle zeroed and, for a unit diagonal,
+// ones on the diagonal. The banded GEMM reads every other block of the
+// triangle in place and never reaches past a tile's diagonal block, so the
+// other triangle outside the diagonal blocks is never read. Block (b, y):
+// columns 8 y .. 8 y + 7 of diagonal block b, each thread 4 rows of one
+// column, its loads issued before any store (one memory latency per block).
+template <typename T>
+__global__ __launch_bounds__(256) void diag_copy_kernel(int64_t order, const T *__restrict__ A,
+                                                        int64_t lda, int uplo, int unit,
+                                                        T *__restrict__ W) {
+  const int64_t b0 = (int64_t)blockIdx.x * wgb::kSideBlock;
+  const int64_t row0 = b0 + 4 * (threadIdx.x % 32);
+  const int64_t col = b0 + 8 * blockIdx.y + threadIdx.x / 32;
+  if (col >= order) return;
   const bool lower = uplo == WGB_LOWER;
-  const int nr = order - row < 4 ? (int)(order - row) : 4;
-  for (int64_t col = blockIdx.y; col < order; col += gridDim.y) {
-    // does any of rows row .. row+nr-1 lie in the triangle (diagonal included)?
-    const bool any = lower ? row + nr - 1 >= col : row <= col;
-    if (!any && row / kTriBlock != col / kTriBlock) continue;  // never read
-    F4 v = F4((T)0);
-    if (any) {
-      const T *a = A + row + col * lda;
-      if (VEC && nr == 4) {
-        v = *reinterpret_cast<const F4 *>(a);
-      } else {
+  T v[4];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) v[c] = a[c < nr ? c : 0];
-      }
+  for (int c = 0; c < 4; ++c) {
+    const int64_t r = row0 + c;
+    const bool keep = r < order && (r == col ? !unit : (lower ? r > col : r < col));
+    v[c] = keep ? A[r + col * lda] : (T)0;  // the other triangle: never used, whatever A holds there
+  }
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int64_t r = row + c;
-        if (r == col)
-          v[c] = unit ? (T)1 : v[c];
-        else if (!(lower ? r > col : r < col))
-          v[c] = (T)0;  // the other triangle: never used, whatever it holds
-      }
-    }
-    T *w = W + row + col * ldw;
-    if (nr == 4) {
-      *reinterpret_cast<F4 *>(w) = v;
-    } else {
-      for (int c = 0; c < nr; ++c) w[c] = v[c];
-    }
+  for (int c = 0; c < 4; ++c) {
+    const int64_t r = row0 + c;
+    if (r < order) W[r + col * lda] = (r == col && unit) ? (T)1 : v[c];
   }
 }
 
@@ -1148,6 +1127,17 @@ int gemm_t(wgb_ctx *ctx, int uplo, int transA, int transB, int64_t m, int64_t n,
                          band);
 }
 
+// C = alpha op(A) op(B), one operand banded, its diagonal blocks from side.
+template <typename T>
+int gemm_side_t(wgb_ctx *ctx, int transA, int transB, int64_t m, int64_t n, int64_t k, T alpha,
+                const T *A, int64_t lda, const T *B, int64_t ldb, T *C, int64_t ldc, int band,
+                const T *side) {
+  if constexpr (sizeof(T) == 4)
+    return wgb::gemm_side_f32(ctx, transA, transB, m, n, k, alpha, A, lda, B, ldb, C, ldc, band, side);
+  else
+    return wgb::gemm_side_f64(ctx, transA, transB, m, n, k, alpha, A, lda, B, ldb, C, ldc, band, side);
+}
+
 // ssyr2k / dsyr2k. fp64 keeps reference BLAS's quick return
 // (src/dsyr2k/dsyr2k.mjs:172-174): alpha = 0 or k = 0 with beta = 1 leaves C.
 template <typename T>
@@ -1241,9 +1231,11 @@ int symm(wgb_ctx *ctx, int side, int uplo, int transB, int64_t m, int64_t n, T a
   return WGB_OK;
 }
 
-// strmm / dtrmm: the triangle copied with zeros elsewhere, B copied, one
-// GEMM whose tiles run only the k-tiles the triangle reaches (banded tiles;
-// wgblas's dtrmm multiplies the whole copy, src/dtrmm/dtrmm.mjs:21-27).
+// strmm / dtrmm: B copied, the triangle's diagonal blocks copied with zeros
+// in the other triangle, one GEMM whose tiles run only the k-tiles the
+// triangle reaches (banded tiles), reading the triangle in place outside its
+// diagonal blocks (wgblas's dtrmm multiplies a whole dense copy,
+// src/dtrmm/dtrmm.mjs:21-27).
 template <typename T>
 int trmm(wgb_ctx *ctx, int side, int uplo, int transA, int diag, int64_t m, int64_t n, T alpha,
          const T *A, int64_t lda, T *B, int64_t ldb) {
@@ -1259,28 +1251,24 @@ int trmm(wgb_ctx *ctx, int side, int uplo, int transA, int diag, int64_t m, int6
   } else {
     const bool left = side == WGB_LEFT;
     const int64_t order = left ? m : n;
-    const int64_t ldw = round4(order), ldbc = round4(m);
-    if ((st = wgb::ensure_op_workspace(ctx, (size_t)(ldw * order + ldbc * n) * sizeof(T)))) return st;
+    // W: the triangle's diagonal blocks at A's leading dimension; Bc: B's
+    // copy (the product overwrites B), 16-byte aligned after W
+    const int64_t wlen = round4(lda * order), ldbc = round4(m);
+    if ((st = wgb::ensure_op_workspace(ctx, (size_t)(wlen + ldbc * n) * sizeof(T)))) return st;
     T *W = static_cast<T *>(ctx->op_ws);
-    T *Bc = W + ldw * order;  // 16-byte aligned: ldw is a multiple of 4
-    const int64_t gy = order < 4096 ? order : 4096;
-    const dim3 grid((unsigned)((order + 1023) / 1024), (unsigned)gy);
-    // VEC loads 4 elements at once: A aligned to 4 elements (16 or 32 bytes)
-    if (lda % 4 == 0 && ((uintptr_t)A % (4 * sizeof(T))) == 0)
-      triangle_copy_kernel<T, true><<<grid, 256, 0, ctx->stream>>>(order, A, lda, uplo,
-                                                                   diag == WGB_UNIT, W, ldw);
-    else
-      triangle_copy_kernel<T, false><<<grid, 256, 0, ctx->stream>>>(order, A, lda, uplo,
-                                                                    diag == WGB_UNIT, W, ldw);
-    WGB_CHECK_LAUNCH("triangle_copy_kernel");
+    T *Bc = W + wlen;
+    const int64_t nblk = (order + wgb::kSideBlock - 1) / wgb::kSideBlock;
+    diag_copy_kernel<T><<<dim3((unsigned)nblk, wgb::kSideBlock / 8), 256, 0, ctx->stream>>>(
+        order, A, lda, uplo, diag == WGB_UNIT, W);
+    WGB_CHECK_LAUNCH("diag_copy_kernel");
     WGB_CHECK_HIP(hipMemcpy2DAsync(Bc, (size_t)ldbc * sizeof(T), B, (size_t)ldb * sizeof(T),
                                    (size_t)m * sizeof(T), (size_t)n, hipMemcpyDeviceToDevice,
                                    ctx->stream));
     const bool op_lower = (uplo == WGB_LOWER) != (transA == WGB_TRANS);
-    st = left ? gemm_t<T>(ctx, 0, transA, WGB_NO_TRANS, m, n, m, alpha, W, ldw, Bc, ldbc, (T)0, B,
-                          ldb, op_lower ? wgb::kBandALower : wgb::kBandAUpper)
-              : gemm_t<T>(ctx, 0, WGB_NO_TRANS, transA, m, n, n, alpha, Bc, ldbc, W, ldw, (T)0, B,
-                          ldb, op_lower ? wgb::kBandBLower : wgb::kBandBUpper);
+    st = left ? gemm_side_t<T>(ctx, transA, WGB_NO_TRANS, m, n, m, alpha, A, lda, Bc, ldbc, B, ldb,
+                               op_lower ? wgb::kBandALower : wgb::kBandAUpper, W)
+              : gemm_side_t<T>(ctx, WGB_NO_TRANS, transA, m, n, n, alpha, Bc, ldbc, A, lda, B, ldb,
+                               op_lower ? wgb::kBandBLower : wgb::kBandBUpper, W);
   }
   if (st) return st;
   wgb::timing_end(ctx);

@@ -54,6 +54,11 @@ module.exports = {
     const src = ctxOf(c).buffers.get(b.buf);
     new Uint8Array(arr.buffer, arr.byteOffset, arr.byteLength).set(src.subarray(0, arr.byteLength));
   },
-  // for the test: which contexts are alive / were destroyed
-  _stub: { live: () => [...live.keys()], destroyed: () => destroyed.slice() },
+  // for the tests: which contexts are alive / were destroyed, and a
+  // buffer's bytes (cpu_addon.cjs computes on them)
+  _stub: {
+    live: () => [...live.keys()],
+    destroyed: () => destroyed.slice(),
+    bytes: (c, b) => ctxOf(c).buffers.get(b.buf),
+  },
 };

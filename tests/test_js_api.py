@@ -18,7 +18,10 @@ benchmark-mode cases (a second device, cleanup of one device) to the same
 parity cases. Both GPU processes are skipped: each once ended in a SIGSEGV
 during node's process teardown, after every case had passed, with no GPU
 fault, and the cause is not shown. The C ABI under them runs on the GPU from
-pytest (every test_gpu_*.py, test_gpu_contexts.py for the device handling).
+pytest (every test_gpu_*.py, test_gpu_contexts.py for the device handling),
+and both suites run on the CPU through the JS layer's own routines with
+cpu_addon.cjs, a host-memory stand-in for the whole addon, which also fails
+them on a planted mistake.
 """
 import os
 import shutil
@@ -82,6 +85,44 @@ def test_js_random_matches_reference_golden():
 def test_js_package_subpaths_resolve_with_declarations():
     out = run_node("package_exports.mjs")
     assert int(out.strip().splitlines()[-1].split()[0]) > 30
+
+
+def _stand_in(script, *args, plant=None):
+    env = dict(os.environ, WGBLAS_HIP_ADDON=os.path.join(ROOT, "tests", "js", "cpu_addon.cjs"))
+    if plant:
+        env["CPU_ADDON_PLANT"] = plant
+    return subprocess.run([NODE, os.path.join(ROOT, "tests", "js", script), *args], cwd=ROOT, env=env,
+                          capture_output=True, text=True, timeout=600)
+
+
+@pytest.mark.parametrize("script,args,minimum", [("validation.mjs", ("--gpu",), 2541 + 250),
+                                                 ("gpu_api.mjs", (), 280)])
+def test_js_gpu_suites_through_a_cpu_stand_in_addon(script, args, minimum):
+    """The two node GPU suites (skipped on the GPU, below) through the JS
+    layer's own routines, with cpu_addon.cjs in place of the Node-API addon:
+    a host-memory stand-in for every addon call that computes in float64
+    under the C ABI's semantics. Every case the GPU run holds (the
+    reference's edge cases and validation specs, GpuMatrix / GpuVector
+    residency in both layouts with ld padding, the parity fixtures, the
+    random fixtures under the reference's metrics, init's cache, cleanup of
+    one device, benchmark mode's gpuTimeMs) must pass: the JS layer maps
+    each call onto the C ABI correctly. The kernels behind the C ABI are the
+    pytest GPU suites' part."""
+    res = _stand_in(script, *args)
+    tail = "\n".join((res.stdout + res.stderr).splitlines()[-20:])
+    assert res.returncode == 0 and " 0 failed" in res.stdout, tail
+    assert int(res.stdout.strip().splitlines()[-1].split()[0]) >= minimum, tail
+
+
+@pytest.mark.parametrize("plant", ["trans", "uplo", "amax"])
+def test_js_cpu_stand_in_suite_fails_on_a_planted_mistake(plant):
+    """The same run with one mistake planted in the stand-in (gemm reading
+    op(A) as A, triangle routines writing the whole of C, isamax keeping the
+    last of equal magnitudes) fails: the suite checks results, so a wrong
+    mapping in the JS layer would fail it the same way."""
+    res = _stand_in("validation.mjs", "--gpu", plant=plant)
+    last = res.stdout.strip().splitlines()[-1]
+    assert res.returncode != 0 and int(last.split()[2]) > 0, last
 
 
 @pytest.mark.gpu
